@@ -1,0 +1,162 @@
+/*
+ * qmla.h -- C ABI of libqmla.so, the gfx950 (MI355X) absorbed-MLA latent-KV decode library.
+ *
+ * Plain pointers, sizes and strides only. Every entry point is asynchronous on the stream it is
+ * given, allocates nothing, never synchronizes the device, and returns 0 or a negative QMLA_ERR_*
+ * code (no exceptions cross the boundary). Safe to record into a HIP graph: no host reads of
+ * device data, no memsets.
+ *
+ * Reference interfaces replaced (paths relative to the reference repository):
+ *   qmla_decode           <- decode_attention_fwd(q, k_buffer, v_buffer, o, lse, req_to_token,
+ *                            b_seq_len, attn_logits, num_kv_splits, sm_scale, page_size, logit_cap,
+ *                            k_scale, v_scale, is_mla, rms_offset, rms_bf16, rms_log8, qrows)
+ *                            qwen_mla/ops/mla_decode_attention.py:1264-1359 (stage 1 :297-586,
+ *                            stage 2 :1064-1181), and the FlashInfer run() it dispatches to instead
+ *                            qwen_mla/fi_decode.py:338-384 / kernels/qwen_mla.cuh:1386-1480
+ *   qmla_decode_2pass     <- _decode_mla_two_pass qwen_mla/ops/mla_decode_attention.py:778-849
+ *                            (_mla2p_scores_kernel :602-678, _mla2p_pv_kernel :681-764)
+ *   qmla_combine          <- _decode_softmax_reducev_fwd / _fwd_kernel_stage2
+ *                            qwen_mla/ops/mla_decode_attention.py:1064-1181
+ *   qmla_workspace_bytes  <- the split-K scratch sizing of splitk_cap / splitk_reserve_bytes
+ *                            qwen_mla/mla_impl.py:89-111 and _RankPlan._workspace_bytes
+ *                            qwen_mla/fi_decode.py:170-179
+ *   qmla_cache_write_fp8  <- QwenMLATritonImpl.do_kv_cache_update qwen_mla/mla_impl.py:309-342
+ *   qmla_gather_cache     <- gather_cache_torch qwen_mla/ops/mla_gather.py:28-76
+ */
+#ifndef QMLA_H
+#define QMLA_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define QMLA_ABI_VERSION 1
+
+/* error codes */
+#define QMLA_OK 0
+#define QMLA_ERR_NULL (-1)        /* a required pointer is NULL */
+#define QMLA_ERR_SHAPE (-2)       /* unsupported or inconsistent dimension */
+#define QMLA_ERR_ALIGN (-3)       /* a row, page or base address is not 16-byte aligned */
+#define QMLA_ERR_WORKSPACE (-4)   /* workspace missing or smaller than qmla_workspace_bytes() */
+#define QMLA_ERR_MODE (-5)        /* unknown dtype / rms mode / split mode */
+#define QMLA_ERR_LAUNCH (-6)      /* the HIP launch itself failed */
+#define QMLA_ERR_NOKERNEL (-7)    /* no compiled kernel instance for this shape */
+
+/* cache element formats */
+#define QMLA_KV_BF16 0
+#define QMLA_KV_FP8 1             /* OCP e4m3fn, one per-layer scale for latent and rope */
+
+/* rms (score divisor) tail formats, qwen_mla/mla_impl.py:125-145 and
+ * qwen_mla/ops/mla_decode_attention.py:466-505 */
+#define QMLA_RMS_NONE 0           /* rms_offset < 0: no divide */
+#define QMLA_RMS_BF16 1           /* bf16 cache: one bf16 element per head */
+#define QMLA_RMS_LOG8 2           /* fp8 cache: uint8 code c, rms = 2^(-3 + c*6/255) */
+#define QMLA_RMS_BF16_BYTES 3     /* fp8 cache: two bytes per head holding a raw bf16 */
+#define QMLA_RMS_E4M3 4           /* fp8 cache: one e4m3 byte per head, times k_scale */
+
+/* output / lse element types */
+#define QMLA_DT_BF16 0
+#define QMLA_DT_F32 1
+#define QMLA_DT_F16 2
+
+/*
+ * One decode call. Dimensions:
+ *   rows       query rows as the caller flattened them (one per decode token; spec-verify
+ *              requests contribute qrows consecutive rows sharing a block-table row, as built by
+ *              MLATritonMetadataBuilder._build_decode, qwen_mla/mla_impl.py:628-662)
+ *   heads      query heads per row; rms_heads rms slots per cached token (normally == heads)
+ *   d_c        latent columns (kv_lora_rank); with groups = G > 1 (GLA) head h reads only the
+ *              d_c/G columns of group h / (heads/G), and out holds d_c/G columns per head
+ *   rope_w     rope columns after the latent; scores read cache columns [0, d_c + rope_w)
+ * Strides are in ELEMENTS of the tensor they index (cache strides in cache elements).
+ */
+typedef struct qmla_decode_params {
+  /* queries (bf16): q_nope [rows, heads, d_c/G], q_pe [rows, heads, rope_w] */
+  const void* q_nope;
+  int64_t q_nope_stride_row, q_nope_stride_head;
+  const void* q_pe;
+  int64_t q_pe_stride_row, q_pe_stride_head;
+
+  /* paged cache [num_pages, page_size, (1,) row]: element (page, slot, col) at
+   * kv_cache + page*page_stride + slot*token_stride + col */
+  const void* kv_cache;
+  int64_t page_stride, token_stride;
+  int32_t kv_dtype;               /* QMLA_KV_* */
+  int32_t page_size;
+  int32_t d_c, rope_w;
+  int32_t rms_offset;             /* element offset of the rms tail in the row, < 0 = none */
+  int32_t rms_mode;               /* QMLA_RMS_* */
+  const float* k_scale;           /* device fp32 scalar, NULL = 1.0 (fp8 dequant and e4m3 rms) */
+  float sm_scale;
+  float logit_cap;                /* > 0: cap * tanh(s / cap) after scaling */
+
+  /* block table [rows, bt_stride] int32 and seq_lens [rows] int32 (device) */
+  const int32_t* block_table;
+  int64_t bt_stride;
+  const int32_t* seq_lens;
+  int32_t rows, heads, rms_heads;
+  int32_t qrows;                  /* > 1: fold each run of qrows rows into one request so the
+                                     cache is read once; row j of a request of length L sees
+                                     its first L - (qrows-1-j) tokens */
+  int32_t groups;                 /* latent groups (1, or 2 for GLA-g2) */
+
+  /* outputs: out [rows, heads, d_c/G] (out_dtype), lse [rows, heads] (lse_dtype, may be NULL),
+   * natural-log LSE */
+  void* out;
+  int64_t out_stride_row, out_stride_head;
+  int32_t out_dtype;
+  void* lse;
+  int64_t lse_stride_row;
+  int32_t lse_dtype;
+
+  /* split-K. num_splits > 0: the reference's fixed split count; split s of a request of length
+   * L covers [s*per, min((s+1)*per, L)) with per = ceil(ceil(L/S)/split_align)*split_align
+   * (split_align 0 = no rounding), and the partials live in the caller's workspace in the
+   * reference layout attn_logits[rows, heads, S, d_c/G + 1] (strides below, in floats).
+   * num_splits == 0: balanced mode. Every workgroup gets the same number of 64-token tiles
+   * across request boundaries; partials go to the workspace at qmla_workspace_bytes() size and
+   * the ws_stride_* fields are ignored. */
+  int32_t num_splits;
+  int32_t split_align;
+  float* workspace;
+  size_t workspace_bytes;
+  int64_t ws_stride_row, ws_stride_head, ws_stride_split;
+
+  /* balanced mode only: workgroups to launch, 0 = one per compute unit times occupancy */
+  int32_t num_workgroups;
+} qmla_decode_params;
+
+/* ABI version (QMLA_ABI_VERSION) and a static build string. */
+int qmla_version(void);
+const char* qmla_build_info(void);
+
+/* Workspace bytes qmla_decode needs for these params (0 when no workspace is needed). For
+ * num_splits > 0 this is rows*heads*num_splits*(d_c/G + 1)*4; for balanced mode it covers the
+ * maximum number of partial segments. Pure host arithmetic, no device access except the
+ * compute-unit count of the current device (queried once). */
+size_t qmla_workspace_bytes(const qmla_decode_params* p);
+
+/* Decode: scores, online softmax and P.V over the paged latent rows (split-K partials where the
+ * split mode needs them) followed by the LSE combine, all on `stream` (a hipStream_t). */
+int qmla_decode(const qmla_decode_params* p, void* stream);
+
+/* The two passes alone, reference-shaped: the partial (stage 1) pass writes attn_logits in the
+ * workspace; qmla_combine (stage 2) merges them into out / lse. Fixed-split mode only. */
+int qmla_decode_partial(const qmla_decode_params* p, void* stream);
+int qmla_combine(const qmla_decode_params* p, void* stream);
+
+/* Wide-latent two-pass decode (scores pass into fp32 scratch, then P.V over latent column
+ * slices), fixed-split mode, followed by the combine. scratch must hold
+ * qmla_decode_2pass_scratch_bytes(p) bytes. */
+size_t qmla_decode_2pass_scratch_bytes(const qmla_decode_params* p, int64_t max_tokens);
+int qmla_decode_2pass(const qmla_decode_params* p, void* scratch, size_t scratch_bytes,
+                      int64_t max_tokens, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* QMLA_H */

@@ -1,0 +1,383 @@
+"""CPU oracle for absorbed-MLA latent-KV decode attention.
+
+TEST INFRASTRUCTURE ONLY. This module is the checker, never the product: only the test suite
+(`tests/`), `__graft_entry__.smoke()` and the `cpu_baseline` leg of `bench.py` may import it. The
+product path (`qmla`) never calls it and fails loudly when its HIP library is missing.
+
+It restates, on the CPU, the arithmetic of the reference plugin's decode path:
+
+* paged cache rows `[latent d_c | rope W | rms tail | pad]` addressed through a block table
+  (ops/mla_decode_attention.py:412-440, mla_impl.py:148-165);
+* the per-(token, head) score divisor in its four storage modes
+  (ops/mla_decode_attention.py:466-505, mla_impl.py:125-145);
+* FP8 e4m3fn latent/rope with one per-layer scale (ops/mla_decode_attention.py:451-463,
+  mla_impl.py:309-342);
+* scores `(q_lat.c + q_pe.r) / rms * sm_scale`, optional tanh cap, softmax, `o = P.c`, natural-log
+  LSE (ops/mla_decode_attention.py:453-586, :1125-1137; tests/test_decode_numerics.py:25-44);
+* split-KV partials and their LSE combine with the reference's tile-aligned split bounds
+  (ops/mla_decode_attention.py:383-396, :1097-1137);
+* spec-verify row flattening (mla_impl.py:628-662) and the grouped-latent (GLA) head/column mapping
+  (mla_impl.py:182-194, qwen3_5_mla.py:58-73);
+* the FP8 cache-row writer (mla_impl.py:309-342) and the prefill context gather
+  (ops/mla_gather.py:28-76).
+
+Floating-point work runs in float32 torch on the CPU; byte work (e4m3fn and log8 codes) is numpy
+bit arithmetic. Every function is pinned by tests against closed forms, brute force on tiny
+inputs, torch's own float8_e4m3fn conversion, and the known answers quoted in the reference's
+docstrings and tests (tests/test_oracle_*.py).
+"""
+from __future__ import annotations
+
+import math
+
+import numpy as np
+import torch
+
+# rms log8 code range: rms = 2 ** (LO + code * (HI - LO) / 255)  (mla_impl.py:132)
+RMS_LOG2_LO, RMS_LOG2_HI = -3.0, 3.0
+E4M3_MAX = 448.0
+
+KV_BF16, KV_FP8 = "bf16", "fp8"
+# rms tail formats: one bf16 element per head in a bf16 cache; for an FP8 cache a uint8 log2 code,
+# two raw bf16 bytes, or one e4m3 byte scaled like the row (mla_impl.py:125-145).
+RMS_NONE, RMS_BF16, RMS_LOG8, RMS_BF16_BYTES, RMS_E4M3 = "none", "bf16", "log8", "bf16_bytes", "e4m3"
+
+
+# ------------------------------------------------------------------------------------------------
+# e4m3fn (OCP FP8: 1 sign, 4 exponent bits with bias 7, 3 mantissa bits, no inf, NaN = S.1111.111)
+# ------------------------------------------------------------------------------------------------
+def _e4m3_table() -> np.ndarray:
+    t = np.zeros(256, dtype=np.float32)
+    for b in range(256):
+        s = -1.0 if b & 0x80 else 1.0
+        e = (b >> 3) & 0xF
+        m = b & 7
+        if e == 15 and m == 7:
+            t[b] = np.nan
+        elif e == 0:
+            t[b] = s * (m / 8.0) * 2.0 ** -6
+        else:
+            t[b] = s * (1.0 + m / 8.0) * 2.0 ** (e - 7)
+    return t
+
+
+E4M3_TABLE = _e4m3_table()
+
+
+def e4m3_decode(b: np.ndarray) -> np.ndarray:
+    """uint8 e4m3fn codes -> float32 values (exact)."""
+    return E4M3_TABLE[np.asarray(b, dtype=np.uint8)]
+
+
+def e4m3_encode(x: np.ndarray) -> np.ndarray:
+    """float32 values already clamped to [-448, 448] -> e4m3fn codes, round to nearest even.
+
+    Restates `.to(torch.float8_e4m3fn)` after the writer's clamp (mla_impl.py:331-332). Works in
+    float64 so every step is exact; NaN inputs map to 0x7F.
+    """
+    x = np.asarray(x, dtype=np.float32).astype(np.float64)
+    out = np.zeros(x.shape, dtype=np.uint8)
+    sign = np.where(np.signbit(x), 0x80, 0).astype(np.uint8)
+    a = np.abs(x)
+    nan = np.isnan(a)
+    a = np.where(nan, 0.0, np.minimum(a, E4M3_MAX))
+    # subnormal grid: multiples of 2^-9 below 2^-6
+    sub = a < 2.0 ** -6
+    q_sub = np.rint(a / 2.0 ** -9)                      # 0..8; 8 rounds up to the first normal
+    code_sub = q_sub.astype(np.int64)                   # exponent field 0 (or 1 when q_sub == 8)
+    # normal: a = 2^e * (1 + m/8), e in [-6, 8]
+    with np.errstate(divide="ignore"):
+        e = np.floor(np.log2(np.where(sub, 1.0, a)))
+    e = np.clip(e, -6, 8)
+    frac = np.where(sub, 0.0, a / 2.0 ** e)             # in [1, 2)
+    q = np.rint((frac - 1.0) * 8.0)                     # 0..8
+    carry = q >= 8
+    e = np.where(carry, e + 1, e)
+    q = np.where(carry, 0, q)
+    code_norm = ((e + 7).astype(np.int64) << 3) | q.astype(np.int64)
+    code_norm = np.minimum(code_norm, 0x7E)             # 448 is the largest finite value
+    code = np.where(sub, code_sub, code_norm)
+    out = (code.astype(np.uint8) | sign)
+    out = np.where(nan, np.uint8(0x7F), out).astype(np.uint8)
+    return out
+
+
+def f32_to_bf16_bits(x: np.ndarray) -> np.ndarray:
+    """float32 -> bfloat16 bit patterns, round to nearest even (NaN kept quiet)."""
+    u = np.asarray(x, dtype=np.float32).view(np.uint32).astype(np.uint64)
+    rounded = (u + 0x7FFF + ((u >> 16) & 1)) >> 16
+    nan = np.isnan(np.asarray(x, dtype=np.float32))
+    rounded = np.where(nan, (u >> 16) | 0x40, rounded)
+    return rounded.astype(np.uint16)
+
+
+def bf16_bits_to_f32(b: np.ndarray) -> np.ndarray:
+    return (np.asarray(b, dtype=np.uint16).astype(np.uint32) << 16).view(np.float32)
+
+
+# ------------------------------------------------------------------------------------------------
+# rms divisor codes
+# ------------------------------------------------------------------------------------------------
+def log8_encode(rms: np.ndarray) -> np.ndarray:
+    """rms (float32) -> uint8 code, as the FP8 row writer stores it (mla_impl.py:333-336).
+
+    `(log2(max(rms, 1e-30)) - LO) * (255 / (HI - LO))`, rounded half-to-even, clamped to [0, 255].
+    The products and the subtraction are float32 operations as in the writer; log2 is evaluated
+    correctly rounded to float32 (through float64).
+    """
+    r = np.maximum(np.asarray(rms, dtype=np.float32), np.float32(1e-30))
+    lg = np.log2(r.astype(np.float64)).astype(np.float32)
+    code = (lg - np.float32(RMS_LOG2_LO)) * np.float32(255.0 / (RMS_LOG2_HI - RMS_LOG2_LO))
+    return np.clip(np.rint(code.astype(np.float32)), 0, 255).astype(np.uint8)
+
+
+def log8_decode(code: np.ndarray) -> np.ndarray:
+    """uint8 code -> rms = 2^(-3 + code * 6/255) (ops/mla_decode_attention.py:470-479)."""
+    c = np.asarray(code, dtype=np.float64)
+    return np.exp2(RMS_LOG2_LO + c * ((RMS_LOG2_HI - RMS_LOG2_LO) / 255.0)).astype(np.float32)
+
+
+# ------------------------------------------------------------------------------------------------
+# paged rows
+# ------------------------------------------------------------------------------------------------
+def gather_rows(cache_u8: torch.Tensor, block_table: torch.Tensor, b: int, length: int,
+                page_size: int) -> torch.Tensor:
+    """Rows [length, row_bytes] of sequence b: token n lives at page block_table[b, n // P],
+    slot n % P (ops/mla_decode_attention.py:412-440)."""
+    if length == 0:
+        return cache_u8.new_zeros((0, cache_u8.shape[-1]))
+    n = torch.arange(length)
+    pages = block_table[b, n // page_size].long()
+    return cache_u8[pages, n % page_size]
+
+
+def dequant_rows(rows: torch.Tensor, *, d_c: int, rope_w: int, kv: str, k_scale: float):
+    """Latent and rope of each row as float32. fp8 rows decode e4m3fn and multiply by the one
+    per-layer scale shared by latent and rope (ops/mla_decode_attention.py:451-463)."""
+    if kv == KV_BF16:
+        el = rows.contiguous().view(torch.bfloat16).float()
+        return el[:, :d_c], el[:, d_c:d_c + rope_w]
+    vals = torch.from_numpy(e4m3_decode(rows[:, :d_c + rope_w].numpy())) * np.float32(k_scale)
+    return vals[:, :d_c], vals[:, d_c:d_c + rope_w]
+
+
+def decode_rms(rows: torch.Tensor, *, rms_offset: int, n_heads: int, kv: str, mode: str,
+               k_scale: float) -> torch.Tensor:
+    """Per-(token, head) divisor [L, n_heads] in float32; rms <= 0 reads as 1
+    (ops/mla_decode_attention.py:466-505). rms_offset is in cache elements."""
+    L = rows.shape[0]
+    if mode == RMS_NONE:
+        return torch.ones(L, n_heads)
+    if kv == KV_BF16:
+        assert mode == RMS_BF16
+        el = rows.contiguous().view(torch.bfloat16).float()
+        r = el[:, rms_offset:rms_offset + n_heads]
+    elif mode == RMS_LOG8:
+        r = torch.from_numpy(log8_decode(rows[:, rms_offset:rms_offset + n_heads].numpy()))
+    elif mode == RMS_BF16_BYTES:
+        raw = rows[:, rms_offset:rms_offset + 2 * n_heads].contiguous()
+        r = raw.view(torch.bfloat16).float()
+    elif mode == RMS_E4M3:
+        r = torch.from_numpy(e4m3_decode(rows[:, rms_offset:rms_offset + n_heads].numpy())) * np.float32(k_scale)
+    else:
+        raise ValueError(mode)
+    return torch.where(r > 0, r, torch.ones_like(r))
+
+
+# ------------------------------------------------------------------------------------------------
+# decode
+# ------------------------------------------------------------------------------------------------
+def _scores(q_lat, q_pe, c, r, rms, sm_scale, logit_cap):
+    """[H, L] scores: divide by rms, then scale, then optional tanh cap
+    (ops/mla_decode_attention.py:453-514)."""
+    s = q_lat @ c.T
+    if q_pe is not None and q_pe.shape[-1]:
+        s = s + q_pe @ r.T
+    s = s / rms.T
+    s = s * sm_scale
+    if logit_cap > 0:
+        s = logit_cap * torch.tanh(s / logit_cap)
+    return s
+
+
+def mla_decode(q_lat: torch.Tensor, q_pe: torch.Tensor | None, cache_u8: torch.Tensor,
+               block_table: torch.Tensor, seq_lens: torch.Tensor, *, page_size: int, d_c: int,
+               rope_w: int, rms_offset: int, kv: str, rms_mode: str, k_scale: float = 1.0,
+               sm_scale: float, logit_cap: float = 0.0, rms_heads: int | None = None,
+               groups: int = 1, rms_head_of_row=None):
+    """Full (unsplit) decode for every query row.
+
+    q_lat [R, H, d_c/groups] absorbed latent queries, q_pe [R, H, W] rope queries. Row i attends to
+    the first seq_lens[i] tokens of block_table[i]. With `groups` > 1 (GLA) head h belongs to group
+    g = h // (H/groups) and reads latent columns [g*d_c/G, (g+1)*d_c/G) for both scores and values
+    (mla_impl.py:182-194). `rms_head_of_row(h)` maps a query head to its rms slot (default h).
+    Returns o [R, H, d_c/groups] and natural-log lse [R, H], float32.
+    """
+    R, H, dcg = q_lat.shape
+    assert dcg * groups == d_c
+    n_rms = rms_heads if rms_heads is not None else H
+    hpg = H // groups
+    o = torch.zeros(R, H, dcg)
+    lse = torch.full((R, H), -math.inf)
+    for i in range(R):
+        L = int(seq_lens[i])
+        if L <= 0:
+            continue
+        rows = gather_rows(cache_u8, block_table, i, L, page_size)
+        c, r = dequant_rows(rows, d_c=d_c, rope_w=rope_w, kv=kv, k_scale=k_scale)
+        rms = decode_rms(rows, rms_offset=rms_offset, n_heads=n_rms, kv=kv, mode=rms_mode,
+                         k_scale=k_scale)
+        heads = torch.arange(H)
+        rh = heads if rms_head_of_row is None else torch.tensor([rms_head_of_row(int(h)) for h in heads])
+        rms_h = rms[:, rh]
+        for g in range(groups):
+            hs = slice(g * hpg, (g + 1) * hpg)
+            cg = c[:, g * dcg:(g + 1) * dcg]
+            s = _scores(q_lat[i, hs].float(), None if q_pe is None else q_pe[i, hs].float(), cg, r,
+                        rms_h[:, hs], sm_scale, logit_cap)
+            m = s.max(dim=-1, keepdim=True).values
+            p = torch.exp(s - m)
+            l = p.sum(-1, keepdim=True)
+            o[i, hs] = (p @ cg) / l
+            lse[i, hs] = (m + torch.log(l)).squeeze(-1)
+    return o, lse
+
+
+def split_bounds(L: int, num_splits: int, align: int) -> list[tuple[int, int]]:
+    """[start, end) of each split: per = ceil(ceil(L/S)/align)*align when align > 0, else
+    ceil(L/S); empty splits have end <= start (ops/mla_decode_attention.py:389-396, :1101-1108)."""
+    per = -(-L // num_splits)
+    if align > 0:
+        per = -(-per // align) * align
+    out = []
+    for s in range(num_splits):
+        a = per * s
+        out.append((a, min(a + per, L)))
+    return out
+
+
+def mla_decode_partials(q_lat, q_pe, cache_u8, block_table, seq_lens, *, num_splits: int, align: int,
+                        page_size, d_c, rope_w, rms_offset, kv, rms_mode, k_scale=1.0, sm_scale,
+                        logit_cap=0.0):
+    """Split-KV partials in the reference workspace format [R, H, S, d_c + 1]: normalized partial
+    output in [..., :d_c] and the split's natural-log LSE in [..., d_c]
+    (ops/mla_decode_attention.py:562-586). Empty splits stay NaN (never written)."""
+    R, H, _ = q_lat.shape
+    att = torch.full((R, H, num_splits, d_c + 1), math.nan)
+    for i in range(R):
+        L = int(seq_lens[i])
+        rows_all = gather_rows(cache_u8, block_table, i, L, page_size)
+        c_all, r_all = dequant_rows(rows_all, d_c=d_c, rope_w=rope_w, kv=kv, k_scale=k_scale)
+        rms_all = decode_rms(rows_all, rms_offset=rms_offset, n_heads=H, kv=kv, mode=rms_mode, k_scale=k_scale)
+        for s_idx, (a, e) in enumerate(split_bounds(L, num_splits, align)):
+            if e <= a:
+                continue
+            s = _scores(q_lat[i].float(), None if q_pe is None else q_pe[i].float(), c_all[a:e],
+                        r_all[a:e], rms_all[a:e], sm_scale, logit_cap)
+            m = s.max(-1, keepdim=True).values
+            p = torch.exp(s - m)
+            l = p.sum(-1, keepdim=True)
+            att[i, :, s_idx, :d_c] = (p @ c_all[a:e]) / l
+            att[i, :, s_idx, d_c] = (m + torch.log(l)).squeeze(-1)
+    return att
+
+
+def combine_partials(att: torch.Tensor, seq_lens: torch.Tensor, *, num_splits: int, align: int):
+    """LSE-weighted merge of split partials, skipping empty splits with the same bounds as the
+    partial pass (ops/mla_decode_attention.py:1097-1137). Returns o [R, H, Dv], lse [R, H]."""
+    R, H, S, D1 = att.shape
+    dv = D1 - 1
+    o = torch.zeros(R, H, dv)
+    lse = torch.full((R, H), -math.inf)
+    for i in range(R):
+        L = int(seq_lens[i])
+        live = [s for s, (a, e) in enumerate(split_bounds(L, num_splits, align)) if e > a]
+        if not live:
+            continue
+        ls = att[i, :, live, dv]                        # [H, n]
+        m = ls.max(-1, keepdim=True).values
+        w = torch.exp(ls - m)
+        o[i] = (w[..., None] * att[i, :, live, :dv]).sum(1) / w.sum(-1, keepdim=True)
+        lse[i] = (m + torch.log(w.sum(-1, keepdim=True))).squeeze(-1)
+    return o, lse
+
+
+# ------------------------------------------------------------------------------------------------
+# spec-verify flattening
+# ------------------------------------------------------------------------------------------------
+def flatten_verify(block_table: np.ndarray, seq_lens: np.ndarray, q: int):
+    """One decode row per query token: row j of a request with q tokens and total length L
+    attends to the first max(L - (q-1-j), 0) tokens and shares the request's block-table row
+    (mla_impl.py:628-662)."""
+    n, width = block_table.shape
+    bt = np.repeat(block_table[:, None, :], q, axis=1).reshape(n * q, width)
+    offs = np.arange(1 - q, 1, dtype=np.int64)
+    sl = np.maximum(seq_lens.astype(np.int64)[:, None] + offs[None, :], 0).reshape(-1)
+    return bt.astype(block_table.dtype), sl.astype(seq_lens.dtype)
+
+
+# ------------------------------------------------------------------------------------------------
+# FP8 cache-row writer and prefill gather
+# ------------------------------------------------------------------------------------------------
+def fp8_row_bytes(kv_c: np.ndarray, k_pe: np.ndarray, *, packed_rope: int, n_heads: int,
+                  k_scale: float, rms_mode: str) -> np.ndarray:
+    """FP8 cache row bytes [n, d_c + packed_rope + n_heads*(1|2)] (mla_impl.py:328-339).
+
+    Latent and rope: `(x.float() * (1/k_scale)).clamp(-448, 448)` then e4m3fn, all float32.
+    rms (k_pe[:, packed_rope : packed_rope + n_heads]): a log8 code, or its bf16 bytes.
+    """
+    inv = np.float32(1.0) / np.float32(k_scale)
+    lat = e4m3_encode(np.clip(np.asarray(kv_c, np.float32) * inv, -E4M3_MAX, E4M3_MAX))
+    rope = e4m3_encode(np.clip(np.asarray(k_pe[:, :packed_rope], np.float32) * inv, -E4M3_MAX, E4M3_MAX))
+    rms = np.asarray(k_pe[:, packed_rope:packed_rope + n_heads], np.float32)
+    if rms_mode == RMS_LOG8:
+        rb = log8_encode(rms)
+    elif rms_mode == RMS_BF16_BYTES:
+        rb = f32_to_bf16_bits(rms).view(np.uint8).reshape(rms.shape[0], -1)
+    else:
+        raise ValueError(rms_mode)
+    return np.concatenate([lat, rope, rb], axis=1)
+
+
+def fp8_cache_write(cache_flat: np.ndarray, slots: np.ndarray, rows: np.ndarray) -> None:
+    """Write rows into a flat [num_slots, row] uint8 cache view; slot -1 (padding) is redirected
+    to slot 0, the never-read null block (mla_impl.py:340-342)."""
+    s = np.maximum(np.asarray(slots, np.int64), 0)
+    cache_flat[s, :rows.shape[1]] = rows
+
+
+def gather_context(cache_u8: np.ndarray, block_table: np.ndarray, cu_seq_lens: np.ndarray,
+                   token_to_seq: np.ndarray, num_tokens: int, seq_starts: np.ndarray | None, *,
+                   kv: str, scale: float = 1.0, rms_offset: int = 0, n_heads: int = 0,
+                   rms_mode: str = RMS_NONE) -> np.ndarray:
+    """Prefill context gather into bf16 rows (returned as uint16 bit patterns)
+    (ops/mla_gather.py:28-76).
+
+    Row j: s = token_to_seq[j]; tok = j - cu_seq_lens[s] (+ seq_starts[s]); the page is
+    block_table[s, tok // P]. bf16 caches copy the row; FP8 rows decode latent+rope as
+    bf16(e4m3 * scale) and the rms tail per mode into one bf16 element per head at rms_offset.
+    """
+    P = cache_u8.shape[1]
+    j = np.arange(num_tokens)
+    s = token_to_seq[:num_tokens].astype(np.int64)
+    tok = j - cu_seq_lens.astype(np.int64)[s]
+    if seq_starts is not None:
+        tok = tok + seq_starts.astype(np.int64)[s]
+    blk = block_table[s, tok // P].astype(np.int64)
+    rows = cache_u8[blk, tok % P].reshape(num_tokens, -1)
+    if kv == KV_BF16:
+        return rows.view(np.uint16)
+    width = rows.shape[1]
+    out = np.zeros((num_tokens, width), dtype=np.uint16)
+    sc = np.float32(scale)
+    if rms_mode == RMS_E4M3:
+        out[:, :rms_offset + n_heads] = f32_to_bf16_bits(e4m3_decode(rows[:, :rms_offset + n_heads]) * sc)
+        return out
+    out[:, :rms_offset] = f32_to_bf16_bits(e4m3_decode(rows[:, :rms_offset]) * sc)
+    code = rows[:, rms_offset:rms_offset + n_heads]
+    if rms_mode == RMS_LOG8:
+        out[:, rms_offset:rms_offset + n_heads] = f32_to_bf16_bits(log8_decode(code))
+    else:
+        raw = rows[:, rms_offset:rms_offset + 2 * n_heads].copy().view(np.uint16)
+        out[:, rms_offset:rms_offset + n_heads] = raw
+    return out

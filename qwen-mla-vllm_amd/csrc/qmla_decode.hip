@@ -1,0 +1,1037 @@
+// qmla_decode.hip -- gfx950 (MI355X) absorbed-MLA decode over a paged latent KV cache.
+//
+// One workgroup = 4 waves (one per SIMD) owns a contiguous token range of one request and ALL of
+// its query rows (every head, every spec-verify token, every latent group), so each cached row is
+// read from HBM exactly once per call. Per 64-token tile:
+//   * the paged rows [latent | rope | rms] stream global -> LDS with 16-byte LDS-DMA loads through
+//     an S-stage ring (page ids are DMA'd 2(S-1) tiles ahead so no VGPR waits on the block table);
+//   * QK^T on MFMA 16x16x32 bf16: query fragments stay in VGPRs for the whole segment, key
+//     fragments come from LDS (fp8 e4m3 rows converted exactly to bf16 in registers, the per-layer
+//     scale folded into the fp32 score);
+//   * scores are divided by the per-(token, head) rms decoded from the row tail, scaled into the
+//     log2 domain, masked (split end, spec-verify causal limit), and fed to an online softmax whose
+//     row max / row sum are reduced across the 16 lanes of a row (DPP/permute) and across waves in
+//     LDS;
+//   * P (bf16) goes through LDS; P.V runs on MFMA with the value fragments read transposed straight
+//     from the staged rows by ds_read_b64_tr_b8 / _b16 (no separate V copy), each wave owning a
+//     column slice of the latent output.
+// Split-K partials use the reference attn_logits layout [rows, heads, S, Dv+1] (fixed mode) or a
+// balanced plan where every workgroup gets the same number of tiles (balanced mode), and an
+// LSE-weighted combine kernel merges them.
+//
+// Reference semantics: qwen_mla/ops/mla_decode_attention.py:297-586 (stage 1), :1064-1137 (stage 2),
+// :1264-1359 (entry, verify folding); qwen_mla/mla_impl.py:125-145 (rms tail formats).
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+#include <string.h>
+
+#include "qmla.h"
+#include "qmla_device.h"
+
+namespace qmla {
+
+constexpr int TILE = 64;   // tokens per tile
+constexpr int NWAVE = 4;   // waves per workgroup
+constexpr int NTHR = NWAVE * 64;
+
+struct KParams {
+  const __bf16* q_nope;
+  int64_t qn_sr, qn_sh;
+  const __bf16* q_pe;
+  int64_t qp_sr, qp_sh;
+  const char* kv;
+  int64_t page_stride_b, token_stride_b;  // bytes
+  int page_size;
+  int rope_w;
+  int rms_off_b;  // byte offset of the rms tail inside a row
+  const float* k_scale;
+  float sm_scale, logit_cap;
+  const int* bt;
+  int64_t bt_stride;
+  const int* seq_lens;
+  int n_req;      // requests = rows / qrows
+  int qrows, hpg; // verify tokens per request, heads per latent group
+  int heads;      // heads per row (= groups * hpg)
+  void* out;
+  int64_t o_sr, o_sh;
+  int out_dt;
+  void* lse;
+  int64_t lse_sr;
+  int lse_dt;
+  int num_splits, split_align;
+  float* ws;
+  int64_t ws_sr, ws_sh, ws_ss;
+  // balanced mode
+  int nwg;
+  int* plan;        // [0] = chunk (tiles per workgroup), [1] = total tiles, [2 + b] = prefix C_b
+  float* part_o;    // [(nwg + n_req), qrows*heads, Dv]
+  float* part_lse;  // [(nwg + n_req), qrows*heads]
+};
+
+__device__ __forceinline__ void store_out(void* base, int dt, int64_t idx, float v) {
+  if (dt == QMLA_DT_BF16) reinterpret_cast<__bf16*>(base)[idx] = (__bf16)v;
+  else if (dt == QMLA_DT_F16) reinterpret_cast<_Float16*>(base)[idx] = (_Float16)v;
+  else reinterpret_cast<float*>(base)[idx] = v;
+}
+
+// Steady-state wait for tile t: every wave issues, per tile, its share of the CPR data DMAs
+// (instructions i = wave, wave+4, ...) and wave 0 also one page-id DMA. After data(t) come exactly
+// S-2 such tile groups, so "vmcnt <= that count" means data(t) (and all earlier loads) landed.
+template <int S, int CPR>
+__device__ __forceinline__ void wait_steady(int wave) {
+  if (wave == 0) wait_vmcnt<(S - 2) * ((CPR + 3) / 4 + 1)>();
+  else if (wave == 1) wait_vmcnt<(S - 2) * ((CPR + 2) / 4)>();
+  else if (wave == 2) wait_vmcnt<(S - 2) * ((CPR + 1) / 4)>();
+  else wait_vmcnt<(S - 2) * (CPR / 4)>();
+}
+
+// Compile-time shape of one kernel instance.
+//   EB   cache element bytes (1 = fp8 e4m3fn, 2 = bf16)
+//   RMS  QMLA_RMS_* tail format
+//   DCG  latent columns per group, G groups (d_c = G*DCG)
+//   WP   rope columns padded to a multiple of 64 (scores read [latent | rope_w], rest masked)
+//   MB   16-row MFMA blocks per group (rows per group = qrows * heads/G <= 16*MB)
+//   S    LDS ring stages, CPR 16-byte chunks loaded per row (row bytes in LDS = 16*CPR)
+template <int EB_, int RMS_, int DCG_, int WP_, int MB_, int G_, int S_, int CPR_, bool CAP_>
+struct Cfg {
+  static constexpr int EB = EB_, RMS = RMS_, DCG = DCG_, WP = WP_, MB = MB_, G = G_, S = S_;
+  static constexpr int CPR = CPR_;
+  static constexpr bool CAP = CAP_;
+  static constexpr int DC = G * DCG;
+  static constexpr int RB = 16 * CPR;              // LDS row stride (bytes)
+  static constexpr int STAGE = TILE * RB;          // bytes per stage
+  static constexpr int WPG = NWAVE / G;            // waves per group
+  static constexpr int TBW = (TILE / 16) / WPG;    // 16-token score blocks per wave
+  static constexpr int KQ = (DCG + WP) / 32;       // k-steps of the score product
+  static constexpr int KP = KQ / 2;                // k-step pairs (64 columns each)
+  static constexpr int NCOL = DCG / WPG;           // output columns per wave
+  static constexpr int CB = NCOL / 16;             // 16-column output blocks per wave
+  static constexpr int ROWS = 16 * MB;
+  static constexpr int PSTRIDE = TILE * 2 + 16;    // bf16 P row stride in LDS (bytes, padded)
+  static_assert(WP % 64 == 0 && DCG % 64 == 0, "64-column pairs");
+  static_assert(NWAVE % G == 0 && (TILE / 16) % WPG == 0 && DCG % (16 * WPG) == 0, "wave split");
+  static_assert(S >= 2, "ring");
+};
+
+template <class C>
+struct Smem {
+  char kv[C::S][C::STAGE];
+  int pid[2 * C::S][TILE];
+  char p[C::G][C::ROWS][C::PSTRIDE];
+  float red[2][NWAVE][C::ROWS];
+  int flag[NWAVE];
+};
+
+// Everything a segment needs to know about where its results go.
+struct SegOut {
+  bool final_out;       // write normalized output + lse directly
+  float* po;            // partial output base of this request (query-row 0 of it)
+  int64_t po_sr, po_sh; // float strides for (verify token of the request, head)
+  float* plse;          // balanced-mode lse base (nullptr: lse stored after the Dv columns)
+  int64_t plse_sr;
+};
+
+// One contiguous token range [tok_a, tok_e) of request `req` (length L), all query rows.
+//
+// Score layout (S^T = K . Q^T on MFMA): lane (n = head column ln16, lg) of head block mb holds the
+// scores of tokens tb*16 + 4*lg + i (i = 0..3) for query row mb*16 + ln16, so the per-row
+// softmax reductions over a 16-token block are 3 in-lane ops plus 2 cross-lane steps. The value
+// accumulator (O = P . V) keeps the D layout: lane (col ln16, lg) holds rows mb*16 + 4*lg + i.
+template <class C>
+__device__ __forceinline__ void process_segment(const KParams& p, Smem<C>& sm, int req, int tok_a, int tok_e,
+                                                int L, const SegOut& so, float kscale) {
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform -> SGPR
+  const int g = wave / C::WPG, wl = wave % C::WPG;
+  const int ln16 = lane & 15, lg = lane >> 4;
+  const int qrows = p.qrows, hpg = p.hpg;
+  const int nrows = qrows * hpg;  // valid rows per group
+  const int row0 = req * qrows;   // first flattened query row of this request
+  const int* bt = p.bt + (int64_t)(row0 + qrows - 1) * p.bt_stride;
+  const int ntiles = (tok_e - tok_a + TILE - 1) / TILE;
+  const int P = p.page_size;
+  constexpr int RMS_EB = (C::RMS == QMLA_RMS_BF16 || C::RMS == QMLA_RMS_BF16_BYTES) ? 2 : 1;
+
+  // ---- this lane's score row (query row mb*16 + ln16 of group g) ----
+  int rms_b[C::MB];    // byte offset of the row's rms inside a staged cache row
+  int lim_off[C::MB];  // qrows-1-jq: verify token jq sees the first L-(qrows-1-jq) tokens
+#pragma unroll
+  for (int mb = 0; mb < C::MB; ++mb) {
+    const int r = mb * 16 + ln16;
+    const int rr = r < nrows ? r : nrows - 1;
+    const int jq = rr / hpg, h = rr - jq * hpg;
+    rms_b[mb] = p.rms_off_b + (g * hpg + h) * RMS_EB;
+    lim_off[mb] = qrows - 1 - jq;
+  }
+
+  // ---- page-id and data DMA issue ----
+  auto issue_pid = [&](int t) {
+    int tok = tok_a + t * TILE + lane;
+    tok = tok < tok_e ? tok : tok_e - 1;
+    dma4(bt + tok / P, reinterpret_cast<char*>(sm.pid[t % (2 * C::S)]));
+  };
+  auto issue_data = [&](int t) {
+    const int tok0 = tok_a + t * TILE;
+    const int* pidt = sm.pid[t % (2 * C::S)];
+    char* dst = sm.kv[t % C::S];
+    if (tok0 / P == (tok0 + TILE - 1) / P && p.token_stride_b == C::RB) {
+      // the 64 rows are consecutive in one page: one contiguous block (rows past tok_e are still
+      // inside the page and get masked)
+      const char* base = p.kv + (int64_t)pidt[0] * p.page_stride_b + (int64_t)(tok0 % P) * p.token_stride_b;
+#pragma unroll
+      for (int i0 = 0; i0 < C::CPR; i0 += NWAVE) {
+        const int i = i0 + wave;
+        if (i < C::CPR) dma16(base + (i * 64 + lane) * 16, dst + i * 1024);
+      }
+      return;
+    }
+    int tok = tok0 + lane;
+    tok = tok < tok_e ? tok : tok_e - 1;
+    const int64_t off = (int64_t)pidt[lane] * p.page_stride_b + (int64_t)(tok % P) * p.token_stride_b;
+    const int off_lo = (int)(uint32_t)off, off_hi = (int)(uint32_t)((uint64_t)off >> 32);
+#pragma unroll
+    for (int i0 = 0; i0 < C::CPR; i0 += NWAVE) {
+      const int i = i0 + wave;
+      if (i < C::CPR) {
+        const int c = i * 64 + lane;
+        const int tk = c / C::CPR, piece = c - tk * C::CPR;
+        const uint32_t lo = (uint32_t)__shfl(off_lo, tk), hi = (uint32_t)__shfl(off_hi, tk);
+        const int64_t roff = (int64_t)(((uint64_t)hi << 32) | lo);
+        dma16(p.kv + roff + piece * 16, dst + i * 1024);
+      }
+    }
+  };
+
+  // ---- query fragments (B operand of S^T): pair jj, lane group lg holds q columns
+  //      64*jj + 16*lg .. +16 of query row mb*16 + ln16; zero outside [latent | rope_w) ----
+  bf16x8 qf[C::MB][C::KQ];
+#pragma unroll
+  for (int mb = 0; mb < C::MB; ++mb) {
+    const int r = mb * 16 + ln16;
+    const bool rv = r < nrows;
+    const int rr = rv ? r : 0;
+    const int jq = rr / hpg, h = rr - jq * hpg;
+    const int64_t qrow = row0 + jq, head = g * hpg + h;
+    const __bf16* qn = p.q_nope + qrow * p.qn_sr + head * p.qn_sh;
+    const __bf16* qp = p.q_pe + qrow * p.qp_sr + head * p.qp_sh;
+#pragma unroll
+    for (int jj = 0; jj < C::KP; ++jj) {
+      const int kcol = 64 * jj + 16 * lg;
+#pragma unroll
+      for (int half = 0; half < 2; ++half) {
+        bf16x8 v;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) v[e] = (__bf16)0.0f;
+        if (rv) {
+          const int col = kcol + 8 * half;
+          if (col < C::DCG) {
+            v = *reinterpret_cast<const bf16x8*>(qn + col);
+          } else {
+            const int pc = col - C::DCG;
+            if (pc + 8 <= p.rope_w) {
+              v = *reinterpret_cast<const bf16x8*>(qp + pc);
+            } else if (pc < p.rope_w) {
+#pragma unroll
+              for (int e = 0; e < 8; ++e) {
+                const int c = pc + e < p.rope_w ? pc + e : p.rope_w - 1;
+                const __bf16 x = qp[c];
+                v[e] = pc + e < p.rope_w ? x : (__bf16)0.0f;
+              }
+            }
+          }
+        }
+        qf[mb][2 * jj + half] = v;
+      }
+    }
+  }
+
+  f32x4 acc[C::MB][C::CB];
+  float mref[C::MB], l_run[C::MB];  // per query row ln16 of block mb (log2 domain reference max)
+#pragma unroll
+  for (int mb = 0; mb < C::MB; ++mb) {
+#pragma unroll
+    for (int cb = 0; cb < C::CB; ++cb) acc[mb][cb] = f32x4{0.f, 0.f, 0.f, 0.f};
+    mref[mb] = kNegInf;
+    l_run[mb] = 0.f;
+  }
+
+  const float c2 = p.sm_scale * kscale * kLog2e;   // raw q.k -> log2-domain score (before /rms)
+  const float capc = p.logit_cap;
+  const int latent_cols_end = C::DCG + p.rope_w;  // valid score columns (group-local k space)
+
+  // ---- prologue: page ids for tiles 0 .. S-2, wait; then S-1 pseudo-iterations issuing
+  //      pid(t + S-1) and data(t) exactly like the steady-state loop below ----
+  if (wave == 0) {
+#pragma unroll
+    for (int t = 0; t < C::S - 1; ++t) issue_pid(t);
+  }
+  wait_vmcnt<0>();
+  lds_barrier();
+#pragma unroll
+  for (int t = 0; t < C::S - 1; ++t) {
+    if (wave == 0) issue_pid(t + C::S - 1);
+    if (t < ntiles) issue_data(t);
+  }
+
+  for (int t = 0; t < ntiles; ++t) {
+    // wait for this wave's DMA of tile t (and everything issued before it), then publish
+    if (t + C::S - 2 < ntiles) wait_steady<C::S, C::CPR>(wave);
+    else wait_vmcnt<0>();
+    lds_barrier();  // (A) tile t visible; every wave is done with tile t-1
+    if (wave == 0) issue_pid(t + 2 * C::S - 2);
+    if (t + C::S - 1 < ntiles) issue_data(t + C::S - 1);
+
+    const char* kvs = sm.kv[t % C::S];
+    const int tok0 = tok_a + t * TILE;
+
+    // ---- scores S^T = K . Q^T ----
+    f32x4 sacc[C::MB][C::TBW];
+#pragma unroll
+    for (int mb = 0; mb < C::MB; ++mb)
+#pragma unroll
+      for (int tb = 0; tb < C::TBW; ++tb) sacc[mb][tb] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int tbi = 0; tbi < C::TBW; ++tbi) {
+      const int tb = wl + tbi * C::WPG;
+      const char* rowp = kvs + (tb * 16 + ln16) * C::RB;
+      // one 64-column pair ahead: LDS reads of pair jj+1 overlap the MFMAs of pair jj
+      i32x4 cur0, cur1, nxt0, nxt1;
+      auto load_pair = [&](int jj, i32x4& r0, i32x4& r1) {
+        const int kcol = 64 * jj + 16 * lg;
+        const int cbyte = (kcol < C::DCG ? g * C::DCG + kcol : C::DC + kcol - C::DCG) * C::EB;
+        r0 = lds_read_b128(rowp + cbyte);
+        if constexpr (C::EB == 2) r1 = lds_read_b128(rowp + cbyte + 16);
+      };
+      load_pair(0, cur0, cur1);
+#pragma unroll
+      for (int jj = 0; jj < C::KP; ++jj) {
+        if (jj + 1 < C::KP) load_pair(jj + 1, nxt0, nxt1);
+        const int kcol = 64 * jj + 16 * lg;
+        bf16x8 ka, kb;
+        if constexpr (C::EB == 1) {
+          fp8x16_to_bf16(cur0, ka, kb);
+        } else {
+          ka = __builtin_bit_cast(bf16x8, cur0);
+          kb = __builtin_bit_cast(bf16x8, cur1);
+        }
+        if (jj * 64 + 64 > C::DCG + (C::WP - 64) && kcol + 16 > latent_cols_end) {
+          // columns past the rope width (padding up to a 64-column pair): zero them so
+          // whatever bytes follow the rope (rms codes, padding) cannot leak NaN into scores
+#pragma unroll
+          for (int e = 0; e < 8; ++e) {
+            if (kcol + e >= latent_cols_end) ka[e] = (__bf16)0.0f;
+            if (kcol + 8 + e >= latent_cols_end) kb[e] = (__bf16)0.0f;
+          }
+        }
+#pragma unroll
+        for (int mb = 0; mb < C::MB; ++mb) {
+          sacc[mb][tbi] = mfma16(ka, qf[mb][2 * jj], sacc[mb][tbi]);
+          sacc[mb][tbi] = mfma16(kb, qf[mb][2 * jj + 1], sacc[mb][tbi]);
+        }
+        cur0 = nxt0;
+        cur1 = nxt1;
+        __builtin_amdgcn_sched_barrier(0);
+      }
+    }
+
+    // ---- rms divide, scale to log2 units, mask; tile max per query row ----
+    float lmax[C::MB];
+#pragma unroll
+    for (int mb = 0; mb < C::MB; ++mb) lmax[mb] = kNegInf;
+#pragma unroll
+    for (int tbi = 0; tbi < C::TBW; ++tbi) {
+      const int tb = wl + tbi * C::WPG;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int tt = tb * 16 + 4 * lg + i;
+        const int tok = tok0 + tt;
+        const char* rowp = kvs + tt * C::RB;
+#pragma unroll
+        for (int mb = 0; mb < C::MB; ++mb) {
+          float rinv = 1.0f;
+          if constexpr (C::RMS == QMLA_RMS_LOG8) {
+            const float code = (float)(uint32_t)(uint8_t)rowp[rms_b[mb]];
+            rinv = fast_exp2(3.0f - code * (6.0f / 255.0f));
+          } else if constexpr (C::RMS == QMLA_RMS_BF16 || C::RMS == QMLA_RMS_BF16_BYTES) {
+            const float r = bf16_bits_to_f32(*reinterpret_cast<const uint16_t*>(rowp + rms_b[mb]));
+            rinv = r > 0.f ? __builtin_amdgcn_rcpf(r) : 1.0f;
+          } else if constexpr (C::RMS == QMLA_RMS_E4M3) {
+            const float r = fp8_to_f32((uint8_t)rowp[rms_b[mb]]) * kscale;
+            rinv = r > 0.f ? __builtin_amdgcn_rcpf(r) : 1.0f;
+          }
+          float v;
+          if constexpr (C::CAP) {
+            const float sn = sacc[mb][tbi][i] * (c2 * kLn2) * rinv;   // natural-unit score
+            const float x = sn / capc;
+            const float th = 1.0f - 2.0f / (fast_exp2(2.0f * kLog2e * x) + 1.0f);
+            v = capc * th * kLog2e;
+          } else {
+            v = sacc[mb][tbi][i] * c2 * rinv;
+          }
+          int lim = tok_e;
+          if (qrows > 1) { const int lv = L - lim_off[mb]; lim = lv < lim ? lv : lim; }
+          v = tok < lim ? v : kNegInf;
+          sacc[mb][tbi][i] = v;
+          lmax[mb] = fmaxf(lmax[mb], v);
+        }
+      }
+    }
+#pragma unroll
+    for (int mb = 0; mb < C::MB; ++mb) {
+      lmax[mb] = fmaxf(lmax[mb], __shfl_xor(lmax[mb], 16));
+      lmax[mb] = fmaxf(lmax[mb], __shfl_xor(lmax[mb], 32));
+    }
+
+    // ---- optimistic softmax: P = exp2(s - mref) with the reference max of earlier tiles. A row
+    //      whose tile max exceeds its reference by more than 8 (P > 256) or that had no reference
+    //      yet raises the flag; then every wave rebuilds its P block against the new reference
+    //      (a second exchange) and the accumulator is rescaled. ----
+    float psum[C::MB];
+    auto write_p = [&]() {
+#pragma unroll
+      for (int mb = 0; mb < C::MB; ++mb) psum[mb] = 0.f;
+#pragma unroll
+      for (int tbi = 0; tbi < C::TBW; ++tbi) {
+        const int tb = wl + tbi * C::WPG;
+#pragma unroll
+        for (int mb = 0; mb < C::MB; ++mb) {
+          const float sh = mref[mb] == kNegInf ? 0.f : mref[mb];
+          bf16x4 pk;
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const float e = fast_exp2(sacc[mb][tbi][i] - sh);
+            psum[mb] += e;
+            pk[i] = (__bf16)e;
+          }
+          *reinterpret_cast<bf16x4*>(&sm.p[g][mb * 16 + ln16][(tb * 16 + 4 * lg) * 2]) = pk;
+        }
+      }
+#pragma unroll
+      for (int mb = 0; mb < C::MB; ++mb) {
+        psum[mb] += __shfl_xor(psum[mb], 16);
+        psum[mb] += __shfl_xor(psum[mb], 32);
+      }
+    };
+    bool need = false;
+#pragma unroll
+    for (int mb = 0; mb < C::MB; ++mb) need |= lmax[mb] > mref[mb] + 8.0f;
+    const bool need_w = __builtin_amdgcn_ballot_w64(need) != 0;
+    if (!need_w) write_p();
+    if (lg == 0) {
+#pragma unroll
+      for (int mb = 0; mb < C::MB; ++mb) {
+        sm.red[0][wave][mb * 16 + ln16] = lmax[mb];
+        if (!need_w) sm.red[1][wave][mb * 16 + ln16] = psum[mb];
+      }
+    }
+    if (lane == 0) sm.flag[wave] = need_w ? 1 : 0;
+    lds_barrier();  // (B)
+    const bool any = (sm.flag[0] | sm.flag[1] | sm.flag[2] | sm.flag[3]) != 0;
+    float alpha[C::MB];
+    if (any) {
+#pragma unroll
+      for (int mb = 0; mb < C::MB; ++mb) {
+        float gm = mref[mb];
+#pragma unroll
+        for (int w = 0; w < C::WPG; ++w) gm = fmaxf(gm, sm.red[0][g * C::WPG + w][mb * 16 + ln16]);
+        alpha[mb] = mref[mb] == kNegInf ? 0.f : fast_exp2(mref[mb] - gm);
+        mref[mb] = gm;
+      }
+      write_p();
+      if (lg == 0) {
+#pragma unroll
+        for (int mb = 0; mb < C::MB; ++mb) sm.red[1][wave][mb * 16 + ln16] = psum[mb];
+      }
+      lds_barrier();  // (B')
+    } else {
+#pragma unroll
+      for (int mb = 0; mb < C::MB; ++mb) alpha[mb] = 1.0f;
+    }
+#pragma unroll
+    for (int mb = 0; mb < C::MB; ++mb) {
+      float ts = 0.f;
+#pragma unroll
+      for (int w = 0; w < C::WPG; ++w) ts += sm.red[1][g * C::WPG + w][mb * 16 + ln16];
+      l_run[mb] = l_run[mb] * alpha[mb] + ts;
+    }
+    if (any) {
+#pragma unroll
+      for (int mb = 0; mb < C::MB; ++mb)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const float a = __shfl(alpha[mb], 4 * lg + i);   // alpha of accumulator row 4*lg+i
+#pragma unroll
+          for (int cb = 0; cb < C::CB; ++cb) acc[mb][cb][i] *= a;
+        }
+    }
+
+    // ---- P.V: wave owns columns [g*DCG + wl*NCOL, +NCOL) ----
+#pragma unroll
+    for (int kk = 0; kk < TILE / 32; ++kk) {
+      bf16x8 pf[C::MB];
+#pragma unroll
+      for (int mb = 0; mb < C::MB; ++mb)
+        pf[mb] = *reinterpret_cast<const bf16x8*>(&sm.p[g][mb * 16 + ln16][(kk * 32 + 8 * lg) * 2]);
+      // value fragment of column block cb, read transposed from the staged rows
+      auto load_v = [&](int cb, i32x2& r0, i16x4& t0, i16x4& t1) {
+        const int col0 = g * C::DCG + wl * C::NCOL + cb * 16;
+        if constexpr (C::EB == 1) {
+          r0 = lds_read_tr8(kvs + (kk * 32 + 8 * lg + (ln16 >> 1)) * C::RB + col0 + 8 * (ln16 & 1));
+        } else {
+          const char* a = kvs + (kk * 32 + 8 * lg + (ln16 >> 2)) * C::RB + (col0 + 4 * (ln16 & 3)) * 2;
+          t0 = lds_read_tr16(a);
+          t1 = lds_read_tr16(a + 4 * C::RB);
+        }
+      };
+      i32x2 vr, vrn;
+      i16x4 vt0, vt1, vt0n, vt1n;
+      load_v(0, vr, vt0, vt1);
+#pragma unroll
+      for (int cb = 0; cb < C::CB; ++cb) {
+        if (cb + 1 < C::CB) load_v(cb + 1, vrn, vt0n, vt1n);
+        bf16x8 vf;
+        if constexpr (C::EB == 1) {
+          vf = fp8x8_to_bf16(vr);
+        } else {
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            vf[e] = __builtin_bit_cast(__bf16, (short)vt0[e]);
+            vf[4 + e] = __builtin_bit_cast(__bf16, (short)vt1[e]);
+          }
+        }
+#pragma unroll
+        for (int mb = 0; mb < C::MB; ++mb) acc[mb][cb] = mfma16(pf[mb], vf, acc[mb][cb]);
+        vr = vrn;
+        vt0 = vt0n;
+        vt1 = vt1n;
+        __builtin_amdgcn_sched_barrier(0);
+      }
+    }
+  }
+  wait_vmcnt<0>();  // trailing page-id loads must land before the LDS ring is reused
+
+  // ---- epilogue: normalized output (final or partial) and natural-log lse ----
+#pragma unroll
+  for (int mb = 0; mb < C::MB; ++mb)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int r = mb * 16 + 4 * lg + i;
+      const float l = __shfl(l_run[mb], 4 * lg + i);
+      const float m = __shfl(mref[mb], 4 * lg + i);
+      if (r >= nrows) continue;
+      const int jq = r / hpg, h = r - jq * hpg;
+      const int head = g * hpg + h;
+      const float inv = l > 0.f ? kscale / l : 0.f;   // fp8 values were accumulated unscaled
+      const float lse_v = l > 0.f ? (m + fast_log2(l)) * kLn2 : kNegInf;
+      if (so.final_out) {
+        const int64_t ob = (int64_t)(row0 + jq) * p.o_sr + (int64_t)head * p.o_sh + wl * C::NCOL + ln16;
+#pragma unroll
+        for (int cb = 0; cb < C::CB; ++cb) store_out(p.out, p.out_dt, ob + cb * 16, acc[mb][cb][i] * inv);
+        if (wl == 0 && ln16 == 0 && p.lse)
+          store_out(p.lse, p.lse_dt, (int64_t)(row0 + jq) * p.lse_sr + head, lse_v);
+      } else {
+        float* ob = so.po + (int64_t)jq * so.po_sr + (int64_t)head * so.po_sh + wl * C::NCOL + ln16;
+#pragma unroll
+        for (int cb = 0; cb < C::CB; ++cb) ob[cb * 16] = acc[mb][cb][i] * inv;
+        if (wl == 0 && ln16 == 0) {
+          if (so.plse) so.plse[(int64_t)jq * so.plse_sr + head] = lse_v;
+          else so.po[(int64_t)jq * so.po_sr + (int64_t)head * so.po_sh + C::DCG] = lse_v;
+        }
+      }
+    }
+  lds_barrier();  // LDS ring and P buffers free for the next segment
+}
+
+// request length: the last flattened row of the request carries it (mla_impl.py:628-662)
+__device__ __forceinline__ int req_len(const KParams& p, int req) {
+  int L = p.seq_lens[(int64_t)req * p.qrows + p.qrows - 1];
+  return L > 0 ? L : 0;
+}
+
+template <class C>
+__global__ __launch_bounds__(NTHR, 1) void partial_kernel(const KParams p) {
+  __shared__ __attribute__((aligned(16))) Smem<C> sm;
+  // the per-layer scale dequantizes fp8 rows (and e4m3 rms codes); a bf16 cache ignores it, as
+  // the reference does (mla_decode_attention.py:451-463)
+  const float kscale = (C::EB == 1 && p.k_scale) ? *p.k_scale : 1.0f;
+  if (p.num_splits > 0) {
+    // fixed splits: grid (S, n_req); bounds as the reference's stage 1 (mla_decode_attention.py:389-396)
+    const int s = blockIdx.x, req = blockIdx.y;
+    const int L = req_len(p, req);
+    int per = (L + p.num_splits - 1) / p.num_splits;
+    if (p.split_align > 0) per = (per + p.split_align - 1) / p.split_align * p.split_align;
+    const int a = per * s;
+    const int e = a + per < L ? a + per : L;
+    if (e <= a) return;
+    SegOut so;
+    so.final_out = p.num_splits == 1;
+    so.po = p.ws + (int64_t)req * p.qrows * p.ws_sr + (int64_t)s * p.ws_ss;
+    so.po_sr = p.ws_sr;
+    so.po_sh = p.ws_sh;
+    so.plse = nullptr;
+    so.plse_sr = 0;
+    process_segment<C>(p, sm, req, a, e, L, so, kscale);
+    return;
+  }
+  // balanced: workgroup w owns global tiles [w*chunk, (w+1)*chunk) of the concatenated requests
+  const int w = blockIdx.x;
+  const int chunk = p.plan[0], total = p.plan[1];
+  const int* pref = p.plan + 2;
+  int lo = w * chunk, hi = lo + chunk < total ? lo + chunk : total;
+  if (lo >= hi) return;
+  // first request whose tile range [pref[b], pref[b+1]) contains lo
+  int b0 = 0, b1 = p.n_req - 1;
+  while (b0 < b1) {
+    const int mid = (b0 + b1 + 1) >> 1;
+    if (pref[mid] <= lo) b0 = mid; else b1 = mid - 1;
+  }
+  const int nrow = p.qrows * p.heads;
+  for (int b = b0; b < p.n_req && pref[b] < hi; ++b) {
+    const int c0 = pref[b], c1 = pref[b + 1];
+    if (c1 <= lo) continue;
+    const int t_lo = (lo > c0 ? lo : c0) - c0, t_hi = (hi < c1 ? hi : c1) - c0;
+    const int L = req_len(p, b);
+    const int a = t_lo * TILE, e = t_hi * TILE < L ? t_hi * TILE : L;
+    if (e <= a) continue;
+    SegOut so;
+    so.final_out = (t_lo == 0 && t_hi == c1 - c0);
+    const int64_t slot = (int64_t)w + b;
+    so.po = p.part_o + slot * nrow * C::DCG;
+    so.po_sr = (int64_t)p.heads * C::DCG;
+    so.po_sh = C::DCG;
+    so.plse = p.part_lse + slot * nrow;
+    so.plse_sr = p.heads;
+    process_segment<C>(p, sm, b, a, e, L, so, kscale);
+  }
+}
+
+// Balanced plan: tiles per request, prefix sums, per-workgroup chunk. One workgroup.
+__global__ __launch_bounds__(1024) void plan_kernel(const int* seq_lens, int n_req, int qrows, int nwg,
+                                                    int* plan) {
+  __shared__ int wsum[16];
+  __shared__ int carry;
+  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+  if (tid == 0) carry = 0;
+  __syncthreads();
+  for (int base = 0; base < n_req; base += 1024) {
+    const int b = base + tid;
+    int n = 0;
+    if (b < n_req) {
+      int L = seq_lens[(int64_t)b * qrows + qrows - 1];
+      n = L > 0 ? (L + TILE - 1) / TILE : 0;
+    }
+    // inclusive wave scan
+    int x = n;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+      const int y = __shfl_up(x, o);
+      if (lane >= o) x += y;
+    }
+    if (lane == 63) wsum[wv] = x;
+    __syncthreads();
+    int before = carry;
+    for (int k = 0; k < wv; ++k) before += wsum[k];
+    if (b < n_req) plan[2 + b] = before + x - n;  // exclusive prefix
+    __syncthreads();
+    if (tid == 0) {
+      int t = carry;
+      for (int k = 0; k < 16; ++k) t += wsum[k];
+      carry = t;
+      for (int k = 0; k < 16; ++k) wsum[k] = 0;
+    }
+    __syncthreads();
+  }
+  if (tid == 0) {
+    const int total = carry;
+    plan[2 + n_req] = total;
+    plan[1] = total;
+    plan[0] = total > 0 ? (total + nwg - 1) / nwg : 1;
+  }
+}
+
+// LSE-weighted combine (mla_decode_attention.py:1064-1137). One wave per (row, head).
+// fixed mode: partials in the reference attn_logits layout, split bounds recomputed exactly as in
+// the partial pass; balanced mode: partial slots w + b for the workgroups that touched request b.
+__global__ __launch_bounds__(64) void combine_kernel(const KParams p, int dv) {
+  const int head = blockIdx.x, row = blockIdx.y;   // row = flattened query row
+  const int lane = threadIdx.x;
+  const int req = row / p.qrows, jq = row - req * p.qrows;
+  const int L = req_len(p, req);
+  const int64_t obase = (int64_t)row * p.o_sr + (int64_t)head * p.o_sh;
+  float m = kNegInf, l = 0.f;
+  float acc[32];
+  const int nper = (dv + 63) / 64;
+#pragma unroll
+  for (int k = 0; k < 32; ++k) acc[k] = 0.f;
+  if (p.num_splits > 0) {
+    int per = (L + p.num_splits - 1) / p.num_splits;
+    if (p.split_align > 0) per = (per + p.split_align - 1) / p.split_align * p.split_align;
+    const float* base = p.ws + (int64_t)row * p.ws_sr + (int64_t)head * p.ws_sh;
+    for (int s = 0; s < p.num_splits; ++s) {
+      const int a = per * s, e = a + per < L ? a + per : L;
+      if (e <= a) continue;
+      const float* ps = base + (int64_t)s * p.ws_ss;
+      const float ls = ps[dv];
+      const float mn = fmaxf(m, ls);
+      if (mn == kNegInf) continue;
+      const float sc_old = __expf(m - mn), sc_new = __expf(ls - mn);
+      l = l * sc_old + sc_new;
+#pragma unroll
+      for (int k = 0; k < 32; ++k)
+        if (k < nper) {
+          const int c = lane + 64 * k;
+          acc[k] = acc[k] * sc_old + (c < dv ? ps[c] : 0.f) * sc_new;
+        }
+      m = mn;
+    }
+  } else {
+    const int chunk = p.plan[0];
+    const int c0 = p.plan[2 + req], c1 = p.plan[3 + req];
+    if (c1 > c0) {
+      const int w0 = c0 / chunk, w1 = (c1 - 1) / chunk;
+      if (w0 == w1) return;   // single segment: the partial pass wrote the final output
+      const int nrow = p.qrows * p.heads;
+      const int rloc = jq * p.heads + head;
+      for (int w = w0; w <= w1; ++w) {
+        const int64_t slot = (int64_t)w + req;
+        const float ls = p.part_lse[slot * nrow + rloc];
+        const float mn = fmaxf(m, ls);
+        if (mn == kNegInf) continue;
+        const float sc_old = __expf(m - mn), sc_new = __expf(ls - mn);
+        l = l * sc_old + sc_new;
+        const float* ps = p.part_o + (slot * nrow + rloc) * (int64_t)dv;
+#pragma unroll
+        for (int k = 0; k < 32; ++k)
+          if (k < nper) {
+            const int c = lane + 64 * k;
+            acc[k] = acc[k] * sc_old + (c < dv ? ps[c] : 0.f) * sc_new;
+          }
+        m = mn;
+      }
+    }
+  }
+  const float inv = l > 0.f ? 1.0f / l : 0.f;
+#pragma unroll
+  for (int k = 0; k < 32; ++k)
+    if (k < nper) {
+      const int c = lane + 64 * k;
+      if (c < dv) store_out(p.out, p.out_dt, obase + c, acc[k] * inv);
+    }
+  if (lane == 0 && p.lse)
+    store_out(p.lse, p.lse_dt, (int64_t)row * p.lse_sr + head, l > 0.f ? m + __logf(l) : kNegInf);
+}
+
+}  // namespace qmla
+
+// ================================================================================================
+// host side: validation, instance selection, launches, C ABI
+// ================================================================================================
+namespace qmla {
+
+typedef void (*PartialFn)(const KParams);
+
+struct Inst {
+  int eb, rms, dcg, wp, mb, g, s, cpr;
+  bool cap;
+  PartialFn fn;
+};
+
+#define QMLA_INST(EB, RMS, DCG, WP, MB, G, S, CPR, CAP) \
+  {EB, RMS, DCG, WP, MB, G, S, CPR, CAP, &partial_kernel<Cfg<EB, RMS, DCG, WP, MB, G, S, CPR, CAP>>}
+
+// One entry per compiled shape. Rows are [latent | rope | rms | pad]; CPR*16 bytes are staged.
+static const Inst kInst[] = {
+    // bf16 cache, d_c 512, rope 64, 24 heads (rms 24 bf16): 1200 B staged
+    QMLA_INST(2, QMLA_RMS_BF16, 512, 64, 2, 1, 2, 75, false),
+    QMLA_INST(2, QMLA_RMS_BF16, 512, 64, 2, 1, 2, 75, true),
+    QMLA_INST(2, QMLA_RMS_NONE, 512, 64, 2, 1, 2, 72, false),
+    // fp8 e4m3 cache + log8 rms codes, d_c 512, rope 64, 24 heads: 600 B -> 608 staged
+    QMLA_INST(1, QMLA_RMS_LOG8, 512, 64, 2, 1, 3, 38, false),
+    QMLA_INST(1, QMLA_RMS_LOG8, 512, 64, 2, 1, 3, 38, true),
+    QMLA_INST(1, QMLA_RMS_BF16_BYTES, 512, 64, 2, 1, 3, 39, false),
+    QMLA_INST(1, QMLA_RMS_E4M3, 512, 64, 2, 1, 3, 38, false),
+    // GLA-g2: two latent groups of 256, 12 heads each, 4 verify tokens -> 48 rows per group
+    QMLA_INST(1, QMLA_RMS_LOG8, 256, 64, 3, 2, 3, 38, false),
+};
+
+static int g_cu_count[64];
+
+static int cu_count() {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  if (g_cu_count[dev] == 0) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0)
+      n = 256;
+    g_cu_count[dev] = n;
+  }
+  return g_cu_count[dev];
+}
+
+static int elem_bytes(int kv_dtype) { return kv_dtype == QMLA_KV_FP8 ? 1 : 2; }
+
+static int rms_elem_bytes(const qmla_decode_params* p) {
+  switch (p->rms_mode) {
+    case QMLA_RMS_BF16: return 2;
+    case QMLA_RMS_BF16_BYTES: return 2;
+    case QMLA_RMS_LOG8: return 1;
+    case QMLA_RMS_E4M3: return 1;
+    default: return 0;
+  }
+}
+
+static int wp_of(int rope_w) { return (rope_w + 63) / 64 * 64; }
+
+// staged bytes per row: scores read [0, (d_c + WP)*EB) (the padded pair is masked but still read),
+// plus the rms tail
+static int64_t needed_row_bytes(const qmla_decode_params* p) {
+  const int eb = elem_bytes(p->kv_dtype);
+  int64_t need = (int64_t)(p->d_c + wp_of(p->rope_w)) * eb;
+  if (p->rms_mode != QMLA_RMS_NONE) {
+    const int64_t rms_end = (int64_t)p->rms_offset * eb + (int64_t)p->rms_heads * rms_elem_bytes(p);
+    if (rms_end > need) need = rms_end;
+  }
+  return need;
+}
+
+static bool aligned16(const void* ptr) { return ((uintptr_t)ptr & 15) == 0; }
+
+static int validate(const qmla_decode_params* p) {
+  if (!p) return QMLA_ERR_NULL;
+  if (!p->q_nope || !p->kv_cache || !p->block_table || !p->seq_lens || !p->out) return QMLA_ERR_NULL;
+  if (p->rope_w > 0 && !p->q_pe) return QMLA_ERR_NULL;
+  if (p->kv_dtype != QMLA_KV_BF16 && p->kv_dtype != QMLA_KV_FP8) return QMLA_ERR_MODE;
+  if (p->out_dtype < 0 || p->out_dtype > 2 || (p->lse && (p->lse_dtype < 0 || p->lse_dtype > 2)))
+    return QMLA_ERR_MODE;
+  if (p->kv_dtype == QMLA_KV_BF16) {
+    if (p->rms_mode != QMLA_RMS_NONE && p->rms_mode != QMLA_RMS_BF16) return QMLA_ERR_MODE;
+  } else {
+    if (p->rms_mode != QMLA_RMS_NONE && p->rms_mode != QMLA_RMS_LOG8 &&
+        p->rms_mode != QMLA_RMS_BF16_BYTES && p->rms_mode != QMLA_RMS_E4M3)
+      return QMLA_ERR_MODE;
+  }
+  if ((p->rms_mode == QMLA_RMS_NONE) != (p->rms_offset < 0)) return QMLA_ERR_MODE;
+  if (p->rows < 0 || p->heads <= 0 || p->qrows <= 0 || p->groups <= 0 || p->d_c <= 0 || p->rope_w < 0 ||
+      p->page_size <= 0)
+    return QMLA_ERR_SHAPE;
+  if (p->rows % p->qrows) return QMLA_ERR_SHAPE;
+  if (p->heads % p->groups || p->d_c % p->groups) return QMLA_ERR_SHAPE;
+  if (p->rms_mode != QMLA_RMS_NONE && (p->rms_heads < p->heads / p->groups * p->groups || p->rms_heads <= 0))
+    return QMLA_ERR_SHAPE;
+  if (p->num_splits < 0 || p->split_align < 0) return QMLA_ERR_SHAPE;
+  const int eb = elem_bytes(p->kv_dtype);
+  if (!aligned16(p->kv_cache) || (p->page_stride * eb) % 16 || (p->token_stride * eb) % 16) return QMLA_ERR_ALIGN;
+  if (needed_row_bytes(p) > p->token_stride * eb && p->page_size > 1) return QMLA_ERR_SHAPE;
+  if (!aligned16(p->q_nope) || (p->q_nope_stride_row * 2) % 16 || (p->q_nope_stride_head * 2) % 16)
+    return QMLA_ERR_ALIGN;
+  if (p->rope_w > 0 && (!aligned16(p->q_pe) || (p->q_pe_stride_row * 2) % 16 || (p->q_pe_stride_head * 2) % 16))
+    return QMLA_ERR_ALIGN;
+  return QMLA_OK;
+}
+
+static const Inst* find_inst(const qmla_decode_params* p) {
+  const int eb = elem_bytes(p->kv_dtype);
+  const int dcg = p->d_c / p->groups;
+  const int hpg = p->heads / p->groups;
+  const int rows_pg = p->qrows * hpg;
+  const int64_t need = needed_row_bytes(p);
+  const bool cap = p->logit_cap > 0.f;
+  const Inst* best = nullptr;
+  for (const Inst& in : kInst) {
+    if (in.eb != eb || in.rms != p->rms_mode || in.dcg != dcg || in.g != p->groups || in.cap != cap) continue;
+    if (in.wp != wp_of(p->rope_w)) continue;
+    if (rows_pg > 16 * in.mb) continue;
+    if ((int64_t)in.cpr * 16 < need) continue;
+    if ((int64_t)in.cpr * 16 > p->token_stride * eb) continue;   // never read past the row
+    if (!best || in.mb < best->mb || (in.mb == best->mb && in.cpr < best->cpr)) best = &in;
+  }
+  return best;
+}
+
+static int balanced_nwg(const qmla_decode_params* p) {
+  return p->num_workgroups > 0 ? p->num_workgroups : cu_count();
+}
+
+struct BalancedLayout {
+  size_t plan_off, lse_off, o_off, total;
+};
+
+static BalancedLayout balanced_layout(const qmla_decode_params* p) {
+  const int64_t n_req = p->rows / p->qrows;
+  const int64_t nwg = balanced_nwg(p);
+  const int64_t nrow = (int64_t)p->qrows * p->heads;
+  const int64_t dv = p->d_c / p->groups;
+  const int64_t slots = nwg + n_req;
+  auto up = [](size_t x) { return (x + 255) / 256 * 256; };
+  BalancedLayout b;
+  b.plan_off = 0;
+  b.lse_off = up((size_t)(3 + n_req) * 4);
+  b.o_off = b.lse_off + up((size_t)(slots * nrow) * 4);
+  b.total = b.o_off + up((size_t)(slots * nrow * dv) * 4);
+  return b;
+}
+
+static KParams make_kparams(const qmla_decode_params* p) {
+  KParams k;
+  const int eb = elem_bytes(p->kv_dtype);
+  k.q_nope = reinterpret_cast<const __bf16*>(p->q_nope);
+  k.qn_sr = p->q_nope_stride_row;
+  k.qn_sh = p->q_nope_stride_head;
+  k.q_pe = reinterpret_cast<const __bf16*>(p->q_pe ? p->q_pe : p->q_nope);
+  k.qp_sr = p->q_pe_stride_row;
+  k.qp_sh = p->q_pe_stride_head;
+  k.kv = reinterpret_cast<const char*>(p->kv_cache);
+  k.page_stride_b = p->page_stride * eb;
+  k.token_stride_b = p->token_stride * eb;
+  k.page_size = p->page_size;
+  k.rope_w = p->rope_w;
+  k.rms_off_b = p->rms_offset >= 0 ? p->rms_offset * eb : 0;
+  k.k_scale = p->k_scale;
+  k.sm_scale = p->sm_scale;
+  k.logit_cap = p->logit_cap;
+  k.bt = p->block_table;
+  k.bt_stride = p->bt_stride;
+  k.seq_lens = p->seq_lens;
+  k.n_req = p->rows / p->qrows;
+  k.qrows = p->qrows;
+  k.hpg = p->heads / p->groups;
+  k.heads = p->heads;
+  k.out = p->out;
+  k.o_sr = p->out_stride_row;
+  k.o_sh = p->out_stride_head;
+  k.out_dt = p->out_dtype;
+  k.lse = p->lse;
+  k.lse_sr = p->lse_stride_row;
+  k.lse_dt = p->lse_dtype;
+  k.num_splits = p->num_splits;
+  k.split_align = p->split_align;
+  k.ws = p->workspace;
+  k.ws_sr = p->ws_stride_row;
+  k.ws_sh = p->ws_stride_head;
+  k.ws_ss = p->ws_stride_split;
+  k.nwg = 0;
+  k.plan = nullptr;
+  k.part_o = nullptr;
+  k.part_lse = nullptr;
+  if (p->num_splits == 0 && p->workspace) {
+    const BalancedLayout bl = balanced_layout(p);
+    char* base = reinterpret_cast<char*>(p->workspace);
+    k.nwg = balanced_nwg(p);
+    k.plan = reinterpret_cast<int*>(base + bl.plan_off);
+    k.part_lse = reinterpret_cast<float*>(base + bl.lse_off);
+    k.part_o = reinterpret_cast<float*>(base + bl.o_off);
+  }
+  return k;
+}
+
+static int launch(const void* fn, dim3 grid, dim3 block, void** args, hipStream_t st) {
+  if (grid.x == 0 || grid.y == 0 || grid.z == 0) return QMLA_OK;
+  hipError_t e = hipLaunchKernel(fn, grid, block, args, 0, st);
+  return e == hipSuccess ? QMLA_OK : QMLA_ERR_LAUNCH;
+}
+
+static int run_partial(const qmla_decode_params* p, const Inst* in, KParams& k, hipStream_t st) {
+  void* args[] = {&k};
+  if (p->num_splits > 0)
+    return launch((const void*)in->fn, dim3(p->num_splits, k.n_req, 1), dim3(NTHR, 1, 1), args, st);
+  return launch((const void*)in->fn, dim3(k.nwg, 1, 1), dim3(NTHR, 1, 1), args, st);
+}
+
+static int run_combine(const qmla_decode_params* p, KParams& k, hipStream_t st) {
+  int dv = p->d_c / p->groups;
+  void* args[] = {&k, &dv};
+  return launch((const void*)&combine_kernel, dim3(p->heads, p->rows, 1), dim3(64, 1, 1), args, st);
+}
+
+static int run_plan(const qmla_decode_params* p, KParams& k, hipStream_t st) {
+  const int* sl = p->seq_lens;
+  int n_req = k.n_req, qrows = k.qrows, nwg = k.nwg;
+  int* plan = k.plan;
+  void* args[] = {&sl, &n_req, &qrows, &nwg, &plan};
+  return launch((const void*)&plan_kernel, dim3(1, 1, 1), dim3(1024, 1, 1), args, st);
+}
+
+}  // namespace qmla
+
+using namespace qmla;
+
+extern "C" {
+
+int qmla_version(void) { return QMLA_ABI_VERSION; }
+
+const char* qmla_build_info(void) {
+  return "qmla gfx950: LDS-DMA paged rows, MFMA 16x16x32 bf16 QK/PV, tr8/tr16 value reads, "
+         "fixed and balanced split-K + LSE combine";
+}
+
+size_t qmla_workspace_bytes(const qmla_decode_params* p) {
+  if (!p || p->rows <= 0 || p->qrows <= 0 || p->groups <= 0) return 0;
+  const int64_t dv = p->d_c / p->groups;
+  if (p->num_splits > 0) {
+    if (p->num_splits == 1) return 0;
+    return (size_t)p->rows * p->heads * p->num_splits * (dv + 1) * 4;
+  }
+  return balanced_layout(p).total;
+}
+
+int qmla_decode_partial(const qmla_decode_params* p, void* stream) {
+  int rc = validate(p);
+  if (rc) return rc;
+  if (p->num_splits <= 0) return QMLA_ERR_MODE;
+  if (p->num_splits > 1 && !p->workspace) return QMLA_ERR_WORKSPACE;
+  const Inst* in = find_inst(p);
+  if (!in) return QMLA_ERR_NOKERNEL;
+  KParams k = make_kparams(p);
+  return run_partial(p, in, k, (hipStream_t)stream);
+}
+
+int qmla_combine(const qmla_decode_params* p, void* stream) {
+  int rc = validate(p);
+  if (rc) return rc;
+  if (p->num_splits <= 0) return QMLA_ERR_MODE;
+  if (p->num_splits == 1) return QMLA_OK;
+  if (!p->workspace) return QMLA_ERR_WORKSPACE;
+  if (p->d_c / p->groups > 2048) return QMLA_ERR_SHAPE;
+  KParams k = make_kparams(p);
+  return run_combine(p, k, (hipStream_t)stream);
+}
+
+int qmla_decode(const qmla_decode_params* p, void* stream) {
+  int rc = validate(p);
+  if (rc) return rc;
+  if (p->d_c / p->groups > 2048) return QMLA_ERR_SHAPE;
+  const Inst* in = find_inst(p);
+  if (!in) return QMLA_ERR_NOKERNEL;
+  hipStream_t st = (hipStream_t)stream;
+  if (p->num_splits > 0) {
+    if (p->num_splits > 1 && !p->workspace) return QMLA_ERR_WORKSPACE;
+    KParams k = make_kparams(p);
+    rc = run_partial(p, in, k, st);
+    if (rc || p->num_splits == 1) return rc;
+    return run_combine(p, k, st);
+  }
+  if (!p->workspace) return QMLA_ERR_WORKSPACE;
+  if (p->workspace_bytes < qmla_workspace_bytes(p)) return QMLA_ERR_WORKSPACE;
+  if (!aligned16(p->workspace)) return QMLA_ERR_ALIGN;
+  KParams k = make_kparams(p);
+  rc = run_plan(p, k, st);
+  if (rc) return rc;
+  rc = run_partial(p, in, k, st);
+  if (rc) return rc;
+  return run_combine(p, k, st);
+}
+
+size_t qmla_decode_2pass_scratch_bytes(const qmla_decode_params* p, int64_t max_tokens) {
+  (void)p;
+  (void)max_tokens;
+  return 0;
+}
+
+int qmla_decode_2pass(const qmla_decode_params* p, void* scratch, size_t scratch_bytes, int64_t max_tokens,
+                      void* stream) {
+  (void)p; (void)scratch; (void)scratch_bytes; (void)max_tokens; (void)stream;
+  return QMLA_ERR_NOKERNEL;
+}
+
+}  // extern "C"

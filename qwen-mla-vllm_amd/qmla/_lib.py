@@ -1,0 +1,132 @@
+"""ctypes binding of libqmla.so (the C ABI declared in include/qmla.h).
+
+torch is imported first on purpose: torch ships the HIP runtime (libamdhip64.so.7) and the library
+must bind to that same runtime instance so streams and device pointers are shared.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import pathlib
+
+import torch  # noqa: F401  (loads the HIP runtime the library binds to)
+
+LIB_NAME = "libqmla.so"
+LIB_PATH = pathlib.Path(__file__).resolve().parent / LIB_NAME
+
+ABI_VERSION = 1
+
+# error codes (include/qmla.h)
+OK = 0
+ERR_NULL, ERR_SHAPE, ERR_ALIGN, ERR_WORKSPACE, ERR_MODE, ERR_LAUNCH, ERR_NOKERNEL = -1, -2, -3, -4, -5, -6, -7
+ERR_NAMES = {
+    ERR_NULL: "QMLA_ERR_NULL (a required pointer is NULL)",
+    ERR_SHAPE: "QMLA_ERR_SHAPE (unsupported or inconsistent dimension)",
+    ERR_ALIGN: "QMLA_ERR_ALIGN (row, page or base address not 16-byte aligned)",
+    ERR_WORKSPACE: "QMLA_ERR_WORKSPACE (workspace missing or too small)",
+    ERR_MODE: "QMLA_ERR_MODE (unknown dtype / rms mode / split mode)",
+    ERR_LAUNCH: "QMLA_ERR_LAUNCH (HIP launch failed)",
+    ERR_NOKERNEL: "QMLA_ERR_NOKERNEL (no compiled kernel instance for this shape)",
+}
+
+KV_BF16, KV_FP8 = 0, 1
+RMS_NONE, RMS_BF16, RMS_LOG8, RMS_BF16_BYTES, RMS_E4M3 = 0, 1, 2, 3, 4
+DT_BF16, DT_F32, DT_F16 = 0, 1, 2
+
+
+class DecodeParams(ctypes.Structure):
+    """Mirror of `qmla_decode_params` (include/qmla.h); field order and types must match."""
+
+    _fields_ = [
+        ("q_nope", ctypes.c_void_p),
+        ("q_nope_stride_row", ctypes.c_int64),
+        ("q_nope_stride_head", ctypes.c_int64),
+        ("q_pe", ctypes.c_void_p),
+        ("q_pe_stride_row", ctypes.c_int64),
+        ("q_pe_stride_head", ctypes.c_int64),
+        ("kv_cache", ctypes.c_void_p),
+        ("page_stride", ctypes.c_int64),
+        ("token_stride", ctypes.c_int64),
+        ("kv_dtype", ctypes.c_int32),
+        ("page_size", ctypes.c_int32),
+        ("d_c", ctypes.c_int32),
+        ("rope_w", ctypes.c_int32),
+        ("rms_offset", ctypes.c_int32),
+        ("rms_mode", ctypes.c_int32),
+        ("k_scale", ctypes.c_void_p),
+        ("sm_scale", ctypes.c_float),
+        ("logit_cap", ctypes.c_float),
+        ("block_table", ctypes.c_void_p),
+        ("bt_stride", ctypes.c_int64),
+        ("seq_lens", ctypes.c_void_p),
+        ("rows", ctypes.c_int32),
+        ("heads", ctypes.c_int32),
+        ("rms_heads", ctypes.c_int32),
+        ("qrows", ctypes.c_int32),
+        ("groups", ctypes.c_int32),
+        ("out", ctypes.c_void_p),
+        ("out_stride_row", ctypes.c_int64),
+        ("out_stride_head", ctypes.c_int64),
+        ("out_dtype", ctypes.c_int32),
+        ("lse", ctypes.c_void_p),
+        ("lse_stride_row", ctypes.c_int64),
+        ("lse_dtype", ctypes.c_int32),
+        ("num_splits", ctypes.c_int32),
+        ("split_align", ctypes.c_int32),
+        ("workspace", ctypes.c_void_p),
+        ("workspace_bytes", ctypes.c_size_t),
+        ("ws_stride_row", ctypes.c_int64),
+        ("ws_stride_head", ctypes.c_int64),
+        ("ws_stride_split", ctypes.c_int64),
+        ("num_workgroups", ctypes.c_int32),
+    ]
+
+
+# every function include/qmla.h declares, with its ctypes signature
+_P = ctypes.POINTER(DecodeParams)
+SIGNATURES = {
+    "qmla_version": (ctypes.c_int, []),
+    "qmla_build_info": (ctypes.c_char_p, []),
+    "qmla_workspace_bytes": (ctypes.c_size_t, [_P]),
+    "qmla_decode": (ctypes.c_int, [_P, ctypes.c_void_p]),
+    "qmla_decode_partial": (ctypes.c_int, [_P, ctypes.c_void_p]),
+    "qmla_combine": (ctypes.c_int, [_P, ctypes.c_void_p]),
+    "qmla_decode_2pass_scratch_bytes": (ctypes.c_size_t, [_P, ctypes.c_int64]),
+    "qmla_decode_2pass": (ctypes.c_int, [_P, ctypes.c_void_p, ctypes.c_size_t, ctypes.c_int64, ctypes.c_void_p]),
+}
+
+_lib = None
+
+
+class QmlaError(RuntimeError):
+    def __init__(self, fn: str, code: int):
+        super().__init__(f"{fn} failed: {ERR_NAMES.get(code, code)}")
+        self.code = code
+
+
+def lib() -> ctypes.CDLL:
+    """Load libqmla.so once. Raises if it has not been built: there is no fallback path."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    path = os.environ.get("QMLA_LIB", str(LIB_PATH))
+    if not os.path.exists(path):
+        raise ImportError(f"{path} is missing: build the HIP library first "
+                          f"(python -c 'import __graft_entry__ as g; g.build()')")
+    handle = ctypes.CDLL(path)
+    for name, (res, args) in SIGNATURES.items():
+        fn = getattr(handle, name)
+        fn.restype = res
+        fn.argtypes = args
+    ver = handle.qmla_version()
+    if ver != ABI_VERSION:
+        raise ImportError(f"{path}: ABI version {ver}, expected {ABI_VERSION}")
+    _lib = handle
+    return _lib
+
+
+def check(fn: str, code: int) -> None:
+    if code != OK:
+        if code == ERR_NOKERNEL:
+            raise NotImplementedError(f"{fn}: {ERR_NAMES[code]}")
+        raise QmlaError(fn, code)

@@ -1,0 +1,106 @@
+"""GPU parity: the HIP decode against the CPU oracle on the same seeded inputs.
+
+Tolerances (max-abs on the output, fp32 oracle): 1e-2 for a bf16 cache, 3e-2 for an fp8 cache.
+LSE (natural log) within 1e-2.
+"""
+import math
+
+import pytest
+import torch
+
+from tests.mla_cases import make_case, ora, run_oracle, uniform_lens
+
+pytestmark = pytest.mark.gpu
+
+TOL = {"bf16": 1e-2, "fp8": 3e-2}
+
+
+def _report(name, o, lse, ro, rl):
+    err = (o.float().cpu() - ro).abs().max().item()
+    lerr = (lse.float().cpu() - rl).abs().max().item()
+    print(f"[{name}] max-abs {err:.3e} lse {lerr:.3e}", flush=True)
+    return err, lerr
+
+
+@pytest.mark.parametrize("kv,rms_mode", [("bf16", "bf16"), ("fp8", "log8"), ("fp8", "bf16_bytes"), ("fp8", "e4m3")])
+def test_forward_balanced(gpu, kv, rms_mode):
+    import qmla
+    lens = [1, 63, 64, 65, 700, 2047, 3000, 129]
+    c = make_case(batch=len(lens), heads=24, d_c=512, rope_w=64, page_size=64, lens=lens, kv=kv,
+                  rms_mode=rms_mode, seed=5, device=gpu, rms="spread", amp=2.0 if kv == "fp8" else 1.0)
+    o, lse = qmla.forward(c.q_nope, c.q_pe, c.cache, c.block_table, c.seq_lens, page_size=c.page_size,
+                          sm_scale=c.sm_scale, kv_fp8=kv == "fp8", fp8_rms={"log8": "log8", "bf16_bytes": "bf16",
+                                                                          "e4m3": "e4m3", "bf16": "log8"}[rms_mode],
+                          k_scale=c.k_scale, num_workgroups=5)
+    torch.cuda.synchronize()
+    ro, rl = run_oracle(c)
+    err, lerr = _report(f"balanced {kv}/{rms_mode}", o, lse, ro, rl)
+    assert err < TOL[kv] and lerr < 1e-2
+
+
+@pytest.mark.parametrize("splits", [1, 3, 8])
+@pytest.mark.parametrize("kv", ["bf16", "fp8"])
+def test_reference_surface(gpu, kv, splits):
+    """decode_attention_fwd: q = [latent | rope | tail], attn_logits partials, in-place outputs."""
+    import qmla
+    lens = [900, 77, 1600, 513]
+    c = make_case(batch=len(lens), heads=24, d_c=512, rope_w=64, page_size=64, lens=lens, kv=kv, seed=7,
+                  device=gpu, rms="spread")
+    B, H = c.q_nope.shape[:2]
+    q = torch.zeros(B, H, c.row - 0, dtype=torch.bfloat16, device=gpu)
+    q[..., :512] = c.q_nope
+    q[..., 512:576] = c.q_pe
+    q[..., 576:] = 7.0          # tail columns must be ignored (Lk = rms_offset)
+    o = torch.full((B, H, 512), float("nan"), dtype=torch.bfloat16, device=gpu)
+    lse = torch.zeros(B, H, dtype=torch.float32, device=gpu)
+    logits = torch.full((B, H, splits, 513), float("nan"), dtype=torch.float32, device=gpu)
+    cache = c.cache if kv == "bf16" else c.cache.view(torch.float8_e4m3fn)
+    qmla.decode_attention_fwd(q, cache, cache[..., :512], o, lse, c.block_table, c.seq_lens, logits, splits,
+                              c.sm_scale, c.page_size, k_scale=c.k_scale, is_mla=True, rms_offset=576,
+                              rms_log8=kv == "fp8")
+    torch.cuda.synchronize()
+    ro, rl = run_oracle(c)
+    err, lerr = _report(f"ref-surface {kv} S={splits}", o, lse, ro, rl)
+    assert err < TOL[kv] and lerr < 1e-2
+    if splits > 1:
+        # the partials follow the reference bounds and layout exactly
+        from tests.mla_cases import cache_bytes, ORACLE_RMS
+        ks = float(c.k_scale.cpu()) if c.k_scale is not None else 1.0
+        att = ora.mla_decode_partials(c.q_nope.cpu().float(), c.q_pe.cpu().float(), cache_bytes(c),
+                                      c.block_table.cpu(), c.seq_lens.cpu(), num_splits=splits, align=16,
+                                      page_size=c.page_size, d_c=512, rope_w=64, rms_offset=576, kv=kv,
+                                      rms_mode=ORACLE_RMS[c.rms_mode], k_scale=ks, sm_scale=c.sm_scale)
+        got = logits.cpu()
+        written = ~torch.isnan(att[..., 0])
+        assert torch.equal(written, ~torch.isnan(got[..., 0])), "split bounds differ from the reference"
+        perr = (got[written] - att[written]).abs().max().item()
+        print(f"  partial max-abs {perr:.3e}")
+        assert perr < TOL[kv]
+
+
+def test_small_pages_config1(gpu):
+    """B=4, ctx 2048, 16-token pages with a random-permutation block table, bf16 (config 1 shape)."""
+    import qmla
+    c = make_case(batch=4, heads=24, d_c=512, rope_w=64, page_size=16, lens=[2048] * 4, kv="bf16", seed=0,
+                  device=gpu)
+    o, lse = qmla.forward(c.q_nope, c.q_pe, c.cache, c.block_table, c.seq_lens, page_size=16,
+                          sm_scale=c.sm_scale, num_workgroups=7)
+    torch.cuda.synchronize()
+    ro, rl = run_oracle(c)
+    err, lerr = _report("config1 P16", o, lse, ro, rl)
+    assert err < 1e-2 and lerr < 1e-2
+
+
+def test_gla_verify(gpu):
+    """GLA-g2 (2 x 256 latent, 12 heads per group) with 4-token causal verify rows, fp8 + log8."""
+    import qmla
+    lens = [300, 1000, 64, 2100, 5]
+    c = make_case(batch=len(lens), heads=24, d_c=512, rope_w=64, page_size=64, lens=lens, kv="fp8",
+                  rms_mode="log8", seed=4, device=gpu, qrows=4, groups=2, rms="spread")
+    o, lse = qmla.forward(c.q_nope, c.q_pe, c.cache, c.block_table, c.seq_lens, d_c=512, page_size=64,
+                          sm_scale=c.sm_scale, kv_fp8=True, fp8_rms="log8", k_scale=c.k_scale, qrows=4,
+                          groups=2, num_workgroups=6)
+    torch.cuda.synchronize()
+    ro, rl = run_oracle(c)
+    err, lerr = _report("gla-g2 verify", o, lse, ro, rl)
+    assert err < 3e-2 and lerr < 1e-2
