@@ -1,0 +1,262 @@
+#!/usr/bin/env python3
+"""MLA decode throughput on one MI355X: tokens/s and achieved HBM GB/s.
+
+Default workload (the headline metric): FP8 e4m3 latent KV with 1-byte log2 rms codes, B=128
+decode rows, 24 heads sharing one latent row, d_c=512, d_r=64, 64-token pages behind a
+random-permutation block table, context lengths lognormal (median 16384, sigma 0.5) clipped to
+[1024, 65536], latent/rope drawn N(0,1) x4 against a per-layer scale calibrated on the unscaled
+draw, seed 2. Inputs are resident in HBM before timing.
+
+Prints ONE JSON line. `value` = decode rows per second of the whole call (plan + decode + combine)
+at one layer; `roofline` reports the decode kernel's algorithmic bytes over its own average
+duration (HIP events on the stream it runs on); `cpu_baseline` times the CPU oracle on a fixed
+sample of the same workload on this host's cores.
+
+    python bench.py [--steps K] [--warmup W] [--workload fp8_b128|bf16_b64|gla_b48] [--no-cpu]
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import pathlib
+import statistics
+import sys
+import time
+
+REPO = pathlib.Path(__file__).resolve().parent
+for p in (REPO, REPO / "qwen-mla-vllm_amd"):
+    if str(p) not in sys.path:
+        sys.path.insert(0, str(p))
+
+METRIC = "MLA decode tokens/s + achieved HBM GB/s (% peak), B=128 ctx16k fp8 latent KV"
+HBM_PEAK_GBPS = 8000.0
+
+WORKLOADS = {
+    # name: (make_case kwargs, description)
+    "fp8_b128": dict(batch=128, heads=24, d_c=512, rope_w=64, page_size=64, kv="fp8", rms_mode="log8", seed=2,
+                     amp=4.0, lens=("lognormal", 16384, 0.5, 1024, 65536)),
+    "bf16_b64": dict(batch=64, heads=24, d_c=512, rope_w=64, page_size=64, kv="bf16", rms_mode="bf16", seed=1,
+                     amp=1.0, lens=("uniform", 4096, 32768)),
+    "gla_b48": dict(batch=48, heads=24, d_c=512, rope_w=64, page_size=64, kv="fp8", rms_mode="log8", seed=4,
+                    amp=1.0, lens=("uniform", 8192, 32768), qrows=4, groups=2),
+}
+
+
+def make_workload(name, device):
+    from qmla.synth import lognormal_lens, make_case, uniform_lens
+    w = dict(WORKLOADS[name])
+    spec = w.pop("lens")
+    if spec[0] == "lognormal":
+        lens = lognormal_lens(w["batch"], spec[1], spec[2], spec[3], spec[4], seed=w["seed"])
+    else:
+        lens = uniform_lens(w["batch"], spec[1], spec[2], seed=w["seed"])
+    return make_case(lens=lens, device=device, rms="row", **w), spec
+
+
+def kernel_bytes(case) -> int:
+    """Algorithmic bytes the decode kernel reads: cached rows (latent + rope + rms, padding
+    excluded), queries, block-table entries and lengths."""
+    import torch
+    e = 1 if case.kv == "fp8" else 2
+    r = 2 if case.rms_mode in ("bf16", "bf16_bytes") else 1
+    n_req = case.seq_lens.shape[0] // case.qrows
+    L = case.seq_lens.view(n_req, case.qrows)[:, -1].to(torch.int64)
+    toks = int(L.sum())
+    rows, H = case.q_nope.shape[0], case.heads
+    dv = case.d_c // case.groups
+    pages = int(((L + case.page_size - 1) // case.page_size).sum())
+    return toks * (case.d_c * e + case.rope_w * e + H * r) + rows * H * (dv + case.rope_w) * 2 + pages * 4 + rows * 4
+
+
+def cpu_baseline(case, sample_every: int, budget_s: float):
+    """The CPU oracle on a fixed sample of the workload's requests (every k-th), timed on this host's
+    cores; returns decode rows per second scaled per request."""
+    import torch
+    from oracle import mla_oracle as ora
+    cores = len(os.sched_getaffinity(0))
+    torch.set_num_threads(cores)
+    n_req = case.seq_lens.shape[0] // case.qrows
+    picks = list(range(0, n_req, sample_every))
+    rows = [b * case.qrows + j for b in picks for j in range(case.qrows)]
+    # compact CPU copy of just the sampled requests' pages
+    P = case.page_size
+    bt = case.block_table.cpu()
+    sl = case.seq_lens.cpu()
+    page_ids, new_bt = [], torch.zeros(len(rows), bt.shape[1], dtype=torch.int32)
+    for i, r in enumerate(rows):
+        n = max(1, -(-int(sl[r]) // P))
+        base = len(page_ids)
+        if i % case.qrows == 0:
+            page_ids.extend(int(x) for x in bt[r, :n])
+            first = base
+        new_bt[i, :n] = torch.arange(first, first + n, dtype=torch.int32)
+    idx = torch.tensor(page_ids, dtype=torch.long, device=case.cache.device)
+    cache = case.cache.index_select(0, idx).cpu().contiguous()
+    cache = cache.view(torch.uint8).reshape(cache.shape[0], P, -1)
+    rms_map = {"bf16": ora.RMS_BF16, "log8": ora.RMS_LOG8, "bf16_bytes": ora.RMS_BF16_BYTES,
+               "e4m3": ora.RMS_E4M3, "none": ora.RMS_NONE}
+    qn = case.q_nope.cpu().float()[rows]
+    qp = case.q_pe.cpu().float()[rows]
+    sll = sl[rows]
+    ks = float(case.k_scale.cpu()) if case.k_scale is not None else 1.0
+
+    def run():
+        ora.mla_decode(qn, qp, cache, new_bt, sll, page_size=P, d_c=case.d_c, rope_w=case.rope_w,
+                       rms_offset=case.rms_offset, kv=case.kv, rms_mode=rms_map[case.rms_mode], k_scale=ks,
+                       sm_scale=case.sm_scale, rms_heads=case.heads, groups=case.groups)
+
+    times = []
+    t_all = time.perf_counter()
+    while True:
+        t0 = time.perf_counter()
+        run()
+        times.append(time.perf_counter() - t0)
+        if time.perf_counter() - t_all > budget_s or len(times) >= 3:
+            break
+    t = statistics.median(times)
+    toks = int(sll.to(torch.int64).sum())
+    return {"value": round(len(rows) / t, 3), "unit": "tokens/s", "cores": cores, "kind": "port",
+            "sample": f"{len(picks)} of {n_req} requests (every {sample_every}th, {len(rows)} rows, "
+                      f"{toks} cached tokens), fp32 torch oracle, median of {len(times)} runs "
+                      f"({t:.2f} s each), scaled per request"}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--workload", default="fp8_b128", choices=sorted(WORKLOADS))
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--cpu-every", type=int, default=2)
+    ap.add_argument("--cpu-budget", type=float, default=20.0)
+    ap.add_argument("--copy-calib-mib", type=int, default=0,
+                    help="also run a plain device copy of this many MiB (FETCH/WRITE_SIZE calibration)")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(json.dumps({"error": "this build measures one GPU only: the decode shards by request "
+                                   "(no collectives); run with --gpus 1"}))
+        sys.exit(2)
+
+    import torch
+    import qmla
+    from qmla import _lib
+    from qmla.decode import Workspace, build_params, workspace_bytes
+
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    case, spec = make_workload(args.workload, dev)
+    rows, H = case.q_nope.shape[0], case.heads
+    dv = case.d_c // case.groups
+    out = torch.empty(rows, H, dv, dtype=torch.bfloat16, device=dev)
+    lse = torch.empty(rows, H, dtype=torch.float32, device=dev)
+    kv = _lib.KV_FP8 if case.kv == "fp8" else _lib.KV_BF16
+    mode = {"bf16": _lib.RMS_BF16, "log8": _lib.RMS_LOG8, "bf16_bytes": _lib.RMS_BF16_BYTES,
+            "e4m3": _lib.RMS_E4M3}[case.rms_mode]
+    args_p = dict(q_nope=case.q_nope, q_pe=case.q_pe, kv_cache=case.cache, block_table=case.block_table,
+                  seq_lens=case.seq_lens, out=out, lse=lse, d_c=case.d_c, rope_w=case.rope_w,
+                  rms_offset=case.rms_offset, rms_mode=mode, kv=kv, page_size=case.page_size,
+                  sm_scale=case.sm_scale, k_scale=case.k_scale, qrows=case.qrows, groups=case.groups,
+                  num_splits=0, split_align=0)
+    ws = Workspace().reserve(workspace_bytes(build_params(**args_p)), dev)
+    p = build_params(workspace=ws, **args_p)
+    lib = qmla.lib()
+    st = torch.cuda.current_stream().cuda_stream
+
+    def step():
+        _lib.check("qmla_decode", lib.qmla_decode(p, st))
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+
+    # timed region 1: the whole call, K steps back to back
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    t_wall = time.perf_counter()
+    e0.record()
+    for _ in range(args.steps):
+        step()
+    e1.record()
+    torch.cuda.synchronize()
+    t_wall = time.perf_counter() - t_wall
+    ms = e0.elapsed_time(e1) / args.steps
+
+    # timed region 2: the same call stage by stage, events around the decode kernel
+    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True),
+            torch.cuda.Event(enable_timing=True)) for _ in range(args.steps)]
+    for a, b, c in evs:
+        _lib.check("qmla_plan", lib.qmla_plan(p, st))
+        a.record()
+        _lib.check("qmla_decode_partial", lib.qmla_decode_partial(p, st))
+        b.record()
+        _lib.check("qmla_combine", lib.qmla_combine(p, st))
+        c.record()
+    torch.cuda.synchronize()
+    part_ms = statistics.mean(a.elapsed_time(b) for a, b, _ in evs)
+    comb_ms = statistics.mean(b.elapsed_time(c) for _, b, c in evs)
+
+    if args.copy_calib_mib:
+        n = args.copy_calib_mib << 20
+        src = torch.empty(n, dtype=torch.uint8, device=dev).fill_(1)
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+
+    n_req = rows // case.qrows
+    toks_cached = int(case.seq_lens.view(n_req, case.qrows)[:, -1].to(torch.int64).sum())
+    from qmla.synth import algorithmic_bytes
+    call_bytes = algorithmic_bytes(case)
+    k_bytes = kernel_bytes(case)
+    value = rows / (ms / 1e3)
+    gbps = call_bytes / (ms / 1e3) / 1e9
+    k_gbps = k_bytes / (part_ms / 1e3) / 1e9
+    traffic = None
+    tf = REPO / "profiles" / f"traffic_{args.workload}.json"
+    if tf.exists():
+        try:
+            traffic = json.loads(tf.read_text()).get("hbm_bytes_per_launch")
+        except (ValueError, OSError):
+            traffic = None
+
+    cpu = None
+    if not args.no_cpu:
+        cpu = cpu_baseline(case, args.cpu_every, args.cpu_budget)
+
+    ctx = (f"lognormal median {spec[1]} sigma {spec[2]} clipped [{spec[3]}, {spec[4]}]" if spec[0] == "lognormal"
+           else f"uniform [{spec[1]}, {spec[2]}]")
+    res = {
+        "metric": METRIC,
+        "value": round(value, 1),
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": ("fp8-e4m3 cache, bf16 MFMA, fp32 softmax" if case.kv == "fp8" else "bf16 cache, bf16 MFMA, fp32 softmax"),
+        "data": "synthetic",
+        "config": {"workload": f"mla_decode_{args.workload}", "batch": n_req, "rows": rows, "heads": H,
+                   "d_c": case.d_c, "d_r": case.rope_w, "page_size": case.page_size, "kv": case.kv,
+                   "rms": case.rms_mode, "ctx": ctx, "cached_tokens": toks_cached, "qrows": case.qrows,
+                   "groups": case.groups, "split": "balanced", "row_bytes": case.row * (1 if case.kv == "fp8" else 2)},
+        "gbps": round(gbps, 1),
+        "hbm_frac": round(gbps / HBM_PEAK_GBPS, 4),
+        "decode_kernel_us": round(part_ms * 1e3, 2),
+        "combine_us": round(comb_ms * 1e3, 2),
+        "wall_s_timed": round(t_wall, 3),
+        "roofline": {"bound": "hbm", "achieved": round(k_gbps, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
+                     "frac": round(k_gbps / HBM_PEAK_GBPS, 4), "traffic": traffic,
+                     "algorithmic_bytes_per_launch": k_bytes},
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(res), flush=True)
+
+
+if __name__ == "__main__":
+    main()

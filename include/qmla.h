@@ -143,8 +143,14 @@ size_t qmla_workspace_bytes(const qmla_decode_params* p);
  * split mode needs them) followed by the LSE combine, all on `stream` (a hipStream_t). */
 int qmla_decode(const qmla_decode_params* p, void* stream);
 
-/* The two passes alone, reference-shaped: the partial (stage 1) pass writes attn_logits in the
- * workspace; qmla_combine (stage 2) merges them into out / lse. Fixed-split mode only. */
+/* The stages of qmla_decode, callable one by one on the same stream and params:
+ *   qmla_plan            balanced mode only: per-request tile counts and prefix sums into the
+ *                        workspace (one small workgroup; no host involvement)
+ *   qmla_decode_partial  the decode pass (stage 1, qwen_mla/ops/mla_decode_attention.py:297-586):
+ *                        partials into attn_logits (fixed mode) or the balanced workspace, and the
+ *                        final out / lse directly for requests a single workgroup covered
+ *   qmla_combine         the LSE merge (stage 2, qwen_mla/ops/mla_decode_attention.py:1064-1137) */
+int qmla_plan(const qmla_decode_params* p, void* stream);
 int qmla_decode_partial(const qmla_decode_params* p, void* stream);
 int qmla_combine(const qmla_decode_params* p, void* stream);
 

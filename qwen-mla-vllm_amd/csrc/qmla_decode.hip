@@ -975,13 +975,34 @@ size_t qmla_workspace_bytes(const qmla_decode_params* p) {
   return balanced_layout(p).total;
 }
 
+static int check_balanced_ws(const qmla_decode_params* p) {
+  if (!p->workspace) return QMLA_ERR_WORKSPACE;
+  if (p->workspace_bytes < qmla_workspace_bytes(p)) return QMLA_ERR_WORKSPACE;
+  if (!aligned16(p->workspace)) return QMLA_ERR_ALIGN;
+  return QMLA_OK;
+}
+
+int qmla_plan(const qmla_decode_params* p, void* stream) {
+  int rc = validate(p);
+  if (rc) return rc;
+  if (p->num_splits != 0) return QMLA_ERR_MODE;
+  rc = check_balanced_ws(p);
+  if (rc) return rc;
+  KParams k = make_kparams(p);
+  return run_plan(p, k, (hipStream_t)stream);
+}
+
 int qmla_decode_partial(const qmla_decode_params* p, void* stream) {
   int rc = validate(p);
   if (rc) return rc;
-  if (p->num_splits <= 0) return QMLA_ERR_MODE;
-  if (p->num_splits > 1 && !p->workspace) return QMLA_ERR_WORKSPACE;
+  if (p->d_c / p->groups > 2048) return QMLA_ERR_SHAPE;
   const Inst* in = find_inst(p);
   if (!in) return QMLA_ERR_NOKERNEL;
+  if (p->num_splits > 1 && !p->workspace) return QMLA_ERR_WORKSPACE;
+  if (p->num_splits == 0) {
+    rc = check_balanced_ws(p);
+    if (rc) return rc;
+  }
   KParams k = make_kparams(p);
   return run_partial(p, in, k, (hipStream_t)stream);
 }
@@ -989,10 +1010,13 @@ int qmla_decode_partial(const qmla_decode_params* p, void* stream) {
 int qmla_combine(const qmla_decode_params* p, void* stream) {
   int rc = validate(p);
   if (rc) return rc;
-  if (p->num_splits <= 0) return QMLA_ERR_MODE;
   if (p->num_splits == 1) return QMLA_OK;
-  if (!p->workspace) return QMLA_ERR_WORKSPACE;
   if (p->d_c / p->groups > 2048) return QMLA_ERR_SHAPE;
+  if (p->num_splits > 1 && !p->workspace) return QMLA_ERR_WORKSPACE;
+  if (p->num_splits == 0) {
+    rc = check_balanced_ws(p);
+    if (rc) return rc;
+  }
   KParams k = make_kparams(p);
   return run_combine(p, k, (hipStream_t)stream);
 }
@@ -1011,9 +1035,8 @@ int qmla_decode(const qmla_decode_params* p, void* stream) {
     if (rc || p->num_splits == 1) return rc;
     return run_combine(p, k, st);
   }
-  if (!p->workspace) return QMLA_ERR_WORKSPACE;
-  if (p->workspace_bytes < qmla_workspace_bytes(p)) return QMLA_ERR_WORKSPACE;
-  if (!aligned16(p->workspace)) return QMLA_ERR_ALIGN;
+  rc = check_balanced_ws(p);
+  if (rc) return rc;
   KParams k = make_kparams(p);
   rc = run_plan(p, k, st);
   if (rc) return rc;

@@ -89,6 +89,7 @@ SIGNATURES = {
     "qmla_build_info": (ctypes.c_char_p, []),
     "qmla_workspace_bytes": (ctypes.c_size_t, [_P]),
     "qmla_decode": (ctypes.c_int, [_P, ctypes.c_void_p]),
+    "qmla_plan": (ctypes.c_int, [_P, ctypes.c_void_p]),
     "qmla_decode_partial": (ctypes.c_int, [_P, ctypes.c_void_p]),
     "qmla_combine": (ctypes.c_int, [_P, ctypes.c_void_p]),
     "qmla_decode_2pass_scratch_bytes": (ctypes.c_size_t, [_P, ctypes.c_int64]),
