@@ -31,8 +31,8 @@
 
 namespace qmla {
 
-constexpr int TILE = 64;   // tokens per tile
-constexpr int NWAVE = 4;   // waves per workgroup
+constexpr int PLAN_TILE = 64;  // balancing granularity of the balanced plan (tokens)
+constexpr int NWAVE = 4;       // waves per workgroup
 constexpr int NTHR = NWAVE * 64;
 
 struct KParams {
@@ -75,51 +75,92 @@ __device__ __forceinline__ void store_out(void* base, int dt, int64_t idx, float
   else reinterpret_cast<float*>(base)[idx] = v;
 }
 
-// Steady-state wait for tile t: every wave issues, per tile, its share of the CPR data DMAs
-// (instructions i = wave, wave+4, ...) and wave 0 also one page-id DMA. After data(t) come exactly
-// S-2 such tile groups, so "vmcnt <= that count" means data(t) (and all earlier loads) landed.
-template <int S, int CPR>
-__device__ __forceinline__ void wait_steady(int wave) {
-  if (wave == 0) wait_vmcnt<(S - 2) * ((CPR + 3) / 4 + 1)>();
-  else if (wave == 1) wait_vmcnt<(S - 2) * ((CPR + 2) / 4)>();
-  else if (wave == 2) wait_vmcnt<(S - 2) * ((CPR + 1) / 4)>();
-  else wait_vmcnt<(S - 2) * (CPR / 4)>();
-}
-
 // Compile-time shape of one kernel instance.
 //   EB   cache element bytes (1 = fp8 e4m3fn, 2 = bf16)
 //   RMS  QMLA_RMS_* tail format
 //   DCG  latent columns per group, G groups (d_c = G*DCG)
 //   WP   rope columns padded to a multiple of 64 (scores read [latent | rope_w], rest masked)
 //   MB   16-row MFMA blocks per group (rows per group = qrows * heads/G <= 16*MB)
-//   S    LDS ring stages, CPR 16-byte chunks loaded per row (row bytes in LDS = 16*CPR)
-template <int EB_, int RMS_, int DCG_, int WP_, int MB_, int G_, int S_, int CPR_, bool CAP_>
+//   S    LDS ring stages, CPR 16-byte chunks staged per row (LDS row = 16*CPR bytes)
+//   TILE tokens per pipeline step (32 or 64), WGPC workgroups resident per compute unit
+//
+// Work split inside a workgroup (4 waves, WPG = 4/G per latent group):
+//   scores  the group's (16-token block, 16-row block) items are dealt to its waves so that a
+//           wave owns a fixed set of MBW row blocks (MSPLIT = MB/MBW wave sets) and TBW token
+//           blocks; its query fragments (B operand) stay in VGPRs for the whole segment.
+//   P.V     each wave owns NCOL latent output columns for all rows of its group.
+template <int EB_, int RMS_, int DCG_, int WP_, int MB_, int G_, int S_, int CPR_, bool CAP_, int TILE_, int WGPC_>
 struct Cfg {
   static constexpr int EB = EB_, RMS = RMS_, DCG = DCG_, WP = WP_, MB = MB_, G = G_, S = S_;
   static constexpr int CPR = CPR_;
   static constexpr bool CAP = CAP_;
+  static constexpr int TILE = TILE_, WGPC = WGPC_;
   static constexpr int DC = G * DCG;
   static constexpr int RB = 16 * CPR;              // LDS row stride (bytes)
   static constexpr int STAGE = TILE * RB;          // bytes per stage
+  static constexpr int NTB = TILE / 16;            // 16-token blocks per tile
   static constexpr int WPG = NWAVE / G;            // waves per group
-  static constexpr int TBW = (TILE / 16) / WPG;    // 16-token score blocks per wave
+  // Row blocks are split across waves only when the token blocks alone cannot occupy every wave
+  // (two-per-CU 32-token tiles); otherwise each wave scores all row blocks of its own token blocks,
+  // so every staged key row is read from LDS and converted exactly once.
+  static constexpr int MSPLIT = (NTB % WPG == 0) ? 1 : ((WPG % MB == 0) ? MB : 1);
+  static constexpr int MBW = MB / MSPLIT;          // row blocks per wave (scores)
+  static constexpr int WPM = WPG / MSPLIT;         // waves sharing a row-block set
+  static constexpr int TBW = NTB / WPM;            // token blocks per wave (scores)
   static constexpr int KQ = (DCG + WP) / 32;       // k-steps of the score product
   static constexpr int KP = KQ / 2;                // k-step pairs (64 columns each)
   static constexpr int NCOL = DCG / WPG;           // output columns per wave
   static constexpr int CB = NCOL / 16;             // 16-column output blocks per wave
   static constexpr int ROWS = 16 * MB;
   static constexpr int PSTRIDE = TILE * 2 + 16;    // bf16 P row stride in LDS (bytes, padded)
+  static constexpr int NI = (TILE * CPR + 63) / 64;          // DMA instructions per tile
+  static constexpr int NDMA = (NI + NWAVE - 1) / NWAVE;      // ... per wave (at most)
   static_assert(WP % 64 == 0 && DCG % 64 == 0, "64-column pairs");
-  static_assert(NWAVE % G == 0 && (TILE / 16) % WPG == 0 && DCG % (16 * WPG) == 0, "wave split");
-  static_assert(S >= 2, "ring");
+  static_assert(NWAVE % G == 0 && DCG % (16 * WPG) == 0, "column split");
+  static_assert(NTB % WPM == 0 && TBW >= 1, "token-block split");
+  static_assert(TILE % 32 == 0 && PLAN_TILE % TILE == 0, "tile");
+  static_assert(S >= 2 && CPR >= 16, "ring");
 };
+
+// Staged rows are rotated by 16-byte chunks: chunk c of LDS row r sits at position
+// (c + (r & 15)) mod CPR. The 608/1200-byte row stride alone puts rows r and r+4 on the same LDS
+// banks; with the rotation the 16 rows a K-fragment or V^T read touches start 16*7*r bytes apart
+// (mod 256), which is conflict-free.
+template <int CPR>
+__device__ __forceinline__ int rot_pos(int c, int r) {
+  int p = c + (r & 15);
+  return p >= CPR ? p - CPR : p;
+}
+// byte offset of byte b (within the staged row) of LDS row r
+template <int CPR>
+__device__ __forceinline__ int lds_byte(int r, int b) {
+  return r * (16 * CPR) + 16 * rot_pos<CPR>(b >> 4, r) + (b & 15);
+}
+
+// DMA instructions wave `wave` issues per tile (instructions i = wave, wave+4, ... < NI)
+template <class C>
+__device__ __forceinline__ constexpr int dma_per_wave(int wave) {
+  return (C::NI - wave + NWAVE - 1) / NWAVE;
+}
+// Steady-state wait for tile t: after data(t) each wave has issued S-2 more tile groups (its
+// data DMAs, plus one page-id DMA for wave 0), so "vmcnt <= that count" means data(t) and
+// everything before it landed.
+template <class C>
+__device__ __forceinline__ void wait_steady(int wave) {
+  if (wave == 0) wait_vmcnt<(C::S - 2) * (dma_per_wave<C>(0) + 1)>();
+  else if (wave == 1) wait_vmcnt<(C::S - 2) * dma_per_wave<C>(1)>();
+  else if (wave == 2) wait_vmcnt<(C::S - 2) * dma_per_wave<C>(2)>();
+  else wait_vmcnt<(C::S - 2) * dma_per_wave<C>(3)>();
+}
 
 template <class C>
 struct Smem {
   char kv[C::S][C::STAGE];
-  int pid[2 * C::S][TILE];
+  int pid[2 * C::S][C::TILE];
   char p[C::G][C::ROWS][C::PSTRIDE];
-  float red[2][NWAVE][C::ROWS];
+  float red[2][NWAVE][C::ROWS];   // per-wave row max / row sum of the current tile
+  float alpha[C::G][C::ROWS];     // accumulator rescale of the current tile (when any row moved)
+  float fin[2][C::G][C::ROWS];    // final reference max / sum per row (epilogue)
   int flag[NWAVE];
 };
 
@@ -134,16 +175,18 @@ struct SegOut {
 
 // One contiguous token range [tok_a, tok_e) of request `req` (length L), all query rows.
 //
-// Score layout (S^T = K . Q^T on MFMA): lane (n = head column ln16, lg) of head block mb holds the
+// Score layout (S^T = K . Q^T on MFMA): lane (n = row column ln16, lg) of row block mb holds the
 // scores of tokens tb*16 + 4*lg + i (i = 0..3) for query row mb*16 + ln16, so the per-row
 // softmax reductions over a 16-token block are 3 in-lane ops plus 2 cross-lane steps. The value
 // accumulator (O = P . V) keeps the D layout: lane (col ln16, lg) holds rows mb*16 + 4*lg + i.
 template <class C>
 __device__ __forceinline__ void process_segment(const KParams& p, Smem<C>& sm, int req, int tok_a, int tok_e,
                                                 int L, const SegOut& so, float kscale) {
+  constexpr int TILE = C::TILE;
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform -> SGPR
   const int g = wave / C::WPG, wl = wave % C::WPG;
+  const int mgrp = wl / C::WPM, wt = wl % C::WPM;   // row-block set and token-block phase (scores)
   const int ln16 = lane & 15, lg = lane >> 4;
   const int qrows = p.qrows, hpg = p.hpg;
   const int nrows = qrows * hpg;  // valid rows per group
@@ -153,62 +196,79 @@ __device__ __forceinline__ void process_segment(const KParams& p, Smem<C>& sm, i
   const int P = p.page_size;
   constexpr int RMS_EB = (C::RMS == QMLA_RMS_BF16 || C::RMS == QMLA_RMS_BF16_BYTES) ? 2 : 1;
 
-  // ---- this lane's score row (query row mb*16 + ln16 of group g) ----
-  int rms_b[C::MB];    // byte offset of the row's rms inside a staged cache row
-  int lim_off[C::MB];  // qrows-1-jq: verify token jq sees the first L-(qrows-1-jq) tokens
+  // ---- this lane's score rows: (mgrp*MBW + mbl)*16 + ln16 of group g ----
+  int rms_b[C::MBW];    // byte offset of the row's rms inside a staged cache row
+  int lim_off[C::MBW];  // qrows-1-jq: verify token jq sees the first L-(qrows-1-jq) tokens
 #pragma unroll
-  for (int mb = 0; mb < C::MB; ++mb) {
-    const int r = mb * 16 + ln16;
+  for (int mbl = 0; mbl < C::MBW; ++mbl) {
+    const int r = (mgrp * C::MBW + mbl) * 16 + ln16;
     const int rr = r < nrows ? r : nrows - 1;
     const int jq = rr / hpg, h = rr - jq * hpg;
-    rms_b[mb] = p.rms_off_b + (g * hpg + h) * RMS_EB;
-    lim_off[mb] = qrows - 1 - jq;
+    rms_b[mbl] = p.rms_off_b + (g * hpg + h) * RMS_EB;
+    lim_off[mbl] = qrows - 1 - jq;
   }
 
   // ---- page-id and data DMA issue ----
+  // LDS chunk q = 64*i + lane of a stage holds row q / CPR, position q % CPR, i.e. global chunk
+  // (position - (row & 15)) mod CPR; its byte offset inside a contiguous tile is fixed per
+  // (instruction, lane), so it is computed once here.
+  uint32_t doff[C::NDMA];
+#pragma unroll
+  for (int j = 0; j < C::NDMA; ++j) {
+    int q = (wave + NWAVE * j) * 64 + lane;
+    q = q < TILE * C::CPR ? q : TILE * C::CPR - 1;
+    const int r = q / C::CPR, pp = q - r * C::CPR;
+    int c = pp - (r & 15);
+    c = c < 0 ? c + C::CPR : c;
+    doff[j] = (uint32_t)(r * C::RB + 16 * c);
+  }
+  const bool lane_live_last = (C::NI * 64 == TILE * C::CPR) ||
+                              ((wave + NWAVE * (C::NDMA - 1)) * 64 + lane < TILE * C::CPR);
   auto issue_pid = [&](int t) {
     int tok = tok_a + t * TILE + lane;
     tok = tok < tok_e ? tok : tok_e - 1;
-    dma4(bt + tok / P, reinterpret_cast<char*>(sm.pid[t % (2 * C::S)]));
+    if (lane < TILE) dma4(bt + tok / P, reinterpret_cast<char*>(sm.pid[t % (2 * C::S)]));
   };
   auto issue_data = [&](int t) {
     const int tok0 = tok_a + t * TILE;
     const int* pidt = sm.pid[t % (2 * C::S)];
     char* dst = sm.kv[t % C::S];
     if (tok0 / P == (tok0 + TILE - 1) / P && p.token_stride_b == C::RB) {
-      // the 64 rows are consecutive in one page: one contiguous block (rows past tok_e are still
-      // inside the page and get masked)
-      const char* base = p.kv + (int64_t)pidt[0] * p.page_stride_b + (int64_t)(tok0 % P) * p.token_stride_b;
+      // the TILE rows are consecutive in one page: one contiguous block, addressed through a
+      // buffer resource so the per-tile cost is scalar (rows past tok_e stay inside the page)
+      const int page = __builtin_amdgcn_readfirstlane(pidt[0]);
+      const char* base = p.kv + (int64_t)page * p.page_stride_b + (int64_t)(tok0 % P) * p.token_stride_b;
+      const __amdgpu_buffer_rsrc_t rsrc = make_rsrc(base, (uint32_t)(TILE * C::RB));
 #pragma unroll
-      for (int i0 = 0; i0 < C::CPR; i0 += NWAVE) {
-        const int i = i0 + wave;
-        if (i < C::CPR) dma16(base + (i * 64 + lane) * 16, dst + i * 1024);
+      for (int j = 0; j < C::NDMA; ++j) {
+        const int i = wave + NWAVE * j;
+        if (i < C::NI && (j < C::NDMA - 1 || lane_live_last)) dma16_buf(rsrc, doff[j], dst + i * 1024);
       }
       return;
     }
-    int tok = tok0 + lane;
+    int tok = tok0 + (lane < TILE ? lane : TILE - 1);
     tok = tok < tok_e ? tok : tok_e - 1;
-    const int64_t off = (int64_t)pidt[lane] * p.page_stride_b + (int64_t)(tok % P) * p.token_stride_b;
+    const int64_t off = (int64_t)pidt[lane < TILE ? lane : TILE - 1] * p.page_stride_b +
+                        (int64_t)(tok % P) * p.token_stride_b;
     const int off_lo = (int)(uint32_t)off, off_hi = (int)(uint32_t)((uint64_t)off >> 32);
 #pragma unroll
-    for (int i0 = 0; i0 < C::CPR; i0 += NWAVE) {
-      const int i = i0 + wave;
-      if (i < C::CPR) {
-        const int c = i * 64 + lane;
-        const int tk = c / C::CPR, piece = c - tk * C::CPR;
+    for (int j = 0; j < C::NDMA; ++j) {
+      const int i = wave + NWAVE * j;
+      if (i < C::NI) {
+        const int tk = (int)(doff[j] / (uint32_t)C::RB), cb = (int)(doff[j] - (uint32_t)tk * C::RB);
         const uint32_t lo = (uint32_t)__shfl(off_lo, tk), hi = (uint32_t)__shfl(off_hi, tk);
         const int64_t roff = (int64_t)(((uint64_t)hi << 32) | lo);
-        dma16(p.kv + roff + piece * 16, dst + i * 1024);
+        if (j < C::NDMA - 1 || lane_live_last) dma16(p.kv + roff + cb, dst + i * 1024);
       }
     }
   };
 
   // ---- query fragments (B operand of S^T): pair jj, lane group lg holds q columns
-  //      64*jj + 16*lg .. +16 of query row mb*16 + ln16; zero outside [latent | rope_w) ----
-  bf16x8 qf[C::MB][C::KQ];
+  //      64*jj + 16*lg .. +16 of query row (mgrp*MBW + mbl)*16 + ln16; zero outside [latent | rope_w) ----
+  bf16x8 qf[C::MBW][C::KQ];
 #pragma unroll
-  for (int mb = 0; mb < C::MB; ++mb) {
-    const int r = mb * 16 + ln16;
+  for (int mbl = 0; mbl < C::MBW; ++mbl) {
+    const int r = (mgrp * C::MBW + mbl) * 16 + ln16;
     const bool rv = r < nrows;
     const int rr = rv ? r : 0;
     const int jq = rr / hpg, h = rr - jq * hpg;
@@ -241,19 +301,21 @@ __device__ __forceinline__ void process_segment(const KParams& p, Smem<C>& sm, i
             }
           }
         }
-        qf[mb][2 * jj + half] = v;
+        qf[mbl][2 * jj + half] = v;
       }
     }
   }
 
   f32x4 acc[C::MB][C::CB];
-  float mref[C::MB], l_run[C::MB];  // per query row ln16 of block mb (log2 domain reference max)
 #pragma unroll
-  for (int mb = 0; mb < C::MB; ++mb) {
+  for (int mb = 0; mb < C::MB; ++mb)
 #pragma unroll
     for (int cb = 0; cb < C::CB; ++cb) acc[mb][cb] = f32x4{0.f, 0.f, 0.f, 0.f};
-    mref[mb] = kNegInf;
-    l_run[mb] = 0.f;
+  float mref[C::MBW], l_run[C::MBW];  // per score row (log2-domain reference max, running sum)
+#pragma unroll
+  for (int mbl = 0; mbl < C::MBW; ++mbl) {
+    mref[mbl] = kNegInf;
+    l_run[mbl] = 0.f;
   }
 
   const float c2 = p.sm_scale * kscale * kLog2e;   // raw q.k -> log2-domain score (before /rms)
@@ -276,7 +338,7 @@ __device__ __forceinline__ void process_segment(const KParams& p, Smem<C>& sm, i
 
   for (int t = 0; t < ntiles; ++t) {
     // wait for this wave's DMA of tile t (and everything issued before it), then publish
-    if (t + C::S - 2 < ntiles) wait_steady<C::S, C::CPR>(wave);
+    if (t + C::S - 2 < ntiles) wait_steady<C>(wave);
     else wait_vmcnt<0>();
     lds_barrier();  // (A) tile t visible; every wave is done with tile t-1
     if (wave == 0) issue_pid(t + 2 * C::S - 2);
@@ -285,35 +347,35 @@ __device__ __forceinline__ void process_segment(const KParams& p, Smem<C>& sm, i
     const char* kvs = sm.kv[t % C::S];
     const int tok0 = tok_a + t * TILE;
 
-    // ---- scores S^T = K . Q^T ----
-    f32x4 sacc[C::MB][C::TBW];
-#pragma unroll
-    for (int mb = 0; mb < C::MB; ++mb)
-#pragma unroll
-      for (int tb = 0; tb < C::TBW; ++tb) sacc[mb][tb] = f32x4{0.f, 0.f, 0.f, 0.f};
+    // ---- scores S^T = K . Q^T for this wave's (token block, row block) items: every 64-column
+    //      pair of the block's rows is read up front, and each row block accumulates on two
+    //      independent MFMA chains (even / odd pairs) ----
+    f32x4 sacc[C::MBW][C::TBW];
 #pragma unroll
     for (int tbi = 0; tbi < C::TBW; ++tbi) {
-      const int tb = wl + tbi * C::WPG;
-      const char* rowp = kvs + (tb * 16 + ln16) * C::RB;
-      // one 64-column pair ahead: LDS reads of pair jj+1 overlap the MFMAs of pair jj
-      i32x4 cur0, cur1, nxt0, nxt1;
-      auto load_pair = [&](int jj, i32x4& r0, i32x4& r1) {
-        const int kcol = 64 * jj + 16 * lg;
-        const int cbyte = (kcol < C::DCG ? g * C::DCG + kcol : C::DC + kcol - C::DCG) * C::EB;
-        r0 = lds_read_b128(rowp + cbyte);
-        if constexpr (C::EB == 2) r1 = lds_read_b128(rowp + cbyte + 16);
-      };
-      load_pair(0, cur0, cur1);
+      const int tb = wt + tbi * C::WPM;
+      const int krow = tb * 16 + ln16;
+      const char* rowp = kvs + krow * C::RB;
+      i32x4 kr0[C::KP], kr1[C::KP];
 #pragma unroll
       for (int jj = 0; jj < C::KP; ++jj) {
-        if (jj + 1 < C::KP) load_pair(jj + 1, nxt0, nxt1);
+        const int kcol = 64 * jj + 16 * lg;
+        const int cbyte = (kcol < C::DCG ? g * C::DCG + kcol : C::DC + kcol - C::DCG) * C::EB;
+        kr0[jj] = lds_read_b128(rowp + 16 * rot_pos<C::CPR>(cbyte >> 4, krow));
+        if constexpr (C::EB == 2) kr1[jj] = lds_read_b128(rowp + 16 * rot_pos<C::CPR>((cbyte >> 4) + 1, krow));
+      }
+      f32x4 s2[C::MBW][2];
+#pragma unroll
+      for (int mbl = 0; mbl < C::MBW; ++mbl) s2[mbl][0] = s2[mbl][1] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int jj = 0; jj < C::KP; ++jj) {
         const int kcol = 64 * jj + 16 * lg;
         bf16x8 ka, kb;
         if constexpr (C::EB == 1) {
-          fp8x16_to_bf16(cur0, ka, kb);
+          fp8x16_to_bf16(kr0[jj], ka, kb);
         } else {
-          ka = __builtin_bit_cast(bf16x8, cur0);
-          kb = __builtin_bit_cast(bf16x8, cur1);
+          ka = __builtin_bit_cast(bf16x8, kr0[jj]);
+          kb = __builtin_bit_cast(bf16x8, kr1[jj]);
         }
         if (jj * 64 + 64 > C::DCG + (C::WP - 64) && kcol + 16 > latent_cols_end) {
           // columns past the rope width (padding up to a 64-column pair): zero them so
@@ -325,201 +387,227 @@ __device__ __forceinline__ void process_segment(const KParams& p, Smem<C>& sm, i
           }
         }
 #pragma unroll
-        for (int mb = 0; mb < C::MB; ++mb) {
-          sacc[mb][tbi] = mfma16(ka, qf[mb][2 * jj], sacc[mb][tbi]);
-          sacc[mb][tbi] = mfma16(kb, qf[mb][2 * jj + 1], sacc[mb][tbi]);
+        for (int mbl = 0; mbl < C::MBW; ++mbl) {
+          s2[mbl][jj & 1] = mfma16(ka, qf[mbl][2 * jj], s2[mbl][jj & 1]);
+          s2[mbl][jj & 1] = mfma16(kb, qf[mbl][2 * jj + 1], s2[mbl][jj & 1]);
         }
-        cur0 = nxt0;
-        cur1 = nxt1;
-        __builtin_amdgcn_sched_barrier(0);
       }
+#pragma unroll
+      for (int mbl = 0; mbl < C::MBW; ++mbl) sacc[mbl][tbi] = s2[mbl][0] + s2[mbl][1];
     }
 
-    // ---- rms divide, scale to log2 units, mask; tile max per query row ----
-    float lmax[C::MB];
-#pragma unroll
-    for (int mb = 0; mb < C::MB; ++mb) lmax[mb] = kNegInf;
+    // ---- rms divisors of this lane's (token, row) scores, read before the V^T reads go out ----
+    float rinv_t[C::TBW][4][C::MBW];
 #pragma unroll
     for (int tbi = 0; tbi < C::TBW; ++tbi) {
-      const int tb = wl + tbi * C::WPG;
+      const int tb = wt + tbi * C::WPM;
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const int tt = tb * 16 + 4 * lg + i;
-        const int tok = tok0 + tt;
-        const char* rowp = kvs + tt * C::RB;
 #pragma unroll
-        for (int mb = 0; mb < C::MB; ++mb) {
+        for (int mbl = 0; mbl < C::MBW; ++mbl) {
           float rinv = 1.0f;
-          if constexpr (C::RMS == QMLA_RMS_LOG8) {
-            const float code = (float)(uint32_t)(uint8_t)rowp[rms_b[mb]];
-            rinv = fast_exp2(3.0f - code * (6.0f / 255.0f));
-          } else if constexpr (C::RMS == QMLA_RMS_BF16 || C::RMS == QMLA_RMS_BF16_BYTES) {
-            const float r = bf16_bits_to_f32(*reinterpret_cast<const uint16_t*>(rowp + rms_b[mb]));
-            rinv = r > 0.f ? __builtin_amdgcn_rcpf(r) : 1.0f;
-          } else if constexpr (C::RMS == QMLA_RMS_E4M3) {
-            const float r = fp8_to_f32((uint8_t)rowp[rms_b[mb]]) * kscale;
-            rinv = r > 0.f ? __builtin_amdgcn_rcpf(r) : 1.0f;
+          if constexpr (C::RMS != QMLA_RMS_NONE) {
+            const char* rp = kvs + lds_byte<C::CPR>(tt, rms_b[mbl]);
+            if constexpr (C::RMS == QMLA_RMS_LOG8) {
+              const float code = (float)(uint32_t)(uint8_t)rp[0];
+              rinv = fast_exp2(3.0f - code * (6.0f / 255.0f));
+            } else if constexpr (C::RMS == QMLA_RMS_BF16 || C::RMS == QMLA_RMS_BF16_BYTES) {
+              const float r = bf16_bits_to_f32(*reinterpret_cast<const uint16_t*>(rp));
+              rinv = r > 0.f ? __builtin_amdgcn_rcpf(r) : 1.0f;
+            } else if constexpr (C::RMS == QMLA_RMS_E4M3) {
+              const float r = fp8_to_f32((uint8_t)rp[0]) * kscale;
+              rinv = r > 0.f ? __builtin_amdgcn_rcpf(r) : 1.0f;
+            }
           }
+          rinv_t[tbi][i][mbl] = rinv;
+        }
+      }
+    }
+
+    // ---- value fragments for P.V, read transposed from the staged rows; they complete while
+    //      the softmax below runs ----
+    i32x2 vraw[TILE / 32][C::CB][C::EB];
+#pragma unroll
+    for (int kk = 0; kk < TILE / 32; ++kk)
+#pragma unroll
+      for (int cb = 0; cb < C::CB; ++cb) {
+        const int col0 = g * C::DCG + wl * C::NCOL + cb * 16;
+        if constexpr (C::EB == 1) {
+          const int vr = kk * 32 + 8 * lg + (ln16 >> 1);
+          vraw[kk][cb][0] = lds_read_tr8_async(kvs + lds_byte<C::CPR>(vr, col0 + 8 * (ln16 & 1)));
+        } else {
+          const int vr = kk * 32 + 8 * lg + (ln16 >> 2);
+          const int vb = (col0 + 4 * (ln16 & 3)) * 2;
+          vraw[kk][cb][0] = lds_read_tr16_async(kvs + lds_byte<C::CPR>(vr, vb));
+          vraw[kk][cb][C::EB - 1] = lds_read_tr16_async(kvs + lds_byte<C::CPR>(vr + 4, vb));
+        }
+      }
+
+    // ---- divide by rms, scale to log2 units, mask; tile max per score row ----
+    float lmax[C::MBW];
+#pragma unroll
+    for (int mbl = 0; mbl < C::MBW; ++mbl) lmax[mbl] = kNegInf;
+#pragma unroll
+    for (int tbi = 0; tbi < C::TBW; ++tbi) {
+      const int tb = wt + tbi * C::WPM;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int tok = tok0 + tb * 16 + 4 * lg + i;
+#pragma unroll
+        for (int mbl = 0; mbl < C::MBW; ++mbl) {
+          const float rinv = rinv_t[tbi][i][mbl];
           float v;
           if constexpr (C::CAP) {
-            const float sn = sacc[mb][tbi][i] * (c2 * kLn2) * rinv;   // natural-unit score
+            const float sn = sacc[mbl][tbi][i] * (c2 * kLn2) * rinv;   // natural-unit score
             const float x = sn / capc;
             const float th = 1.0f - 2.0f / (fast_exp2(2.0f * kLog2e * x) + 1.0f);
             v = capc * th * kLog2e;
           } else {
-            v = sacc[mb][tbi][i] * c2 * rinv;
+            v = sacc[mbl][tbi][i] * c2 * rinv;
           }
           int lim = tok_e;
-          if (qrows > 1) { const int lv = L - lim_off[mb]; lim = lv < lim ? lv : lim; }
+          if (qrows > 1) { const int lv = L - lim_off[mbl]; lim = lv < lim ? lv : lim; }
           v = tok < lim ? v : kNegInf;
-          sacc[mb][tbi][i] = v;
-          lmax[mb] = fmaxf(lmax[mb], v);
+          sacc[mbl][tbi][i] = v;
+          lmax[mbl] = fmaxf(lmax[mbl], v);
         }
       }
     }
 #pragma unroll
-    for (int mb = 0; mb < C::MB; ++mb) {
-      lmax[mb] = fmaxf(lmax[mb], __shfl_xor(lmax[mb], 16));
-      lmax[mb] = fmaxf(lmax[mb], __shfl_xor(lmax[mb], 32));
-    }
+    for (int mbl = 0; mbl < C::MBW; ++mbl) lmax[mbl] = max_lg(lmax[mbl]);
 
     // ---- optimistic softmax: P = exp2(s - mref) with the reference max of earlier tiles. A row
     //      whose tile max exceeds its reference by more than 8 (P > 256) or that had no reference
     //      yet raises the flag; then every wave rebuilds its P block against the new reference
     //      (a second exchange) and the accumulator is rescaled. ----
-    float psum[C::MB];
+    float psum[C::MBW];
     auto write_p = [&]() {
 #pragma unroll
-      for (int mb = 0; mb < C::MB; ++mb) psum[mb] = 0.f;
+      for (int mbl = 0; mbl < C::MBW; ++mbl) psum[mbl] = 0.f;
 #pragma unroll
       for (int tbi = 0; tbi < C::TBW; ++tbi) {
-        const int tb = wl + tbi * C::WPG;
+        const int tb = wt + tbi * C::WPM;
 #pragma unroll
-        for (int mb = 0; mb < C::MB; ++mb) {
-          const float sh = mref[mb] == kNegInf ? 0.f : mref[mb];
+        for (int mbl = 0; mbl < C::MBW; ++mbl) {
+          const float sh = mref[mbl] == kNegInf ? 0.f : mref[mbl];
           bf16x4 pk;
 #pragma unroll
           for (int i = 0; i < 4; ++i) {
-            const float e = fast_exp2(sacc[mb][tbi][i] - sh);
-            psum[mb] += e;
+            const float e = fast_exp2(sacc[mbl][tbi][i] - sh);
+            psum[mbl] += e;
             pk[i] = (__bf16)e;
           }
-          *reinterpret_cast<bf16x4*>(&sm.p[g][mb * 16 + ln16][(tb * 16 + 4 * lg) * 2]) = pk;
+          *reinterpret_cast<bf16x4*>(&sm.p[g][(mgrp * C::MBW + mbl) * 16 + ln16][(tb * 16 + 4 * lg) * 2]) = pk;
         }
       }
 #pragma unroll
-      for (int mb = 0; mb < C::MB; ++mb) {
-        psum[mb] += __shfl_xor(psum[mb], 16);
-        psum[mb] += __shfl_xor(psum[mb], 32);
-      }
+      for (int mbl = 0; mbl < C::MBW; ++mbl) psum[mbl] = sum_lg(psum[mbl]);
     };
     bool need = false;
 #pragma unroll
-    for (int mb = 0; mb < C::MB; ++mb) need |= lmax[mb] > mref[mb] + 8.0f;
+    for (int mbl = 0; mbl < C::MBW; ++mbl) need |= lmax[mbl] > mref[mbl] + 8.0f;
     const bool need_w = __builtin_amdgcn_ballot_w64(need) != 0;
     if (!need_w) write_p();
     if (lg == 0) {
 #pragma unroll
-      for (int mb = 0; mb < C::MB; ++mb) {
-        sm.red[0][wave][mb * 16 + ln16] = lmax[mb];
-        if (!need_w) sm.red[1][wave][mb * 16 + ln16] = psum[mb];
+      for (int mbl = 0; mbl < C::MBW; ++mbl) {
+        sm.red[0][wave][(mgrp * C::MBW + mbl) * 16 + ln16] = lmax[mbl];
+        if (!need_w) sm.red[1][wave][(mgrp * C::MBW + mbl) * 16 + ln16] = psum[mbl];
       }
     }
     if (lane == 0) sm.flag[wave] = need_w ? 1 : 0;
     lds_barrier();  // (B)
     const bool any = (sm.flag[0] | sm.flag[1] | sm.flag[2] | sm.flag[3]) != 0;
-    float alpha[C::MB];
+    float alpha[C::MBW];
     if (any) {
 #pragma unroll
-      for (int mb = 0; mb < C::MB; ++mb) {
-        float gm = mref[mb];
+      for (int mbl = 0; mbl < C::MBW; ++mbl) {
+        const int r = (mgrp * C::MBW + mbl) * 16 + ln16;
+        float gm = mref[mbl];
 #pragma unroll
-        for (int w = 0; w < C::WPG; ++w) gm = fmaxf(gm, sm.red[0][g * C::WPG + w][mb * 16 + ln16]);
-        alpha[mb] = mref[mb] == kNegInf ? 0.f : fast_exp2(mref[mb] - gm);
-        mref[mb] = gm;
+        for (int w = 0; w < C::WPM; ++w) gm = fmaxf(gm, sm.red[0][g * C::WPG + mgrp * C::WPM + w][r]);
+        alpha[mbl] = mref[mbl] == kNegInf ? 0.f : fast_exp2(mref[mbl] - gm);
+        mref[mbl] = gm;
+        if (wt == 0 && lg == 0) sm.alpha[g][r] = alpha[mbl];
       }
       write_p();
       if (lg == 0) {
 #pragma unroll
-        for (int mb = 0; mb < C::MB; ++mb) sm.red[1][wave][mb * 16 + ln16] = psum[mb];
+        for (int mbl = 0; mbl < C::MBW; ++mbl) sm.red[1][wave][(mgrp * C::MBW + mbl) * 16 + ln16] = psum[mbl];
       }
       lds_barrier();  // (B')
     } else {
 #pragma unroll
-      for (int mb = 0; mb < C::MB; ++mb) alpha[mb] = 1.0f;
+      for (int mbl = 0; mbl < C::MBW; ++mbl) alpha[mbl] = 1.0f;
     }
 #pragma unroll
-    for (int mb = 0; mb < C::MB; ++mb) {
+    for (int mbl = 0; mbl < C::MBW; ++mbl) {
       float ts = 0.f;
 #pragma unroll
-      for (int w = 0; w < C::WPG; ++w) ts += sm.red[1][g * C::WPG + w][mb * 16 + ln16];
-      l_run[mb] = l_run[mb] * alpha[mb] + ts;
+      for (int w = 0; w < C::WPM; ++w) ts += sm.red[1][g * C::WPG + mgrp * C::WPM + w][(mgrp * C::MBW + mbl) * 16 + ln16];
+      l_run[mbl] = l_run[mbl] * alpha[mbl] + ts;
     }
     if (any) {
+      // rescale every accumulator row of the group (row owners published alpha before B')
 #pragma unroll
       for (int mb = 0; mb < C::MB; ++mb)
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-          const float a = __shfl(alpha[mb], 4 * lg + i);   // alpha of accumulator row 4*lg+i
+          const float a = sm.alpha[g][mb * 16 + 4 * lg + i];
 #pragma unroll
           for (int cb = 0; cb < C::CB; ++cb) acc[mb][cb][i] *= a;
         }
     }
 
-    // ---- P.V: wave owns columns [g*DCG + wl*NCOL, +NCOL) ----
+    // ---- P.V: wave owns columns [g*DCG + wl*NCOL, +NCOL) for all rows of its group ----
 #pragma unroll
     for (int kk = 0; kk < TILE / 32; ++kk) {
       bf16x8 pf[C::MB];
 #pragma unroll
       for (int mb = 0; mb < C::MB; ++mb)
         pf[mb] = *reinterpret_cast<const bf16x8*>(&sm.p[g][mb * 16 + ln16][(kk * 32 + 8 * lg) * 2]);
-      // value fragment of column block cb, read transposed from the staged rows
-      auto load_v = [&](int cb, i32x2& r0, i16x4& t0, i16x4& t1) {
-        const int col0 = g * C::DCG + wl * C::NCOL + cb * 16;
-        if constexpr (C::EB == 1) {
-          r0 = lds_read_tr8(kvs + (kk * 32 + 8 * lg + (ln16 >> 1)) * C::RB + col0 + 8 * (ln16 & 1));
-        } else {
-          const char* a = kvs + (kk * 32 + 8 * lg + (ln16 >> 2)) * C::RB + (col0 + 4 * (ln16 & 3)) * 2;
-          t0 = lds_read_tr16(a);
-          t1 = lds_read_tr16(a + 4 * C::RB);
-        }
-      };
-      i32x2 vr, vrn;
-      i16x4 vt0, vt1, vt0n, vt1n;
-      load_v(0, vr, vt0, vt1);
 #pragma unroll
       for (int cb = 0; cb < C::CB; ++cb) {
-        if (cb + 1 < C::CB) load_v(cb + 1, vrn, vt0n, vt1n);
+        i32x2 c0 = vraw[kk][cb][0], c1 = vraw[kk][cb][C::EB - 1];
+        if constexpr (C::EB == 1) lds_wait(c0);
+        else lds_wait(c0, c1);
         bf16x8 vf;
         if constexpr (C::EB == 1) {
-          vf = fp8x8_to_bf16(vr);
+          vf = fp8x8_to_bf16(c0);
         } else {
+          const i16x4 v0 = __builtin_bit_cast(i16x4, c0), v1 = __builtin_bit_cast(i16x4, c1);
 #pragma unroll
           for (int e = 0; e < 4; ++e) {
-            vf[e] = __builtin_bit_cast(__bf16, (short)vt0[e]);
-            vf[4 + e] = __builtin_bit_cast(__bf16, (short)vt1[e]);
+            vf[e] = __builtin_bit_cast(__bf16, (short)v0[e]);
+            vf[4 + e] = __builtin_bit_cast(__bf16, (short)v1[e]);
           }
         }
 #pragma unroll
         for (int mb = 0; mb < C::MB; ++mb) acc[mb][cb] = mfma16(pf[mb], vf, acc[mb][cb]);
-        vr = vrn;
-        vt0 = vt0n;
-        vt1 = vt1n;
-        __builtin_amdgcn_sched_barrier(0);
       }
     }
   }
   wait_vmcnt<0>();  // trailing page-id loads must land before the LDS ring is reused
 
-  // ---- epilogue: normalized output (final or partial) and natural-log lse ----
+  // ---- epilogue: the row owners publish (reference max, sum); every wave normalizes its
+  //      columns and writes the output (final or partial) and natural-log lse ----
+  if (wt == 0 && lg == 0) {
+#pragma unroll
+    for (int mbl = 0; mbl < C::MBW; ++mbl) {
+      sm.fin[0][g][(mgrp * C::MBW + mbl) * 16 + ln16] = mref[mbl];
+      sm.fin[1][g][(mgrp * C::MBW + mbl) * 16 + ln16] = l_run[mbl];
+    }
+  }
+  lds_barrier();
 #pragma unroll
   for (int mb = 0; mb < C::MB; ++mb)
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int r = mb * 16 + 4 * lg + i;
-      const float l = __shfl(l_run[mb], 4 * lg + i);
-      const float m = __shfl(mref[mb], 4 * lg + i);
       if (r >= nrows) continue;
+      const float m = sm.fin[0][g][r];
+      const float l = sm.fin[1][g][r];
       const int jq = r / hpg, h = r - jq * hpg;
       const int head = g * hpg + h;
       const float inv = l > 0.f ? kscale / l : 0.f;   // fp8 values were accumulated unscaled
@@ -550,7 +638,7 @@ __device__ __forceinline__ int req_len(const KParams& p, int req) {
 }
 
 template <class C>
-__global__ __launch_bounds__(NTHR, 1) void partial_kernel(const KParams p) {
+__global__ __launch_bounds__(NTHR, C::WGPC) void partial_kernel(const KParams p) {
   __shared__ __attribute__((aligned(16))) Smem<C> sm;
   // the per-layer scale dequantizes fp8 rows (and e4m3 rms codes); a bf16 cache ignores it, as
   // the reference does (mla_decode_attention.py:451-463)
@@ -592,7 +680,7 @@ __global__ __launch_bounds__(NTHR, 1) void partial_kernel(const KParams p) {
     if (c1 <= lo) continue;
     const int t_lo = (lo > c0 ? lo : c0) - c0, t_hi = (hi < c1 ? hi : c1) - c0;
     const int L = req_len(p, b);
-    const int a = t_lo * TILE, e = t_hi * TILE < L ? t_hi * TILE : L;
+    const int a = t_lo * PLAN_TILE, e = t_hi * PLAN_TILE < L ? t_hi * PLAN_TILE : L;
     if (e <= a) continue;
     SegOut so;
     so.final_out = (t_lo == 0 && t_hi == c1 - c0);
@@ -619,7 +707,7 @@ __global__ __launch_bounds__(1024) void plan_kernel(const int* seq_lens, int n_r
     int n = 0;
     if (b < n_req) {
       int L = seq_lens[(int64_t)b * qrows + qrows - 1];
-      n = L > 0 ? (L + TILE - 1) / TILE : 0;
+      n = L > 0 ? (L + PLAN_TILE - 1) / PLAN_TILE : 0;
     }
     // inclusive wave scan
     int x = n;
@@ -650,13 +738,12 @@ __global__ __launch_bounds__(1024) void plan_kernel(const int* seq_lens, int n_r
   }
 }
 
-// LSE-weighted combine (mla_decode_attention.py:1064-1137). One wave per (row, head).
-// fixed mode: partials in the reference attn_logits layout, split bounds recomputed exactly as in
-// the partial pass; balanced mode: partial slots w + b for the workgroups that touched request b.
+// LSE-weighted combine, fixed-split mode (mla_decode_attention.py:1064-1137): one wave per
+// (row, head); split bounds recomputed exactly as in the partial pass, empty splits skipped.
 __global__ __launch_bounds__(64) void combine_kernel(const KParams p, int dv) {
   const int head = blockIdx.x, row = blockIdx.y;   // row = flattened query row
   const int lane = threadIdx.x;
-  const int req = row / p.qrows, jq = row - req * p.qrows;
+  const int req = row / p.qrows;
   const int L = req_len(p, req);
   const int64_t obase = (int64_t)row * p.o_sr + (int64_t)head * p.o_sh;
   float m = kNegInf, l = 0.f;
@@ -664,52 +751,25 @@ __global__ __launch_bounds__(64) void combine_kernel(const KParams p, int dv) {
   const int nper = (dv + 63) / 64;
 #pragma unroll
   for (int k = 0; k < 32; ++k) acc[k] = 0.f;
-  if (p.num_splits > 0) {
-    int per = (L + p.num_splits - 1) / p.num_splits;
-    if (p.split_align > 0) per = (per + p.split_align - 1) / p.split_align * p.split_align;
-    const float* base = p.ws + (int64_t)row * p.ws_sr + (int64_t)head * p.ws_sh;
-    for (int s = 0; s < p.num_splits; ++s) {
-      const int a = per * s, e = a + per < L ? a + per : L;
-      if (e <= a) continue;
-      const float* ps = base + (int64_t)s * p.ws_ss;
-      const float ls = ps[dv];
-      const float mn = fmaxf(m, ls);
-      if (mn == kNegInf) continue;
-      const float sc_old = __expf(m - mn), sc_new = __expf(ls - mn);
-      l = l * sc_old + sc_new;
+  int per = (L + p.num_splits - 1) / p.num_splits;
+  if (p.split_align > 0) per = (per + p.split_align - 1) / p.split_align * p.split_align;
+  const float* base = p.ws + (int64_t)row * p.ws_sr + (int64_t)head * p.ws_sh;
+  for (int s = 0; s < p.num_splits; ++s) {
+    const int a = per * s, e = a + per < L ? a + per : L;
+    if (e <= a) continue;
+    const float* ps = base + (int64_t)s * p.ws_ss;
+    const float ls = ps[dv];
+    const float mn = fmaxf(m, ls);
+    if (mn == kNegInf) continue;
+    const float sc_old = __expf(m - mn), sc_new = __expf(ls - mn);
+    l = l * sc_old + sc_new;
 #pragma unroll
-      for (int k = 0; k < 32; ++k)
-        if (k < nper) {
-          const int c = lane + 64 * k;
-          acc[k] = acc[k] * sc_old + (c < dv ? ps[c] : 0.f) * sc_new;
-        }
-      m = mn;
-    }
-  } else {
-    const int chunk = p.plan[0];
-    const int c0 = p.plan[2 + req], c1 = p.plan[3 + req];
-    if (c1 > c0) {
-      const int w0 = c0 / chunk, w1 = (c1 - 1) / chunk;
-      if (w0 == w1) return;   // single segment: the partial pass wrote the final output
-      const int nrow = p.qrows * p.heads;
-      const int rloc = jq * p.heads + head;
-      for (int w = w0; w <= w1; ++w) {
-        const int64_t slot = (int64_t)w + req;
-        const float ls = p.part_lse[slot * nrow + rloc];
-        const float mn = fmaxf(m, ls);
-        if (mn == kNegInf) continue;
-        const float sc_old = __expf(m - mn), sc_new = __expf(ls - mn);
-        l = l * sc_old + sc_new;
-        const float* ps = p.part_o + (slot * nrow + rloc) * (int64_t)dv;
-#pragma unroll
-        for (int k = 0; k < 32; ++k)
-          if (k < nper) {
-            const int c = lane + 64 * k;
-            acc[k] = acc[k] * sc_old + (c < dv ? ps[c] : 0.f) * sc_new;
-          }
-        m = mn;
+    for (int k = 0; k < 32; ++k)
+      if (k < nper) {
+        const int c = lane + 64 * k;
+        acc[k] = acc[k] * sc_old + (c < dv ? ps[c] : 0.f) * sc_new;
       }
-    }
+    m = mn;
   }
   const float inv = l > 0.f ? 1.0f / l : 0.f;
 #pragma unroll
@@ -720,6 +780,96 @@ __global__ __launch_bounds__(64) void combine_kernel(const KParams p, int dv) {
     }
   if (lane == 0 && p.lse)
     store_out(p.lse, p.lse_dt, (int64_t)row * p.lse_sr + head, l > 0.f ? m + __logf(l) : kNegInf);
+}
+
+// LSE-weighted combine, balanced mode: one 256-thread workgroup per (query row, block of CH_HB
+// heads). Request b's partials sit in slots w + b for the workgroups w0..w1 that touched it; a
+// request covered by one workgroup was finished by the partial pass and is skipped here. All
+// segment LSEs are fetched at once into LDS and turned into weights; the partial outputs are
+// then read in unrolled batches so the loads of a batch are in flight together.
+constexpr int CH_HB = 8;
+constexpr int CH_SEG = 32;   // segments whose weights are staged per pass
+__global__ __launch_bounds__(256) void combine_bal_kernel(const KParams p, int dv) {
+  const int hblk = blockIdx.x, row = blockIdx.y;
+  const int tid = threadIdx.x;
+  const int req = row / p.qrows, jq = row - req * p.qrows;
+  const int h0 = hblk * CH_HB;
+  const int nh = p.heads - h0 < CH_HB ? p.heads - h0 : CH_HB;
+  const int chunk = p.plan[0];
+  const int c0 = p.plan[2 + req], c1 = p.plan[3 + req];
+  __shared__ float s_lse[CH_SEG][CH_HB];
+  __shared__ float s_m[CH_HB], s_inv[CH_HB];
+  if (c1 <= c0) {  // empty request: zero output, -inf lse
+    for (int h = 0; h < nh; ++h)
+      for (int c = tid; c < dv; c += 256)
+        store_out(p.out, p.out_dt, (int64_t)row * p.o_sr + (int64_t)(h0 + h) * p.o_sh + c, 0.f);
+    if (tid < nh && p.lse) store_out(p.lse, p.lse_dt, (int64_t)row * p.lse_sr + h0 + tid, kNegInf);
+    return;
+  }
+  const int w0 = c0 / chunk, w1 = (c1 - 1) / chunk;
+  if (w0 == w1) return;
+  const int nseg = w1 - w0 + 1;
+  const int64_t nrow = (int64_t)p.qrows * p.heads;
+  const int rl0 = jq * p.heads + h0;
+  // pass 1: max and sum of exp over all segments, per head
+  float m = kNegInf, l = 0.f;
+  for (int s0 = 0; s0 < nseg; s0 += CH_SEG) {
+    const int ns = nseg - s0 < CH_SEG ? nseg - s0 : CH_SEG;
+    if (tid < ns * CH_HB) {
+      const int sg = tid / CH_HB, h = tid - sg * CH_HB;
+      s_lse[sg][h] = h < nh ? p.part_lse[((int64_t)w0 + s0 + sg + req) * nrow + rl0 + h] : kNegInf;
+    }
+    __syncthreads();
+    if (tid < nh) {
+      float mm = m;
+      for (int sg = 0; sg < ns; ++sg) mm = fmaxf(mm, s_lse[sg][tid]);
+      if (mm != kNegInf) {
+        l = m == kNegInf ? 0.f : l * __expf(m - mm);
+        for (int sg = 0; sg < ns; ++sg) l += __expf(s_lse[sg][tid] - mm);
+        m = mm;
+      }
+    }
+    __syncthreads();
+  }
+  if (tid < nh) {
+    s_m[tid] = m;
+    s_inv[tid] = l > 0.f ? 1.0f / l : 0.f;
+    if (p.lse) store_out(p.lse, p.lse_dt, (int64_t)row * p.lse_sr + h0 + tid, l > 0.f ? m + __logf(l) : kNegInf);
+  }
+  __syncthreads();
+  // pass 2: weighted sum of the partial outputs, 4 segments per unrolled batch
+  for (int c = tid; c < dv; c += 256) {
+    float acc[CH_HB];
+#pragma unroll
+    for (int h = 0; h < CH_HB; ++h) acc[h] = 0.f;
+    for (int s0 = 0; s0 < nseg; s0 += 4) {
+      float v[4][CH_HB], ls[4][CH_HB];
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        const int sg = s0 + k < nseg ? s0 + k : nseg - 1;
+        const int64_t slot = (int64_t)w0 + sg + req;
+        const float* pl = p.part_lse + slot * nrow + rl0;
+        const float* po = p.part_o + (slot * nrow + rl0) * (int64_t)dv + c;
+#pragma unroll
+        for (int h = 0; h < CH_HB; ++h) {
+          const int hh = h < nh ? h : 0;
+          v[k][h] = po[(int64_t)hh * dv];
+          ls[k][h] = s0 + k < nseg ? pl[hh] : kNegInf;
+        }
+      }
+#pragma unroll
+      for (int k = 0; k < 4; ++k)
+#pragma unroll
+        for (int h = 0; h < CH_HB; ++h) {
+          const float wgt = ls[k][h] == kNegInf ? 0.f : __expf(ls[k][h] - s_m[h]);
+          acc[h] += wgt * v[k][h];
+        }
+    }
+#pragma unroll
+    for (int h = 0; h < CH_HB; ++h)
+      if (h < nh)
+        store_out(p.out, p.out_dt, (int64_t)row * p.o_sr + (int64_t)(h0 + h) * p.o_sh + c, acc[h] * s_inv[h]);
+  }
 }
 
 }  // namespace qmla
@@ -734,25 +884,27 @@ typedef void (*PartialFn)(const KParams);
 struct Inst {
   int eb, rms, dcg, wp, mb, g, s, cpr;
   bool cap;
+  int tile, wgpc;
   PartialFn fn;
 };
 
-#define QMLA_INST(EB, RMS, DCG, WP, MB, G, S, CPR, CAP) \
-  {EB, RMS, DCG, WP, MB, G, S, CPR, CAP, &partial_kernel<Cfg<EB, RMS, DCG, WP, MB, G, S, CPR, CAP>>}
+#define QMLA_INST(EB, RMS, DCG, WP, MB, G, S, CPR, CAP, TILE, WGPC)                        \
+  {EB, RMS, DCG, WP, MB, G, S, CPR, CAP, TILE, WGPC,                                         \
+   &partial_kernel<Cfg<EB, RMS, DCG, WP, MB, G, S, CPR, CAP, TILE, WGPC>>}
 
 // One entry per compiled shape. Rows are [latent | rope | rms | pad]; CPR*16 bytes are staged.
 static const Inst kInst[] = {
+    // fp8 e4m3 cache + log8 rms codes, d_c 512, rope 64, up to 32 rows (24 heads): 608 B staged
+    QMLA_INST(1, QMLA_RMS_LOG8, 512, 64, 2, 1, 3, 38, false, 64, 1),
+    QMLA_INST(1, QMLA_RMS_LOG8, 512, 64, 2, 1, 3, 38, true, 64, 1),
+    QMLA_INST(1, QMLA_RMS_BF16_BYTES, 512, 64, 2, 1, 3, 39, false, 64, 1),
+    QMLA_INST(1, QMLA_RMS_E4M3, 512, 64, 2, 1, 3, 38, false, 64, 1),
     // bf16 cache, d_c 512, rope 64, 24 heads (rms 24 bf16): 1200 B staged
-    QMLA_INST(2, QMLA_RMS_BF16, 512, 64, 2, 1, 2, 75, false),
-    QMLA_INST(2, QMLA_RMS_BF16, 512, 64, 2, 1, 2, 75, true),
-    QMLA_INST(2, QMLA_RMS_NONE, 512, 64, 2, 1, 2, 72, false),
-    // fp8 e4m3 cache + log8 rms codes, d_c 512, rope 64, 24 heads: 600 B -> 608 staged
-    QMLA_INST(1, QMLA_RMS_LOG8, 512, 64, 2, 1, 3, 38, false),
-    QMLA_INST(1, QMLA_RMS_LOG8, 512, 64, 2, 1, 3, 38, true),
-    QMLA_INST(1, QMLA_RMS_BF16_BYTES, 512, 64, 2, 1, 3, 39, false),
-    QMLA_INST(1, QMLA_RMS_E4M3, 512, 64, 2, 1, 3, 38, false),
+    QMLA_INST(2, QMLA_RMS_BF16, 512, 64, 2, 1, 2, 75, false, 64, 1),
+    QMLA_INST(2, QMLA_RMS_BF16, 512, 64, 2, 1, 2, 75, true, 64, 1),
+    QMLA_INST(2, QMLA_RMS_NONE, 512, 64, 2, 1, 2, 72, false, 64, 1),
     // GLA-g2: two latent groups of 256, 12 heads each, 4 verify tokens -> 48 rows per group
-    QMLA_INST(1, QMLA_RMS_LOG8, 256, 64, 3, 2, 3, 38, false),
+    QMLA_INST(1, QMLA_RMS_LOG8, 256, 64, 3, 2, 3, 38, false, 64, 1),
 };
 
 static int g_cu_count[64];
@@ -849,8 +1001,12 @@ static const Inst* find_inst(const qmla_decode_params* p) {
   return best;
 }
 
+static const Inst* find_inst(const qmla_decode_params* p);
+
 static int balanced_nwg(const qmla_decode_params* p) {
-  return p->num_workgroups > 0 ? p->num_workgroups : cu_count();
+  if (p->num_workgroups > 0) return p->num_workgroups;
+  const Inst* in = find_inst(p);
+  return cu_count() * (in ? in->wgpc : 1);
 }
 
 struct BalancedLayout {
@@ -941,6 +1097,9 @@ static int run_partial(const qmla_decode_params* p, const Inst* in, KParams& k, 
 static int run_combine(const qmla_decode_params* p, KParams& k, hipStream_t st) {
   int dv = p->d_c / p->groups;
   void* args[] = {&k, &dv};
+  if (p->num_splits == 0)
+    return launch((const void*)&combine_bal_kernel, dim3((p->heads + CH_HB - 1) / CH_HB, p->rows, 1),
+                  dim3(256, 1, 1), args, st);
   return launch((const void*)&combine_kernel, dim3(p->heads, p->rows, 1), dim3(64, 1, 1), args, st);
 }
 

@@ -70,17 +70,46 @@ __device__ __forceinline__ i32x4 lds_read_b128(const char* p) {
   return *reinterpret_cast<const i32x4*>(p);
 }
 
-__device__ __forceinline__ i32x2 lds_read_tr8(const char* p) {
-  return __builtin_amdgcn_ds_read_tr8_b64_v2i32(QMLA_LDS(i32x2, p));
+__device__ __forceinline__ uint32_t lds_addr(const char* p) {
+  return (uint32_t)(uintptr_t)QMLA_LDS(const char, p);
 }
 
-__device__ __forceinline__ i16x4 lds_read_tr16(const char* p) {
-  return __builtin_amdgcn_ds_read_tr16_b64_v4i16(QMLA_LDS(i16x4, p));
+// Transposed LDS reads issued as inline asm: through the builtin the compiler cannot tell them
+// apart from the LDS-DMA writes still in flight and waits for vmcnt(0) before each one, which
+// drains the prefetch ring mid-tile. The result is NOT ready on return: pass it through
+// lds_wait() before use.
+__device__ __forceinline__ i32x2 lds_read_tr8_async(const char* p) {
+  i32x2 r;
+  asm volatile("ds_read_b64_tr_b8 %0, %1" : "=v"(r) : "v"(lds_addr(p)));
+  return r;
+}
+__device__ __forceinline__ i32x2 lds_read_tr16_async(const char* p) {
+  i32x2 r;
+  asm volatile("ds_read_b64_tr_b16 %0, %1" : "=v"(r) : "v"(lds_addr(p)));
+  return r;
+}
+// wait for all outstanding LDS reads of this wave; `v` is threaded through so its consumers
+// cannot be scheduled before the wait
+template <class T>
+__device__ __forceinline__ void lds_wait(T& v) {
+  asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(v));
+}
+template <class T, class U>
+__device__ __forceinline__ void lds_wait(T& v, U& w) {
+  asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(v), "+v"(w));
 }
 
 // 16 bytes per lane, global -> LDS (wave-uniform LDS base; lane l writes base + 16*l)
 __device__ __forceinline__ void dma16(const void* gsrc, char* lds_base) {
   __builtin_amdgcn_global_load_lds(gsrc, QMLA_LDS(void, lds_base), 16, 0, 0);
+}
+// 16 bytes per lane from a buffer resource (base in SGPRs, per-lane byte offset voff); lanes
+// whose offset falls outside the resource read zeros
+__device__ __forceinline__ void dma16_buf(__amdgpu_buffer_rsrc_t rsrc, uint32_t voff, char* lds_base) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, QMLA_LDS(void, lds_base), 16, voff, 0, 0, 0);
+}
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, 0x00020000);
 }
 // 4 bytes per lane (lane l writes base + 4*l)
 __device__ __forceinline__ void dma4(const void* gsrc, char* lds_base) {
@@ -92,6 +121,23 @@ template <int N>
 __device__ __forceinline__ void wait_vmcnt() {
   static_assert(N >= 0 && N < 64, "vmcnt range");
   __builtin_amdgcn_s_waitcnt((N & 0xF) | ((N >> 4) << 14) | (0x7 << 4) | (0xF << 8));
+}
+
+// max / sum over the 4 lanes {l, l^16, l^32, l^48} (the 4 lane groups of a 16-lane column), with
+// VALU lane swaps: permlane16_swap pairs rows r and r^1 of 16 lanes, permlane32_swap the two
+// 32-lane halves; whichever element of the returned pair is the lane's own value, the other is
+// its partner's.
+__device__ __forceinline__ float max_lg(float v) {
+  auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  v = fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
+  auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
+}
+__device__ __forceinline__ float sum_lg(float v) {
+  auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  v = __uint_as_float(a[0]) + __uint_as_float(a[1]);
+  auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return __uint_as_float(b[0]) + __uint_as_float(b[1]);
 }
 
 // max / sum over the 16 lanes that share (lane / 16)
@@ -110,12 +156,13 @@ __device__ __forceinline__ float sum16(float v) {
   return v;
 }
 
-// Workgroup barrier that orders LDS only. __syncthreads() also waits for every outstanding global
-// load (vmcnt(0)), which would drain the LDS-DMA prefetch ring at every barrier.
+// Workgroup barrier for LDS traffic only. Both __syncthreads() and an LDS-scoped fence make the
+// compiler wait for every outstanding global load first (LDS-DMA writes are counted by vmcnt),
+// which would drain the DMA prefetch ring at every barrier. This waits for the wave's own LDS
+// reads/writes (lgkmcnt) and the barrier; the "memory" clobber keeps the compiler from moving
+// memory accesses across it. DMA data is published by an explicit vmcnt wait before it.
 __device__ __forceinline__ void lds_barrier() {
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
-  __builtin_amdgcn_s_barrier();
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+  asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
 }
 
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
