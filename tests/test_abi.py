@@ -1,0 +1,165 @@
+"""The C ABI without a GPU: libqmla.so loads, exports every function include/qmla.h declares,
+mirrors its struct, and rejects bad parameter blocks with the documented error codes before any
+device work (fake, never dereferenced pointers)."""
+from __future__ import annotations
+
+import ctypes
+import pathlib
+import re
+
+import pytest
+import torch
+
+import qmla
+from qmla import _lib
+from qmla.decode import build_params
+
+HEADER = pathlib.Path(__file__).resolve().parent.parent / "include" / "qmla.h"
+
+
+def _declared_functions() -> list[str]:
+    text = re.sub(r"/\*.*?\*/", "", HEADER.read_text(), flags=re.S)
+    return sorted(set(re.findall(r"^[A-Za-z_][\w\s\*]*?\b(qmla_\w+)\s*\(", text, flags=re.M)))
+
+
+def test_header_functions_exported_and_bound():
+    names = _declared_functions()
+    assert "qmla_decode" in names and len(names) >= 9
+    lib = _lib.lib()
+    for n in names:
+        assert hasattr(lib, n), n
+        assert n in _lib.SIGNATURES, f"{n} has no ctypes signature"
+    assert set(_lib.SIGNATURES) == set(names)
+
+
+def test_version_and_constants_match_header():
+    text = HEADER.read_text()
+    consts = dict(re.findall(r"#define (QMLA_\w+) \(?(-?\d+)\)?", text))
+    assert int(consts["QMLA_ABI_VERSION"]) == _lib.lib().qmla_version() == _lib.ABI_VERSION
+    assert b"gfx950" in _lib.lib().qmla_build_info()
+    for name, val in [("QMLA_ERR_NULL", _lib.ERR_NULL), ("QMLA_ERR_SHAPE", _lib.ERR_SHAPE),
+                      ("QMLA_ERR_ALIGN", _lib.ERR_ALIGN), ("QMLA_ERR_WORKSPACE", _lib.ERR_WORKSPACE),
+                      ("QMLA_ERR_MODE", _lib.ERR_MODE), ("QMLA_ERR_NOKERNEL", _lib.ERR_NOKERNEL),
+                      ("QMLA_KV_FP8", _lib.KV_FP8), ("QMLA_RMS_LOG8", _lib.RMS_LOG8),
+                      ("QMLA_RMS_E4M3", _lib.RMS_E4M3), ("QMLA_DT_F32", _lib.DT_F32)]:
+        assert int(consts[name]) == val, name
+
+
+def test_struct_mirror_matches_header_field_order():
+    text = HEADER.read_text()
+    body = text[text.index("typedef struct qmla_decode_params"):text.index("} qmla_decode_params;")]
+    body = re.sub(r"/\*.*?\*/", "", body, flags=re.S)
+    fields = []
+    for decl in body.split("{", 1)[1].split(";"):
+        decl = decl.strip()
+        if not decl:
+            continue
+        names = [re.sub(r"[\*\s]", "", x).split()[-1] if x.strip() else "" for x in decl.split(",")]
+        first = re.findall(r"(\w+)\s*$", decl.split(",")[0])[0]
+        fields.append(first)
+        fields.extend(n for n in names[1:])
+    assert fields == [f[0] for f in _lib.DecodeParams._fields_]
+
+
+def _valid_params(**over) -> _lib.DecodeParams:
+    """A parameter block for H=24, d_c=512, rope 64, fp8 + log8, 608-byte rows, fake 16B-aligned pointers."""
+    p = _lib.DecodeParams()
+    base = 0x10000
+    p.q_nope, p.q_nope_stride_row, p.q_nope_stride_head = base, 24 * 512, 512
+    p.q_pe, p.q_pe_stride_row, p.q_pe_stride_head = base + 0x100000, 24 * 64, 64
+    p.kv_cache, p.page_stride, p.token_stride = base + 0x200000, 64 * 608, 608
+    p.kv_dtype, p.page_size, p.d_c, p.rope_w = _lib.KV_FP8, 64, 512, 64
+    p.rms_offset, p.rms_mode = 576, _lib.RMS_LOG8
+    p.sm_scale = 0.04
+    p.block_table, p.bt_stride, p.seq_lens = base + 0x300000, 256, base + 0x400000
+    p.rows, p.heads, p.rms_heads, p.qrows, p.groups = 8, 24, 24, 1, 1
+    p.out, p.out_stride_row, p.out_stride_head, p.out_dtype = base + 0x500000, 24 * 512, 512, _lib.DT_BF16
+    p.lse, p.lse_stride_row, p.lse_dtype = base + 0x600000, 24, _lib.DT_F32
+    p.num_splits = 4
+    p.workspace = base + 0x700000
+    p.workspace_bytes = 1 << 30
+    p.ws_stride_row, p.ws_stride_head, p.ws_stride_split = 24 * 4 * 513, 4 * 513, 513
+    for k, v in over.items():
+        setattr(p, k, v)
+    return p
+
+
+@pytest.mark.parametrize("over,code", [
+    (dict(q_nope=None), _lib.ERR_NULL),
+    (dict(kv_cache=None), _lib.ERR_NULL),
+    (dict(q_pe=None), _lib.ERR_NULL),
+    (dict(kv_dtype=7), _lib.ERR_MODE),
+    (dict(rms_mode=_lib.RMS_BF16), _lib.ERR_MODE),          # bf16 rms element in an fp8 cache
+    (dict(rms_offset=-1), _lib.ERR_MODE),                    # mode says rms, offset says none
+    (dict(out_dtype=9), _lib.ERR_MODE),
+    (dict(kv_cache=0x200008), _lib.ERR_ALIGN),
+    (dict(token_stride=600), _lib.ERR_ALIGN),
+    (dict(q_nope_stride_head=500), _lib.ERR_ALIGN),
+    (dict(rows=9, qrows=2), _lib.ERR_SHAPE),
+    (dict(heads=24, groups=5), _lib.ERR_SHAPE),
+    (dict(token_stride=512, page_stride=64 * 512), _lib.ERR_SHAPE),   # row narrower than latent+rope
+    (dict(d_c=384, rms_offset=448), _lib.ERR_NOKERNEL),
+    (dict(workspace=None), _lib.ERR_WORKSPACE),
+])
+def test_error_codes(over, code):
+    lib = _lib.lib()
+    p = _valid_params(**over)
+    assert lib.qmla_decode(ctypes.byref(p), None) == code
+    if code != _lib.ERR_NOKERNEL and code != _lib.ERR_WORKSPACE:
+        assert lib.qmla_decode_partial(ctypes.byref(p), None) == code
+        assert lib.qmla_combine(ctypes.byref(p), None) == code
+
+
+def test_null_params_and_balanced_workspace_errors():
+    lib = _lib.lib()
+    assert lib.qmla_decode(None, None) == _lib.ERR_NULL
+    assert lib.qmla_workspace_bytes(None) == 0
+    p = _valid_params(num_splits=0, num_workgroups=16, workspace_bytes=0)
+    assert lib.qmla_plan(ctypes.byref(p), None) == _lib.ERR_WORKSPACE
+    p = _valid_params(num_splits=3)
+    assert lib.qmla_plan(ctypes.byref(p), None) == _lib.ERR_MODE
+
+
+def test_workspace_bytes_arithmetic():
+    lib = _lib.lib()
+    p = _valid_params(num_splits=4)
+    assert lib.qmla_workspace_bytes(ctypes.byref(p)) == 8 * 24 * 4 * 513 * 4
+    p = _valid_params(num_splits=1)
+    assert lib.qmla_workspace_bytes(ctypes.byref(p)) == 0
+    small = lib.qmla_workspace_bytes(ctypes.byref(_valid_params(num_splits=0, num_workgroups=16)))
+    big = lib.qmla_workspace_bytes(ctypes.byref(_valid_params(num_splits=0, num_workgroups=64)))
+    # balanced: (workgroups + requests) partial slots of H x (d_c + lse) floats, plus the plan
+    assert big - small >= 48 * 24 * 513 * 4
+    assert small >= (16 + 8) * 24 * 513 * 4
+
+
+def test_build_params_reads_real_strides():
+    q = torch.empty(6, 24, 576, dtype=torch.bfloat16)
+    qn, qp = q[..., :512], q[..., 512:]
+    cache = torch.empty(10, 64, 1, 608, dtype=torch.uint8)[2:9]       # a view: page stride from the tensor
+    bt = torch.zeros(6, 40, dtype=torch.int32)
+    sl = torch.zeros(6, dtype=torch.int32)
+    out = torch.empty(6, 24, 512, dtype=torch.bfloat16)
+    lse = torch.empty(6, 24)
+    p = build_params(q_nope=qn, q_pe=qp, kv_cache=cache, block_table=bt, seq_lens=sl, out=out, lse=lse, d_c=512,
+                     rope_w=64, rms_offset=576, rms_mode=_lib.RMS_LOG8, kv=_lib.KV_FP8, page_size=64,
+                     sm_scale=0.1, qrows=2)
+    assert (p.q_nope_stride_row, p.q_nope_stride_head) == (24 * 576, 576)
+    assert p.q_pe == qn.data_ptr() + 512 * 2
+    assert (p.page_stride, p.token_stride) == (64 * 608, 608)
+    assert p.kv_cache == cache.data_ptr() and p.bt_stride == 40
+    assert (p.rows, p.heads, p.rms_heads, p.qrows) == (6, 24, 24, 2)
+    assert p.out_dtype == _lib.DT_BF16 and p.lse_dtype == _lib.DT_F32
+    flat = torch.empty(640, 1, 608, dtype=torch.uint8)                  # 3-D [pages*P, 1, row]
+    p3 = build_params(q_nope=qn, q_pe=qp, kv_cache=flat, block_table=bt, seq_lens=sl, out=out, lse=None,
+                      d_c=512, rope_w=64, rms_offset=576, rms_mode=_lib.RMS_LOG8, kv=_lib.KV_FP8, page_size=64,
+                      sm_scale=0.1)
+    assert (p3.page_stride, p3.token_stride) == (64 * 608, 608) and p3.lse is None
+
+
+def test_product_path_refuses_cpu_tensors():
+    case_q = torch.zeros(1, 24, 512, dtype=torch.bfloat16)
+    with pytest.raises(RuntimeError, match="GPU only"):
+        qmla.forward(case_q, torch.zeros(1, 24, 64, dtype=torch.bfloat16),
+                     torch.zeros(1, 64, 1, 608, dtype=torch.uint8), torch.zeros(1, 1, dtype=torch.int32),
+                     torch.ones(1, dtype=torch.int32), page_size=64, sm_scale=0.1, kv_fp8=True)
