@@ -70,6 +70,28 @@ def kernel_bytes(case) -> int:
     return toks * (case.d_c * e + case.rope_w * e + H * r) + rows * H * (dv + case.rope_w) * 2 + pages * 4 + rows * 4
 
 
+def measured_traffic(workload: str):
+    """HBM bytes per decode launch from the committed counter summary of this workload
+    (FETCH_SIZE + WRITE_SIZE, each scaled by what it reads for a 1 GiB copy), or None."""
+    f = REPO / "profiles" / f"traffic_mla_decode_{workload}.md"
+    if not f.exists():
+        return None
+    for line in f.read_text().splitlines():
+        if line.startswith("hbm_bytes_per_launch:"):
+            return int(line.split(":", 1)[1])
+    return None
+
+
+def cpu_model() -> str:
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
 def cpu_baseline(case, sample_every: int, budget_s: float):
     """The CPU oracle on a fixed sample of the workload's requests (every k-th), timed on this host's
     cores; returns decode rows per second scaled per request."""
@@ -118,6 +140,7 @@ def cpu_baseline(case, sample_every: int, budget_s: float):
     t = statistics.median(times)
     toks = int(sll.to(torch.int64).sum())
     return {"value": round(len(rows) / t, 3), "unit": "tokens/s", "cores": cores, "kind": "port",
+            "cpu": cpu_model(),
             "sample": f"{len(picks)} of {n_req} requests (every {sample_every}th, {len(rows)} rows, "
                       f"{toks} cached tokens), fp32 torch oracle, median of {len(times)} runs "
                       f"({t:.2f} s each), scaled per request"}
@@ -214,13 +237,7 @@ def main():
     value = rows / (ms / 1e3)
     gbps = call_bytes / (ms / 1e3) / 1e9
     k_gbps = k_bytes / (part_ms / 1e3) / 1e9
-    traffic = None
-    tf = REPO / "profiles" / f"traffic_{args.workload}.json"
-    if tf.exists():
-        try:
-            traffic = json.loads(tf.read_text()).get("hbm_bytes_per_launch")
-        except (ValueError, OSError):
-            traffic = None
+    traffic = measured_traffic(args.workload)
 
     cpu = None
     if not args.no_cpu:
@@ -239,7 +256,9 @@ def main():
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": ("fp8-e4m3 cache, bf16 MFMA, fp32 softmax" if case.kv == "fp8" else "bf16 cache, bf16 MFMA, fp32 softmax"),
+        "dtype": "bf16",
+        "storage": ("e4m3 latent/rope + u8 log8 rms; bf16 MFMA operands, fp32 accumulate and softmax"
+                    if case.kv == "fp8" else "bf16 cache; bf16 MFMA operands, fp32 accumulate and softmax"),
         "data": "synthetic",
         "config": {"workload": f"mla_decode_{args.workload}", "batch": n_req, "rows": rows, "heads": H,
                    "d_c": case.d_c, "d_r": case.rope_w, "page_size": case.page_size, "kv": case.kv,
