@@ -41,15 +41,22 @@ WORKLOADS = {
                      amp=1.0, lens=("uniform", 4096, 32768)),
     "gla_b48": dict(batch=48, heads=24, d_c=512, rope_w=64, page_size=64, kv="fp8", rms_mode="log8", seed=4,
                     amp=1.0, lens=("uniform", 8192, 32768), qrows=4, groups=2),
+    # wide latent: 16 fixed splits in the reference's attn_logits layout, then the combine
+    "wide_b32": dict(batch=32, heads=24, d_c=1792, rope_w=64, page_size=1600, kv="bf16", rms_mode="bf16", seed=3,
+                     amp=1.0, lens=("fixed", 65536), splits=16),
 }
+CPU_EVERY = {"wide_b32": 8}
 
 
 def make_workload(name, device):
     from qmla.synth import lognormal_lens, make_case, uniform_lens
     w = dict(WORKLOADS[name])
     spec = w.pop("lens")
+    w.pop("splits", None)
     if spec[0] == "lognormal":
         lens = lognormal_lens(w["batch"], spec[1], spec[2], spec[3], spec[4], seed=w["seed"])
+    elif spec[0] == "fixed":
+        lens = [spec[1]] * w["batch"]
     else:
         lens = uniform_lens(w["batch"], spec[1], spec[2], seed=w["seed"])
     return make_case(lens=lens, device=device, rms="row", **w), spec
@@ -153,7 +160,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--workload", default="fp8_b128", choices=sorted(WORKLOADS))
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--cpu-every", type=int, default=2)
+    ap.add_argument("--cpu-every", type=int, default=0, help="oracle on every k-th request (0: per workload)")
     ap.add_argument("--cpu-budget", type=float, default=20.0)
     ap.add_argument("--copy-calib-mib", type=int, default=0,
                     help="also run a plain device copy of this many MiB (FETCH/WRITE_SIZE calibration)")
@@ -183,8 +190,16 @@ def main():
                   rms_offset=case.rms_offset, rms_mode=mode, kv=kv, page_size=case.page_size,
                   sm_scale=case.sm_scale, k_scale=case.k_scale, qrows=case.qrows, groups=case.groups,
                   num_splits=0, split_align=0)
-    ws = Workspace().reserve(workspace_bytes(build_params(**args_p)), dev)
-    p = build_params(workspace=ws, **args_p)
+    splits = WORKLOADS[args.workload].get("splits", 0)
+    if splits:
+        # fixed splits with the reference's attn_logits [B, H, S, Dv+1] partials
+        logits = torch.empty(rows, H, splits, dv + 1, dtype=torch.float32, device=dev)
+        args_p.update(num_splits=splits, split_align=16 if case.page_size % 16 == 0 else 0)
+        p = build_params(workspace=logits, ws_strides=(logits.stride(0), logits.stride(1), logits.stride(2)),
+                         **args_p)
+    else:
+        ws = Workspace().reserve(workspace_bytes(build_params(**args_p)), dev)
+        p = build_params(workspace=ws, **args_p)
     lib = qmla.lib()
     st = torch.cuda.current_stream().cuda_stream
 
@@ -211,7 +226,8 @@ def main():
     evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True),
             torch.cuda.Event(enable_timing=True)) for _ in range(args.steps)]
     for a, b, c in evs:
-        _lib.check("qmla_plan", lib.qmla_plan(p, st))
+        if not splits:
+            _lib.check("qmla_plan", lib.qmla_plan(p, st))
         a.record()
         _lib.check("qmla_decode_partial", lib.qmla_decode_partial(p, st))
         b.record()
@@ -241,10 +257,14 @@ def main():
 
     cpu = None
     if not args.no_cpu:
-        cpu = cpu_baseline(case, args.cpu_every, args.cpu_budget)
+        cpu = cpu_baseline(case, args.cpu_every or CPU_EVERY.get(args.workload, 2), args.cpu_budget)
 
-    ctx = (f"lognormal median {spec[1]} sigma {spec[2]} clipped [{spec[3]}, {spec[4]}]" if spec[0] == "lognormal"
-           else f"uniform [{spec[1]}, {spec[2]}]")
+    if spec[0] == "lognormal":
+        ctx = f"lognormal median {spec[1]} sigma {spec[2]} clipped [{spec[3]}, {spec[4]}]"
+    elif spec[0] == "fixed":
+        ctx = f"{spec[1]} each"
+    else:
+        ctx = f"uniform [{spec[1]}, {spec[2]}]"
     res = {
         "metric": METRIC,
         "value": round(value, 1),
@@ -263,7 +283,7 @@ def main():
         "config": {"workload": f"mla_decode_{args.workload}", "batch": n_req, "rows": rows, "heads": H,
                    "d_c": case.d_c, "d_r": case.rope_w, "page_size": case.page_size, "kv": case.kv,
                    "rms": case.rms_mode, "ctx": ctx, "cached_tokens": toks_cached, "qrows": case.qrows,
-                   "groups": case.groups, "split": "balanced", "row_bytes": case.row * (1 if case.kv == "fp8" else 2)},
+                   "groups": case.groups, "split": f"fixed {splits} + combine" if splits else "balanced", "row_bytes": case.row * (1 if case.kv == "fp8" else 2)},
         "gbps": round(gbps, 1),
         "hbm_frac": round(gbps / HBM_PEAK_GBPS, 4),
         "decode_kernel_us": round(part_ms * 1e3, 2),

@@ -13,15 +13,17 @@
  *                            qwen_mla/ops/mla_decode_attention.py:1264-1359 (stage 1 :297-586,
  *                            stage 2 :1064-1181), and the FlashInfer run() it dispatches to instead
  *                            qwen_mla/fi_decode.py:338-384 / kernels/qwen_mla.cuh:1386-1480
- *   qmla_decode_2pass     <- _decode_mla_two_pass qwen_mla/ops/mla_decode_attention.py:778-849
- *                            (_mla2p_scores_kernel :602-678, _mla2p_pv_kernel :681-764)
+ *                            Wide latents (d_c = 1792), which the reference routes to its two-pass
+ *                            path _decode_mla_two_pass (ops/mla_decode_attention.py:778-849:
+ *                            _mla2p_scores_kernel :602-678, _mla2p_pv_kernel :681-764), go through the
+ *                            same entry points: the library runs them in one pass over the rows with
+ *                            the latent columns split across the waves of a workgroup, so no scores
+ *                            scratch exists and the partials/combine formats are the same.
  *   qmla_combine          <- _decode_softmax_reducev_fwd / _fwd_kernel_stage2
  *                            qwen_mla/ops/mla_decode_attention.py:1064-1181
  *   qmla_workspace_bytes  <- the split-K scratch sizing of splitk_cap / splitk_reserve_bytes
  *                            qwen_mla/mla_impl.py:89-111 and _RankPlan._workspace_bytes
  *                            qwen_mla/fi_decode.py:170-179
- *   qmla_cache_write_fp8  <- QwenMLATritonImpl.do_kv_cache_update qwen_mla/mla_impl.py:309-342
- *   qmla_gather_cache     <- gather_cache_torch qwen_mla/ops/mla_gather.py:28-76
  */
 #ifndef QMLA_H
 #define QMLA_H
@@ -153,13 +155,6 @@ int qmla_decode(const qmla_decode_params* p, void* stream);
 int qmla_plan(const qmla_decode_params* p, void* stream);
 int qmla_decode_partial(const qmla_decode_params* p, void* stream);
 int qmla_combine(const qmla_decode_params* p, void* stream);
-
-/* Wide-latent two-pass decode (scores pass into fp32 scratch, then P.V over latent column
- * slices), fixed-split mode, followed by the combine. scratch must hold
- * qmla_decode_2pass_scratch_bytes(p) bytes. */
-size_t qmla_decode_2pass_scratch_bytes(const qmla_decode_params* p, int64_t max_tokens);
-int qmla_decode_2pass(const qmla_decode_params* p, void* scratch, size_t scratch_bytes,
-                      int64_t max_tokens, void* stream);
 
 #ifdef __cplusplus
 }

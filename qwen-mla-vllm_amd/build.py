@@ -16,19 +16,20 @@ PKG = pathlib.Path(__file__).resolve().parent
 REPO = PKG.parent
 CSRC = PKG / "csrc"
 OUT = PKG / "qmla" / "libqmla.so"
-SOURCES = [CSRC / "qmla_decode.hip"]
-
-HIPCC_FLAGS = [
+COMMON_FLAGS = [
     "--offload-arch=gfx950",
     "-O3",
     "-std=c++17",
     "-fPIC",
-    "-shared",
     "-mcode-object-version=5",
     # no packed-fp32 VALU forms anywhere in the device code
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
-    # keep MFMA accumulators in VGPRs: the online-softmax rescale touches them with VALU ops
-    "-mllvm", "-amdgpu-mfma-vgpr-form",
+]
+# (source, extra flags). MFMA accumulators stay in VGPRs: the online-softmax rescale touches them
+# with VALU ops, and AGPR-resident accumulators make the compiler copy them back and forth.
+SOURCES = [
+    (CSRC / "qmla_decode.hip", ["-mllvm", "-amdgpu-mfma-vgpr-form"]),
+    (CSRC / "qmla_wide.hip", ["-mllvm", "-amdgpu-mfma-vgpr-form"]),
 ]
 
 
@@ -39,20 +40,49 @@ def hipcc() -> str:
     raise RuntimeError("hipcc not found")
 
 
-def build(verbose: bool = False) -> pathlib.Path:
-    tmp = OUT.with_suffix(f".so.tmp{os.getpid()}")
-    cmd = [hipcc(), *HIPCC_FLAGS, f"-I{REPO / 'include'}", f"-I{CSRC}", *map(str, SOURCES), "-o", str(tmp)]
+def _run(cmd, verbose):
     if verbose:
         print(" ".join(cmd), flush=True)
     r = subprocess.run(cmd, capture_output=True, text=True)
     errs = "\n".join(l for l in (r.stderr or "").splitlines() if "packed-fp32-ops" not in l)
     if r.returncode != 0:
-        if tmp.exists():
-            tmp.unlink()
         raise RuntimeError(f"hipcc failed ({r.returncode}):\n{errs}")
     if verbose and errs.strip():
         print(errs, file=sys.stderr)
-    os.replace(tmp, OUT)
+
+
+def build(verbose: bool = False) -> pathlib.Path:
+    """Compile every source to an object (in parallel), link libqmla.so, replace it atomically."""
+    tag = f"tmp{os.getpid()}"
+    objdir = PKG / "qmla" / f".obj_{tag}"
+    objdir.mkdir(exist_ok=True)
+    inc = [f"-I{REPO / 'include'}", f"-I{CSRC}"]
+    tmp = OUT.with_suffix(f".so.{tag}")
+    try:
+        objs, procs = [], []
+        for src, extra in SOURCES:
+            obj = objdir / (src.stem + ".o")
+            cmd = [hipcc(), *COMMON_FLAGS, *extra, *inc, "-c", str(src), "-o", str(obj)]
+            if verbose:
+                print(" ".join(cmd), flush=True)
+            procs.append((cmd, subprocess.Popen(cmd, stdout=subprocess.PIPE, stderr=subprocess.PIPE, text=True)))
+            objs.append(obj)
+        failed = []
+        for cmd, pr in procs:
+            _, err = pr.communicate()
+            err = "\n".join(l for l in (err or "").splitlines() if "packed-fp32-ops" not in l)
+            if pr.returncode != 0:
+                failed.append(f"{' '.join(cmd)}\n{err}")
+            elif verbose and err.strip():
+                print(err, file=sys.stderr)
+        if failed:
+            raise RuntimeError("hipcc failed:\n" + "\n".join(failed))
+        _run([hipcc(), "--offload-arch=gfx950", "-shared", "-fPIC", *map(str, objs), "-o", str(tmp)], verbose)
+        os.replace(tmp, OUT)
+    finally:
+        if tmp.exists():
+            tmp.unlink()
+        shutil.rmtree(objdir, ignore_errors=True)
     return OUT
 
 

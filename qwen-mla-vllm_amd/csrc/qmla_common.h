@@ -1,0 +1,143 @@
+// Shared by the decode translation units of libqmla.so: the kernel parameter block, the output
+// descriptor of one token range, and the split of a launch into token ranges (fixed splits or the
+// balanced plan).
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "qmla.h"
+
+namespace qmla {
+
+constexpr int PLAN_TILE = 64;  // balancing granularity of the balanced plan (tokens)
+
+struct KParams {
+  const __bf16* q_nope;
+  int64_t qn_sr, qn_sh;
+  const __bf16* q_pe;
+  int64_t qp_sr, qp_sh;
+  const char* kv;
+  int64_t page_stride_b, token_stride_b;  // bytes
+  int page_size;
+  int rope_w;
+  int rms_off_b;  // byte offset of the rms tail inside a row
+  const float* k_scale;
+  float sm_scale, logit_cap;
+  const int* bt;
+  int64_t bt_stride;
+  const int* seq_lens;
+  int n_req;      // requests = rows / qrows
+  int qrows, hpg; // verify tokens per request, heads per latent group
+  int heads;      // heads per row (= groups * hpg)
+  void* out;
+  int64_t o_sr, o_sh;
+  int out_dt;
+  void* lse;
+  int64_t lse_sr;
+  int lse_dt;
+  int num_splits, split_align;
+  float* ws;
+  int64_t ws_sr, ws_sh, ws_ss;
+  // balanced mode
+  int nwg;
+  int* plan;        // [0] = chunk (tiles per workgroup), [1] = total tiles, [2 + b] = prefix C_b
+  float* part_o;    // [(nwg + n_req), qrows*heads, Dv]
+  float* part_lse;  // [(nwg + n_req), qrows*heads]
+};
+
+__device__ __forceinline__ void store_out(void* base, int dt, int64_t idx, float v) {
+  if (dt == QMLA_DT_BF16) reinterpret_cast<__bf16*>(base)[idx] = (__bf16)v;
+  else if (dt == QMLA_DT_F16) reinterpret_cast<_Float16*>(base)[idx] = (_Float16)v;
+  else reinterpret_cast<float*>(base)[idx] = v;
+}
+
+// Where the result of one token range goes.
+struct SegOut {
+  bool final_out;       // write normalized output + lse directly
+  float* po;            // partial output base of this request (query-row 0 of it)
+  int64_t po_sr, po_sh; // float strides for (verify token of the request, head)
+  float* plse;          // balanced-mode lse base (nullptr: lse stored after the Dv columns)
+  int64_t plse_sr;
+};
+
+// request length: the last flattened row of the request carries it (mla_impl.py:628-662)
+__device__ __forceinline__ int req_len(const KParams& p, int req) {
+  int L = p.seq_lens[(int64_t)req * p.qrows + p.qrows - 1];
+  return L > 0 ? L : 0;
+}
+
+// Calls f(req, a, e, L, so) for every token range [a, e) this workgroup owns.
+//   fixed splits (num_splits > 0): grid (S, n_req); split s covers [s*per, min((s+1)*per, L)) with
+//     per = ceil(ceil(L/S)/align)*align, as the reference's stage 1 (mla_decode_attention.py:389-396);
+//     partials go to attn_logits [rows, heads, S, Dv+1].
+//   balanced (num_splits == 0): workgroup w owns global PLAN_TILE-token tiles [w*chunk, (w+1)*chunk)
+//     of the concatenated requests; a request it covers alone is finished in place, others leave a
+//     partial in slot w + b.
+template <int DV, class F>
+__device__ __forceinline__ void for_each_segment(const KParams& p, F&& f) {
+  // one call site of f, so the (large, inlined) segment body exists once per kernel
+  const bool fixed = p.num_splits > 0;
+  int b_lo, b_hi, lo = 0, hi = 0;
+  const int* pref = p.plan + 2;
+  if (fixed) {
+    b_lo = blockIdx.y;
+    b_hi = b_lo + 1;
+  } else {
+    const int w = blockIdx.x;
+    const int chunk = p.plan[0], total = p.plan[1];
+    lo = w * chunk;
+    hi = lo + chunk < total ? lo + chunk : total;
+    if (lo >= hi) return;
+    // first request whose tile range [pref[b], pref[b+1]) contains lo
+    int b0 = 0, b1 = p.n_req - 1;
+    while (b0 < b1) {
+      const int mid = (b0 + b1 + 1) >> 1;
+      if (pref[mid] <= lo) b0 = mid; else b1 = mid - 1;
+    }
+    b_lo = b0;
+    b_hi = p.n_req;
+  }
+  const int nrow = p.qrows * p.heads;
+  for (int b = b_lo; b < b_hi; ++b) {
+    const int L = req_len(p, b);
+    int a, e;
+    SegOut so;
+    if (fixed) {
+      const int s = blockIdx.x;
+      int per = (L + p.num_splits - 1) / p.num_splits;
+      if (p.split_align > 0) per = (per + p.split_align - 1) / p.split_align * p.split_align;
+      a = per * s;
+      e = a + per < L ? a + per : L;
+      so.final_out = p.num_splits == 1;
+      so.po = p.ws + (int64_t)b * p.qrows * p.ws_sr + (int64_t)s * p.ws_ss;
+      so.po_sr = p.ws_sr;
+      so.po_sh = p.ws_sh;
+      so.plse = nullptr;
+      so.plse_sr = 0;
+    } else {
+      const int c0 = pref[b], c1 = pref[b + 1];
+      if (c0 >= hi) break;
+      if (c1 <= lo) continue;
+      const int t_lo = (lo > c0 ? lo : c0) - c0, t_hi = (hi < c1 ? hi : c1) - c0;
+      a = t_lo * PLAN_TILE;
+      e = t_hi * PLAN_TILE < L ? t_hi * PLAN_TILE : L;
+      so.final_out = (t_lo == 0 && t_hi == c1 - c0);
+      const int64_t slot = (int64_t)blockIdx.x + b;
+      so.po = p.part_o + slot * nrow * DV;
+      so.po_sr = (int64_t)p.heads * DV;
+      so.po_sh = DV;
+      so.plse = p.part_lse + slot * nrow;
+      so.plse_sr = p.heads;
+    }
+    if (e <= a) continue;
+    f(b, a, e, L, so);
+  }
+}
+
+// ---- host-side interface of the wide-latent translation unit (qmla_wide.hip) ----
+// Index of a compiled wide-latent instance for these params, or -1.
+int wide_select(const qmla_decode_params* p);
+// Launch the wide-latent partial pass of instance `inst` (grid per split mode).
+int wide_launch(int inst, const qmla_decode_params* p, const KParams& k, int nwg, hipStream_t st);
+
+}  // namespace qmla

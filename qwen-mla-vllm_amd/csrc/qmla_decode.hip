@@ -27,53 +27,13 @@
 #include <string.h>
 
 #include "qmla.h"
+#include "qmla_common.h"
 #include "qmla_device.h"
 
 namespace qmla {
 
-constexpr int PLAN_TILE = 64;  // balancing granularity of the balanced plan (tokens)
 constexpr int NWAVE = 4;       // waves per workgroup
 constexpr int NTHR = NWAVE * 64;
-
-struct KParams {
-  const __bf16* q_nope;
-  int64_t qn_sr, qn_sh;
-  const __bf16* q_pe;
-  int64_t qp_sr, qp_sh;
-  const char* kv;
-  int64_t page_stride_b, token_stride_b;  // bytes
-  int page_size;
-  int rope_w;
-  int rms_off_b;  // byte offset of the rms tail inside a row
-  const float* k_scale;
-  float sm_scale, logit_cap;
-  const int* bt;
-  int64_t bt_stride;
-  const int* seq_lens;
-  int n_req;      // requests = rows / qrows
-  int qrows, hpg; // verify tokens per request, heads per latent group
-  int heads;      // heads per row (= groups * hpg)
-  void* out;
-  int64_t o_sr, o_sh;
-  int out_dt;
-  void* lse;
-  int64_t lse_sr;
-  int lse_dt;
-  int num_splits, split_align;
-  float* ws;
-  int64_t ws_sr, ws_sh, ws_ss;
-  // balanced mode
-  int nwg;
-  int* plan;        // [0] = chunk (tiles per workgroup), [1] = total tiles, [2 + b] = prefix C_b
-  float* part_o;    // [(nwg + n_req), qrows*heads, Dv]
-  float* part_lse;  // [(nwg + n_req), qrows*heads]
-};
-
-__device__ __forceinline__ void store_out(void* base, int dt, int64_t idx, float v) {
-  if (dt == QMLA_DT_BF16) reinterpret_cast<__bf16*>(base)[idx] = (__bf16)v;
-  else if (dt == QMLA_DT_F16) reinterpret_cast<_Float16*>(base)[idx] = (_Float16)v;
-  else reinterpret_cast<float*>(base)[idx] = v;
-}
 
 // Compile-time shape of one kernel instance.
 //   EB   cache element bytes (1 = fp8 e4m3fn, 2 = bf16)
@@ -165,14 +125,6 @@ struct Smem {
 };
 
 // Everything a segment needs to know about where its results go.
-struct SegOut {
-  bool final_out;       // write normalized output + lse directly
-  float* po;            // partial output base of this request (query-row 0 of it)
-  int64_t po_sr, po_sh; // float strides for (verify token of the request, head)
-  float* plse;          // balanced-mode lse base (nullptr: lse stored after the Dv columns)
-  int64_t plse_sr;
-};
-
 // One contiguous token range [tok_a, tok_e) of request `req` (length L), all query rows.
 //
 // Score layout (S^T = K . Q^T on MFMA): lane (n = row column ln16, lg) of row block mb holds the
@@ -631,67 +583,15 @@ __device__ __forceinline__ void process_segment(const KParams& p, Smem<C>& sm, i
   lds_barrier();  // LDS ring and P buffers free for the next segment
 }
 
-// request length: the last flattened row of the request carries it (mla_impl.py:628-662)
-__device__ __forceinline__ int req_len(const KParams& p, int req) {
-  int L = p.seq_lens[(int64_t)req * p.qrows + p.qrows - 1];
-  return L > 0 ? L : 0;
-}
-
 template <class C>
 __global__ __launch_bounds__(NTHR, C::WGPC) void partial_kernel(const KParams p) {
   __shared__ __attribute__((aligned(16))) Smem<C> sm;
   // the per-layer scale dequantizes fp8 rows (and e4m3 rms codes); a bf16 cache ignores it, as
   // the reference does (mla_decode_attention.py:451-463)
   const float kscale = (C::EB == 1 && p.k_scale) ? *p.k_scale : 1.0f;
-  if (p.num_splits > 0) {
-    // fixed splits: grid (S, n_req); bounds as the reference's stage 1 (mla_decode_attention.py:389-396)
-    const int s = blockIdx.x, req = blockIdx.y;
-    const int L = req_len(p, req);
-    int per = (L + p.num_splits - 1) / p.num_splits;
-    if (p.split_align > 0) per = (per + p.split_align - 1) / p.split_align * p.split_align;
-    const int a = per * s;
-    const int e = a + per < L ? a + per : L;
-    if (e <= a) return;
-    SegOut so;
-    so.final_out = p.num_splits == 1;
-    so.po = p.ws + (int64_t)req * p.qrows * p.ws_sr + (int64_t)s * p.ws_ss;
-    so.po_sr = p.ws_sr;
-    so.po_sh = p.ws_sh;
-    so.plse = nullptr;
-    so.plse_sr = 0;
+  for_each_segment<C::DCG>(p, [&](int req, int a, int e, int L, const SegOut& so) {
     process_segment<C>(p, sm, req, a, e, L, so, kscale);
-    return;
-  }
-  // balanced: workgroup w owns global tiles [w*chunk, (w+1)*chunk) of the concatenated requests
-  const int w = blockIdx.x;
-  const int chunk = p.plan[0], total = p.plan[1];
-  const int* pref = p.plan + 2;
-  int lo = w * chunk, hi = lo + chunk < total ? lo + chunk : total;
-  if (lo >= hi) return;
-  // first request whose tile range [pref[b], pref[b+1]) contains lo
-  int b0 = 0, b1 = p.n_req - 1;
-  while (b0 < b1) {
-    const int mid = (b0 + b1 + 1) >> 1;
-    if (pref[mid] <= lo) b0 = mid; else b1 = mid - 1;
-  }
-  const int nrow = p.qrows * p.heads;
-  for (int b = b0; b < p.n_req && pref[b] < hi; ++b) {
-    const int c0 = pref[b], c1 = pref[b + 1];
-    if (c1 <= lo) continue;
-    const int t_lo = (lo > c0 ? lo : c0) - c0, t_hi = (hi < c1 ? hi : c1) - c0;
-    const int L = req_len(p, b);
-    const int a = t_lo * PLAN_TILE, e = t_hi * PLAN_TILE < L ? t_hi * PLAN_TILE : L;
-    if (e <= a) continue;
-    SegOut so;
-    so.final_out = (t_lo == 0 && t_hi == c1 - c0);
-    const int64_t slot = (int64_t)w + b;
-    so.po = p.part_o + slot * nrow * C::DCG;
-    so.po_sr = (int64_t)p.heads * C::DCG;
-    so.po_sh = C::DCG;
-    so.plse = p.part_lse + slot * nrow;
-    so.plse_sr = p.heads;
-    process_segment<C>(p, sm, b, a, e, L, so, kscale);
-  }
+  });
 }
 
 // Balanced plan: tiles per request, prefix sums, per-workgroup chunk. One workgroup.
@@ -1121,7 +1021,7 @@ int qmla_version(void) { return QMLA_ABI_VERSION; }
 
 const char* qmla_build_info(void) {
   return "qmla gfx950: LDS-DMA paged rows, MFMA 16x16x32 bf16 QK/PV, tr8/tr16 value reads, "
-         "fixed and balanced split-K + LSE combine";
+         "fixed and balanced split-K + LSE combine, column-split single-pass wide latent (d_c 1792)";
 }
 
 size_t qmla_workspace_bytes(const qmla_decode_params* p) {
@@ -1156,14 +1056,15 @@ int qmla_decode_partial(const qmla_decode_params* p, void* stream) {
   if (rc) return rc;
   if (p->d_c / p->groups > 2048) return QMLA_ERR_SHAPE;
   const Inst* in = find_inst(p);
-  if (!in) return QMLA_ERR_NOKERNEL;
+  const int wi = in ? -1 : wide_select(p);
+  if (!in && wi < 0) return QMLA_ERR_NOKERNEL;
   if (p->num_splits > 1 && !p->workspace) return QMLA_ERR_WORKSPACE;
   if (p->num_splits == 0) {
     rc = check_balanced_ws(p);
     if (rc) return rc;
   }
   KParams k = make_kparams(p);
-  return run_partial(p, in, k, (hipStream_t)stream);
+  return in ? run_partial(p, in, k, (hipStream_t)stream) : wide_launch(wi, p, k, k.nwg, (hipStream_t)stream);
 }
 
 int qmla_combine(const qmla_decode_params* p, void* stream) {
@@ -1185,12 +1086,13 @@ int qmla_decode(const qmla_decode_params* p, void* stream) {
   if (rc) return rc;
   if (p->d_c / p->groups > 2048) return QMLA_ERR_SHAPE;
   const Inst* in = find_inst(p);
-  if (!in) return QMLA_ERR_NOKERNEL;
+  const int wi = in ? -1 : wide_select(p);
+  if (!in && wi < 0) return QMLA_ERR_NOKERNEL;
   hipStream_t st = (hipStream_t)stream;
   if (p->num_splits > 0) {
     if (p->num_splits > 1 && !p->workspace) return QMLA_ERR_WORKSPACE;
     KParams k = make_kparams(p);
-    rc = run_partial(p, in, k, st);
+    rc = in ? run_partial(p, in, k, st) : wide_launch(wi, p, k, 0, st);
     if (rc || p->num_splits == 1) return rc;
     return run_combine(p, k, st);
   }
@@ -1199,21 +1101,9 @@ int qmla_decode(const qmla_decode_params* p, void* stream) {
   KParams k = make_kparams(p);
   rc = run_plan(p, k, st);
   if (rc) return rc;
-  rc = run_partial(p, in, k, st);
+  rc = in ? run_partial(p, in, k, st) : wide_launch(wi, p, k, k.nwg, st);
   if (rc) return rc;
   return run_combine(p, k, st);
-}
-
-size_t qmla_decode_2pass_scratch_bytes(const qmla_decode_params* p, int64_t max_tokens) {
-  (void)p;
-  (void)max_tokens;
-  return 0;
-}
-
-int qmla_decode_2pass(const qmla_decode_params* p, void* scratch, size_t scratch_bytes, int64_t max_tokens,
-                      void* stream) {
-  (void)p; (void)scratch; (void)scratch_bytes; (void)max_tokens; (void)stream;
-  return QMLA_ERR_NOKERNEL;
 }
 
 }  // extern "C"

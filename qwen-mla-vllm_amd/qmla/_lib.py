@@ -92,8 +92,6 @@ SIGNATURES = {
     "qmla_plan": (ctypes.c_int, [_P, ctypes.c_void_p]),
     "qmla_decode_partial": (ctypes.c_int, [_P, ctypes.c_void_p]),
     "qmla_combine": (ctypes.c_int, [_P, ctypes.c_void_p]),
-    "qmla_decode_2pass_scratch_bytes": (ctypes.c_size_t, [_P, ctypes.c_int64]),
-    "qmla_decode_2pass": (ctypes.c_int, [_P, ctypes.c_void_p, ctypes.c_size_t, ctypes.c_int64, ctypes.c_void_p]),
 }
 
 _lib = None

@@ -24,7 +24,7 @@ def _declared_functions() -> list[str]:
 
 def test_header_functions_exported_and_bound():
     names = _declared_functions()
-    assert "qmla_decode" in names and len(names) >= 9
+    assert "qmla_decode" in names and len(names) >= 7
     lib = _lib.lib()
     for n in names:
         assert hasattr(lib, n), n
