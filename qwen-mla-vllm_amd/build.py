@@ -29,7 +29,7 @@ COMMON_FLAGS = [
 # with VALU ops, and AGPR-resident accumulators make the compiler copy them back and forth.
 SOURCES = [
     (CSRC / "qmla_decode.hip", ["-mllvm", "-amdgpu-mfma-vgpr-form"]),
-    (CSRC / "qmla_wide.hip", ["-mllvm", "-amdgpu-mfma-vgpr-form"]),
+    (CSRC / "qmla_cs.hip", ["-mllvm", "-amdgpu-mfma-vgpr-form"]),
 ]
 
 

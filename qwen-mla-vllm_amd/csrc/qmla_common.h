@@ -134,10 +134,10 @@ __device__ __forceinline__ void for_each_segment(const KParams& p, F&& f) {
   }
 }
 
-// ---- host-side interface of the wide-latent translation unit (qmla_wide.hip) ----
-// Index of a compiled wide-latent instance for these params, or -1.
-int wide_select(const qmla_decode_params* p);
-// Launch the wide-latent partial pass of instance `inst` (grid per split mode).
-int wide_launch(int inst, const qmla_decode_params* p, const KParams& k, int nwg, hipStream_t st);
+// ---- host-side interface of the column-split translation unit (qmla_cs.hip) ----
+// Index of a compiled column-split instance for these params, or -1.
+int cs_select(const qmla_decode_params* p);
+// Launch the partial pass of column-split instance `inst` (grid per split mode).
+int cs_launch(int inst, const qmla_decode_params* p, const KParams& k, int nwg, hipStream_t st);
 
 }  // namespace qmla

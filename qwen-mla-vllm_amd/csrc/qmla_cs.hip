@@ -1,0 +1,823 @@
+// qmla_cs.hip -- gfx950 column-split MLA decode: the workgroup's waves split the LATENT COLUMNS.
+//
+// A workgroup owns a contiguous token range of one request and every query row of it, so each
+// cached row is read from HBM once per call. Its waves form a grid
+//     G latent groups  x  NCG column slices  x  NTG token groups
+// Wave (g, c, tg) owns latent columns [c*DCW, (c+1)*DCW) of group g (and a slice of the rope
+// columns) for BOTH the score product and P.V, and the tg-th T-token part of every workgroup tile.
+// It stages only its slice of each of its rows in a private LDS ring and waits for its own DMA;
+// one wave per token group also stages the rms tail for the others. Per tile:
+//   QK       S^T = K . Q^T on MFMA over the wave's columns: partial scores of T tokens x 16*MB rows,
+//            query fragments resident in VGPRs (a column slice of them: ~36-60 VGPRs, not 144+).
+//   sum      the NCG partials of (g, tg) meet in LDS; every wave adds them in the same order, so the
+//            NCG waves hold bit-identical scores and take identical softmax decisions.
+//   softmax  rms divide (codes read with one transposed LDS read per 16 rows), scale, mask, lazily
+//            moving reference max; P stays in registers: the MFMA score layout already is the
+//            A-operand layout of P.V under the token order chosen for the score tiles.
+//   PV       acc[16*MB x DCW] += P . V on MFMA, V^T fragments read with ds_read_b64_tr_b8/_b16.
+// With NTG = 2 the two token groups keep separate (max, sum, acc) and merge in the epilogue.
+// Eight waves (two per SIMD) hide each other's LDS/MFMA latency.
+//
+// Token order inside a 32-token score tile pair (NTB = 2): score tile 0 row m is token m, score
+// tile 1 row m is token 16 + ((m + 8) mod 16). Lane (n, q) then holds tokens {4q..4q+3} and
+// {24+4q..} / {16+4q-8..} -- the set whose V rows (read 8 per 16-lane block by tr_b8) and K rows
+// (16 per half-wave) fall on distinct LDS banks for the odd-16-byte row strides used here.
+//
+// Reference semantics: qwen_mla/ops/mla_decode_attention.py:297-586 (stage 1, incl. the rms divide
+// :466-507 and the verify limit), :1264-1359 (entry); wide latents replace the two-pass path
+// :602-849 with the same single pass.
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "qmla.h"
+#include "qmla_common.h"
+#include "qmla_device.h"
+
+namespace qmla {
+namespace cs {
+
+typedef __attribute__((__vector_size__(4 * sizeof(short)))) short s16x4;
+typedef __attribute__((__vector_size__(8 * sizeof(short)))) short s16x8;
+
+constexpr int PIDN = 512;    // page ids staged per sub-range
+
+__device__ __forceinline__ f32x4 mfma16k16(const s16x4& a, const s16x4& b, const f32x4& c) {
+  return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(a, b, c, 0, 0, 0);
+}
+
+// LDS reads issued as inline asm (through the builtins the compiler waits for every LDS-DMA in
+// flight first); results are valid after lds_wait().
+__device__ __forceinline__ i32x4 ldsr128(const char* p) {
+  i32x4 r;
+  asm volatile("ds_read_b128 %0, %1" : "=v"(r) : "v"(lds_addr(p)));
+  return r;
+}
+__device__ __forceinline__ i32x2 ldsr64(const char* p) {
+  i32x2 r;
+  asm volatile("ds_read_b64 %0, %1" : "=v"(r) : "v"(lds_addr(p)));
+  return r;
+}
+__device__ __forceinline__ int ldsr32(const char* p) {
+  int r;
+  asm volatile("ds_read_b32 %0, %1" : "=v"(r) : "v"(lds_addr(p)));
+  return r;
+}
+__device__ __forceinline__ uint32_t ldsr8(const char* p) {
+  uint32_t r;
+  asm volatile("ds_read_u8 %0, %1" : "=v"(r) : "v"(lds_addr(p)));
+  return r;
+}
+__device__ __forceinline__ uint32_t ldsr16(const char* p) {
+  uint32_t r;
+  asm volatile("ds_read_u16 %0, %1" : "=v"(r) : "v"(lds_addr(p)));
+  return r;
+}
+
+// 4 fp8 bytes -> bf16x4 (exact). Assembled from whole 32-bit words: element-wise bit casts of the
+// packed results have been compiled into a permute that duplicated the low half.
+__device__ __forceinline__ s16x4 fp8x4_to_bf16(int raw) {
+  const bf16x2 a = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(raw, 1.0f, false);
+  const bf16x2 b = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(raw, 1.0f, true);
+  const i32x2 r = {__builtin_bit_cast(int, a), __builtin_bit_cast(int, b)};
+  return __builtin_bit_cast(s16x4, r);
+}
+
+// Compile-time shape of one instance.
+//   EB   cache element bytes (1 = fp8 e4m3fn, 2 = bf16);  RMS  QMLA_RMS_* tail format
+//   DCG  latent columns per group, G latent groups;  NCG column slices per group
+//   NTG  token groups;  NTB 16-token score tiles per token group and tile (T = 16*NTB tokens)
+//   MB   16-row blocks per latent group (rows per group = qrows*heads/G <= 16*MB)
+//   S    LDS ring stages;  CRM 16-byte chunks of the rms tail staged per token;  CAP tanh logit cap
+//   RTR  rms codes read transposed (rows are the heads of one token: G = 1 and qrows = 1)
+template <int EB_, int RMS_, int DCG_, int G_, int NCG_, int NTG_, int NTB_, int MB_, int S_, int CRM_,
+          bool CAP_, bool RTR_>
+struct CS {
+  static constexpr int EB = EB_, RMS = RMS_, DCG = DCG_, G = G_, NCG = NCG_, NTG = NTG_, NTB = NTB_;
+  static constexpr int MB = MB_, S = S_, CRM = CRM_;
+  static constexpr bool CAP = CAP_, RTR = RTR_;
+  static constexpr int NW = G * NCG * NTG, NTHR = 64 * NW;
+  static constexpr int T = 16 * NTB, TT = NTG * T;
+  static constexpr int DC = G * DCG;
+  static constexpr int DCW = DCG / NCG;                  // latent columns per wave
+  static constexpr int KS = DCW / 32;                    // 32-column k-steps
+  static constexpr int CB = DCW / 16;                    // 16-column output blocks
+  static constexpr int RW = NCG >= 4 ? 16 : 64 / NCG;    // rope columns per wave (NCG 8: waves c < 4)
+  static constexpr int CL = DCW * EB / 16;               // latent chunks of a row slice
+  static constexpr int CR = RW * EB / 16;                // rope chunks
+  static constexpr int CPW = (CL + CR) | 1;              // odd 16-byte count: conflict-free rows
+  static constexpr int RS = 16 * CPW;                    // LDS row stride
+  static constexpr int NCH = T * CPW;                    // chunks per tile per wave
+  static constexpr int NI = (NCH + 63) / 64;             // DMA instructions per tile per wave
+  static constexpr int SB = NCH * 16;                    // stage bytes per wave
+  static constexpr int RB = (RMS == QMLA_RMS_NONE) ? 0 : ((RMS == QMLA_RMS_BF16 || RMS == QMLA_RMS_BF16_BYTES) ? 2 : 1);
+  static constexpr int RRS = 16 * (CRM > 0 ? CRM : 1);   // staged rms row bytes
+  static constexpr int NRI = CRM > 0 ? (T * CRM + 63) / 64 : 0;   // rms DMA instructions per tile
+  static constexpr int ROWS = 16 * MB;
+  static constexpr int XBW = NTB * MB;                   // partial-score f32x4 per lane
+  static_assert(DCG % (32 * NCG) == 0, "whole 32-column k-steps per wave");
+  static_assert(NTB == 1 || NTB == 2, "score tiles per token group");
+  static_assert(EB == 2 || NTB == 2, "fp8 values are read 8 tokens at a time");
+  static_assert(RW == 16 || RW == 32 || RW == 64, "rope slice");
+  static_assert((S - 1) * (NI + NRI) < 64, "vmcnt range");
+  static_assert(!RTR || CRM * 16 >= RB * ROWS, "transposed rms reads cover all row heads");
+};
+
+template <class C>
+struct Smem {
+  char ring[C::S][C::NW][C::SB];
+  char rms[C::S + 1][C::NTG][C::T * C::RRS];   // S+1 deep: read after the exchange
+  f32x4 xb[C::NW][C::XBW][64];                 // partial scores
+  int pid[PIDN];
+};
+
+
+// score tile tb, tile row m -> token offset inside the token group's T tokens
+__device__ __forceinline__ constexpr int tok_of(int tb, int m) { return tb == 0 ? m : 16 + ((m + 8) & 15); }
+// k-slot 8q + r of the P.V product (NTB = 2) -> token offset: the lane's scores in order
+__device__ __forceinline__ constexpr int vtok(int q, int r) { return r < 4 ? tok_of(0, 4 * q + r) : tok_of(1, 4 * q + r - 4); }
+
+template <class C>
+__device__ __forceinline__ void wait_tile(bool steady, bool rms_wave) {
+  if (!steady) wait_vmcnt<0>();
+  else if (rms_wave) wait_vmcnt<(C::S - 1) * (C::NI + C::NRI)>();
+  else wait_vmcnt<(C::S - 1) * C::NI>();
+}
+
+// One contiguous token range [ta, te) of request `req` (length L), all query rows.
+template <class C>
+__device__ __forceinline__ void segment(const KParams& p, Smem<C>& sm, int req, int ta, int te, int L,
+                                        const SegOut& so, float kscale) {
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int tg = w / (C::G * C::NCG);
+  const int g = (w / C::NCG) % C::G;
+  const int c = w % C::NCG;
+  const bool rms_wave = (C::CRM > 0) && (w % (C::G * C::NCG)) == 0;   // (g 0, c 0) of each token group
+  const bool has_rope = C::NCG < 8 || c < 4;
+  const int rope_col = C::NCG >= 4 ? 16 * (c & 3) : C::RW * c;
+  const int ln16 = lane & 15, lg = lane >> 4;
+  const int hpg = p.hpg;
+  const int rows_pg = p.qrows * hpg;
+  const int row0 = req * p.qrows;
+  const int P = p.page_size;
+  const int64_t TS = p.token_stride_b, PS = p.page_stride_b;
+  const int* btrow = p.bt + (int64_t)row0 * p.bt_stride;
+  const float csc = p.sm_scale * kLog2e * kscale;
+  const float cap2 = p.logit_cap * kLog2e;
+
+  // ---- query fragments (B operands) for this wave's columns; zero for padding rows ----
+  bf16x8 qf[C::KS][C::MB];
+  constexpr int RKS = C::RW == 64 ? 2 : 1;
+  bf16x8 qr8[RKS][C::MB];   // RW 32/64: 16x16x32 steps
+  s16x4 qr4[C::MB];         // RW 16: one 16x16x16 step
+  int lim[C::MB], hb[C::MB];
+#pragma unroll
+  for (int mb = 0; mb < C::MB; ++mb) {
+    const int r = ln16 + 16 * mb;
+    const bool ok = r < rows_pg;
+    const int jq = ok ? r / hpg : 0, hh = ok ? r - jq * hpg : 0;
+    const int head = g * hpg + hh;
+    // verify row jq of the request sees its first L - (qrows-1-jq) tokens (mla_impl.py:628-662)
+    const int lr = L - (p.qrows - 1 - jq);
+    lim[mb] = ok ? (lr < te ? lr : te) : 0;
+    hb[mb] = ok ? head * C::RB : 0;
+    const __bf16* qn = p.q_nope + (int64_t)(row0 + jq) * p.qn_sr + (int64_t)head * p.qn_sh + c * C::DCW + 8 * lg;
+#pragma unroll
+    for (int ks = 0; ks < C::KS; ++ks) {
+      bf16x8 v = *reinterpret_cast<const bf16x8*>(qn + 32 * ks);
+      if (!ok) v = bf16x8{};
+      qf[ks][mb] = v;
+    }
+    const __bf16* qp = p.q_pe + (int64_t)(row0 + jq) * p.qp_sr + (int64_t)head * p.qp_sh + rope_col;
+    if constexpr (C::RW == 16) {
+      s16x4 v = *reinterpret_cast<const s16x4*>(qp + 4 * lg);
+      if (!ok || !has_rope) v = s16x4{};
+      qr4[mb] = v;
+    } else {
+#pragma unroll
+      for (int k = 0; k < RKS; ++k) {
+        bf16x8 v = *reinterpret_cast<const bf16x8*>(qp + 32 * k + 8 * lg);
+        if (!ok) v = bf16x8{};
+        qr8[k][mb] = v;
+      }
+    }
+  }
+  // smallest row limit: tiles below it need no masking
+  const int limmin = L - (p.qrows - 1) < te ? L - (p.qrows - 1) : te;
+
+  // ---- DMA source of chunk i of the wave's tile slice: row i / CPW, chunk i % CPW of
+  //      [latent slice | rope slice | pad]; recomputed at every issue rather than held ----
+  const int lat_off = (g * C::DCG + c * C::DCW) * C::EB;
+  const int rope_off = C::DC * C::EB + rope_col * C::EB;
+  auto src_off = [&](int k, int ln, int& row) {
+    const int i = 64 * k + ln;
+    const int t = i / C::CPW, ch = i - t * C::CPW;
+    int off;
+    if (ch < C::CL) off = lat_off + 16 * ch;
+    else if (ch < C::CL + C::CR) off = rope_off + 16 * (ch - C::CL);
+    else off = 0;
+    row = i < C::NCH ? t : 0;
+    return off;
+  };
+
+  float mref[C::MB], lpart[C::MB];
+  f32x4 acc[C::MB][C::CB];
+#pragma unroll
+  for (int mb = 0; mb < C::MB; ++mb) {
+    mref[mb] = kNegInf;
+    lpart[mb] = 0.f;
+#pragma unroll
+    for (int cb = 0; cb < C::CB; ++cb) acc[mb][cb] = f32x4{0.f, 0.f, 0.f, 0.f};
+  }
+
+  // sub-ranges of at most PIDN pages, in whole tiles
+  int sub = (PIDN - 1) * P;
+  sub = sub < C::TT ? C::TT : sub / C::TT * C::TT;
+  const bool uni = (P % C::TT) == 0 && (ta % C::TT) == 0;   // every tile within one page
+  for (int sa = ta; sa < te; sa += sub) {
+    const int se = te - sa < sub ? te : sa + sub;
+    const int pbase = sa / P;
+    const int np = (se - 1) / P - pbase + 1;
+    wait_vmcnt<0>();
+    lds_barrier();   // every wave is done with the previous sub-range's page ids
+    for (int i = tid; i < np; i += C::NTHR) sm.pid[i] = btrow[pbase + i];
+    __syncthreads();
+    const int nt = (se - sa + C::TT - 1) / C::TT;
+
+    auto issue = [&](int t) {
+      const int tok0 = sa + t * C::TT;
+      const int nvalid = se - tok0 < C::TT ? se - tok0 : C::TT;
+      char* dst = sm.ring[t % C::S][w];
+      char* rdst = sm.rms[t % (C::S + 1)][tg];
+      int ln = lane;
+      asm volatile("" : "+v"(ln));   // keep the offsets from being hoisted out of the tile loop
+      if (uni) {
+        const int pg = __builtin_amdgcn_readfirstlane(sm.pid[tok0 / P - pbase]);
+        const char* base = p.kv + (int64_t)pg * PS + (int64_t)(tok0 % P) * TS;
+        // rows past the range end read as zeros (outside the resource)
+        const __amdgpu_buffer_rsrc_t rs = make_rsrc(base, (uint32_t)(nvalid * TS));
+        const int tb0 = tg * C::T;
+#pragma unroll
+        for (int k = 0; k < C::NI; ++k) {
+          int row;
+          const int off = src_off(k, ln, row);
+          if (64 * k + 64 <= C::NCH || 64 * k + ln < C::NCH)
+            dma16_buf(rs, (uint32_t)((tb0 + row) * (int)TS + off), dst + k * 1024);
+        }
+        if (rms_wave) {
+#pragma unroll
+          for (int k = 0; k < C::NRI; ++k) {
+            const int j = 64 * k + ln;
+            const int row = j / (C::CRM > 0 ? C::CRM : 1);
+            if (64 * k + 64 <= C::T * C::CRM || j < C::T * C::CRM)
+              dma16_buf(rs, (uint32_t)((tb0 + row) * (int)TS + p.rms_off_b + 16 * (j - row * C::CRM)), rdst + k * 1024);
+          }
+        }
+      } else {
+        // pages change inside a tile: per-lane page lookup; rows past the end repeat the last row
+        const int tb0 = tok0 + tg * C::T;
+        const int nv = se - tb0;   // rows of this token group inside the range (may be <= 0)
+#pragma unroll
+        for (int k = 0; k < C::NI; ++k) {
+          int row;
+          const int off = src_off(k, ln, row);
+          if (64 * k + 64 <= C::NCH || 64 * k + ln < C::NCH) {
+            const int rr = row < nv ? row : (nv > 0 ? nv - 1 : 0);
+            const int tok = nv > 0 ? tb0 + rr : se - 1;
+            const int q = tok / P;
+            const int pg = sm.pid[q - pbase];
+            dma16(p.kv + (int64_t)pg * PS + (int64_t)(tok - q * P) * TS + off, dst + k * 1024);
+          }
+        }
+        if (rms_wave) {
+#pragma unroll
+          for (int k = 0; k < C::NRI; ++k) {
+            const int j = 64 * k + ln;
+            const int row = j / (C::CRM > 0 ? C::CRM : 1);
+            if (64 * k + 64 <= C::T * C::CRM || j < C::T * C::CRM) {
+              const int rr = row < nv ? row : (nv > 0 ? nv - 1 : 0);
+              const int tok = nv > 0 ? tb0 + rr : se - 1;
+              const int q = tok / P;
+              const int pg = sm.pid[q - pbase];
+              dma16(p.kv + (int64_t)pg * PS + (int64_t)(tok - q * P) * TS + p.rms_off_b + 16 * (j - row * C::CRM),
+                    rdst + k * 1024);
+            }
+          }
+        }
+      }
+    };
+
+    for (int t = 0; t < C::S && t < nt; ++t) issue(t);
+
+#pragma clang loop unroll(disable)
+    for (int t = 0; t < nt; ++t) {
+      wait_tile<C>(t + C::S - 1 < nt, rms_wave);
+      const char* st = sm.ring[t % C::S][w];
+      const int tok0 = sa + t * C::TT + tg * C::T;   // this token group's first token
+
+      // ---- partial scores over this wave's columns ----
+      f32x4 sp[C::NTB][C::MB];
+#pragma unroll
+      for (int tb = 0; tb < C::NTB; ++tb) {
+#pragma unroll
+        for (int mb = 0; mb < C::MB; ++mb) sp[tb][mb] = f32x4{0.f, 0.f, 0.f, 0.f};
+        const char* kr = st + tok_of(tb, ln16) * C::RS;
+        if constexpr (C::EB == 1) {
+          i32x2 kv[C::KS];
+#pragma unroll
+          for (int ks = 0; ks < C::KS; ++ks) kv[ks] = ldsr64(kr + 32 * ks + 8 * lg);
+          if constexpr (C::RW == 16) {
+            int rv = ldsr32(kr + 16 * C::CL + 4 * lg);
+#pragma unroll
+            for (int ks = 0; ks < C::KS; ++ks) {
+              lds_wait(kv[ks]);
+              const bf16x8 kf = fp8x8_to_bf16(kv[ks]);
+#pragma unroll
+              for (int mb = 0; mb < C::MB; ++mb) sp[tb][mb] = mfma16(kf, qf[ks][mb], sp[tb][mb]);
+            }
+            lds_wait(rv);
+            if (has_rope) {
+              const s16x4 rf = fp8x4_to_bf16(rv);
+#pragma unroll
+              for (int mb = 0; mb < C::MB; ++mb) sp[tb][mb] = mfma16k16(rf, qr4[mb], sp[tb][mb]);
+            }
+          } else {
+            i32x2 rv[RKS];
+#pragma unroll
+            for (int k = 0; k < RKS; ++k) rv[k] = ldsr64(kr + 16 * C::CL + 32 * k + 8 * lg);
+#pragma unroll
+            for (int ks = 0; ks < C::KS; ++ks) {
+              lds_wait(kv[ks]);
+              const bf16x8 kf = fp8x8_to_bf16(kv[ks]);
+#pragma unroll
+              for (int mb = 0; mb < C::MB; ++mb) sp[tb][mb] = mfma16(kf, qf[ks][mb], sp[tb][mb]);
+            }
+#pragma unroll
+            for (int k = 0; k < RKS; ++k) {
+              lds_wait(rv[k]);
+              const bf16x8 rf = fp8x8_to_bf16(rv[k]);
+#pragma unroll
+              for (int mb = 0; mb < C::MB; ++mb) sp[tb][mb] = mfma16(rf, qr8[k][mb], sp[tb][mb]);
+            }
+          }
+        } else {
+          constexpr int KB = 4;   // k-steps per batch of LDS reads
+#pragma unroll
+          for (int k0 = 0; k0 < C::KS; k0 += KB) {
+            i32x4 kv[KB];
+#pragma unroll
+            for (int j = 0; j < KB; ++j)
+              if (k0 + j < C::KS) kv[j] = ldsr128(kr + 64 * (k0 + j) + 16 * lg);
+#pragma unroll
+            for (int j = 0; j < KB; ++j)
+              if (k0 + j < C::KS) {
+                lds_wait(kv[j]);
+                const bf16x8 kf = __builtin_bit_cast(bf16x8, kv[j]);
+#pragma unroll
+                for (int mb = 0; mb < C::MB; ++mb) sp[tb][mb] = mfma16(kf, qf[k0 + j][mb], sp[tb][mb]);
+              }
+          }
+          if constexpr (C::RW == 16) {
+            i32x2 rv = ldsr64(kr + 16 * C::CL + 8 * lg);
+            lds_wait(rv);
+            if (has_rope) {
+              const s16x4 rf = __builtin_bit_cast(s16x4, rv);
+#pragma unroll
+              for (int mb = 0; mb < C::MB; ++mb) sp[tb][mb] = mfma16k16(rf, qr4[mb], sp[tb][mb]);
+            }
+          } else {
+#pragma unroll
+            for (int k = 0; k < RKS; ++k) {
+              i32x4 rv = ldsr128(kr + 16 * C::CL + 64 * k + 16 * lg);
+              lds_wait(rv);
+              const bf16x8 rf = __builtin_bit_cast(bf16x8, rv);
+#pragma unroll
+              for (int mb = 0; mb < C::MB; ++mb) sp[tb][mb] = mfma16(rf, qr8[k][mb], sp[tb][mb]);
+            }
+          }
+        }
+      }
+
+      // ---- sum the NCG partials of (g, tg) in slice order ----
+#pragma unroll
+      for (int tb = 0; tb < C::NTB; ++tb)
+#pragma unroll
+        for (int mb = 0; mb < C::MB; ++mb) sm.xb[w][tb * C::MB + mb][lane] = sp[tb][mb];
+      lds_barrier();
+      f32x4 s[C::NTB][C::MB];
+      {
+        const int w0 = w - c;   // slice 0 of this (g, tg)
+#pragma unroll
+        for (int x = 0; x < C::XBW; ++x) {
+          f32x4 a;
+#pragma unroll
+          for (int v0 = 0; v0 < C::NCG; v0 += 4) {
+            i32x4 xr[4];
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+              if (v0 + j < C::NCG) xr[j] = ldsr128(reinterpret_cast<const char*>(&sm.xb[w0 + v0 + j][x][lane]));
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+              if (v0 + j < C::NCG) {
+                lds_wait(xr[j]);
+                const f32x4 y = __builtin_bit_cast(f32x4, xr[j]);
+                a = (v0 + j == 0) ? y : a + y;
+              }
+          }
+          s[x / C::MB][x % C::MB] = a;
+        }
+      }
+      lds_barrier();   // the partial-score buffer is free again
+
+      // ---- this tile's rms divisors. The rms ring is S+1 deep: the loader refills a stage for
+      //      tile t+S only after the first barrier of tile t, by which time every wave has read the
+      //      stages of tiles before t; tile t's own stage is not touched ----
+      float rinv[C::NTB][C::MB][4];
+      if constexpr (C::RMS == QMLA_RMS_NONE) {
+#pragma unroll
+        for (int tb = 0; tb < C::NTB; ++tb)
+#pragma unroll
+          for (int mb = 0; mb < C::MB; ++mb)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) rinv[tb][mb][e] = 1.0f;
+      } else {
+        const char* rs = sm.rms[t % (C::S + 1)][tg];
+        uint32_t code[C::NTB][C::MB][4];
+        if constexpr (C::RTR && C::RB == 1) {
+          // one tr_b8 read per 16 rows: lane (n, q) gets head 16mb+n of the 8 tokens vtok(q, 0..7)
+          i32x2 raw[C::MB];
+          const int rr = vtok(lg, ln16 >> 1);
+#pragma unroll
+          for (int mb = 0; mb < C::MB; ++mb) raw[mb] = lds_read_tr8_async(rs + rr * C::RRS + 16 * mb + 8 * (ln16 & 1));
+#pragma unroll
+          for (int mb = 0; mb < C::MB; ++mb) {
+            lds_wait(raw[mb]);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+              code[0][mb][e] = ((uint32_t)raw[mb][0] >> (8 * e)) & 0xFF;
+              if constexpr (C::NTB == 2) code[1][mb][e] = ((uint32_t)raw[mb][1] >> (8 * e)) & 0xFF;
+            }
+          }
+        } else if constexpr (C::RTR && C::RB == 2) {
+          // tr_b16: lanes 4r..4r+3 of a 16-lane block supply token row r; lane n gets head 16mb+n
+#pragma unroll
+          for (int tb = 0; tb < C::NTB; ++tb) {
+            i32x2 raw[C::MB];
+            const int rr = tok_of(tb, 4 * lg + (ln16 >> 2));
+#pragma unroll
+            for (int mb = 0; mb < C::MB; ++mb)
+              raw[mb] = lds_read_tr16_async(rs + rr * C::RRS + 32 * mb + 8 * (ln16 & 3));
+#pragma unroll
+            for (int mb = 0; mb < C::MB; ++mb) {
+              lds_wait(raw[mb]);
+              code[tb][mb][0] = (uint32_t)raw[mb][0] & 0xFFFF;
+              code[tb][mb][1] = (uint32_t)raw[mb][0] >> 16;
+              code[tb][mb][2] = (uint32_t)raw[mb][1] & 0xFFFF;
+              code[tb][mb][3] = (uint32_t)raw[mb][1] >> 16;
+            }
+          }
+        } else {
+          // general rows (verify tokens, latent groups): one read per score
+#pragma unroll
+          for (int tb = 0; tb < C::NTB; ++tb)
+#pragma unroll
+            for (int mb = 0; mb < C::MB; ++mb)
+#pragma unroll
+              for (int e = 0; e < 4; ++e) {
+                const char* a = rs + tok_of(tb, 4 * lg + e) * C::RRS + hb[mb];
+                code[tb][mb][e] = C::RB == 1 ? ldsr8(a) : ldsr16(a);
+              }
+#pragma unroll
+          for (int tb = 0; tb < C::NTB; ++tb)
+#pragma unroll
+            for (int mb = 0; mb < C::MB; ++mb)
+#pragma unroll
+              for (int e = 0; e < 4; ++e) lds_wait(code[tb][mb][e]);
+        }
+#pragma unroll
+        for (int tb = 0; tb < C::NTB; ++tb)
+#pragma unroll
+          for (int mb = 0; mb < C::MB; ++mb)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+              const uint32_t cd = code[tb][mb][e];
+              float ri;
+              if constexpr (C::RMS == QMLA_RMS_LOG8) {
+                // 1 / 2^(-3 + c*6/255) = 2^(3 - c*6/255)  (ops/mla_decode_attention.py:470-479)
+                ri = fast_exp2(fmaf((float)cd, -6.0f / 255.0f, 3.0f));
+              } else if constexpr (C::RMS == QMLA_RMS_E4M3) {
+                const float rv = fp8_to_f32(cd) * kscale;
+                ri = rv > 0.f ? __builtin_amdgcn_rcpf(rv) : 1.0f;
+              } else {
+                const float rv = bf16_bits_to_f32(cd);
+                ri = rv > 0.f ? __builtin_amdgcn_rcpf(rv) : 1.0f;
+              }
+              rinv[tb][mb][e] = ri;
+            }
+      }
+
+      // ---- scale to log2 units, cap, mask; tile max per row ----
+      const bool full = tok0 + C::T <= limmin;
+      float tmax[C::MB];
+#pragma unroll
+      for (int mb = 0; mb < C::MB; ++mb) {
+        float m = kNegInf;
+#pragma unroll
+        for (int tb = 0; tb < C::NTB; ++tb)
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            float v = s[tb][mb][e] * rinv[tb][mb][e] * csc;
+            if constexpr (C::CAP) {
+              // cap * tanh(x / cap) in log2 units: tanh(y) = 1 - 2 / (exp(2y) + 1)
+              const float y = v / cap2;
+              const float e2 = fast_exp2(2.0f * kLog2e * y);
+              v = cap2 * (1.0f - 2.0f / (e2 + 1.0f));
+            }
+            if (!full && tok0 + tok_of(tb, 4 * lg + e) >= lim[mb]) v = kNegInf;
+            s[tb][mb][e] = v;
+            m = fmaxf(m, v);
+          }
+        tmax[mb] = max_lg(m);
+      }
+      // lazy reference max: it moves only when a tile max exceeds it by more than 8 (P <= 2^8)
+      bool need = false;
+#pragma unroll
+      for (int mb = 0; mb < C::MB; ++mb) need |= tmax[mb] > mref[mb] + 8.0f;
+      if (__builtin_amdgcn_ballot_w64(need)) {
+#pragma unroll
+        for (int mb = 0; mb < C::MB; ++mb) {
+          const float mn = tmax[mb] > mref[mb] + 8.0f ? tmax[mb] : mref[mb];
+          const float alpha = mref[mb] == kNegInf ? 0.f : fast_exp2(mref[mb] - mn);
+          lpart[mb] *= alpha;
+          mref[mb] = mn;
+          // accumulator rows 4*lg + i live in lanes 4*lg + i of the score layout
+          float al[4];
+#pragma unroll
+          for (int i = 0; i < 4; ++i) al[i] = __shfl(alpha, 4 * lg + i);
+#pragma unroll
+          for (int cb = 0; cb < C::CB; ++cb)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) acc[mb][cb][i] *= al[i];
+        }
+      }
+
+      // ---- P (bf16) in the A layout of P.V, row sums ----
+      bf16x8 pa8[C::MB];
+      s16x4 pa4[C::MB];
+#pragma unroll
+      for (int mb = 0; mb < C::MB; ++mb) {
+        const float mu = mref[mb] == kNegInf ? 0.f : mref[mb];
+#pragma unroll
+        for (int tb = 0; tb < C::NTB; ++tb)
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const float pv = fast_exp2(s[tb][mb][e] - mu);
+            lpart[mb] += pv;
+            if constexpr (C::NTB == 2) pa8[mb][4 * tb + e] = (__bf16)pv;
+            else pa4[mb][e] = __builtin_bit_cast(short, (__bf16)pv);
+          }
+      }
+
+      // ---- P.V over this wave's columns ----
+      if constexpr (C::EB == 1) {
+        // tr_b8: lanes 2r, 2r+1 of block q supply token row vtok(q, r); lane n gets column n
+        const char* vb = st + vtok(lg, ln16 >> 1) * C::RS + 8 * (ln16 & 1);
+        constexpr int VB = 4;
+#pragma unroll
+        for (int c0 = 0; c0 < C::CB; c0 += VB) {
+          i32x2 vr[VB];
+#pragma unroll
+          for (int j = 0; j < VB; ++j)
+            if (c0 + j < C::CB) vr[j] = lds_read_tr8_async(vb + 16 * (c0 + j));
+#pragma unroll
+          for (int j = 0; j < VB; ++j)
+            if (c0 + j < C::CB) {
+              lds_wait(vr[j]);
+              const bf16x8 vf = fp8x8_to_bf16(vr[j]);
+#pragma unroll
+              for (int mb = 0; mb < C::MB; ++mb) acc[mb][c0 + j] = mfma16(pa8[mb], vf, acc[mb][c0 + j]);
+            }
+        }
+      } else if constexpr (C::NTB == 2) {
+        // tr_b16 twice: k-slots 8q..8q+3 (score tile 0) and 8q+4..8q+7 (score tile 1)
+        const char* v0 = st + tok_of(0, 4 * lg + (ln16 >> 2)) * C::RS + 8 * (ln16 & 3);
+        const char* v1 = st + tok_of(1, 4 * lg + (ln16 >> 2)) * C::RS + 8 * (ln16 & 3);
+        constexpr int VB = 4;
+#pragma unroll
+        for (int c0 = 0; c0 < C::CB; c0 += VB) {
+          i32x2 va[VB], vc[VB];
+#pragma unroll
+          for (int j = 0; j < VB; ++j)
+            if (c0 + j < C::CB) {
+              va[j] = lds_read_tr16_async(v0 + 32 * (c0 + j));
+              vc[j] = lds_read_tr16_async(v1 + 32 * (c0 + j));
+            }
+#pragma unroll
+          for (int j = 0; j < VB; ++j)
+            if (c0 + j < C::CB) {
+              lds_wait(va[j], vc[j]);
+              const s16x4 a = __builtin_bit_cast(s16x4, va[j]), b = __builtin_bit_cast(s16x4, vc[j]);
+              s16x8 ab;
+#pragma unroll
+              for (int e = 0; e < 4; ++e) {
+                ab[e] = a[e];
+                ab[4 + e] = b[e];
+              }
+              const bf16x8 vf = __builtin_bit_cast(bf16x8, ab);
+#pragma unroll
+              for (int mb = 0; mb < C::MB; ++mb) acc[mb][c0 + j] = mfma16(pa8[mb], vf, acc[mb][c0 + j]);
+            }
+        }
+      } else {
+        const char* vb = st + (4 * lg + (ln16 >> 2)) * C::RS + 8 * (ln16 & 3);
+        constexpr int VB = 7;
+#pragma unroll
+        for (int c0 = 0; c0 < C::CB; c0 += VB) {
+          i32x2 vr[VB];
+#pragma unroll
+          for (int j = 0; j < VB; ++j)
+            if (c0 + j < C::CB) vr[j] = lds_read_tr16_async(vb + 32 * (c0 + j));
+#pragma unroll
+          for (int j = 0; j < VB; ++j)
+            if (c0 + j < C::CB) {
+              lds_wait(vr[j]);
+              const s16x4 vf = __builtin_bit_cast(s16x4, vr[j]);
+#pragma unroll
+              for (int mb = 0; mb < C::MB; ++mb) acc[mb][c0 + j] = mfma16k16(pa4[mb], vf, acc[mb][c0 + j]);
+            }
+        }
+      }
+      if (t + C::S < nt) issue(t + C::S);
+    }
+  }
+  wait_vmcnt<0>();
+
+  // ---- epilogue: per-row sums; merge the token groups; normalize and write ----
+  float lrow[C::MB];
+#pragma unroll
+  for (int mb = 0; mb < C::MB; ++mb) lrow[mb] = sum_lg(lpart[mb]);
+  if constexpr (C::NTG == 2) {
+    // token group 1 hands (max, sum, acc) to token group 0 through the (now idle) ring
+    lds_barrier();
+    float* xa = reinterpret_cast<float*>(&sm.ring[0][0][0]);
+    const int slot = w % (C::G * C::NCG);
+    float* mine = xa + (size_t)slot * (C::MB * C::CB * 4 + 2 * C::MB) * 64;
+    if (tg == 1) {
+#pragma unroll
+      for (int mb = 0; mb < C::MB; ++mb) {
+#pragma unroll
+        for (int cb = 0; cb < C::CB; ++cb)
+#pragma unroll
+          for (int i = 0; i < 4; ++i) mine[((mb * C::CB + cb) * 4 + i) * 64 + lane] = acc[mb][cb][i];
+        mine[(C::MB * C::CB * 4 + 2 * mb) * 64 + lane] = mref[mb];
+        mine[(C::MB * C::CB * 4 + 2 * mb + 1) * 64 + lane] = lrow[mb];
+      }
+    }
+    lds_barrier();
+    if (tg == 1) return;
+#pragma unroll
+    for (int mb = 0; mb < C::MB; ++mb) {
+      const float m1 = mine[(C::MB * C::CB * 4 + 2 * mb) * 64 + lane];
+      const float l1 = mine[(C::MB * C::CB * 4 + 2 * mb + 1) * 64 + lane];
+      const float mm = fmaxf(mref[mb], m1);
+      const float a0 = mref[mb] == kNegInf ? 0.f : fast_exp2(mref[mb] - mm);
+      const float a1 = m1 == kNegInf ? 0.f : fast_exp2(m1 - mm);
+      lrow[mb] = lrow[mb] * a0 + l1 * a1;
+      mref[mb] = mm;
+      float b0[4], b1[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        b0[i] = __shfl(a0, 4 * lg + i);
+        b1[i] = __shfl(a1, 4 * lg + i);
+      }
+#pragma unroll
+      for (int cb = 0; cb < C::CB; ++cb)
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+          acc[mb][cb][i] = acc[mb][cb][i] * b0[i] + mine[((mb * C::CB + cb) * 4 + i) * 64 + lane] * b1[i];
+    }
+  }
+#pragma unroll
+  for (int mb = 0; mb < C::MB; ++mb) {
+    const float l = lrow[mb];
+    const float lse_v = l > 0.f ? (mref[mb] + fast_log2(l)) * kLn2 : kNegInf;
+    const float inv = l > 0.f ? kscale / l : 0.f;   // fp8 values were accumulated unscaled
+    float iv[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) iv[i] = __shfl(inv, 4 * lg + i);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int r = 16 * mb + 4 * lg + i;
+      if (r >= rows_pg) continue;
+      const int jq = r / hpg, hh = r - jq * hpg;
+      const int head = g * hpg + hh;
+      const int col = c * C::DCW + ln16;
+      if (so.final_out) {
+        const int64_t ob = (int64_t)(row0 + jq) * p.o_sr + (int64_t)head * p.o_sh + col;
+        if (p.out_dt == QMLA_DT_BF16) {
+          __bf16* o = reinterpret_cast<__bf16*>(p.out) + ob;
+#pragma unroll
+          for (int cb = 0; cb < C::CB; ++cb) o[16 * cb] = (__bf16)(acc[mb][cb][i] * iv[i]);
+        } else if (p.out_dt == QMLA_DT_F16) {
+          _Float16* o = reinterpret_cast<_Float16*>(p.out) + ob;
+#pragma unroll
+          for (int cb = 0; cb < C::CB; ++cb) o[16 * cb] = (_Float16)(acc[mb][cb][i] * iv[i]);
+        } else {
+          float* o = reinterpret_cast<float*>(p.out) + ob;
+#pragma unroll
+          for (int cb = 0; cb < C::CB; ++cb) o[16 * cb] = acc[mb][cb][i] * iv[i];
+        }
+      } else {
+        float* ob = so.po + (int64_t)jq * so.po_sr + (int64_t)head * so.po_sh + col;
+#pragma unroll
+        for (int cb = 0; cb < C::CB; ++cb) ob[16 * cb] = acc[mb][cb][i] * iv[i];
+      }
+    }
+    // lse from the score layout (row ln16 + 16mb), one lane per row
+    const int r = ln16 + 16 * mb;
+    if (c == 0 && lg == 0 && r < rows_pg) {
+      const int jq = r / hpg, hh = r - jq * hpg;
+      const int head = g * hpg + hh;
+      if (so.final_out) {
+        if (p.lse) store_out(p.lse, p.lse_dt, (int64_t)(row0 + jq) * p.lse_sr + head, lse_v);
+      } else if (so.plse) {
+        so.plse[(int64_t)jq * so.plse_sr + head] = lse_v;
+      } else {
+        so.po[(int64_t)jq * so.po_sr + (int64_t)head * so.po_sh + C::DCG] = lse_v;
+      }
+    }
+  }
+}
+
+template <class C>
+__global__ __launch_bounds__(C::NTHR, 1) void cs_kernel(const KParams p) {
+  static_assert(sizeof(Smem<C>) <= 163840, "LDS budget of a workgroup");
+  static_assert(C::NTG == 1 || (C::NW / C::NTG) * (C::MB * C::CB * 4 + 2 * C::MB) * 64 * 4 <= C::S * C::NW * C::SB,
+                "token-group merge fits in the ring");
+  __shared__ __attribute__((aligned(16))) Smem<C> sm;
+  // the per-layer scale dequantizes fp8 rows (and e4m3 rms codes); a bf16 cache ignores it, as
+  // the reference does (mla_decode_attention.py:451-463)
+  const float kscale = (C::EB == 1 && p.k_scale) ? *p.k_scale : 1.0f;
+  for_each_segment<C::DCG>(p, [&](int req, int a, int e, int L, const SegOut& so) {
+    segment<C>(p, sm, req, a, e, L, so, kscale);
+    // the next range starts its sub-range set-up with a full barrier; nothing else to reset
+  });
+}
+
+struct Inst {
+  int eb, rms, dcg, g, mb, crm, nthr;
+  bool cap, rtr;
+  void (*fn)(const KParams);
+};
+
+#define QMLA_CS(EB, RMS, DCG, G, NCG, NTG, NTB, MB, S, CRM, CAP, RTR)                                \
+  {EB, RMS, DCG, G, MB, CRM, CS<EB, RMS, DCG, G, NCG, NTG, NTB, MB, S, CRM, CAP, RTR>::NTHR, CAP, RTR, \
+   &cs_kernel<CS<EB, RMS, DCG, G, NCG, NTG, NTB, MB, S, CRM, CAP, RTR>>}
+
+// One entry per compiled shape (rope 64; rows [latent | rope | rms | pad]).
+static const Inst kInst[] = {
+    // bf16 cache, d_c 1792 (the reference's two-pass widths): 8 column slices, 16-token tiles
+    QMLA_CS(2, QMLA_RMS_BF16, 1792, 1, 8, 1, 1, 2, 2, 4, false, true),
+    QMLA_CS(2, QMLA_RMS_NONE, 1792, 1, 8, 1, 1, 2, 2, 0, false, false),
+};
+
+}  // namespace cs
+
+int cs_select(const qmla_decode_params* p) {
+  if (p->rope_w != 64) return -1;
+  const int eb = p->kv_dtype == QMLA_KV_FP8 ? 1 : 2;
+  const int dcg = p->d_c / p->groups;
+  const int hpg = p->heads / p->groups;
+  const int rows_pg = p->qrows * hpg;
+  const bool cap = p->logit_cap > 0.f;
+  const int64_t ts = p->token_stride * eb;
+  for (int i = 0; i < (int)(sizeof(cs::kInst) / sizeof(cs::kInst[0])); ++i) {
+    const cs::Inst& in = cs::kInst[i];
+    if (in.eb != eb || in.rms != p->rms_mode || in.dcg != dcg || in.g != p->groups || in.cap != cap) continue;
+    if (rows_pg > 16 * in.mb) continue;
+    if (in.rtr && (p->qrows != 1 || p->groups != 1)) continue;
+    if ((int64_t)p->d_c * eb + 64 * eb > ts) continue;     // latent + rope inside the row
+    if (in.crm > 0) {
+      const int rb = (p->rms_mode == QMLA_RMS_BF16 || p->rms_mode == QMLA_RMS_BF16_BYTES) ? 2 : 1;
+      const int64_t roff = (int64_t)p->rms_offset * eb;
+      const int need = in.rtr ? 16 * in.mb * rb : p->heads * rb;   // transposed reads cover 16*MB heads
+      if (need > 16 * in.crm || roff % 16 || roff + 16 * in.crm > ts) continue;
+      if (!in.rtr && p->rms_heads * rb > 16 * in.crm) continue;
+    }
+    return i;
+  }
+  return -1;
+}
+
+int cs_launch(int inst, const qmla_decode_params* p, const KParams& k, int nwg, hipStream_t st) {
+  KParams kk = k;
+  void* args[] = {&kk};
+  dim3 grid = p->num_splits > 0 ? dim3(p->num_splits, k.n_req, 1) : dim3(nwg, 1, 1);
+  if (grid.x == 0 || grid.y == 0) return QMLA_OK;
+  hipError_t e = hipLaunchKernel((const void*)cs::kInst[inst].fn, grid, dim3(cs::kInst[inst].nthr, 1, 1), args, 0, st);
+  return e == hipSuccess ? QMLA_OK : QMLA_ERR_LAUNCH;
+}
+
+}  // namespace qmla

@@ -32,8 +32,6 @@
 
 namespace qmla {
 
-constexpr int NWAVE = 4;       // waves per workgroup
-constexpr int NTHR = NWAVE * 64;
 
 // Compile-time shape of one kernel instance.
 //   EB   cache element bytes (1 = fp8 e4m3fn, 2 = bf16)
@@ -49,9 +47,11 @@ constexpr int NTHR = NWAVE * 64;
 //           wave owns a fixed set of MBW row blocks (MSPLIT = MB/MBW wave sets) and TBW token
 //           blocks; its query fragments (B operand) stay in VGPRs for the whole segment.
 //   P.V     each wave owns NCOL latent output columns for all rows of its group.
-template <int EB_, int RMS_, int DCG_, int WP_, int MB_, int G_, int S_, int CPR_, bool CAP_, int TILE_, int WGPC_>
+template <int EB_, int RMS_, int DCG_, int WP_, int MB_, int G_, int S_, int CPR_, bool CAP_, int TILE_, int WGPC_,
+          int NW_>
 struct Cfg {
   static constexpr int EB = EB_, RMS = RMS_, DCG = DCG_, WP = WP_, MB = MB_, G = G_, S = S_;
+  static constexpr int NW = NW_, NTHR = 64 * NW_;   // waves per workgroup
   static constexpr int CPR = CPR_;
   static constexpr bool CAP = CAP_;
   static constexpr int TILE = TILE_, WGPC = WGPC_;
@@ -59,7 +59,7 @@ struct Cfg {
   static constexpr int RB = 16 * CPR;              // LDS row stride (bytes)
   static constexpr int STAGE = TILE * RB;          // bytes per stage
   static constexpr int NTB = TILE / 16;            // 16-token blocks per tile
-  static constexpr int WPG = NWAVE / G;            // waves per group
+  static constexpr int WPG = NW / G;               // waves per group
   // Row blocks are split across waves only when the token blocks alone cannot occupy every wave
   // (two-per-CU 32-token tiles); otherwise each wave scores all row blocks of its own token blocks,
   // so every staged key row is read from LDS and converted exactly once.
@@ -74,9 +74,9 @@ struct Cfg {
   static constexpr int ROWS = 16 * MB;
   static constexpr int PSTRIDE = TILE * 2 + 16;    // bf16 P row stride in LDS (bytes, padded)
   static constexpr int NI = (TILE * CPR + 63) / 64;          // DMA instructions per tile
-  static constexpr int NDMA = (NI + NWAVE - 1) / NWAVE;      // ... per wave (at most)
+  static constexpr int NDMA = (NI + NW - 1) / NW;            // ... per wave (at most)
   static_assert(WP % 64 == 0 && DCG % 64 == 0, "64-column pairs");
-  static_assert(NWAVE % G == 0 && DCG % (16 * WPG) == 0, "column split");
+  static_assert(NW % G == 0 && DCG % (16 * WPG) == 0, "column split");
   static_assert(NTB % WPM == 0 && TBW >= 1, "token-block split");
   static_assert(TILE % 32 == 0 && PLAN_TILE % TILE == 0, "tile");
   static_assert(S >= 2 && CPR >= 16, "ring");
@@ -100,17 +100,17 @@ __device__ __forceinline__ int lds_byte(int r, int b) {
 // DMA instructions wave `wave` issues per tile (instructions i = wave, wave+4, ... < NI)
 template <class C>
 __device__ __forceinline__ constexpr int dma_per_wave(int wave) {
-  return (C::NI - wave + NWAVE - 1) / NWAVE;
+  return (C::NI - wave + C::NW - 1) / C::NW;
 }
 // Steady-state wait for tile t: after data(t) each wave has issued S-2 more tile groups (its
 // data DMAs, plus one page-id DMA for wave 0), so "vmcnt <= that count" means data(t) and
 // everything before it landed.
 template <class C>
 __device__ __forceinline__ void wait_steady(int wave) {
+  // waves issue either ceil(NI/NW) or floor(NI/NW) data DMAs per tile (wave 0 also the page ids)
   if (wave == 0) wait_vmcnt<(C::S - 2) * (dma_per_wave<C>(0) + 1)>();
-  else if (wave == 1) wait_vmcnt<(C::S - 2) * dma_per_wave<C>(1)>();
-  else if (wave == 2) wait_vmcnt<(C::S - 2) * dma_per_wave<C>(2)>();
-  else wait_vmcnt<(C::S - 2) * dma_per_wave<C>(3)>();
+  else if (dma_per_wave<C>(wave) == dma_per_wave<C>(1)) wait_vmcnt<(C::S - 2) * dma_per_wave<C>(1)>();
+  else wait_vmcnt<(C::S - 2) * dma_per_wave<C>(C::NW - 1)>();
 }
 
 template <class C>
@@ -118,10 +118,10 @@ struct Smem {
   char kv[C::S][C::STAGE];
   int pid[2 * C::S][C::TILE];
   char p[C::G][C::ROWS][C::PSTRIDE];
-  float red[2][NWAVE][C::ROWS];   // per-wave row max / row sum of the current tile
+  float red[2][C::NW][C::ROWS];   // per-wave row max / row sum of the current tile
   float alpha[C::G][C::ROWS];     // accumulator rescale of the current tile (when any row moved)
   float fin[2][C::G][C::ROWS];    // final reference max / sum per row (epilogue)
-  int flag[NWAVE];
+  int flag[C::NW];
 };
 
 // Everything a segment needs to know about where its results go.
@@ -167,7 +167,7 @@ __device__ __forceinline__ void process_segment(const KParams& p, Smem<C>& sm, i
   uint32_t doff[C::NDMA];
 #pragma unroll
   for (int j = 0; j < C::NDMA; ++j) {
-    int q = (wave + NWAVE * j) * 64 + lane;
+    int q = (wave + C::NW * j) * 64 + lane;
     q = q < TILE * C::CPR ? q : TILE * C::CPR - 1;
     const int r = q / C::CPR, pp = q - r * C::CPR;
     int c = pp - (r & 15);
@@ -175,7 +175,7 @@ __device__ __forceinline__ void process_segment(const KParams& p, Smem<C>& sm, i
     doff[j] = (uint32_t)(r * C::RB + 16 * c);
   }
   const bool lane_live_last = (C::NI * 64 == TILE * C::CPR) ||
-                              ((wave + NWAVE * (C::NDMA - 1)) * 64 + lane < TILE * C::CPR);
+                              ((wave + C::NW * (C::NDMA - 1)) * 64 + lane < TILE * C::CPR);
   auto issue_pid = [&](int t) {
     int tok = tok_a + t * TILE + lane;
     tok = tok < tok_e ? tok : tok_e - 1;
@@ -193,7 +193,7 @@ __device__ __forceinline__ void process_segment(const KParams& p, Smem<C>& sm, i
       const __amdgpu_buffer_rsrc_t rsrc = make_rsrc(base, (uint32_t)(TILE * C::RB));
 #pragma unroll
       for (int j = 0; j < C::NDMA; ++j) {
-        const int i = wave + NWAVE * j;
+        const int i = wave + C::NW * j;
         if (i < C::NI && (j < C::NDMA - 1 || lane_live_last)) dma16_buf(rsrc, doff[j], dst + i * 1024);
       }
       return;
@@ -205,7 +205,7 @@ __device__ __forceinline__ void process_segment(const KParams& p, Smem<C>& sm, i
     const int off_lo = (int)(uint32_t)off, off_hi = (int)(uint32_t)((uint64_t)off >> 32);
 #pragma unroll
     for (int j = 0; j < C::NDMA; ++j) {
-      const int i = wave + NWAVE * j;
+      const int i = wave + C::NW * j;
       if (i < C::NI) {
         const int tk = (int)(doff[j] / (uint32_t)C::RB), cb = (int)(doff[j] - (uint32_t)tk * C::RB);
         const uint32_t lo = (uint32_t)__shfl(off_lo, tk), hi = (uint32_t)__shfl(off_hi, tk);
@@ -470,7 +470,10 @@ __device__ __forceinline__ void process_segment(const KParams& p, Smem<C>& sm, i
     }
     if (lane == 0) sm.flag[wave] = need_w ? 1 : 0;
     lds_barrier();  // (B)
-    const bool any = (sm.flag[0] | sm.flag[1] | sm.flag[2] | sm.flag[3]) != 0;
+    int anyf = 0;
+#pragma unroll
+    for (int w = 0; w < C::NW; ++w) anyf |= sm.flag[w];
+    const bool any = anyf != 0;
     float alpha[C::MBW];
     if (any) {
 #pragma unroll
@@ -584,7 +587,7 @@ __device__ __forceinline__ void process_segment(const KParams& p, Smem<C>& sm, i
 }
 
 template <class C>
-__global__ __launch_bounds__(NTHR, C::WGPC) void partial_kernel(const KParams p) {
+__global__ __launch_bounds__(C::NTHR, C::WGPC) void partial_kernel(const KParams p) {
   __shared__ __attribute__((aligned(16))) Smem<C> sm;
   // the per-layer scale dequantizes fp8 rows (and e4m3 rms codes); a bf16 cache ignores it, as
   // the reference does (mla_decode_attention.py:451-463)
@@ -638,48 +641,65 @@ __global__ __launch_bounds__(1024) void plan_kernel(const int* seq_lens, int n_r
   }
 }
 
-// LSE-weighted combine, fixed-split mode (mla_decode_attention.py:1064-1137): one wave per
-// (row, head); split bounds recomputed exactly as in the partial pass, empty splits skipped.
-__global__ __launch_bounds__(64) void combine_kernel(const KParams p, int dv) {
+// LSE-weighted combine, fixed-split mode (mla_decode_attention.py:1064-1137): one 256-thread
+// workgroup per (row, head). Split bounds are recomputed exactly as in the partial pass; the live
+// splits are a prefix [0, nl) (a split is empty only when it starts at or past L). Their weights
+// exp(lse_s - M) / sum are formed once in LDS, then every thread streams its output columns over
+// the live splits, four splits per batch of loads. Empty splits are never read.
+constexpr int CF_MAXS = 1024;   // split count limit of the fixed-mode combine
+__global__ __launch_bounds__(256) void combine_kernel(const KParams p, int dv) {
   const int head = blockIdx.x, row = blockIdx.y;   // row = flattened query row
-  const int lane = threadIdx.x;
+  const int tid = threadIdx.x;
   const int req = row / p.qrows;
   const int L = req_len(p, req);
-  const int64_t obase = (int64_t)row * p.o_sr + (int64_t)head * p.o_sh;
-  float m = kNegInf, l = 0.f;
-  float acc[32];
-  const int nper = (dv + 63) / 64;
-#pragma unroll
-  for (int k = 0; k < 32; ++k) acc[k] = 0.f;
+  __shared__ float s_w[CF_MAXS];
+  __shared__ float s_red[2][4];
   int per = (L + p.num_splits - 1) / p.num_splits;
   if (p.split_align > 0) per = (per + p.split_align - 1) / p.split_align * p.split_align;
-  const float* base = p.ws + (int64_t)row * p.ws_sr + (int64_t)head * p.ws_sh;
-  for (int s = 0; s < p.num_splits; ++s) {
-    const int a = per * s, e = a + per < L ? a + per : L;
-    if (e <= a) continue;
-    const float* ps = base + (int64_t)s * p.ws_ss;
-    const float ls = ps[dv];
-    const float mn = fmaxf(m, ls);
-    if (mn == kNegInf) continue;
-    const float sc_old = __expf(m - mn), sc_new = __expf(ls - mn);
-    l = l * sc_old + sc_new;
-#pragma unroll
-    for (int k = 0; k < 32; ++k)
-      if (k < nper) {
-        const int c = lane + 64 * k;
-        acc[k] = acc[k] * sc_old + (c < dv ? ps[c] : 0.f) * sc_new;
-      }
-    m = mn;
+  const int nl = per > 0 ? ((L + per - 1) / per < p.num_splits ? (L + per - 1) / per : p.num_splits) : 0;
+  const int64_t obase = (int64_t)row * p.o_sr + (int64_t)head * p.o_sh;
+  if (nl == 0) {   // empty row: zero output, -inf lse
+    for (int c = tid; c < dv; c += 256) store_out(p.out, p.out_dt, obase + c, 0.f);
+    if (tid == 0 && p.lse) store_out(p.lse, p.lse_dt, (int64_t)row * p.lse_sr + head, kNegInf);
+    return;
   }
+  const float* base = p.ws + (int64_t)row * p.ws_sr + (int64_t)head * p.ws_sh;
+  // split LSEs -> max -> weights
+  float mloc = kNegInf;
+  for (int s = tid; s < nl; s += 256) {
+    const float v = base[(int64_t)s * p.ws_ss + dv];
+    s_w[s] = v;
+    mloc = fmaxf(mloc, v);
+  }
+  for (int o = 32; o > 0; o >>= 1) mloc = fmaxf(mloc, __shfl_xor(mloc, o));
+  if ((tid & 63) == 0) s_red[0][tid >> 6] = mloc;
+  __syncthreads();
+  const float m = fmaxf(fmaxf(s_red[0][0], s_red[0][1]), fmaxf(s_red[0][2], s_red[0][3]));
+  float sloc = 0.f;
+  for (int s = tid; s < nl; s += 256) {
+    const float e = m == kNegInf ? 0.f : __expf(s_w[s] - m);
+    s_w[s] = e;
+    sloc += e;
+  }
+  for (int o = 32; o > 0; o >>= 1) sloc += __shfl_xor(sloc, o);
+  if ((tid & 63) == 0) s_red[1][tid >> 6] = sloc;
+  __syncthreads();
+  const float l = (s_red[1][0] + s_red[1][1]) + (s_red[1][2] + s_red[1][3]);
   const float inv = l > 0.f ? 1.0f / l : 0.f;
+  if (tid == 0 && p.lse) store_out(p.lse, p.lse_dt, (int64_t)row * p.lse_sr + head, l > 0.f ? m + __logf(l) : kNegInf);
+  for (int c = tid; c < dv; c += 256) {
+    float acc = 0.f;
+    int s = 0;
+    for (; s + 4 <= nl; s += 4) {
+      float x[4];
 #pragma unroll
-  for (int k = 0; k < 32; ++k)
-    if (k < nper) {
-      const int c = lane + 64 * k;
-      if (c < dv) store_out(p.out, p.out_dt, obase + c, acc[k] * inv);
+      for (int k = 0; k < 4; ++k) x[k] = base[(int64_t)(s + k) * p.ws_ss + c];
+#pragma unroll
+      for (int k = 0; k < 4; ++k) acc += s_w[s + k] * x[k];
     }
-  if (lane == 0 && p.lse)
-    store_out(p.lse, p.lse_dt, (int64_t)row * p.lse_sr + head, l > 0.f ? m + __logf(l) : kNegInf);
+    for (; s < nl; ++s) acc += s_w[s] * base[(int64_t)s * p.ws_ss + c];
+    store_out(p.out, p.out_dt, obase + c, acc * inv);
+  }
 }
 
 // LSE-weighted combine, balanced mode: one 256-thread workgroup per (query row, block of CH_HB
@@ -784,27 +804,28 @@ typedef void (*PartialFn)(const KParams);
 struct Inst {
   int eb, rms, dcg, wp, mb, g, s, cpr;
   bool cap;
-  int tile, wgpc;
+  int tile, wgpc, nthr;
   PartialFn fn;
 };
 
-#define QMLA_INST(EB, RMS, DCG, WP, MB, G, S, CPR, CAP, TILE, WGPC)                        \
-  {EB, RMS, DCG, WP, MB, G, S, CPR, CAP, TILE, WGPC,                                         \
-   &partial_kernel<Cfg<EB, RMS, DCG, WP, MB, G, S, CPR, CAP, TILE, WGPC>>}
+#define QMLA_INST(EB, RMS, DCG, WP, MB, G, S, CPR, CAP, TILE, WGPC, NW)                    \
+  {EB, RMS, DCG, WP, MB, G, S, CPR, CAP, TILE, WGPC, 64 * NW,                                \
+   &partial_kernel<Cfg<EB, RMS, DCG, WP, MB, G, S, CPR, CAP, TILE, WGPC, NW>>}
 
 // One entry per compiled shape. Rows are [latent | rope | rms | pad]; CPR*16 bytes are staged.
 static const Inst kInst[] = {
     // fp8 e4m3 cache + log8 rms codes, d_c 512, rope 64, up to 32 rows (24 heads): 608 B staged
-    QMLA_INST(1, QMLA_RMS_LOG8, 512, 64, 2, 1, 3, 38, false, 64, 1),
-    QMLA_INST(1, QMLA_RMS_LOG8, 512, 64, 2, 1, 3, 38, true, 64, 1),
-    QMLA_INST(1, QMLA_RMS_BF16_BYTES, 512, 64, 2, 1, 3, 39, false, 64, 1),
-    QMLA_INST(1, QMLA_RMS_E4M3, 512, 64, 2, 1, 3, 38, false, 64, 1),
+    QMLA_INST(1, QMLA_RMS_LOG8, 512, 64, 2, 1, 3, 38, false, 64, 1, 8),
+    QMLA_INST(1, QMLA_RMS_LOG8, 512, 64, 2, 1, 3, 38, false, 64, 1, 4),
+    QMLA_INST(1, QMLA_RMS_LOG8, 512, 64, 2, 1, 3, 38, true, 64, 1, 4),
+    QMLA_INST(1, QMLA_RMS_BF16_BYTES, 512, 64, 2, 1, 3, 39, false, 64, 1, 4),
+    QMLA_INST(1, QMLA_RMS_E4M3, 512, 64, 2, 1, 3, 38, false, 64, 1, 4),
     // bf16 cache, d_c 512, rope 64, 24 heads (rms 24 bf16): 1200 B staged
-    QMLA_INST(2, QMLA_RMS_BF16, 512, 64, 2, 1, 2, 75, false, 64, 1),
-    QMLA_INST(2, QMLA_RMS_BF16, 512, 64, 2, 1, 2, 75, true, 64, 1),
-    QMLA_INST(2, QMLA_RMS_NONE, 512, 64, 2, 1, 2, 72, false, 64, 1),
+    QMLA_INST(2, QMLA_RMS_BF16, 512, 64, 2, 1, 2, 75, false, 64, 1, 4),
+    QMLA_INST(2, QMLA_RMS_BF16, 512, 64, 2, 1, 2, 75, true, 64, 1, 4),
+    QMLA_INST(2, QMLA_RMS_NONE, 512, 64, 2, 1, 2, 72, false, 64, 1, 4),
     // GLA-g2: two latent groups of 256, 12 heads each, 4 verify tokens -> 48 rows per group
-    QMLA_INST(1, QMLA_RMS_LOG8, 256, 64, 3, 2, 3, 38, false, 64, 1),
+    QMLA_INST(1, QMLA_RMS_LOG8, 256, 64, 3, 2, 3, 38, false, 64, 1, 4),
 };
 
 static int g_cu_count[64];
@@ -871,7 +892,7 @@ static int validate(const qmla_decode_params* p) {
   if (p->heads % p->groups || p->d_c % p->groups) return QMLA_ERR_SHAPE;
   if (p->rms_mode != QMLA_RMS_NONE && (p->rms_heads < p->heads / p->groups * p->groups || p->rms_heads <= 0))
     return QMLA_ERR_SHAPE;
-  if (p->num_splits < 0 || p->split_align < 0) return QMLA_ERR_SHAPE;
+  if (p->num_splits < 0 || p->num_splits > CF_MAXS || p->split_align < 0) return QMLA_ERR_SHAPE;
   const int eb = elem_bytes(p->kv_dtype);
   if (!aligned16(p->kv_cache) || (p->page_stride * eb) % 16 || (p->token_stride * eb) % 16) return QMLA_ERR_ALIGN;
   if (needed_row_bytes(p) > p->token_stride * eb && p->page_size > 1) return QMLA_ERR_SHAPE;
@@ -990,8 +1011,8 @@ static int launch(const void* fn, dim3 grid, dim3 block, void** args, hipStream_
 static int run_partial(const qmla_decode_params* p, const Inst* in, KParams& k, hipStream_t st) {
   void* args[] = {&k};
   if (p->num_splits > 0)
-    return launch((const void*)in->fn, dim3(p->num_splits, k.n_req, 1), dim3(NTHR, 1, 1), args, st);
-  return launch((const void*)in->fn, dim3(k.nwg, 1, 1), dim3(NTHR, 1, 1), args, st);
+    return launch((const void*)in->fn, dim3(p->num_splits, k.n_req, 1), dim3(in->nthr, 1, 1), args, st);
+  return launch((const void*)in->fn, dim3(k.nwg, 1, 1), dim3(in->nthr, 1, 1), args, st);
 }
 
 static int run_combine(const qmla_decode_params* p, KParams& k, hipStream_t st) {
@@ -1000,7 +1021,7 @@ static int run_combine(const qmla_decode_params* p, KParams& k, hipStream_t st) 
   if (p->num_splits == 0)
     return launch((const void*)&combine_bal_kernel, dim3((p->heads + CH_HB - 1) / CH_HB, p->rows, 1),
                   dim3(256, 1, 1), args, st);
-  return launch((const void*)&combine_kernel, dim3(p->heads, p->rows, 1), dim3(64, 1, 1), args, st);
+  return launch((const void*)&combine_kernel, dim3(p->heads, p->rows, 1), dim3(256, 1, 1), args, st);
 }
 
 static int run_plan(const qmla_decode_params* p, KParams& k, hipStream_t st) {
@@ -1055,8 +1076,8 @@ int qmla_decode_partial(const qmla_decode_params* p, void* stream) {
   int rc = validate(p);
   if (rc) return rc;
   if (p->d_c / p->groups > 2048) return QMLA_ERR_SHAPE;
-  const Inst* in = find_inst(p);
-  const int wi = in ? -1 : wide_select(p);
+  const int wi = cs_select(p);
+  const Inst* in = wi >= 0 ? nullptr : find_inst(p);
   if (!in && wi < 0) return QMLA_ERR_NOKERNEL;
   if (p->num_splits > 1 && !p->workspace) return QMLA_ERR_WORKSPACE;
   if (p->num_splits == 0) {
@@ -1064,7 +1085,7 @@ int qmla_decode_partial(const qmla_decode_params* p, void* stream) {
     if (rc) return rc;
   }
   KParams k = make_kparams(p);
-  return in ? run_partial(p, in, k, (hipStream_t)stream) : wide_launch(wi, p, k, k.nwg, (hipStream_t)stream);
+  return in ? run_partial(p, in, k, (hipStream_t)stream) : cs_launch(wi, p, k, k.nwg, (hipStream_t)stream);
 }
 
 int qmla_combine(const qmla_decode_params* p, void* stream) {
@@ -1085,14 +1106,14 @@ int qmla_decode(const qmla_decode_params* p, void* stream) {
   int rc = validate(p);
   if (rc) return rc;
   if (p->d_c / p->groups > 2048) return QMLA_ERR_SHAPE;
-  const Inst* in = find_inst(p);
-  const int wi = in ? -1 : wide_select(p);
+  const int wi = cs_select(p);
+  const Inst* in = wi >= 0 ? nullptr : find_inst(p);
   if (!in && wi < 0) return QMLA_ERR_NOKERNEL;
   hipStream_t st = (hipStream_t)stream;
   if (p->num_splits > 0) {
     if (p->num_splits > 1 && !p->workspace) return QMLA_ERR_WORKSPACE;
     KParams k = make_kparams(p);
-    rc = in ? run_partial(p, in, k, st) : wide_launch(wi, p, k, 0, st);
+    rc = in ? run_partial(p, in, k, st) : cs_launch(wi, p, k, 0, st);
     if (rc || p->num_splits == 1) return rc;
     return run_combine(p, k, st);
   }
@@ -1101,7 +1122,7 @@ int qmla_decode(const qmla_decode_params* p, void* stream) {
   KParams k = make_kparams(p);
   rc = run_plan(p, k, st);
   if (rc) return rc;
-  rc = in ? run_partial(p, in, k, st) : wide_launch(wi, p, k, k.nwg, st);
+  rc = in ? run_partial(p, in, k, st) : cs_launch(wi, p, k, k.nwg, st);
   if (rc) return rc;
   return run_combine(p, k, st);
 }
