@@ -30,6 +30,7 @@ COMMON_FLAGS = [
 SOURCES = [
     (CSRC / "qmla_decode.hip", ["-mllvm", "-amdgpu-mfma-vgpr-form"]),
     (CSRC / "qmla_cs.hip", ["-mllvm", "-amdgpu-mfma-vgpr-form"]),
+    (CSRC / "qmla_ws.hip", ["-mllvm", "-amdgpu-mfma-vgpr-form"]),
 ]
 
 

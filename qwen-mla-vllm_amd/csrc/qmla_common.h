@@ -134,6 +134,10 @@ __device__ __forceinline__ void for_each_segment(const KParams& p, F&& f) {
   }
 }
 
+// ---- host-side interface of the warp-specialized translation unit (qmla_ws.hip) ----
+int ws_select(const qmla_decode_params* p);
+int ws_launch(int inst, const qmla_decode_params* p, const KParams& k, int nwg, hipStream_t st);
+
 // ---- host-side interface of the column-split translation unit (qmla_cs.hip) ----
 // Index of a compiled column-split instance for these params, or -1.
 int cs_select(const qmla_decode_params* p);

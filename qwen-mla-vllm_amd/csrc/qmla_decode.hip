@@ -1076,15 +1076,17 @@ int qmla_decode_partial(const qmla_decode_params* p, void* stream) {
   int rc = validate(p);
   if (rc) return rc;
   if (p->d_c / p->groups > 2048) return QMLA_ERR_SHAPE;
-  const int wi = cs_select(p);
-  const Inst* in = wi >= 0 ? nullptr : find_inst(p);
-  if (!in && wi < 0) return QMLA_ERR_NOKERNEL;
+  const int si = ws_select(p);
+  const int wi = si >= 0 ? -1 : cs_select(p);
+  const Inst* in = (si >= 0 || wi >= 0) ? nullptr : find_inst(p);
+  if (!in && wi < 0 && si < 0) return QMLA_ERR_NOKERNEL;
   if (p->num_splits > 1 && !p->workspace) return QMLA_ERR_WORKSPACE;
   if (p->num_splits == 0) {
     rc = check_balanced_ws(p);
     if (rc) return rc;
   }
   KParams k = make_kparams(p);
+  if (si >= 0) return ws_launch(si, p, k, k.nwg, (hipStream_t)stream);
   return in ? run_partial(p, in, k, (hipStream_t)stream) : cs_launch(wi, p, k, k.nwg, (hipStream_t)stream);
 }
 
@@ -1106,14 +1108,15 @@ int qmla_decode(const qmla_decode_params* p, void* stream) {
   int rc = validate(p);
   if (rc) return rc;
   if (p->d_c / p->groups > 2048) return QMLA_ERR_SHAPE;
-  const int wi = cs_select(p);
-  const Inst* in = wi >= 0 ? nullptr : find_inst(p);
-  if (!in && wi < 0) return QMLA_ERR_NOKERNEL;
+  const int si = ws_select(p);
+  const int wi = si >= 0 ? -1 : cs_select(p);
+  const Inst* in = (si >= 0 || wi >= 0) ? nullptr : find_inst(p);
+  if (!in && wi < 0 && si < 0) return QMLA_ERR_NOKERNEL;
   hipStream_t st = (hipStream_t)stream;
   if (p->num_splits > 0) {
     if (p->num_splits > 1 && !p->workspace) return QMLA_ERR_WORKSPACE;
     KParams k = make_kparams(p);
-    rc = in ? run_partial(p, in, k, st) : cs_launch(wi, p, k, 0, st);
+    rc = si >= 0 ? ws_launch(si, p, k, 0, st) : in ? run_partial(p, in, k, st) : cs_launch(wi, p, k, 0, st);
     if (rc || p->num_splits == 1) return rc;
     return run_combine(p, k, st);
   }
@@ -1122,7 +1125,7 @@ int qmla_decode(const qmla_decode_params* p, void* stream) {
   KParams k = make_kparams(p);
   rc = run_plan(p, k, st);
   if (rc) return rc;
-  rc = in ? run_partial(p, in, k, st) : cs_launch(wi, p, k, k.nwg, st);
+  rc = si >= 0 ? ws_launch(si, p, k, k.nwg, st) : in ? run_partial(p, in, k, st) : cs_launch(wi, p, k, k.nwg, st);
   if (rc) return rc;
   return run_combine(p, k, st);
 }
