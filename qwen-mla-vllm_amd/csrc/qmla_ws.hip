@@ -2,29 +2,33 @@
 // query rows per request: 24 heads, one token each).
 //
 // A workgroup owns a contiguous token range of one request and all its query rows (every cached row
-// is read from HBM once per call). Its 8 waves take two roles, one of each on every SIMD:
-//   score waves (0-3): wave (tb, mb) scores 16 tokens x 16 rows over all 576 columns of a 32-token
-//                      tile (S^T = K . Q^T on MFMA, its query fragments resident in VGPRs), divides
-//                      by the rms, applies the mask and the softmax shift, and writes P (bf16) for
-//                      the tile into LDS;
-//   value waves (4-7): wave v accumulates P . V over latent columns [128v, 128v+128) for all rows,
-//                      one tile behind the score waves, with V^T fragments read by ds_read_b64_tr_b8.
-// So on every SIMD an MFMA+conversion-heavy score step of tile t+1 runs beside the MFMA P.V step of
-// tile t, and the workgroup meets once per tile at a single barrier (P double-buffered in LDS).
-// Rows stream global -> LDS by LDS-DMA through a deep ring (a tile is reused by the value waves one
-// step after the score waves), issued by all 8 waves, each waiting only for its own loads.
+// is read from HBM once per call). Its 12 waves take three roles, one of each on every SIMD:
+//   DMA waves (8-11):   stream 32-token tiles of cache rows global -> LDS by LDS-DMA, A tiles ahead
+//                       of the score waves, into a ring of A+3 stages; each waits only for its own
+//                       loads, so no computing wave ever stalls on the memory pipeline;
+//   score waves (0-3):  wave (tb, mb) scores 16 tokens x 16 rows over all 576 columns of a tile
+//                       (S^T = K . Q^T on MFMA, query fragments resident in VGPRs), divides by the
+//                       rms, applies the mask and the softmax shift, and writes P (bf16) into LDS;
+//   value waves (4-7):  wave v accumulates P . V over latent columns [128v, 128v+128) for all rows,
+//                       two tiles behind the score waves, with V^T fragments from ds_read_b64_tr_b8.
+// The workgroup meets once per tile at one barrier. Inside a step a wave issues all its LDS reads at
+// once and waits for them in order with counted lgkmcnt waits, so the MFMAs start as soon as the
+// first rows arrive.
 //
 // Softmax: every row keeps one reference max shared by its two score waves. P = exp2(s - ref) is
-// written optimistically; if some row's tile max exceeds its reference by more than SHIFT (or the
-// row had none yet), the workgroup takes a rare extra step: the score waves agree on the new
-// reference, rewrite P, and publish the factor by which the value waves rescale their accumulators
-// before they use the tile.
+// written optimistically. One step later, when the barrier has made both halves' tile maxima
+// visible, the score waves check whether some row's tile max exceeds its reference by more than
+// SHIFT (or the row had none yet); if so they agree on the new reference, rewrite that tile's P and
+// publish the factor by which the value waves rescale their accumulators before they use the tile
+// (which they do one step later still, so the check needs no barrier of its own).
 //
 // Reference semantics: qwen_mla/ops/mla_decode_attention.py:297-586 (stage 1: tile loop, fp8
 // dequant :451-463, rms divide :466-507, softmax :553-560, partial store :562-586).
 
 #include <hip/hip_runtime.h>
 #include <stdint.h>
+
+#include <type_traits>
 
 #include "qmla.h"
 #include "qmla_common.h"
@@ -33,58 +37,91 @@
 namespace qmla {
 namespace ws {
 
-constexpr int NW = 8, NTHR = 512;
 constexpr int TILE = 32;          // tokens per tile
 constexpr int PIDN = 512;         // page ids staged per sub-range
 constexpr float SHIFT = 16.0f;    // P <= 2^16 before the reference max moves
+enum Role { SCORE, VALUE, DMA };
 
-__device__ __forceinline__ i32x4 ldsr128(const char* p) {
+__device__ __forceinline__ i32x4 ldsr128(const void* p) {
   i32x4 r;
-  asm volatile("ds_read_b128 %0, %1" : "=v"(r) : "v"(lds_addr(p)));
+  asm volatile("ds_read_b128 %0, %1" : "=v"(r) : "v"(lds_addr(static_cast<const char*>(p))));
   return r;
 }
-__device__ __forceinline__ uint32_t ldsr8(const char* p) {
-  uint32_t r;
-  asm volatile("ds_read_u8 %0, %1" : "=v"(r) : "v"(lds_addr(p)));
+__device__ __forceinline__ i32x2 ldsr64(const void* p) {
+  i32x2 r;
+  asm volatile("ds_read_b64 %0, %1" : "=v"(r) : "v"(lds_addr(static_cast<const char*>(p))));
   return r;
 }
-__device__ __forceinline__ uint32_t ldsr16(const char* p) {
-  uint32_t r;
-  asm volatile("ds_read_u16 %0, %1" : "=v"(r) : "v"(lds_addr(p)));
+__device__ __forceinline__ float ldsr32f(const void* p) {
+  float r;
+  asm volatile("ds_read_b32 %0, %1" : "=v"(r) : "v"(lds_addr(static_cast<const char*>(p))));
   return r;
+}
+__device__ __forceinline__ uint32_t ldsr8(const void* p) {
+  uint32_t r;
+  asm volatile("ds_read_u8 %0, %1" : "=v"(r) : "v"(lds_addr(static_cast<const char*>(p))));
+  return r;
+}
+__device__ __forceinline__ uint32_t ldsr16(const void* p) {
+  uint32_t r;
+  asm volatile("ds_read_u16 %0, %1" : "=v"(r) : "v"(lds_addr(static_cast<const char*>(p))));
+  return r;
+}
+
+// Wait until at most N of this wave's LDS operations are outstanding; LDS operations complete in
+// issue order, so with N = the number issued after the one producing v, v is ready (more younger
+// operations than counted only make the wait longer). The register tie orders v's uses after it.
+template <int N, class T>
+__device__ __forceinline__ void lds_wait_n(T& v) {
+  static_assert(N >= 0 && N <= 15, "lgkmcnt range");
+  asm volatile("s_waitcnt lgkmcnt(%1)" : "+v"(v) : "n"(N));
+}
+constexpr int cmin15(int n) { return n < 15 ? n : 15; }
+
+template <int I, int N, class F>
+__device__ __forceinline__ void static_for(F&& f) {
+  if constexpr (I < N) {
+    f(std::integral_constant<int, I>{});
+    static_for<I + 1, N>(f);
+  }
 }
 
 // Compile-time shape: EB cache element bytes (1 fp8, 2 bf16), RMS tail format, DCG latent columns,
-// S ring stages, CPR 16-byte chunks staged per row, CAP tanh logit cap, RTR rms codes read
-// transposed (query rows are the heads of one token).
-template <int EB_, int RMS_, int DCG_, int S_, int CPR_, bool CAP_, bool RTR_>
+// A tiles in flight ahead of the score waves, CPR 16-byte chunks staged per row, CAP tanh logit
+// cap, RTR rms codes read transposed (query rows are the heads of one token), DW dedicated DMA
+// waves (12 waves; else the value waves issue the DMA after their step: 8 waves).
+template <int EB_, int RMS_, int DCG_, int A_, int CPR_, bool CAP_, bool RTR_, bool DW_>
 struct WS {
-  static constexpr int EB = EB_, RMS = RMS_, DCG = DCG_, S = S_, CPR = CPR_;
-  static constexpr bool CAP = CAP_, RTR = RTR_;
+  static constexpr int EB = EB_, RMS = RMS_, DCG = DCG_, A = A_, S = A_ + 3, CPR = CPR_;
+  static constexpr bool CAP = CAP_, RTR = RTR_, DW = DW_;
+  static constexpr int NW = DW ? 12 : 8, NTHR = 64 * NW;
   static constexpr int RB = 16 * CPR;                 // staged row bytes
   static constexpr int STAGE = TILE * RB;
   static constexpr int NCH = TILE * CPR;              // 16-byte chunks per tile
   static constexpr int NI = (NCH + 63) / 64;          // DMA instructions per tile
-  static constexpr int DPW = (NI + NW - 1) / NW;      // ... per wave (at most)
+  static constexpr int DPW = (NI + 3) / 4;            // ... per DMA wave (at most)
   static constexpr int KQ = (DCG + 64) / 32;          // k-steps of the score product (latent + rope 64)
   static constexpr int KP = KQ / 2;                   // 64-column pairs
   static constexpr int VC = DCG / 4;                  // latent columns per value wave
   static constexpr int CB = VC / 16;
   static constexpr int RMS_EB = (RMS == QMLA_RMS_BF16 || RMS == QMLA_RMS_BF16_BYTES) ? 2 : 1;
+  static constexpr int NCODE = RMS == QMLA_RMS_NONE ? 0 : (RTR && RMS_EB == 1) ? 1 : 4;   // rms reads
+  static constexpr int NKR = KP * EB;                 // K reads of a score step
+  static constexpr int NVR = CB * EB;                 // V reads of a value step
   static constexpr int PST = TILE * 2 + 16;           // P row stride in LDS (bytes)
   static_assert(DCG % 64 == 0 && CPR * 16 >= (DCG + 64) * EB, "row slice");
-  static_assert(S >= 4 && (S - 3) * (DPW + 1) < 64, "ring depth / vmcnt range");
+  static_assert(A >= 2 && A * DPW < 64, "lookahead / vmcnt range");
 };
 
 template <class C>
 struct Smem {
   char kv[C::S][C::STAGE];
-  char p[2][32][C::PST];        // P (bf16) of a tile, double-buffered
-  float tmax[2][2][32];         // [parity][score token block][row] tile max
-  float alpha[2][32];           // [parity][row] accumulator rescale of the rare step
-  int flag[2][4];               // [parity][score wave]
-  float fin[2][2][32];          // epilogue: [max, sum][token block][row]
-  int pid[PIDN];
+  alignas(16) char p[3][32][C::PST];   // P (bf16) of tiles t % 3
+  alignas(16) int flag[3][4];          // [t % 3][row block]: reference moved at tile t
+  alignas(16) float tmax[2][2][32];    // [t & 1][token block][row] tile max
+  alignas(16) float alpha[3][32];      // [t % 3][row] accumulator rescale at tile t
+  alignas(16) float fin[2][2][32];     // epilogue: [max, sum][token block][row]
+  alignas(16) int pid[PIDN];
 };
 
 // rotated row layout: chunk c of staged row r at position (c + (r & 15)) mod CPR
@@ -98,35 +135,34 @@ __device__ __forceinline__ int lbyte(int r, int b) {
   return r * (16 * CPR) + 16 * rot<CPR>(b >> 4, r) + (b & 15);
 }
 
-// DMA instructions wave w issues per tile (instructions w, w+8, ... < NI)
+// DMA instructions DMA wave d issues per tile (instructions d, d+4, ... < NI)
 template <class C>
-__device__ __forceinline__ constexpr int dpw(int w) { return (C::NI - w + NW - 1) / NW; }
+__device__ __forceinline__ constexpr int dpw(int d) { return (C::NI - d + 3) / 4; }
 
-// wait until this wave's loads of tile t landed: at most `ahead` later tiles of its loads remain
-template <class C>
-__device__ __forceinline__ void wait_own(int w, int ahead) {
-  if (ahead <= 0) { wait_vmcnt<0>(); return; }
-  const bool big = dpw<C>(w) == dpw<C>(0);
-  if (ahead >= C::S - 3) {
-    if (big) wait_vmcnt<(C::S - 3) * dpw<C>(0)>();
-    else wait_vmcnt<(C::S - 3) * dpw<C>(NW - 1)>();
+// vmcnt <= ahead * D (ahead tiles of D loads each issued after the awaited one), ahead <= K
+template <int D, int K>
+__device__ __forceinline__ void wait_tiles(int ahead) {
+  if constexpr (K <= 0 || D == 0) {
+    wait_vmcnt<0>();
   } else {
-    wait_vmcnt<0>();   // short tail: drain
+    if (ahead >= K) wait_vmcnt<K * D>();
+    else wait_tiles<D, K - 1>(ahead);
   }
 }
 
 // One contiguous token range [ta, te) of request `req` (length L), all query rows, seen from one
-// role. Both roles run the same sub-range / tile / barrier sequence; only the work between the
-// barriers differs, so each role keeps only its own registers live (score waves the query
-// fragments, value waves the accumulators).
-template <class C, bool SCORER>
+// role. All roles run the same sub-range / tile / barrier sequence; only the work between the
+// barriers differs, so each role keeps only its own registers live.
+template <class C, int ROLE>
 __device__ __forceinline__ void segment_role(const KParams& p, Smem<C>& sm, int req, int ta, int te, int L,
                                              const SegOut& so, float kscale) {
+  constexpr bool ISSUER = ROLE == DMA || (ROLE == VALUE && !C::DW);
+  constexpr int NTHR = C::NTHR;
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int tb = (w >> 1) & 1, smb = w & 1;   // score wave: token block, row block
-  const int vw = w & 3;                        // value wave: column slice
+  const int vw = w & 3;                        // value wave: column slice; DMA wave: instruction lane
   const int ln16 = lane & 15, lg = lane >> 4;
   const int qrows = p.qrows, hpg = p.hpg;
   const int nrows = qrows * hpg;
@@ -134,14 +170,16 @@ __device__ __forceinline__ void segment_role(const KParams& p, Smem<C>& sm, int 
   const int P = p.page_size;
   const int* btrow = p.bt + (int64_t)row0 * p.bt_stride;
   const float c2 = p.sm_scale * kscale * kLog2e;
+  const int r = 16 * smb + ln16;   // score wave: the lane's row
 
-  // ---- score wave: query fragments for rows 16*smb + ln16 (pair jj, lane group lg: columns
-  //      64jj + 16lg .. +16 of [latent | rope]); row limit and rms byte offset ----
-  bf16x8 qf[SCORER ? C::KQ : 1];
+  // ---- score wave: query fragments for row r (pair jj, lane group lg: columns 64jj + 16lg .. +16
+  //      of [latent | rope]); row limit and rms byte offset; softmax state ----
+  bf16x8 qf[ROLE == SCORE ? C::KQ : 1];
   int lim = 0, rms_b = 0;
   float mref = kNegInf, lpart = 0.f;
-  if constexpr (SCORER) {
-    const int r = 16 * smb + ln16;
+  float tmp = kNegInf, ps_pend = 0.f;    // own max and optimistic sum of the last scored tile
+  f32x4 scp = {0.f, 0.f, 0.f, 0.f};      // its scores (log2 domain, masked)
+  if constexpr (ROLE == SCORE) {
     const bool ok = r < nrows;
     const int jq = ok ? r / hpg : 0, h = ok ? r - jq * hpg : 0;
     const int lr = L - (qrows - 1 - jq);
@@ -159,28 +197,62 @@ __device__ __forceinline__ void segment_role(const KParams& p, Smem<C>& sm, int 
     }
   }
   // ---- value wave: accumulator of rows (16mb + 4lg + i) x columns VC*vw + 16cb + ln16 ----
-  f32x4 acc[2][SCORER ? 1 : C::CB];
-  if constexpr (!SCORER) {
+  f32x4 acc[2][ROLE == VALUE ? C::CB : 1];
+  if constexpr (ROLE == VALUE) {
 #pragma unroll
     for (int mb = 0; mb < 2; ++mb)
 #pragma unroll
       for (int cb = 0; cb < C::CB; ++cb) acc[mb][cb] = f32x4{0.f, 0.f, 0.f, 0.f};
   }
-
-  // DMA sources: instruction i = w + 8j covers LDS chunks 64i .. 64i+63 of a stage: staged row
-  // q / CPR, position q % CPR, i.e. row chunk (position - (row & 15)) mod CPR
-  uint32_t doff[C::DPW];
-  int drow[C::DPW];
+  // ---- DMA wave: instruction i = vw + 4j covers LDS chunks 64i .. 64i+63 of a stage: staged row
+  //      q / CPR, position q % CPR, i.e. row chunk (position - (row & 15)) mod CPR ----
+  constexpr int ND = ISSUER ? C::DPW : 1;
+  uint32_t doff[ND];
+  int drow[ND];
+  if constexpr (ISSUER) {
 #pragma unroll
-  for (int j = 0; j < C::DPW; ++j) {
-    int q = (w + NW * j) * 64 + lane;
-    q = q < C::NCH ? q : C::NCH - 1;
-    const int r = q / C::CPR, pp = q - r * C::CPR;
-    int c = pp - (r & 15);
-    c = c < 0 ? c + C::CPR : c;
-    doff[j] = (uint32_t)(r * C::RB + 16 * c);
-    drow[j] = r;
+    for (int j = 0; j < ND; ++j) {
+      int q = (vw + 4 * j) * 64 + lane;
+      q = q < C::NCH ? q : C::NCH - 1;
+      const int rr = q / C::CPR, pp = q - rr * C::CPR;
+      int c = pp - (rr & 15);
+      c = c < 0 ? c + C::CPR : c;
+      doff[j] = (uint32_t)(rr * C::RB + 16 * c);
+      drow[j] = rr;
+    }
   }
+  const bool big = dpw<C>(vw) == C::DPW;
+
+  // score step of tile t: fix tile t-1 against the partner's max (if t >= 1), then score tile t
+  auto fix_decide = [&](float tpart, bool& rare, float& alpha_f, bf16x4& pk_fix) {
+    const float gm = fmaxf(tmp, tpart);
+    const bool ch = gm > mref + SHIFT;
+    rare = __builtin_amdgcn_ballot_w64(ch) != 0;
+    if (!rare) {
+      lpart += ps_pend;
+      return;
+    }
+    const float mn = ch ? gm : mref;
+    alpha_f = ch ? (mref == kNegInf ? 0.f : fast_exp2(mref - mn)) : 1.0f;
+    mref = mn;
+    const float mu = mref == kNegInf ? 0.f : mref;
+    float ps2 = 0.f;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const float e = fast_exp2(scp[i] - mu);
+      ps2 += e;
+      pk_fix[i] = (__bf16)e;
+    }
+    lpart = lpart * alpha_f + ps2;
+  };
+  auto fix_publish = [&](int t, bool rare, float alpha_f, const bf16x4& pk_fix) {
+    const int pt = t % 3;
+    if (rare) {
+      *reinterpret_cast<bf16x4*>(&sm.p[pt][r][(16 * tb + 4 * lg) * 2]) = pk_fix;
+      if (tb == 0 && lg == 0) sm.alpha[pt][r] = alpha_f;
+    }
+    if (tb == 0 && lane == 0) sm.flag[pt][smb] = rare ? 1 : 0;
+  };
 
   int sub = (PIDN - 1) * P;
   sub = sub < TILE ? TILE : sub / TILE * TILE;
@@ -195,9 +267,9 @@ __device__ __forceinline__ void segment_role(const KParams& p, Smem<C>& sm, int 
     const int nt = (se - sa + TILE - 1) / TILE;
     const bool contig = p.token_stride_b == C::RB;
 
-    // issue cursor: tiles are issued in order, so the page of the next tile is tracked
+    // DMA issue cursor: tiles are issued in order, so the page of the next tile is tracked
     // incrementally (no divisions in the tile loop)
-    int ipg = sa / P - pbase, ioff = sa % P;   // page index (staged) and offset of tile `inext`
+    int ipg = sa / P - pbase, ioff = sa % P;
     auto issue = [&](int t) {
       const int tok0 = sa + t * TILE;
       const int nvalid = se - tok0 < TILE ? se - tok0 : TILE;
@@ -208,15 +280,15 @@ __device__ __forceinline__ void segment_role(const KParams& p, Smem<C>& sm, int 
         const char* base = p.kv + (int64_t)pg * p.page_stride_b + (int64_t)ioff * p.token_stride_b;
         const __amdgpu_buffer_rsrc_t rs = make_rsrc(base, (uint32_t)(nvalid * C::RB));
 #pragma unroll
-        for (int j = 0; j < C::DPW; ++j) {
-          const int i = w + NW * j;
+        for (int j = 0; j < ND; ++j) {
+          const int i = vw + 4 * j;
           if (i < C::NI && (i * 64 + 64 <= C::NCH || i * 64 + lane < C::NCH)) dma16_buf(rs, doff[j], dst + i * 1024);
         }
       } else {
         // per-lane page lookup; rows past the range end repeat the last row
 #pragma unroll
-        for (int j = 0; j < C::DPW; ++j) {
-          const int i = w + NW * j;
+        for (int j = 0; j < ND; ++j) {
+          const int i = vw + 4 * j;
           if (i < C::NI && (i * 64 + 64 <= C::NCH || i * 64 + lane < C::NCH)) {
             const int rr = drow[j] < nvalid ? drow[j] : nvalid - 1;
             const int tok = tok0 + rr;
@@ -234,26 +306,50 @@ __device__ __forceinline__ void segment_role(const KParams& p, Smem<C>& sm, int 
         ++ipg;
       }
     };
+    // wait until tile t landed, with tiles t+1 .. last issued after it
+    auto wait_tile = [&](int t, int last) {
+      const int ahead = last - t;
+      if (big) wait_tiles<C::DPW, C::A - 1>(ahead);
+      else wait_tiles<(C::NI % 4 == 0 ? C::DPW : C::DPW - 1), C::A - 1>(ahead);
+    };
 
-    // prologue: tiles 0 .. S-3 in flight, tile 0 landed everywhere
-    for (int t = 0; t < C::S - 2 && t < nt; ++t) issue(t);
-    wait_own<C>(w, nt - 1 < C::S - 3 ? nt - 1 : C::S - 3);
+    // prologue: tiles 0 .. A-1 in flight, tile 0 landed
+    if constexpr (ISSUER) {
+      for (int t = 0; t < C::A && t < nt; ++t) issue(t);
+      wait_tile(0, (C::A < nt ? C::A : nt) - 1);
+    }
     lds_barrier();
 
-    // iteration it: score waves take tile it, value waves tile it-1; one barrier per iteration
-    // (two when the reference max of some row moves)
+    // iteration it: DMA waves issue tile it+A and wait for tile it+1; score waves fix tile it-1 and
+    // score tile it; value waves take tile it-2
 #pragma clang loop unroll(disable)
-    for (int it = 0; it <= nt; ++it) {
-      if (it + C::S - 2 < nt) issue(it + C::S - 2);
-      const int par = it & 1;
-      const int ahead = nt - 1 - (it + 1) < C::S - 3 ? nt - 1 - (it + 1) : C::S - 3;
-      if constexpr (SCORER) {
+    for (int it = 0; it <= nt + 1; ++it) {
+      if constexpr (ROLE == DMA) {
+        if (it + C::A < nt) issue(it + C::A);
+        if (it + 1 < nt) wait_tile(it + 1, it + C::A < nt - 1 ? it + C::A : nt - 1);
+      } else if constexpr (ROLE == SCORE) {
         if (it < nt) {
           const char* kvs = sm.kv[it % C::S];
           const int tok0 = sa + it * TILE;
-          // ---- scores for tokens tok0 + 16tb + (4lg + i), rows 16smb + ln16 ----
+          // ---- LDS reads, in this order: partner max of tile it-1, rms codes, K rows ----
+          float tpart = ldsr32f(&sm.tmax[(it + 1) & 1][tb ^ 1][r]);   // unused at it == 0
           const int krow = 16 * tb + ln16;
           const char* rowp = kvs + krow * C::RB;
+          uint32_t code[4] = {0u, 0u, 0u, 0u};
+          i32x2 craw = {0, 0};
+          if constexpr (C::RMS != QMLA_RMS_NONE) {
+            if constexpr (C::RTR && C::RMS_EB == 1) {
+              // tr_b8: lanes 2r', 2r'+1 of block lg supply token row 16tb + 4lg + (r' & 3); lane n gets head 16smb + n
+              const int rr = 16 * tb + 4 * lg + ((ln16 >> 1) & 3);
+              craw = lds_read_tr8_async(kvs + lbyte<C::CPR>(rr, p.rms_off_b + 16 * smb + 8 * (ln16 & 1)));
+            } else {
+#pragma unroll
+              for (int i = 0; i < 4; ++i) {
+                const char* a = kvs + lbyte<C::CPR>(16 * tb + 4 * lg + i, rms_b);
+                code[i] = C::RMS_EB == 1 ? ldsr8(a) : ldsr16(a);
+              }
+            }
+          }
           i32x4 kr0[C::KP], kr1[C::EB == 2 ? C::KP : 1];
 #pragma unroll
           for (int jj = 0; jj < C::KP; ++jj) {
@@ -261,44 +357,42 @@ __device__ __forceinline__ void segment_role(const KParams& p, Smem<C>& sm, int 
             kr0[jj] = ldsr128(rowp + 16 * rot<C::CPR>(cbyte >> 4, krow));
             if constexpr (C::EB == 2) kr1[jj] = ldsr128(rowp + 16 * rot<C::CPR>((cbyte >> 4) + 1, krow));
           }
-          // rms codes of the lane's 4 tokens
-          uint32_t code[4];
-          if constexpr (C::RMS != QMLA_RMS_NONE) {
-            if constexpr (C::RTR && C::RMS_EB == 1) {
-              // tr_b8: lanes 2r, 2r+1 of block lg supply token row 16tb + 4lg + (r & 3); lane n gets head 16smb + n
-              const int rr = 16 * tb + 4 * lg + ((ln16 >> 1) & 3);
-              i32x2 raw = lds_read_tr8_async(kvs + lbyte<C::CPR>(rr, p.rms_off_b + 16 * smb + 8 * (ln16 & 1)));
-              lds_wait(raw);
-#pragma unroll
-              for (int i = 0; i < 4; ++i) code[i] = ((uint32_t)raw[0] >> (8 * i)) & 0xFF;
-            } else {
-#pragma unroll
-              for (int i = 0; i < 4; ++i) {
-                const char* a = kvs + lbyte<C::CPR>(16 * tb + 4 * lg + i, rms_b);
-                code[i] = C::RMS_EB == 1 ? ldsr8(a) : ldsr16(a);
-              }
-#pragma unroll
-              for (int i = 0; i < 4; ++i) lds_wait(code[i]);
-            }
-          }
+          // ---- reference check of tile it-1 (its writes follow the score product) ----
+          lds_wait_n<cmin15(C::NCODE + C::NKR)>(tpart);
+          bool rare = false;
+          float alpha_f = 1.0f;
+          bf16x4 pk_fix;
+          if (it >= 1) fix_decide(tpart, rare, alpha_f, pk_fix);
+          // ---- S^T = K . Q^T as the K rows arrive ----
           f32x4 s2a = f32x4{0.f, 0.f, 0.f, 0.f}, s2b = s2a;
-#pragma unroll
-          for (int jj = 0; jj < C::KP; ++jj) {
-            lds_wait(kr0[jj]);
+          static_for<0, C::KP>([&](auto jc) {
+            constexpr int jj = decltype(jc)::value;
             bf16x8 ka, kb;
             if constexpr (C::EB == 1) {
+              lds_wait_n<cmin15(C::KP - 1 - jj)>(kr0[jj]);
               fp8x16_to_bf16(kr0[jj], ka, kb);
             } else {
-              lds_wait(kr1[jj]);
+              lds_wait_n<cmin15(2 * (C::KP - 1 - jj) + 1)>(kr0[jj]);
+              lds_wait_n<cmin15(2 * (C::KP - 1 - jj))>(kr1[jj]);
               ka = __builtin_bit_cast(bf16x8, kr0[jj]);
               kb = __builtin_bit_cast(bf16x8, kr1[jj]);
             }
-            if (jj & 1) {
+            if constexpr (jj & 1) {
               s2b = mfma16(ka, qf[2 * jj], s2b);
               s2b = mfma16(kb, qf[2 * jj + 1], s2b);
             } else {
               s2a = mfma16(ka, qf[2 * jj], s2a);
               s2a = mfma16(kb, qf[2 * jj + 1], s2a);
+            }
+          });
+          if constexpr (C::RMS != QMLA_RMS_NONE) {
+            if constexpr (C::RTR && C::RMS_EB == 1) {
+              lds_wait_n<0>(craw);   // landed before the K rows
+#pragma unroll
+              for (int i = 0; i < 4; ++i) code[i] = ((uint32_t)craw[0] >> (8 * i)) & 0xFF;
+            } else {
+#pragma unroll
+              for (int i = 0; i < 4; ++i) lds_wait_n<0>(code[i]);
             }
           }
           f32x4 sc = s2a + s2b;
@@ -329,7 +423,7 @@ __device__ __forceinline__ void segment_role(const KParams& p, Smem<C>& sm, int 
             tm = fmaxf(tm, v);
           }
           tm = max_lg(tm);
-          // ---- optimistic P against the current reference; the rare step fixes it ----
+          // ---- optimistic P against the current reference ----
           const float mu = mref == kNegInf ? 0.f : mref;
           bf16x4 pk;
           float ps = 0.f;
@@ -339,49 +433,31 @@ __device__ __forceinline__ void segment_role(const KParams& p, Smem<C>& sm, int 
             ps += e;
             pk[i] = (__bf16)e;
           }
-          *reinterpret_cast<bf16x4*>(&sm.p[par][16 * smb + ln16][(16 * tb + 4 * lg) * 2]) = pk;
-          if (lg == 0) sm.tmax[par][tb][16 * smb + ln16] = tm;
-          const bool any = __builtin_amdgcn_ballot_w64(tm > mref + SHIFT) != 0;
-          if (lane == 0) sm.flag[par][w] = any ? 1 : 0;
-          wait_own<C>(w, ahead);
-          lds_barrier();
-          const bool rare = (sm.flag[par][0] | sm.flag[par][1] | sm.flag[par][2] | sm.flag[par][3]) != 0;
-          if (!rare) {
-            lpart += ps;
-          } else {
-            const int r = 16 * smb + ln16;
-            const float gm = fmaxf(sm.tmax[par][0][r], sm.tmax[par][1][r]);
-            const float mn = gm > mref + SHIFT ? gm : mref;
-            const float alpha = mref == kNegInf ? 0.f : fast_exp2(mref - mn);
-            mref = mn;
-            const float mu2 = mref == kNegInf ? 0.f : mref;
-            bf16x4 pk2;
-            float ps2 = 0.f;
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-              const float e = fast_exp2(sc[i] - mu2);
-              ps2 += e;
-              pk2[i] = (__bf16)e;
-            }
-            lpart = lpart * alpha + ps2;
-            *reinterpret_cast<bf16x4*>(&sm.p[par][r][(16 * tb + 4 * lg) * 2]) = pk2;
-            if (tb == 0 && lg == 0) sm.alpha[par][r] = alpha;
-            lds_barrier();
-          }
-        } else {
-          // no tile left for the score waves: meet the value waves (no rare step at it == nt)
-          wait_own<C>(w, ahead);
-          lds_barrier();
+          *reinterpret_cast<bf16x4*>(&sm.p[it % 3][r][(16 * tb + 4 * lg) * 2]) = pk;
+          if (lg == 0) sm.tmax[it & 1][tb][r] = tm;
+          if (it >= 1) fix_publish(it - 1, rare, alpha_f, pk_fix);
+          scp = sc;
+          tmp = tm;
+          ps_pend = ps;
+        } else if (it == nt && nt >= 1) {
+          // reference check of the last tile
+          float tpart = ldsr32f(&sm.tmax[(it + 1) & 1][tb ^ 1][r]);
+          lds_wait_n<0>(tpart);
+          bool rare = false;
+          float alpha_f = 1.0f;
+          bf16x4 pk_fix;
+          fix_decide(tpart, rare, alpha_f, pk_fix);
+          fix_publish(it - 1, rare, alpha_f, pk_fix);
         }
       } else {
-        if (it >= 1) {
-          // ---- P . V for tile it-1 over columns VC*vw .. +VC ----
-          const int pv = (it - 1) & 1;
-          const char* kvs = sm.kv[(it - 1) % C::S];
-          bf16x8 pf[2];
+        if (it >= 2) {
+          // ---- P . V for tile j = it-2 over columns VC*vw .. +VC ----
+          const int j = it - 2, pj = j % 3;
+          const char* kvs = sm.kv[j % C::S];
+          i32x2 fl = ldsr64(&sm.flag[pj][0]);
+          i32x4 pr[2];
 #pragma unroll
-          for (int mb = 0; mb < 2; ++mb)
-            pf[mb] = __builtin_bit_cast(bf16x8, ldsr128(&sm.p[pv][16 * mb + ln16][(8 * lg) * 2]));
+          for (int mb = 0; mb < 2; ++mb) pr[mb] = ldsr128(&sm.p[pj][16 * mb + ln16][(8 * lg) * 2]);
           i32x2 vraw[C::CB][C::EB];
 #pragma unroll
           for (int cb = 0; cb < C::CB; ++cb) {
@@ -396,64 +472,72 @@ __device__ __forceinline__ void segment_role(const KParams& p, Smem<C>& sm, int 
               vraw[cb][C::EB - 1] = lds_read_tr16_async(kvs + lbyte<C::CPR>(vr + 4, vb));
             }
           }
-          lds_wait(pf[0], pf[1]);
+          lds_wait_n<cmin15(2 + C::NVR)>(fl);
+          const int f0 = __builtin_amdgcn_readfirstlane(fl[0]), f1 = __builtin_amdgcn_readfirstlane(fl[1]);
+          if (f0 | f1) {
+            // the reference of some row moved at tile j: rescale before adding it
+            i32x4 a0 = ldsr128(&sm.alpha[pj][4 * lg]), a1 = ldsr128(&sm.alpha[pj][16 + 4 * lg]);
+            lds_wait_n<0>(a0);
+            lds_wait_n<0>(a1);
+            const f32x4 al[2] = {__builtin_bit_cast(f32x4, a0), __builtin_bit_cast(f32x4, a1)};
 #pragma unroll
-          for (int cb = 0; cb < C::CB; ++cb) {
-            i32x2 c0 = vraw[cb][0], c1 = vraw[cb][C::EB - 1];
-            if constexpr (C::EB == 1) lds_wait(c0);
-            else lds_wait(c0, c1);
+            for (int mb = 0; mb < 2; ++mb) {
+              if ((mb == 0 ? f0 : f1) == 0) continue;
+#pragma unroll
+              for (int i = 0; i < 4; ++i)
+#pragma unroll
+                for (int cb = 0; cb < C::CB; ++cb) acc[mb][cb][i] *= al[mb][i];
+            }
+          }
+          lds_wait_n<cmin15(C::NVR)>(pr[0]);
+          lds_wait_n<cmin15(C::NVR)>(pr[1]);
+          const bf16x8 pf[2] = {__builtin_bit_cast(bf16x8, pr[0]), __builtin_bit_cast(bf16x8, pr[1])};
+          static_for<0, C::CB>([&](auto cc) {
+            constexpr int cb = decltype(cc)::value;
             bf16x8 vf;
             if constexpr (C::EB == 1) {
-              vf = fp8x8_to_bf16(c0);
+              lds_wait_n<cmin15(C::CB - 1 - cb)>(vraw[cb][0]);
+              vf = fp8x8_to_bf16(vraw[cb][0]);
             } else {
-              const i32x4 w4 = {c0[0], c0[1], c1[0], c1[1]};
+              lds_wait_n<cmin15(2 * (C::CB - 1 - cb) + 1)>(vraw[cb][0]);
+              lds_wait_n<cmin15(2 * (C::CB - 1 - cb))>(vraw[cb][1]);
+              const i32x4 w4 = {vraw[cb][0][0], vraw[cb][0][1], vraw[cb][1][0], vraw[cb][1][1]};
               vf = __builtin_bit_cast(bf16x8, w4);
             }
 #pragma unroll
             for (int mb = 0; mb < 2; ++mb) acc[mb][cb] = mfma16(pf[mb], vf, acc[mb][cb]);
-          }
+          });
         }
-        wait_own<C>(w, ahead);
-        lds_barrier();
-        if (it < nt) {
-          const bool rare = (sm.flag[par][0] | sm.flag[par][1] | sm.flag[par][2] | sm.flag[par][3]) != 0;
-          if (rare) {
-            lds_barrier();   // the score waves published the rescale of tile it
-#pragma unroll
-            for (int mb = 0; mb < 2; ++mb)
-#pragma unroll
-              for (int i = 0; i < 4; ++i) {
-                const float a = sm.alpha[par][16 * mb + 4 * lg + i];
-#pragma unroll
-                for (int cb = 0; cb < C::CB; ++cb) acc[mb][cb][i] *= a;
-              }
-          }
+        if constexpr (ISSUER) {
+          if (it + C::A < nt) issue(it + C::A);
+          if (it + 1 < nt) wait_tile(it + 1, it + C::A < nt - 1 ? it + C::A : nt - 1);
         }
       }
+      lds_barrier();
     }
   }
   wait_vmcnt<0>();
 
   // ---- epilogue: score waves publish (reference max, sum) per row and token block; value waves
   //      normalize their columns and write the output (final or partial) and natural-log lse ----
-  if constexpr (SCORER) {
+  if constexpr (ROLE == SCORE) {
     const float l = sum_lg(lpart);
     if (lg == 0) {
-      sm.fin[0][tb][16 * smb + ln16] = mref;
-      sm.fin[1][tb][16 * smb + ln16] = l;
+      sm.fin[0][tb][r] = mref;
+      sm.fin[1][tb][r] = l;
     }
   }
   lds_barrier();
-  if constexpr (!SCORER) {
+  if constexpr (ROLE == VALUE) {
 #pragma unroll
     for (int mb = 0; mb < 2; ++mb)
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        const int r = 16 * mb + 4 * lg + i;
-        if (r >= nrows) continue;
-        const float m = sm.fin[0][0][r];
-        const float l = sm.fin[1][0][r] + sm.fin[1][1][r];
-        const int jq = r / hpg, h = r - jq * hpg;
+        const int rr = 16 * mb + 4 * lg + i;
+        if (rr >= nrows) continue;
+        const float m = sm.fin[0][0][rr];
+        const float l = sm.fin[1][0][rr] + sm.fin[1][1][rr];
+        const int jq = rr / hpg, h = rr - jq * hpg;
         const float inv = l > 0.f ? kscale / l : 0.f;   // fp8 values were accumulated unscaled
         const float lse_v = l > 0.f ? (m + fast_log2(l)) * kLn2 : kNegInf;
         const int col = C::VC * vw + ln16;
@@ -479,12 +563,14 @@ __device__ __forceinline__ void segment_role(const KParams& p, Smem<C>& sm, int 
 template <class C>
 __device__ __forceinline__ void segment(const KParams& p, Smem<C>& sm, int req, int ta, int te, int L,
                                         const SegOut& so, float kscale) {
-  if (__builtin_amdgcn_readfirstlane(threadIdx.x >> 6) < 4) segment_role<C, true>(p, sm, req, ta, te, L, so, kscale);
-  else segment_role<C, false>(p, sm, req, ta, te, L, so, kscale);
+  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  if (w < 4) segment_role<C, SCORE>(p, sm, req, ta, te, L, so, kscale);
+  else if (!C::DW || w < 8) segment_role<C, VALUE>(p, sm, req, ta, te, L, so, kscale);
+  else if constexpr (C::DW) segment_role<C, DMA>(p, sm, req, ta, te, L, so, kscale);
 }
 
 template <class C>
-__global__ __launch_bounds__(NTHR, 1) void ws_kernel(const KParams p) {
+__global__ __launch_bounds__(C::NTHR, 1) void ws_kernel(const KParams p) {
   static_assert(sizeof(Smem<C>) <= 163840, "LDS budget of a workgroup");
   __shared__ __attribute__((aligned(16))) Smem<C> sm;
   const float kscale = (C::EB == 1 && p.k_scale) ? *p.k_scale : 1.0f;
@@ -496,16 +582,19 @@ __global__ __launch_bounds__(NTHR, 1) void ws_kernel(const KParams p) {
 struct Inst {
   int eb, rms, dcg, cpr;
   bool cap, rtr;
+  int nthr;
   void (*fn)(const KParams);
 };
 
-#define QMLA_WS(EB, RMS, DCG, S, CPR, CAP, RTR) \
-  {EB, RMS, DCG, CPR, CAP, RTR, &ws_kernel<WS<EB, RMS, DCG, S, CPR, CAP, RTR>>}
+#define QMLA_WS(EB, RMS, DCG, A, CPR, CAP, RTR, DW) \
+  {EB, RMS, DCG, CPR, CAP, RTR, WS<EB, RMS, DCG, A, CPR, CAP, RTR, DW>::NTHR, &ws_kernel<WS<EB, RMS, DCG, A, CPR, CAP, RTR, DW>>}
 
 static const Inst kInst[] = {
-    // fp8 e4m3 + log8 codes, d_c 512, rope 64, 24 heads: 608-byte rows, 6-stage ring of 32-token tiles
-    QMLA_WS(1, QMLA_RMS_LOG8, 512, 6, 38, false, true),
-    QMLA_WS(1, QMLA_RMS_LOG8, 512, 6, 38, false, false),
+    // fp8 e4m3 + log8 codes, d_c 512, rope 64, 24 heads: 608-byte rows, 32-token tiles 3 ahead (6 stages)
+    QMLA_WS(1, QMLA_RMS_LOG8, 512, 3, 38, false, true, false),
+    QMLA_WS(1, QMLA_RMS_LOG8, 512, 3, 38, false, false, false),
+    // ... up to 16 heads (592-byte rows), rms codes read per row
+    QMLA_WS(1, QMLA_RMS_LOG8, 512, 3, 37, false, false, false),
 };
 
 }  // namespace ws
@@ -537,7 +626,7 @@ int ws_launch(int inst, const qmla_decode_params* p, const KParams& k, int nwg, 
   void* args[] = {&kk};
   dim3 grid = p->num_splits > 0 ? dim3(p->num_splits, k.n_req, 1) : dim3(nwg, 1, 1);
   if (grid.x == 0 || grid.y == 0) return QMLA_OK;
-  hipError_t e = hipLaunchKernel((const void*)ws::kInst[inst].fn, grid, dim3(ws::NTHR, 1, 1), args, 0, st);
+  hipError_t e = hipLaunchKernel((const void*)ws::kInst[inst].fn, grid, dim3(ws::kInst[inst].nthr, 1, 1), args, 0, st);
   return e == hipSuccess ? QMLA_OK : QMLA_ERR_LAUNCH;
 }
 

@@ -1,0 +1,79 @@
+"""GPU parity of the FP8 + log8 decode shapes served by the warp-specialized kernel (d_c 512, rope 64,
+one latent group, at most 32 query rows per request) against the CPU oracle: verify rows read
+per-row rms codes, pages that tiles straddle, and a context whose score maximum keeps climbing, so
+that the softmax reference moves at many tiles (reference: ops/mla_decode_attention.py:297-586).
+
+Tolerance: max-abs 3e-2 on the output (fp8 cache) beyond the output's own bf16 rounding, lse 1e-2.
+"""
+import pytest
+import torch
+
+from tests.mla_cases import make_case, run_oracle
+
+pytestmark = pytest.mark.gpu
+
+TOL = 3e-2
+REL = 2.0 ** -7
+
+
+def _check(name, c, o, lse):
+    ro, rl = run_oracle(c)
+    d = (o.float().cpu() - ro).abs()
+    excess = (d - REL * ro.abs()).max().item()
+    lg = lse.float().cpu()
+    empty = torch.isneginf(rl)   # rows that see no token: lse -inf and a zero output
+    assert torch.equal(torch.isneginf(lg), empty)
+    lerr = (lg[~empty] - rl[~empty]).abs().max().item()
+    print(f"[{name}] max-abs {d.max().item():.3e} (beyond bf16 rounding {excess:.3e}, tol {TOL}) lse {lerr:.3e}",
+          flush=True)
+    assert excess < TOL and lerr < 1e-2
+
+
+def _forward(c, **kw):
+    import qmla
+    o, lse = qmla.forward(c.q_nope, c.q_pe, c.cache, c.block_table, c.seq_lens, page_size=c.page_size,
+                          sm_scale=c.sm_scale, kv_fp8=True, fp8_rms="log8", k_scale=c.k_scale, qrows=c.qrows, **kw)
+    torch.cuda.synchronize()
+    return o, lse
+
+
+@pytest.mark.parametrize("qrows,heads", [(4, 8), (2, 16)])
+def test_ws_verify_rows(gpu, qrows, heads):
+    """Causal verify rows (row j of a request sees L - (qrows-1-j) tokens), rms codes per row."""
+    lens = [3, 700, 64, 2049, 130]
+    c = make_case(batch=len(lens), heads=heads, d_c=512, rope_w=64, page_size=64, lens=lens, kv="fp8",
+                  rms_mode="log8", seed=11, device=gpu, qrows=qrows, rms="spread")
+    o, lse = _forward(c, num_workgroups=7)
+    _check(f"verify q{qrows} h{heads}", c, o, lse)
+
+
+@pytest.mark.parametrize("page_size", [40, 16, 1])
+def test_ws_straddling_pages(gpu, page_size):
+    """Page sizes that are not multiples of the 32-token tile: tiles gather rows from several pages."""
+    lens = [1000, 77, 333] if page_size > 1 else [300, 45]
+    c = make_case(batch=len(lens), heads=24, d_c=512, rope_w=64, page_size=page_size, lens=lens, kv="fp8",
+                  rms_mode="log8", seed=12, device=gpu, rms="spread")
+    o, lse = _forward(c, num_workgroups=4)
+    _check(f"pages P={page_size}", c, o, lse)
+
+
+def test_ws_climbing_max(gpu):
+    """rms codes fall from 255 to 0 along each request, so the divisor shrinks 64x and the score
+    maximum climbs through the whole context: the reference max moves at many tiles."""
+    lens = [4096, 1500, 5000]
+    P = 64
+    c = make_case(batch=len(lens), heads=24, d_c=512, rope_w=64, page_size=P, lens=lens, kv="fp8",
+                  rms_mode="log8", seed=13, device=gpu, rms="spread", q_amp=3.0)
+    cb = c.cache.view(torch.uint8).view(c.cache.shape[0], P, -1)
+    bt = c.block_table.cpu()
+    for b, L in enumerate(lens):
+        t = torch.arange(L)
+        code = (255 - torch.round(255.0 * t.float() / max(L - 1, 1))).to(torch.uint8)
+        pages = bt[b, t // P].long()
+        slots = t % P
+        cb[pages.to(gpu), slots.to(gpu), c.rms_offset:c.rms_offset + 24] = code.to(gpu)[:, None]
+    o, lse = _forward(c, num_workgroups=6)
+    _check("climbing max", c, o, lse)
+    # the same through fixed splits
+    o2, lse2 = _forward(c, num_splits=5)
+    _check("climbing max, 5 splits", c, o2, lse2)
