@@ -2,18 +2,21 @@
 // query rows per request: 24 heads, one token each).
 //
 // A workgroup owns a contiguous token range of one request and all its query rows (every cached row
-// is read from HBM once per call). Its 12 waves take three roles, one of each on every SIMD:
-//   DMA waves (8-11):   stream 32-token tiles of cache rows global -> LDS by LDS-DMA, A tiles ahead
-//                       of the score waves, into a ring of A+3 stages; each waits only for its own
-//                       loads, so no computing wave ever stalls on the memory pipeline;
+// is read from HBM once per call). Its 8 waves take two roles, one of each on every SIMD:
 //   score waves (0-3):  wave (tb, mb) scores 16 tokens x 16 rows over all 576 columns of a tile
 //                       (S^T = K . Q^T on MFMA, query fragments resident in VGPRs), divides by the
-//                       rms, applies the mask and the softmax shift, and writes P (bf16) into LDS;
+//                       rms, applies the mask and the softmax shift, and writes P (bf16) into LDS.
+//                       With an fp8 cache the K bytes enter the MFMA as stored: the query is split
+//                       into two e4m3 parts (hi + lo, 8 significant bits, as bf16), the latent runs
+//                       on the 16x16x128 fp8 MFMA and the rope on the 16x16x32 one;
 //   value waves (4-7):  wave v accumulates P . V over latent columns [128v, 128v+128) for all rows,
-//                       two tiles behind the score waves, with V^T fragments from ds_read_b64_tr_b8.
-// The workgroup meets once per tile at one barrier. Inside a step a wave issues all its LDS reads at
-// once and waits for them in order with counted lgkmcnt waits, so the MFMAs start as soon as the
-// first rows arrive.
+//                       two tiles behind the score waves, with V^T fragments from ds_read_b64_tr_b8,
+//                       and streams 32-token tiles of cache rows global -> LDS by LDS-DMA, A tiles
+//                       ahead of the score waves, into a ring of A+3 stages (each value wave waits
+//                       only for its own loads). The score waves never touch the memory pipeline.
+// (Other placements of the DMA are compile-time options, see WS::ISS.) The workgroup meets once per
+// tile at one barrier. Inside a step a wave issues all its LDS reads at once and waits for them in
+// order with counted lgkmcnt waits, so the MFMAs start as soon as the first rows arrive.
 //
 // Softmax: every row keeps one reference max shared by its two score waves. P = exp2(s - ref) is
 // written optimistically. One step later, when the barrier has made both halves' tile maxima
@@ -88,18 +91,22 @@ __device__ __forceinline__ void static_for(F&& f) {
 
 // Compile-time shape: EB cache element bytes (1 fp8, 2 bf16), RMS tail format, DCG latent columns,
 // A tiles in flight ahead of the score waves, CPR 16-byte chunks staged per row, CAP tanh logit
-// cap, RTR rms codes read transposed (query rows are the heads of one token), DW dedicated DMA
-// waves (12 waves; else the value waves issue the DMA after their step: 8 waves).
-template <int EB_, int RMS_, int DCG_, int A_, int CPR_, bool CAP_, bool RTR_, bool DW_>
+// cap, RTR rms codes read transposed (query rows are the heads of one token), ISS who issues the
+// DMA: 0 the value waves after their step, 1 the value waves before their step, 2 all 8 waves (score
+// waves after their step, value waves before theirs), 3 four dedicated DMA waves (12 waves).
+template <int EB_, int RMS_, int DCG_, int A_, int CPR_, bool CAP_, bool RTR_, int ISS_>
 struct WS {
   static constexpr int EB = EB_, RMS = RMS_, DCG = DCG_, A = A_, S = A_ + 3, CPR = CPR_;
-  static constexpr bool CAP = CAP_, RTR = RTR_, DW = DW_;
+  static constexpr bool CAP = CAP_, RTR = RTR_;
+  static constexpr int ISS = ISS_;
+  static constexpr bool DW = ISS == 3;
   static constexpr int NW = DW ? 12 : 8, NTHR = 64 * NW;
+  static constexpr int NIW = ISS == 2 ? 8 : 4;        // waves sharing the DMA instructions of a tile
   static constexpr int RB = 16 * CPR;                 // staged row bytes
   static constexpr int STAGE = TILE * RB;
   static constexpr int NCH = TILE * CPR;              // 16-byte chunks per tile
   static constexpr int NI = (NCH + 63) / 64;          // DMA instructions per tile
-  static constexpr int DPW = (NI + 3) / 4;            // ... per DMA wave (at most)
+  static constexpr int DPW = (NI + NIW - 1) / NIW;    // ... per issuing wave (at most)
   static constexpr int KQ = (DCG + 64) / 32;          // k-steps of the score product (latent + rope 64)
   static constexpr int KP = KQ / 2;                   // 64-column pairs
   static constexpr int VC = DCG / 4;                  // latent columns per value wave
@@ -111,6 +118,7 @@ struct WS {
   static constexpr int PST = TILE * 2 + 16;           // P row stride in LDS (bytes)
   static_assert(DCG % 64 == 0 && CPR * 16 >= (DCG + 64) * EB, "row slice");
   static_assert(A >= 2 && A * DPW < 64, "lookahead / vmcnt range");
+  static_assert(EB == 2 || DCG % 128 == 0, "fp8 latent in 128-column MFMA blocks");
 };
 
 template <class C>
@@ -135,9 +143,9 @@ __device__ __forceinline__ int lbyte(int r, int b) {
   return r * (16 * CPR) + 16 * rot<CPR>(b >> 4, r) + (b & 15);
 }
 
-// DMA instructions DMA wave d issues per tile (instructions d, d+4, ... < NI)
+// DMA instructions issuing wave d issues per tile (instructions d, d+NIW, ... < NI)
 template <class C>
-__device__ __forceinline__ constexpr int dpw(int d) { return (C::NI - d + 3) / 4; }
+__device__ __forceinline__ constexpr int dpw(int d) { return (C::NI - d + C::NIW - 1) / C::NIW; }
 
 // vmcnt <= ahead * D (ahead tiles of D loads each issued after the awaited one), ahead <= K
 template <int D, int K>
@@ -156,25 +164,35 @@ __device__ __forceinline__ void wait_tiles(int ahead) {
 template <class C, int ROLE>
 __device__ __forceinline__ void segment_role(const KParams& p, Smem<C>& sm, int req, int ta, int te, int L,
                                              const SegOut& so, float kscale) {
-  constexpr bool ISSUER = ROLE == DMA || (ROLE == VALUE && !C::DW);
+  constexpr bool ISSUER = ROLE == DMA || (ROLE == VALUE && !C::DW) || (ROLE == SCORE && C::ISS == 2);
   constexpr int NTHR = C::NTHR;
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int tb = (w >> 1) & 1, smb = w & 1;   // score wave: token block, row block
-  const int vw = w & 3;                        // value wave: column slice; DMA wave: instruction lane
+  const int vw = w & 3;                        // value wave: column slice
+  const int dw = C::NIW == 8 ? w : (w & 3);    // issuing wave: first DMA instruction of a tile
   const int ln16 = lane & 15, lg = lane >> 4;
   const int qrows = p.qrows, hpg = p.hpg;
   const int nrows = qrows * hpg;
   const int row0 = req * qrows;
   const int P = p.page_size;
   const int* btrow = p.bt + (int64_t)row0 * p.bt_stride;
-  const float c2 = p.sm_scale * kscale * kLog2e;
+  float c2 = p.sm_scale * kscale * kLog2e;
   const int r = 16 * smb + ln16;   // score wave: the lane's row
 
   // ---- score wave: query fragments for row r (pair jj, lane group lg: columns 64jj + 16lg .. +16
   //      of [latent | rope]); row limit and rms byte offset; softmax state ----
-  bf16x8 qf[ROLE == SCORE ? C::KQ : 1];
+  // fp8 cache: the query enters the fp8 MFMAs as two e4m3 parts (q * qs = hi + lo, qs a power of two
+  // per row folded into the score scale), so the K bytes are used as stored: the latent in 128-column
+  // blocks on v_mfma_scale_f32_16x16x128_f8f6f4 (lane group lg holds columns 128b + 32lg .. +32),
+  // the rope on 16x16x32 fp8 (lane group lg holds rope columns 16lg .. +16). bf16 cache: bf16 MFMA.
+  constexpr bool F8 = C::EB == 1;
+  constexpr int NB = C::DCG / 128;       // latent blocks of the fp8 product
+  constexpr bool QS = ROLE == SCORE;
+  bf16x8 qf[!F8 && QS ? C::KQ : 1];
+  i32x8 qh8[F8 && QS ? NB : 1], ql8[F8 && QS ? NB : 1];
+  long qhr[2], qlr[2];
   int lim = 0, rms_b = 0;
   float mref = kNegInf, lpart = 0.f;
   float tmp = kNegInf, ps_pend = 0.f;    // own max and optimistic sum of the last scored tile
@@ -187,13 +205,67 @@ __device__ __forceinline__ void segment_role(const KParams& p, Smem<C>& sm, int 
     rms_b = p.rms_off_b + h * C::RMS_EB;
     const __bf16* qn = p.q_nope + (int64_t)(row0 + jq) * p.qn_sr + (int64_t)h * p.qn_sh;
     const __bf16* qp = p.q_pe + (int64_t)(row0 + jq) * p.qp_sr + (int64_t)h * p.qp_sh;
+    bf16x8 qv[C::KQ];
 #pragma unroll
     for (int k = 0; k < C::KQ; ++k) {
-      const int col = 64 * (k >> 1) + 16 * lg + 8 * (k & 1);
+      const int col = !F8 ? 64 * (k >> 1) + 16 * lg + 8 * (k & 1)
+                          : k < 4 * NB ? 128 * (k >> 2) + 32 * lg + 8 * (k & 3) : C::DCG + 16 * lg + 8 * (k - 4 * NB);
       bf16x8 v = col < C::DCG ? *reinterpret_cast<const bf16x8*>(qn + col)
                               : *reinterpret_cast<const bf16x8*>(qp + (col - C::DCG));
       if (!ok) v = bf16x8{};
-      qf[k] = v;
+      qv[k] = v;
+    }
+    if constexpr (F8) {
+      float mx = 0.f;
+#pragma unroll
+      for (int k = 0; k < C::KQ; ++k)
+#pragma unroll
+        for (int e = 0; e < 8; ++e) mx = fmaxf(mx, fabsf((float)qv[k][e]));
+      mx = max_lg(mx);
+      // |q| * qs in (112, 448]: e4m3 keeps 4 significant bits in hi and 4 more in lo
+      const float ex = mx > 0.f ? fminf(floorf(fast_log2(224.0f / mx)), 126.0f) : 0.0f;
+      const float qs = fast_exp2(ex);
+      c2 = c2 * fast_exp2(-ex);
+      int hq[2 * C::KQ], lq[2 * C::KQ];
+#pragma unroll
+      for (int k = 0; k < C::KQ; ++k) {
+        int h[2], l[2];
+#pragma unroll
+        for (int hw = 0; hw < 2; ++hw) {
+          float v[4], rsd[4];
+#pragma unroll
+          for (int e = 0; e < 4; ++e) v[e] = (float)qv[k][4 * hw + e] * qs;
+          int hb = __builtin_amdgcn_cvt_pk_fp8_f32(v[0], v[1], 0, false);
+          hb = __builtin_amdgcn_cvt_pk_fp8_f32(v[2], v[3], hb, true);
+          rsd[0] = v[0] - __builtin_amdgcn_cvt_f32_fp8(hb, 0);
+          rsd[1] = v[1] - __builtin_amdgcn_cvt_f32_fp8(hb, 1);
+          rsd[2] = v[2] - __builtin_amdgcn_cvt_f32_fp8(hb, 2);
+          rsd[3] = v[3] - __builtin_amdgcn_cvt_f32_fp8(hb, 3);
+          int lb = __builtin_amdgcn_cvt_pk_fp8_f32(rsd[0], rsd[1], 0, false);
+          lb = __builtin_amdgcn_cvt_pk_fp8_f32(rsd[2], rsd[3], lb, true);
+          h[hw] = hb;
+          l[hw] = lb;
+        }
+        hq[2 * k] = h[0];
+        hq[2 * k + 1] = h[1];
+        lq[2 * k] = l[0];
+        lq[2 * k + 1] = l[1];
+      }
+#pragma unroll
+      for (int b = 0; b < NB; ++b)
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          qh8[b][e] = hq[8 * b + e];
+          ql8[b][e] = lq[8 * b + e];
+        }
+#pragma unroll
+      for (int t = 0; t < 2; ++t) {
+        qhr[t] = __builtin_bit_cast(long, i32x2{hq[8 * NB + 2 * t], hq[8 * NB + 2 * t + 1]});
+        qlr[t] = __builtin_bit_cast(long, i32x2{lq[8 * NB + 2 * t], lq[8 * NB + 2 * t + 1]});
+      }
+    } else {
+#pragma unroll
+      for (int k = 0; k < C::KQ; ++k) qf[k] = qv[k];
     }
   }
   // ---- value wave: accumulator of rows (16mb + 4lg + i) x columns VC*vw + 16cb + ln16 ----
@@ -212,7 +284,7 @@ __device__ __forceinline__ void segment_role(const KParams& p, Smem<C>& sm, int 
   if constexpr (ISSUER) {
 #pragma unroll
     for (int j = 0; j < ND; ++j) {
-      int q = (vw + 4 * j) * 64 + lane;
+      int q = (dw + C::NIW * j) * 64 + lane;
       q = q < C::NCH ? q : C::NCH - 1;
       const int rr = q / C::CPR, pp = q - rr * C::CPR;
       int c = pp - (rr & 15);
@@ -221,7 +293,7 @@ __device__ __forceinline__ void segment_role(const KParams& p, Smem<C>& sm, int 
       drow[j] = rr;
     }
   }
-  const bool big = dpw<C>(vw) == C::DPW;
+  const bool big = dpw<C>(dw) == C::DPW;
 
   // score step of tile t: fix tile t-1 against the partner's max (if t >= 1), then score tile t
   auto fix_decide = [&](float tpart, bool& rare, float& alpha_f, bf16x4& pk_fix) {
@@ -281,14 +353,14 @@ __device__ __forceinline__ void segment_role(const KParams& p, Smem<C>& sm, int 
         const __amdgpu_buffer_rsrc_t rs = make_rsrc(base, (uint32_t)(nvalid * C::RB));
 #pragma unroll
         for (int j = 0; j < ND; ++j) {
-          const int i = vw + 4 * j;
+          const int i = dw + C::NIW * j;
           if (i < C::NI && (i * 64 + 64 <= C::NCH || i * 64 + lane < C::NCH)) dma16_buf(rs, doff[j], dst + i * 1024);
         }
       } else {
         // per-lane page lookup; rows past the range end repeat the last row
 #pragma unroll
         for (int j = 0; j < ND; ++j) {
-          const int i = vw + 4 * j;
+          const int i = dw + C::NIW * j;
           if (i < C::NI && (i * 64 + 64 <= C::NCH || i * 64 + lane < C::NCH)) {
             const int rr = drow[j] < nvalid ? drow[j] : nvalid - 1;
             const int tok = tok0 + rr;
@@ -310,7 +382,7 @@ __device__ __forceinline__ void segment_role(const KParams& p, Smem<C>& sm, int 
     auto wait_tile = [&](int t, int last) {
       const int ahead = last - t;
       if (big) wait_tiles<C::DPW, C::A - 1>(ahead);
-      else wait_tiles<(C::NI % 4 == 0 ? C::DPW : C::DPW - 1), C::A - 1>(ahead);
+      else wait_tiles<(C::NI % C::NIW == 0 ? C::DPW : C::DPW - 1), C::A - 1>(ahead);
     };
 
     // prologue: tiles 0 .. A-1 in flight, tile 0 landed
@@ -354,7 +426,8 @@ __device__ __forceinline__ void segment_role(const KParams& p, Smem<C>& sm, int 
 #pragma unroll
           for (int jj = 0; jj < C::KP; ++jj) {
             const int cbyte = (64 * jj + 16 * lg) * C::EB;
-            kr0[jj] = ldsr128(rowp + 16 * rot<C::CPR>(cbyte >> 4, krow));
+            const int ch = !F8 ? cbyte >> 4 : jj < 2 * NB ? 8 * (jj >> 1) + 2 * lg + (jj & 1) : C::DCG / 16 + lg;
+            kr0[jj] = ldsr128(rowp + 16 * rot<C::CPR>(ch, krow));
             if constexpr (C::EB == 2) kr1[jj] = ldsr128(rowp + 16 * rot<C::CPR>((cbyte >> 4) + 1, krow));
           }
           // ---- reference check of tile it-1 (its writes follow the score product) ----
@@ -364,25 +437,39 @@ __device__ __forceinline__ void segment_role(const KParams& p, Smem<C>& sm, int 
           bf16x4 pk_fix;
           if (it >= 1) fix_decide(tpart, rare, alpha_f, pk_fix);
           // ---- S^T = K . Q^T as the K rows arrive ----
-          f32x4 s2a = f32x4{0.f, 0.f, 0.f, 0.f}, s2b = s2a;
+          f32x4 s2a = f32x4{0.f, 0.f, 0.f, 0.f}, s2b = s2a, s2c = s2a, s2d = s2a;
           static_for<0, C::KP>([&](auto jc) {
             constexpr int jj = decltype(jc)::value;
-            bf16x8 ka, kb;
-            if constexpr (C::EB == 1) {
-              lds_wait_n<cmin15(C::KP - 1 - jj)>(kr0[jj]);
-              fp8x16_to_bf16(kr0[jj], ka, kb);
+            if constexpr (F8) {
+              if constexpr (jj < 2 * NB && (jj & 1)) {
+                // latent block jj/2: 32 bytes per lane from reads jj-1, jj
+                lds_wait_n<cmin15(C::KP - 1 - jj)>(kr0[jj]);
+                lds_wait_n<cmin15(C::KP - jj)>(kr0[jj - 1]);
+                const i32x8 ka = {kr0[jj - 1][0], kr0[jj - 1][1], kr0[jj - 1][2], kr0[jj - 1][3],
+                                  kr0[jj][0], kr0[jj][1], kr0[jj][2], kr0[jj][3]};
+                s2a = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(ka, qh8[jj >> 1], s2a, 0, 0, 0, 127, 0, 127);
+                s2b = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(ka, ql8[jj >> 1], s2b, 0, 0, 0, 127, 0, 127);
+              } else if constexpr (jj == 2 * NB) {
+                lds_wait_n<cmin15(C::KP - 1 - jj)>(kr0[jj]);
+                const long k0 = __builtin_bit_cast(long, i32x2{kr0[jj][0], kr0[jj][1]});
+                const long k1 = __builtin_bit_cast(long, i32x2{kr0[jj][2], kr0[jj][3]});
+                s2c = __builtin_amdgcn_mfma_f32_16x16x32_fp8_fp8(k0, qhr[0], s2c, 0, 0, 0);
+                s2d = __builtin_amdgcn_mfma_f32_16x16x32_fp8_fp8(k0, qlr[0], s2d, 0, 0, 0);
+                s2c = __builtin_amdgcn_mfma_f32_16x16x32_fp8_fp8(k1, qhr[1], s2c, 0, 0, 0);
+                s2d = __builtin_amdgcn_mfma_f32_16x16x32_fp8_fp8(k1, qlr[1], s2d, 0, 0, 0);
+              }
             } else {
               lds_wait_n<cmin15(2 * (C::KP - 1 - jj) + 1)>(kr0[jj]);
               lds_wait_n<cmin15(2 * (C::KP - 1 - jj))>(kr1[jj]);
-              ka = __builtin_bit_cast(bf16x8, kr0[jj]);
-              kb = __builtin_bit_cast(bf16x8, kr1[jj]);
-            }
-            if constexpr (jj & 1) {
-              s2b = mfma16(ka, qf[2 * jj], s2b);
-              s2b = mfma16(kb, qf[2 * jj + 1], s2b);
-            } else {
-              s2a = mfma16(ka, qf[2 * jj], s2a);
-              s2a = mfma16(kb, qf[2 * jj + 1], s2a);
+              const bf16x8 ka = __builtin_bit_cast(bf16x8, kr0[jj]);
+              const bf16x8 kb = __builtin_bit_cast(bf16x8, kr1[jj]);
+              if constexpr (jj & 1) {
+                s2b = mfma16(ka, qf[2 * jj], s2b);
+                s2b = mfma16(kb, qf[2 * jj + 1], s2b);
+              } else {
+                s2a = mfma16(ka, qf[2 * jj], s2a);
+                s2a = mfma16(kb, qf[2 * jj + 1], s2a);
+              }
             }
           });
           if constexpr (C::RMS != QMLA_RMS_NONE) {
@@ -395,7 +482,7 @@ __device__ __forceinline__ void segment_role(const KParams& p, Smem<C>& sm, int 
               for (int i = 0; i < 4; ++i) lds_wait_n<0>(code[i]);
             }
           }
-          f32x4 sc = s2a + s2b;
+          f32x4 sc = (s2a + s2c) + (s2b + s2d);
           // ---- rms divide, scale, cap, mask ----
           float tm = kNegInf;
 #pragma unroll
@@ -449,7 +536,14 @@ __device__ __forceinline__ void segment_role(const KParams& p, Smem<C>& sm, int 
           fix_decide(tpart, rare, alpha_f, pk_fix);
           fix_publish(it - 1, rare, alpha_f, pk_fix);
         }
+        if constexpr (ISSUER) {
+          if (it + C::A < nt) issue(it + C::A);
+          if (it + 1 < nt) wait_tile(it + 1, it + C::A < nt - 1 ? it + C::A : nt - 1);
+        }
       } else {
+        if constexpr (ISSUER && C::ISS >= 1) {
+          if (it + C::A < nt) issue(it + C::A);
+        }
         if (it >= 2) {
           // ---- P . V for tile j = it-2 over columns VC*vw .. +VC ----
           const int j = it - 2, pj = j % 3;
@@ -509,7 +603,7 @@ __device__ __forceinline__ void segment_role(const KParams& p, Smem<C>& sm, int 
           });
         }
         if constexpr (ISSUER) {
-          if (it + C::A < nt) issue(it + C::A);
+          if (C::ISS == 0 && it + C::A < nt) issue(it + C::A);
           if (it + 1 < nt) wait_tile(it + 1, it + C::A < nt - 1 ? it + C::A : nt - 1);
         }
       }
@@ -586,15 +680,15 @@ struct Inst {
   void (*fn)(const KParams);
 };
 
-#define QMLA_WS(EB, RMS, DCG, A, CPR, CAP, RTR, DW) \
-  {EB, RMS, DCG, CPR, CAP, RTR, WS<EB, RMS, DCG, A, CPR, CAP, RTR, DW>::NTHR, &ws_kernel<WS<EB, RMS, DCG, A, CPR, CAP, RTR, DW>>}
+#define QMLA_WS(EB, RMS, DCG, A, CPR, CAP, RTR, ISS) \
+  {EB, RMS, DCG, CPR, CAP, RTR, WS<EB, RMS, DCG, A, CPR, CAP, RTR, ISS>::NTHR, &ws_kernel<WS<EB, RMS, DCG, A, CPR, CAP, RTR, ISS>>}
 
 static const Inst kInst[] = {
     // fp8 e4m3 + log8 codes, d_c 512, rope 64, 24 heads: 608-byte rows, 32-token tiles 3 ahead (6 stages)
-    QMLA_WS(1, QMLA_RMS_LOG8, 512, 3, 38, false, true, false),
-    QMLA_WS(1, QMLA_RMS_LOG8, 512, 3, 38, false, false, false),
+    QMLA_WS(1, QMLA_RMS_LOG8, 512, 3, 38, false, true, 1),
+    QMLA_WS(1, QMLA_RMS_LOG8, 512, 3, 38, false, false, 1),
     // ... up to 16 heads (592-byte rows), rms codes read per row
-    QMLA_WS(1, QMLA_RMS_LOG8, 512, 3, 37, false, false, false),
+    QMLA_WS(1, QMLA_RMS_LOG8, 512, 3, 37, false, false, 1),
 };
 
 }  // namespace ws
