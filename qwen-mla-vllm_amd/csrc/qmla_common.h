@@ -66,6 +66,38 @@ __device__ __forceinline__ int req_len(const KParams& p, int req) {
   return L > 0 ? L : 0;
 }
 
+// Tokens per split in the fixed-split mode: ceil(ceil(L/S)/align)*align (mla_decode_attention.py:389-396).
+__device__ __forceinline__ int split_len(const KParams& p, int L) {
+  int per = (L + p.num_splits - 1) / p.num_splits;
+  if (p.split_align > 0) per = (per + p.split_align - 1) / p.split_align * p.split_align;
+  return per;
+}
+
+// Output of request b's token range in this workgroup: fixed splits write the reference's
+// attn_logits row of split blockIdx.x; the balanced mode writes slot blockIdx.x + b of the partial
+// buffers; final_out (the workgroup covers the whole request) writes the normalized output directly.
+template <int DV>
+__device__ __forceinline__ SegOut seg_out(const KParams& p, int b, bool final_out) {
+  SegOut so;
+  so.final_out = final_out;
+  if (p.num_splits > 0) {
+    so.po = p.ws + (int64_t)b * p.qrows * p.ws_sr + (int64_t)blockIdx.x * p.ws_ss;
+    so.po_sr = p.ws_sr;
+    so.po_sh = p.ws_sh;
+    so.plse = nullptr;
+    so.plse_sr = 0;
+  } else {
+    const int nrow = p.qrows * p.heads;
+    const int64_t slot = (int64_t)blockIdx.x + b;
+    so.po = p.part_o + slot * nrow * DV;
+    so.po_sr = (int64_t)p.heads * DV;
+    so.po_sh = DV;
+    so.plse = p.part_lse + slot * nrow;
+    so.plse_sr = p.heads;
+  }
+  return so;
+}
+
 // Calls f(req, a, e, L, so) for every token range [a, e) this workgroup owns.
 //   fixed splits (num_splits > 0): grid (S, n_req); split s covers [s*per, min((s+1)*per, L)) with
 //     per = ceil(ceil(L/S)/align)*align, as the reference's stage 1 (mla_decode_attention.py:389-396);
@@ -97,23 +129,15 @@ __device__ __forceinline__ void for_each_segment(const KParams& p, F&& f) {
     b_lo = b0;
     b_hi = p.n_req;
   }
-  const int nrow = p.qrows * p.heads;
   for (int b = b_lo; b < b_hi; ++b) {
     const int L = req_len(p, b);
     int a, e;
     SegOut so;
     if (fixed) {
-      const int s = blockIdx.x;
-      int per = (L + p.num_splits - 1) / p.num_splits;
-      if (p.split_align > 0) per = (per + p.split_align - 1) / p.split_align * p.split_align;
-      a = per * s;
+      const int per = split_len(p, L);
+      a = per * (int)blockIdx.x;
       e = a + per < L ? a + per : L;
-      so.final_out = p.num_splits == 1;
-      so.po = p.ws + (int64_t)b * p.qrows * p.ws_sr + (int64_t)s * p.ws_ss;
-      so.po_sr = p.ws_sr;
-      so.po_sh = p.ws_sh;
-      so.plse = nullptr;
-      so.plse_sr = 0;
+      so = seg_out<DV>(p, b, p.num_splits == 1);
     } else {
       const int c0 = pref[b], c1 = pref[b + 1];
       if (c0 >= hi) break;
@@ -121,13 +145,7 @@ __device__ __forceinline__ void for_each_segment(const KParams& p, F&& f) {
       const int t_lo = (lo > c0 ? lo : c0) - c0, t_hi = (hi < c1 ? hi : c1) - c0;
       a = t_lo * PLAN_TILE;
       e = t_hi * PLAN_TILE < L ? t_hi * PLAN_TILE : L;
-      so.final_out = (t_lo == 0 && t_hi == c1 - c0);
-      const int64_t slot = (int64_t)blockIdx.x + b;
-      so.po = p.part_o + slot * nrow * DV;
-      so.po_sr = (int64_t)p.heads * DV;
-      so.po_sh = DV;
-      so.plse = p.part_lse + slot * nrow;
-      so.plse_sr = p.heads;
+      so = seg_out<DV>(p, b, t_lo == 0 && t_hi == c1 - c0);
     }
     if (e <= a) continue;
     f(b, a, e, L, so);

@@ -1,8 +1,15 @@
 // qmla_ws.hip -- gfx950 warp-specialized MLA decode for one latent group (d_c 512, rope 64, <= 32
 // query rows per request: 24 heads, one token each).
 //
-// A workgroup owns a contiguous token range of one request and all its query rows (every cached row
-// is read from HBM once per call). Its 8 waves take two roles, one of each on every SIMD:
+// A workgroup owns a contiguous range of the concatenated requests' tokens (balanced mode) or one
+// split of one request (fixed splits), with all query rows, so every cached row is read from HBM
+// once per call. It walks its range as ONE sequence of 32-token tiles across request boundaries:
+// the DMA keeps streaming into the next request while the last tiles of the previous one are still
+// being scored and accumulated, so a request boundary costs no pipeline fill or drain. The pieces of
+// the range (one per request) and their page ids are staged in LDS once per window (a window holds up
+// to NSEG pieces and PIDN pages; a range that needs more is walked in several windows).
+//
+// Its 8 waves take two roles, one of each on every SIMD:
 //   score waves (0-3):  wave (tb, mb) scores 16 tokens x 16 rows over all 576 columns of a tile
 //                       (S^T = K . Q^T on MFMA, query fragments resident in VGPRs), divides by the
 //                       rms, applies the mask and the softmax shift, and writes P (bf16) into LDS.
@@ -11,12 +18,12 @@
 //                       on the 16x16x128 fp8 MFMA and the rope on the 16x16x32 one;
 //   value waves (4-7):  wave v accumulates P . V over latent columns [128v, 128v+128) for all rows,
 //                       two tiles behind the score waves, with V^T fragments from ds_read_b64_tr_b8,
-//                       and streams 32-token tiles of cache rows global -> LDS by LDS-DMA, A tiles
-//                       ahead of the score waves, into a ring of A+3 stages (each value wave waits
-//                       only for its own loads). The score waves never touch the memory pipeline.
-// (Other placements of the DMA are compile-time options, see WS::ISS.) The workgroup meets once per
-// tile at one barrier. Inside a step a wave issues all its LDS reads at once and waits for them in
-// order with counted lgkmcnt waits, so the MFMAs start as soon as the first rows arrive.
+//                       writes a request's output when its last tile is in, and streams the tiles
+//                       global -> LDS by LDS-DMA, A tiles ahead of the score waves, into a ring of
+//                       A+3 stages (each value wave waits only for its own loads).
+// The workgroup meets once per tile at one barrier. Inside a step a wave issues all its LDS reads at
+// once and waits for them in order with counted lgkmcnt waits, so the MFMAs start as soon as the
+// first rows arrive.
 //
 // Softmax: every row keeps one reference max shared by its two score waves. P = exp2(s - ref) is
 // written optimistically. One step later, when the barrier has made both halves' tile maxima
@@ -41,9 +48,11 @@ namespace qmla {
 namespace ws {
 
 constexpr int TILE = 32;          // tokens per tile
-constexpr int PIDN = 512;         // page ids staged per sub-range
+constexpr int NSEG = 64;          // pieces per window (one per lane of the wave that plans it)
+constexpr int PIDN = 1024;        // page ids per window
 constexpr float SHIFT = 16.0f;    // P <= 2^16 before the reference max moves
-enum Role { SCORE, VALUE, DMA };
+enum Role { SCORE, VALUE };
+enum { SEG_FIRST = 1, SEG_LAST = 2, SEG_FINAL = 4 };
 
 __device__ __forceinline__ i32x4 ldsr128(const void* p) {
   i32x4 r;
@@ -53,6 +62,11 @@ __device__ __forceinline__ i32x4 ldsr128(const void* p) {
 __device__ __forceinline__ i32x2 ldsr64(const void* p) {
   i32x2 r;
   asm volatile("ds_read_b64 %0, %1" : "=v"(r) : "v"(lds_addr(static_cast<const char*>(p))));
+  return r;
+}
+__device__ __forceinline__ int ldsr32(const void* p) {
+  int r;
+  asm volatile("ds_read_b32 %0, %1" : "=v"(r) : "v"(lds_addr(static_cast<const char*>(p))));
   return r;
 }
 __device__ __forceinline__ float ldsr32f(const void* p) {
@@ -74,6 +88,7 @@ __device__ __forceinline__ uint32_t ldsr16(const void* p) {
 // Wait until at most N of this wave's LDS operations are outstanding; LDS operations complete in
 // issue order, so with N = the number issued after the one producing v, v is ready (more younger
 // operations than counted only make the wait longer). The register tie orders v's uses after it.
+// No scalar memory load is ever outstanding inside the tile loop, so the count is LDS-only.
 template <int N, class T>
 __device__ __forceinline__ void lds_wait_n(T& v) {
   static_assert(N >= 0 && N <= 15, "lgkmcnt range");
@@ -89,26 +104,36 @@ __device__ __forceinline__ void static_for(F&& f) {
   }
 }
 
+__device__ __forceinline__ int wave_incl_sum(int x) {
+  const int lane = threadIdx.x & 63;
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    const int y = __shfl_up(x, o, 64);
+    if (lane >= o) x += y;
+  }
+  return x;
+}
+__device__ __forceinline__ int lanes_below(uint64_t m) {
+  return __builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0));
+}
+
 // Compile-time shape: EB cache element bytes (1 fp8, 2 bf16), RMS tail format, DCG latent columns,
 // A tiles in flight ahead of the score waves, CPR 16-byte chunks staged per row, CAP tanh logit
-// cap, RTR rms codes read transposed (query rows are the heads of one token), ISS who issues the
-// DMA: 0 the value waves after their step, 1 the value waves before their step, 2 all 8 waves (score
-// waves after their step, value waves before theirs), 3 four dedicated DMA waves (12 waves).
+// cap, RTR rms codes read transposed (query rows are the heads of one token), ISS when the value
+// waves issue a tile's DMA: 1 before their step, 0 after it.
 template <int EB_, int RMS_, int DCG_, int A_, int CPR_, bool CAP_, bool RTR_, int ISS_>
 struct WS {
   static constexpr int EB = EB_, RMS = RMS_, DCG = DCG_, A = A_, S = A_ + 3, CPR = CPR_;
   static constexpr bool CAP = CAP_, RTR = RTR_;
   static constexpr int ISS = ISS_;
-  static constexpr bool DW = ISS == 3;
-  static constexpr int NW = DW ? 12 : 8, NTHR = 64 * NW;
-  static constexpr int NIW = ISS == 2 ? 8 : 4;        // waves sharing the DMA instructions of a tile
+  static constexpr int NW = 8, NTHR = 64 * NW;
   static constexpr int RB = 16 * CPR;                 // staged row bytes
   static constexpr int STAGE = TILE * RB;
   static constexpr int NCH = TILE * CPR;              // 16-byte chunks per tile
   static constexpr int NI = (NCH + 63) / 64;          // DMA instructions per tile
-  static constexpr int DPW = (NI + NIW - 1) / NIW;    // ... per issuing wave (at most)
+  static constexpr int DPW = (NI + 3) / 4;            // ... per value wave (at most)
   static constexpr int KQ = (DCG + 64) / 32;          // k-steps of the score product (latent + rope 64)
-  static constexpr int KP = KQ / 2;                   // 64-column pairs
+  static constexpr int KP = KQ / 2;                   // 16-byte K reads per lane and tile
   static constexpr int VC = DCG / 4;                  // latent columns per value wave
   static constexpr int CB = VC / 16;
   static constexpr int RMS_EB = (RMS == QMLA_RMS_BF16 || RMS == QMLA_RMS_BF16_BYTES) ? 2 : 1;
@@ -121,15 +146,24 @@ struct WS {
   static_assert(EB == 2 || DCG % 128 == 0, "fp8 latent in 128-column MFMA blocks");
 };
 
+// one piece of the workgroup's range: tokens [ta, te) of request req (length L); nt tiles; its pages
+// start at window page index pf
+struct SegD {
+  int req, ta, te, L;
+  int nt, pf, fl, pad;
+};
+
 template <class C>
 struct Smem {
   char kv[C::S][C::STAGE];
-  alignas(16) char p[3][32][C::PST];   // P (bf16) of tiles t % 3
-  alignas(16) int flag[3][4];          // [t % 3][row block]: reference moved at tile t
-  alignas(16) float tmax[2][2][32];    // [t & 1][token block][row] tile max
-  alignas(16) float alpha[3][32];      // [t % 3][row] accumulator rescale at tile t
-  alignas(16) float fin[2][2][32];     // epilogue: [max, sum][token block][row]
+  alignas(16) char p[3][32][C::PST];   // P (bf16) of tiles g % 3
+  alignas(16) int flag[3][4];          // [g % 3][row block]: reference moved at tile g
+  alignas(16) float tmax[2][2][32];    // [g & 1][token block][row] tile max
+  alignas(16) float alpha[3][32];      // [g % 3][row] accumulator rescale at tile g
+  alignas(16) float fin[2][2][2][32];  // [piece & 1][max, sum][token block][row] of a finished request
+  alignas(16) SegD seg[NSEG];
   alignas(16) int pid[PIDN];
+  int win[4];                          // pieces, tiles, pages of the window; another window follows
 };
 
 // rotated row layout: chunk c of staged row r at position (c + (r & 15)) mod CPR
@@ -143,9 +177,9 @@ __device__ __forceinline__ int lbyte(int r, int b) {
   return r * (16 * CPR) + 16 * rot<CPR>(b >> 4, r) + (b & 15);
 }
 
-// DMA instructions issuing wave d issues per tile (instructions d, d+NIW, ... < NI)
+// DMA instructions value wave d issues per tile (instructions d, d+4, ... < NI)
 template <class C>
-__device__ __forceinline__ constexpr int dpw(int d) { return (C::NI - d + C::NIW - 1) / C::NIW; }
+__device__ __forceinline__ constexpr int dpw(int d) { return (C::NI - d + 3) / 4; }
 
 // vmcnt <= ahead * D (ahead tiles of D loads each issued after the awaited one), ahead <= K
 template <int D, int K>
@@ -158,83 +192,194 @@ __device__ __forceinline__ void wait_tiles(int ahead) {
   }
 }
 
-// One contiguous token range [ta, te) of request `req` (length L), all query rows, seen from one
-// role. All roles run the same sub-range / tile / barrier sequence; only the work between the
-// barriers differs, so each role keeps only its own registers live.
+// Wave-wide: the last request b in [0, n_req) whose first plan tile pref[b] <= lo (64-ary search;
+// pref is nondecreasing with pref[0] = 0).
+__device__ int find_first_req(const int* pref, int n_req, int lo) {
+  const int lane = threadIdx.x & 63;
+  int base = 0, len = n_req;
+  while (len > 1) {
+    const int step = (len + 63) >> 6;
+    const int idx = base + lane * step;
+    const bool ok = lane * step < len && pref[idx] <= lo;
+    const uint64_t m = __builtin_amdgcn_ballot_w64(ok);   // lane 0 always: pref[base] <= lo
+    const int last = 63 - __builtin_clzll(m);
+    base += last * step;
+    const int rem = len - last * step;
+    len = step < rem ? step : rem;
+  }
+  return base;
+}
+
+// Wave 0: the next window of pieces, from request cb at token ctok on, into sm.seg / sm.win.
+// Lane l looks at request cb + l; pieces are taken in request order while their pages fit PIDN (the
+// first piece that does not fit is cut at a page boundary).
+template <class C>
+__device__ void plan_window(const KParams& p, Smem<C>& sm, bool fixed, int lo, int hi, int& cb, int& ctok) {
+  const int lane = threadIdx.x & 63;
+  const int P = p.page_size;
+  const int* pref = p.plan + 2;
+  int nseg = 0, ntot = 0, npg = 0;
+  bool more = true;
+  while (more && nseg == 0) {
+    const int b = cb + lane;
+    int a = 0, e = 0, L = 0, fl = 0;
+    bool beyond;
+    if (fixed) {
+      beyond = lane != 0;
+      if (!beyond) {
+        L = req_len(p, b);
+        const int per = split_len(p, L);
+        const int a0 = per * (int)blockIdx.x;
+        e = a0 + per < L ? a0 + per : L;
+        a = a0 > ctok ? a0 : ctok;
+        fl = (a == a0 ? SEG_FIRST : 0) | SEG_LAST | (p.num_splits == 1 ? SEG_FINAL : 0);
+      }
+    } else {
+      beyond = b >= p.n_req;
+      if (!beyond) {
+        const int c0 = pref[b], c1 = pref[b + 1];
+        beyond = c0 >= hi;
+        if (!beyond && c1 > lo) {
+          L = req_len(p, b);
+          const int t_lo = (lo > c0 ? lo : c0) - c0, t_hi = (hi < c1 ? hi : c1) - c0;
+          const int a0 = t_lo * PLAN_TILE;
+          e = t_hi * PLAN_TILE < L ? t_hi * PLAN_TILE : L;
+          a = lane == 0 && ctok > a0 ? ctok : a0;
+          fl = (a == a0 ? SEG_FIRST : 0) | SEG_LAST | (t_lo == 0 && t_hi == c1 - c0 ? SEG_FINAL : 0);
+        }
+      }
+    }
+    const bool live = !beyond && a < e;
+    const int pages = live ? (e - 1) / P - a / P + 1 : 0;
+    const int cum = wave_incl_sum(pages);
+    const int excl = cum - pages;
+    const bool take = live && excl < PIDN;
+    int et = e;
+    if (take && cum > PIDN) {
+      const int cut = (a / P + (PIDN - excl)) * P;   // page-aligned, > a
+      et = cut < e ? cut : e;
+    }
+    if (et < e) fl &= ~SEG_LAST;
+    const int nt = take ? (et - a + TILE - 1) / TILE : 0;
+    const int npt = take ? (et - 1) / P - a / P + 1 : 0;
+    const uint64_t tm = __builtin_amdgcn_ballot_w64(take);
+    const int tcum = wave_incl_sum(nt);
+    const int pcum = wave_incl_sum(npt);
+    if (take) {
+      SegD d;
+      d.req = b;
+      d.ta = a;
+      d.te = et;
+      d.L = L;
+      d.nt = nt;
+      d.pf = pcum - npt;
+      d.fl = fl;
+      d.pad = 0;
+      sm.seg[lanes_below(tm)] = d;
+    }
+    nseg = __builtin_popcountll(tm);
+    ntot = __shfl(tcum, 63, 64);
+    npg = __shfl(pcum, 63, 64);
+    // cursor: the first live request not finished here; else the range is done if a request at or
+    // past its end was seen; else the next 64 requests
+    const uint64_t um = __builtin_amdgcn_ballot_w64(live && (!take || et < e));
+    const uint64_t bm = __builtin_amdgcn_ballot_w64(beyond);
+    if (um) {
+      const int x = __builtin_ctzll(um);
+      const int etx = __shfl(et, x, 64);
+      const bool tookx = (tm >> x) & 1;
+      cb += x;
+      ctok = tookx ? etx : 0;
+    } else if (bm) {
+      more = false;
+    } else {
+      cb += 64;
+      ctok = 0;
+    }
+  }
+  if (lane == 0) {
+    sm.win[0] = nseg;
+    sm.win[1] = ntot;
+    sm.win[2] = npg;
+    sm.win[3] = more ? 1 : 0;
+  }
+}
+
+// The whole range of this workgroup, seen from one role. All roles run the same window / tile /
+// barrier sequence; only the work between the barriers differs, so each role keeps only its own
+// registers live (score waves the query fragments, value waves the accumulators).
 template <class C, int ROLE>
-__device__ __forceinline__ void segment_role(const KParams& p, Smem<C>& sm, int req, int ta, int te, int L,
-                                             const SegOut& so, float kscale) {
-  constexpr bool ISSUER = ROLE == DMA || (ROLE == VALUE && !C::DW) || (ROLE == SCORE && C::ISS == 2);
+__device__ __forceinline__ void role_main(const KParams& p, Smem<C>& sm, float kscale, bool fixed, int lo,
+                                          int hi) {
   constexpr int NTHR = C::NTHR;
+  constexpr bool F8 = C::EB == 1;
+  constexpr int NB = C::DCG / 128;       // latent blocks of the fp8 product
+  constexpr bool QS = ROLE == SCORE;
+  constexpr int ND = ROLE == VALUE ? C::DPW : 1;
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int tb = (w >> 1) & 1, smb = w & 1;   // score wave: token block, row block
-  const int vw = w & 3;                        // value wave: column slice
-  const int dw = C::NIW == 8 ? w : (w & 3);    // issuing wave: first DMA instruction of a tile
+  const int vw = w & 3;                        // value wave: column slice and DMA instruction lane
   const int ln16 = lane & 15, lg = lane >> 4;
   const int qrows = p.qrows, hpg = p.hpg;
   const int nrows = qrows * hpg;
-  const int row0 = req * qrows;
   const int P = p.page_size;
-  const int* btrow = p.bt + (int64_t)row0 * p.bt_stride;
-  float c2 = p.sm_scale * kscale * kLog2e;
+  const float c2b = p.sm_scale * kscale * kLog2e;
   const int r = 16 * smb + ln16;   // score wave: the lane's row
+  const bool rok = r < nrows;
+  const int jq = rok ? r / hpg : 0, hh = rok ? r - jq * hpg : 0;
+  const int rms_b = p.rms_off_b + hh * C::RMS_EB;
+  const bool contig = p.token_stride_b == C::RB;
 
-  // ---- score wave: query fragments for row r (pair jj, lane group lg: columns 64jj + 16lg .. +16
-  //      of [latent | rope]); row limit and rms byte offset; softmax state ----
-  // fp8 cache: the query enters the fp8 MFMAs as two e4m3 parts (q * qs = hi + lo, qs a power of two
-  // per row folded into the score scale), so the K bytes are used as stored: the latent in 128-column
-  // blocks on v_mfma_scale_f32_16x16x128_f8f6f4 (lane group lg holds columns 128b + 32lg .. +32),
-  // the rope on 16x16x32 fp8 (lane group lg holds rope columns 16lg .. +16). bf16 cache: bf16 MFMA.
-  constexpr bool F8 = C::EB == 1;
-  constexpr int NB = C::DCG / 128;       // latent blocks of the fp8 product
-  constexpr bool QS = ROLE == SCORE;
+  // ---- score wave: query fragments (fp8 cache: e4m3 hi/lo parts scaled per row by a power of two
+  //      folded into c2; the latent in 128-column blocks, lane group lg holding columns
+  //      128b + 32lg .. +32, the rope as two 16x16x32 k-steps over rope columns 16lg .. +16;
+  //      bf16 cache: bf16, pair jj and lane group lg holding columns 64jj + 16lg .. +16) ----
   bf16x8 qf[!F8 && QS ? C::KQ : 1];
   i32x8 qh8[F8 && QS ? NB : 1], ql8[F8 && QS ? NB : 1];
   long qhr[2], qlr[2];
-  int lim = 0, rms_b = 0;
+  bf16x8 qn[QS ? C::KQ : 1];   // the query of a request, loaded at its first tile
+  float c2 = c2b;
   float mref = kNegInf, lpart = 0.f;
   float tmp = kNegInf, ps_pend = 0.f;    // own max and optimistic sum of the last scored tile
   f32x4 scp = {0.f, 0.f, 0.f, 0.f};      // its scores (log2 domain, masked)
-  if constexpr (ROLE == SCORE) {
-    const bool ok = r < nrows;
-    const int jq = ok ? r / hpg : 0, h = ok ? r - jq * hpg : 0;
-    const int lr = L - (qrows - 1 - jq);
-    lim = ok ? (lr < te ? lr : te) : 0;
-    rms_b = p.rms_off_b + h * C::RMS_EB;
-    const __bf16* qn = p.q_nope + (int64_t)(row0 + jq) * p.qn_sr + (int64_t)h * p.qn_sh;
-    const __bf16* qp = p.q_pe + (int64_t)(row0 + jq) * p.qp_sr + (int64_t)h * p.qp_sh;
-    bf16x8 qv[C::KQ];
+  int lim = 0;
+
+  auto load_q = [&](int req) {
+    const int row = req * qrows + jq;
+    const __bf16* qnp = p.q_nope + (int64_t)row * p.qn_sr + (int64_t)hh * p.qn_sh;
+    const __bf16* qpp = p.q_pe + (int64_t)row * p.qp_sr + (int64_t)hh * p.qp_sh;
 #pragma unroll
     for (int k = 0; k < C::KQ; ++k) {
       const int col = !F8 ? 64 * (k >> 1) + 16 * lg + 8 * (k & 1)
                           : k < 4 * NB ? 128 * (k >> 2) + 32 * lg + 8 * (k & 3) : C::DCG + 16 * lg + 8 * (k - 4 * NB);
-      bf16x8 v = col < C::DCG ? *reinterpret_cast<const bf16x8*>(qn + col)
-                              : *reinterpret_cast<const bf16x8*>(qp + (col - C::DCG));
-      if (!ok) v = bf16x8{};
-      qv[k] = v;
+      bf16x8 v = col < C::DCG ? *reinterpret_cast<const bf16x8*>(qnp + col)
+                              : *reinterpret_cast<const bf16x8*>(qpp + (col - C::DCG));
+      if (!rok) v = bf16x8{};
+      qn[k] = v;
     }
+  };
+  auto set_q = [&]() {
     if constexpr (F8) {
       float mx = 0.f;
 #pragma unroll
       for (int k = 0; k < C::KQ; ++k)
 #pragma unroll
-        for (int e = 0; e < 8; ++e) mx = fmaxf(mx, fabsf((float)qv[k][e]));
+        for (int e = 0; e < 8; ++e) mx = fmaxf(mx, fabsf((float)qn[k][e]));
       mx = max_lg(mx);
       // |q| * qs in (112, 448]: e4m3 keeps 4 significant bits in hi and 4 more in lo
       const float ex = mx > 0.f ? fminf(floorf(fast_log2(224.0f / mx)), 126.0f) : 0.0f;
       const float qs = fast_exp2(ex);
-      c2 = c2 * fast_exp2(-ex);
+      c2 = c2b * fast_exp2(-ex);
       int hq[2 * C::KQ], lq[2 * C::KQ];
 #pragma unroll
       for (int k = 0; k < C::KQ; ++k) {
-        int h[2], l[2];
 #pragma unroll
         for (int hw = 0; hw < 2; ++hw) {
           float v[4], rsd[4];
 #pragma unroll
-          for (int e = 0; e < 4; ++e) v[e] = (float)qv[k][4 * hw + e] * qs;
+          for (int e = 0; e < 4; ++e) v[e] = (float)qn[k][4 * hw + e] * qs;
           int hb = __builtin_amdgcn_cvt_pk_fp8_f32(v[0], v[1], 0, false);
           hb = __builtin_amdgcn_cvt_pk_fp8_f32(v[2], v[3], hb, true);
           rsd[0] = v[0] - __builtin_amdgcn_cvt_f32_fp8(hb, 0);
@@ -243,13 +388,9 @@ __device__ __forceinline__ void segment_role(const KParams& p, Smem<C>& sm, int 
           rsd[3] = v[3] - __builtin_amdgcn_cvt_f32_fp8(hb, 3);
           int lb = __builtin_amdgcn_cvt_pk_fp8_f32(rsd[0], rsd[1], 0, false);
           lb = __builtin_amdgcn_cvt_pk_fp8_f32(rsd[2], rsd[3], lb, true);
-          h[hw] = hb;
-          l[hw] = lb;
+          hq[2 * k + hw] = hb;
+          lq[2 * k + hw] = lb;
         }
-        hq[2 * k] = h[0];
-        hq[2 * k + 1] = h[1];
-        lq[2 * k] = l[0];
-        lq[2 * k + 1] = l[1];
       }
 #pragma unroll
       for (int b = 0; b < NB; ++b)
@@ -265,26 +406,28 @@ __device__ __forceinline__ void segment_role(const KParams& p, Smem<C>& sm, int 
       }
     } else {
 #pragma unroll
-      for (int k = 0; k < C::KQ; ++k) qf[k] = qv[k];
+      for (int k = 0; k < C::KQ; ++k) qf[k] = qn[k];
     }
-  }
+  };
+
   // ---- value wave: accumulator of rows (16mb + 4lg + i) x columns VC*vw + 16cb + ln16 ----
   f32x4 acc[2][ROLE == VALUE ? C::CB : 1];
-  if constexpr (ROLE == VALUE) {
+  auto zero_acc = [&]() {
 #pragma unroll
     for (int mb = 0; mb < 2; ++mb)
 #pragma unroll
-      for (int cb = 0; cb < C::CB; ++cb) acc[mb][cb] = f32x4{0.f, 0.f, 0.f, 0.f};
-  }
-  // ---- DMA wave: instruction i = vw + 4j covers LDS chunks 64i .. 64i+63 of a stage: staged row
-  //      q / CPR, position q % CPR, i.e. row chunk (position - (row & 15)) mod CPR ----
-  constexpr int ND = ISSUER ? C::DPW : 1;
+      for (int cb = 0; cb < (ROLE == VALUE ? C::CB : 1); ++cb) acc[mb][cb] = f32x4{0.f, 0.f, 0.f, 0.f};
+  };
+  zero_acc();
+
+  // ---- value wave DMA: instruction i = vw + 4j covers LDS chunks 64i .. 64i+63 of a stage: staged
+  //      row q / CPR, position q % CPR, i.e. row chunk (position - (row & 15)) mod CPR ----
   uint32_t doff[ND];
   int drow[ND];
-  if constexpr (ISSUER) {
+  if constexpr (ROLE == VALUE) {
 #pragma unroll
     for (int j = 0; j < ND; ++j) {
-      int q = (dw + C::NIW * j) * 64 + lane;
+      int q = (vw + 4 * j) * 64 + lane;
       q = q < C::NCH ? q : C::NCH - 1;
       const int rr = q / C::CPR, pp = q - rr * C::CPR;
       int c = pp - (rr & 15);
@@ -293,9 +436,28 @@ __device__ __forceinline__ void segment_role(const KParams& p, Smem<C>& sm, int 
       drow[j] = rr;
     }
   }
-  const bool big = dpw<C>(dw) == C::DPW;
+  const bool big = dpw<C>(vw) == C::DPW;
 
-  // score step of tile t: fix tile t-1 against the partner's max (if t >= 1), then score tile t
+  // reads one piece descriptor (asm reads: no wait on the LDS-DMA in flight); its fields are
+  // wave-uniform, so they live in scalar registers (the DMA's buffer resources are built from them)
+  auto read_seg = [&](int k) {
+    i32x4 a = ldsr128(&sm.seg[k].req);
+    i32x4 b = ldsr128(&sm.seg[k].nt);
+    lds_wait_n<1>(a);
+    lds_wait_n<0>(b);
+    SegD d;
+    d.req = __builtin_amdgcn_readfirstlane(a[0]);
+    d.ta = __builtin_amdgcn_readfirstlane(a[1]);
+    d.te = __builtin_amdgcn_readfirstlane(a[2]);
+    d.L = __builtin_amdgcn_readfirstlane(a[3]);
+    d.nt = __builtin_amdgcn_readfirstlane(b[0]);
+    d.pf = __builtin_amdgcn_readfirstlane(b[1]);
+    d.fl = __builtin_amdgcn_readfirstlane(b[2]);
+    d.pad = 0;
+    return d;
+  };
+
+  // score step helpers: reference check of the previous tile and its publication
   auto fix_decide = [&](float tpart, bool& rare, float& alpha_f, bf16x4& pk_fix) {
     const float gm = fmaxf(tmp, tpart);
     const bool ch = gm > mref + SHIFT;
@@ -317,57 +479,123 @@ __device__ __forceinline__ void segment_role(const KParams& p, Smem<C>& sm, int 
     }
     lpart = lpart * alpha_f + ps2;
   };
-  auto fix_publish = [&](int t, bool rare, float alpha_f, const bf16x4& pk_fix) {
-    const int pt = t % 3;
+  auto fix_publish = [&](int g, bool rare, float alpha_f, const bf16x4& pk_fix) {
+    const int pt = g % 3;
     if (rare) {
       *reinterpret_cast<bf16x4*>(&sm.p[pt][r][(16 * tb + 4 * lg) * 2]) = pk_fix;
       if (tb == 0 && lg == 0) sm.alpha[pt][r] = alpha_f;
     }
     if (tb == 0 && lane == 0) sm.flag[pt][smb] = rare ? 1 : 0;
   };
+  auto publish_fin = [&](int k) {
+    const float l = sum_lg(lpart);
+    if (lg == 0) {
+      sm.fin[k & 1][0][tb][r] = mref;
+      sm.fin[k & 1][1][tb][r] = l;
+    }
+  };
+  // value wave: normalize and write the output of request req, whose sums are in fin[k & 1]
+  auto finalize = [&](int k, int req, int fl) {
+    const SegOut so = seg_out<C::DCG>(p, req, (fl & SEG_FINAL) != 0);
+    const int row0 = req * qrows;
+#pragma unroll
+    for (int mb = 0; mb < 2; ++mb)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int rr = 16 * mb + 4 * lg + i;
+        float m = ldsr32f(&sm.fin[k & 1][0][0][rr]);
+        float l0 = ldsr32f(&sm.fin[k & 1][1][0][rr]);
+        float l1 = ldsr32f(&sm.fin[k & 1][1][1][rr]);
+        lds_wait_n<2>(m);
+        lds_wait_n<1>(l0);
+        lds_wait_n<0>(l1);
+        if (rr >= nrows) continue;
+        const float l = l0 + l1;
+        const int jr = rr / hpg, h = rr - jr * hpg;
+        const float inv = l > 0.f ? kscale / l : 0.f;   // fp8 values were accumulated unscaled
+        const float lse_v = l > 0.f ? (m + fast_log2(l)) * kLn2 : kNegInf;
+        const int col = C::VC * vw + ln16;
+        if (so.final_out) {
+          const int64_t ob = (int64_t)(row0 + jr) * p.o_sr + (int64_t)h * p.o_sh + col;
+#pragma unroll
+          for (int cb = 0; cb < C::CB; ++cb) store_out(p.out, p.out_dt, ob + 16 * cb, acc[mb][cb][i] * inv);
+          if (vw == 0 && ln16 == 0 && p.lse) store_out(p.lse, p.lse_dt, (int64_t)(row0 + jr) * p.lse_sr + h, lse_v);
+        } else {
+          float* ob = so.po + (int64_t)jr * so.po_sr + (int64_t)h * so.po_sh + col;
+#pragma unroll
+          for (int cb = 0; cb < C::CB; ++cb) ob[16 * cb] = acc[mb][cb][i] * inv;
+          if (vw == 0 && ln16 == 0) {
+            if (so.plse) so.plse[(int64_t)jr * so.plse_sr + h] = lse_v;
+            else so.po[(int64_t)jr * so.po_sr + (int64_t)h * so.po_sh + C::DCG] = lse_v;
+          }
+        }
+      }
+    zero_acc();
+  };
 
-  int sub = (PIDN - 1) * P;
-  sub = sub < TILE ? TILE : sub / TILE * TILE;
-  for (int sa = ta; sa < te; sa += sub) {
-    const int se = te - sa < sub ? te : sa + sub;
-    const int pbase = sa / P;
-    const int np = (se - 1) / P - pbase + 1;
-    wait_vmcnt<0>();
-    lds_barrier();   // previous sub-range finished with the page ids and the ring
-    for (int i = tid; i < np; i += NTHR) sm.pid[i] = btrow[pbase + i];
+  // window planning cursor (wave 0 only)
+  int cb = 0, ctok = 0;
+  if (w == 0) cb = fixed ? (int)blockIdx.y : find_first_req(p.plan + 2, p.n_req, lo);
+
+  for (;;) {
+    if (w == 0) plan_window<C>(p, sm, fixed, lo, hi, cb, ctok);
     __syncthreads();
-    const int nt = (se - sa + TILE - 1) / TILE;
-    const bool contig = p.token_stride_b == C::RB;
+    const int nseg = sm.win[0], ntot = sm.win[1], npg = sm.win[2], more = sm.win[3];
+    if (nseg == 0) break;
+    // page ids of the window: page f belongs to the last piece with pf <= f
+    for (int f = tid; f < npg; f += NTHR) {
+      int k0 = 0, k1 = nseg - 1;
+      while (k0 < k1) {
+        const int mid = (k0 + k1 + 1) >> 1;
+        if (sm.seg[mid].pf <= f) k0 = mid;
+        else k1 = mid - 1;
+      }
+      const SegD& d = sm.seg[k0];
+      sm.pid[f] = p.bt[(int64_t)d.req * qrows * p.bt_stride + d.ta / P + (f - d.pf)];
+    }
+    __syncthreads();
 
-    // DMA issue cursor: tiles are issued in order, so the page of the next tile is tracked
-    // incrementally (no divisions in the tile loop)
-    int ipg = sa / P - pbase, ioff = sa % P;
-    auto issue = [&](int t) {
-      const int tok0 = sa + t * TILE;
-      const int nvalid = se - tok0 < TILE ? se - tok0 : TILE;
-      char* dst = sm.kv[t % C::S];
+    // ---- per-role cursors over the window's pieces ----
+    // DMA (value waves): piece ki, tile ti, page cursor (window page index ipg, token offset ioff)
+    int ki = 0, ti = 0, i_ta = 0, i_te = 0, i_nt = 0, i_pf = 0, ipg = 0, ioff = 0, pidv = 0;
+    auto enter_i = [&]() {
+      const SegD d = read_seg(ki);
+      i_ta = d.ta;
+      i_te = d.te;
+      i_nt = d.nt;
+      i_pf = d.pf;
+      ipg = d.pf;
+      ioff = d.ta % P;
+    };
+    // issues tile g (the cursor's) into ring stage g % S and advances the cursor
+    auto issue = [&](int g) {
+      const int tok0 = i_ta + ti * TILE;
+      const int nvalid = i_te - tok0 < TILE ? i_te - tok0 : TILE;
+      char* dst = sm.kv[g % C::S];
       if (contig && ioff + TILE <= P) {
-        // the tile's rows are consecutive in one page; rows past the range end read as zeros
-        const int pg = __builtin_amdgcn_readfirstlane(sm.pid[ipg]);
+        // the tile's rows are consecutive in one page; rows past the piece end read as zeros
+        lds_wait_n<0>(pidv);
+        const int pg = __builtin_amdgcn_readfirstlane(pidv);
         const char* base = p.kv + (int64_t)pg * p.page_stride_b + (int64_t)ioff * p.token_stride_b;
         const __amdgpu_buffer_rsrc_t rs = make_rsrc(base, (uint32_t)(nvalid * C::RB));
 #pragma unroll
         for (int j = 0; j < ND; ++j) {
-          const int i = dw + C::NIW * j;
+          const int i = vw + 4 * j;
           if (i < C::NI && (i * 64 + 64 <= C::NCH || i * 64 + lane < C::NCH)) dma16_buf(rs, doff[j], dst + i * 1024);
         }
       } else {
-        // per-lane page lookup; rows past the range end repeat the last row
+        // per-lane page lookup; rows past the piece end repeat its last row
 #pragma unroll
         for (int j = 0; j < ND; ++j) {
-          const int i = dw + C::NIW * j;
+          const int i = vw + 4 * j;
           if (i < C::NI && (i * 64 + 64 <= C::NCH || i * 64 + lane < C::NCH)) {
             const int rr = drow[j] < nvalid ? drow[j] : nvalid - 1;
             const int tok = tok0 + rr;
             const int q = tok / P;
-            const int pg = sm.pid[q - pbase];
-            const uint32_t cb = doff[j] - (uint32_t)(drow[j] * C::RB);
-            dma16(p.kv + (int64_t)pg * p.page_stride_b + (int64_t)(tok - q * P) * p.token_stride_b + cb,
+            int pg = ldsr32(&sm.pid[i_pf + q - i_ta / P]);
+            lds_wait_n<0>(pg);
+            const uint32_t cbo = doff[j] - (uint32_t)(drow[j] * C::RB);
+            dma16(p.kv + (int64_t)pg * p.page_stride_b + (int64_t)(tok - q * P) * p.token_stride_b + cbo,
                   dst + i * 1024);
           }
         }
@@ -377,34 +605,53 @@ __device__ __forceinline__ void segment_role(const KParams& p, Smem<C>& sm, int 
         ioff -= P;
         ++ipg;
       }
+      if (++ti == i_nt) {
+        ti = 0;
+        if (++ki < nseg) enter_i();
+      }
+      pidv = ldsr32(&sm.pid[ipg < npg ? ipg : npg - 1]);
     };
     // wait until tile t landed, with tiles t+1 .. last issued after it
     auto wait_tile = [&](int t, int last) {
       const int ahead = last - t;
       if (big) wait_tiles<C::DPW, C::A - 1>(ahead);
-      else wait_tiles<(C::NI % C::NIW == 0 ? C::DPW : C::DPW - 1), C::A - 1>(ahead);
+      else wait_tiles<(C::NI % 4 == 0 ? C::DPW : C::DPW - 1), C::A - 1>(ahead);
     };
-
-    // prologue: tiles 0 .. A-1 in flight, tile 0 landed
-    if constexpr (ISSUER) {
-      for (int t = 0; t < C::A && t < nt; ++t) issue(t);
-      wait_tile(0, (C::A < nt ? C::A : nt) - 1);
+    // score: piece ks, tile ts; value: piece kv, tile tv
+    int ks = 0, ts = 0, s_ta = 0, s_nt = 0, s_fl = 0, fl_prev = 0;
+    int kv = 0, tv = 0, v_req = 0, v_nt = 0, v_fl = 0;
+    if constexpr (ROLE == VALUE) {
+      enter_i();
+      pidv = ldsr32(&sm.pid[ipg]);
+      const SegD d = read_seg(0);
+      v_req = d.req;
+      v_nt = d.nt;
+      v_fl = d.fl;
+      // prologue: tiles 0 .. A-1 in flight, tile 0 landed
+      for (int t = 0; t < C::A && t < ntot; ++t) issue(t);
+      wait_tile(0, (C::A < ntot ? C::A : ntot) - 1);
     }
     lds_barrier();
 
-    // iteration it: DMA waves issue tile it+A and wait for tile it+1; score waves fix tile it-1 and
-    // score tile it; value waves take tile it-2
+    // iteration g: value waves issue tile g+A, take tile g-2 and wait for tile g+1; score waves fix
+    // tile g-1 and score tile g
 #pragma clang loop unroll(disable)
-    for (int it = 0; it <= nt + 1; ++it) {
-      if constexpr (ROLE == DMA) {
-        if (it + C::A < nt) issue(it + C::A);
-        if (it + 1 < nt) wait_tile(it + 1, it + C::A < nt - 1 ? it + C::A : nt - 1);
-      } else if constexpr (ROLE == SCORE) {
-        if (it < nt) {
-          const char* kvs = sm.kv[it % C::S];
-          const int tok0 = sa + it * TILE;
-          // ---- LDS reads, in this order: partner max of tile it-1, rms codes, K rows ----
-          float tpart = ldsr32f(&sm.tmax[(it + 1) & 1][tb ^ 1][r]);   // unused at it == 0
+    for (int g = 0; g <= ntot + 1; ++g) {
+      if constexpr (ROLE == SCORE) {
+        if (g < ntot) {
+          if (ts == 0) {
+            const SegD d = read_seg(ks);
+            s_ta = d.ta;
+            s_nt = d.nt;
+            s_fl = d.fl;
+            if (d.fl & SEG_FIRST) load_q(d.req);   // in flight during the reads below, converted after them
+            const int lr = d.L - (qrows - 1 - jq);
+            lim = rok ? (lr < d.te ? lr : d.te) : 0;
+          }
+          const char* kvs = sm.kv[g % C::S];
+          const int tok0 = s_ta + ts * TILE;
+          // ---- LDS reads, in this order: partner max of tile g-1, rms codes, K rows ----
+          float tpart = ldsr32f(&sm.tmax[(g + 1) & 1][tb ^ 1][r]);   // unused at g == 0
           const int krow = 16 * tb + ln16;
           const char* rowp = kvs + krow * C::RB;
           uint32_t code[4] = {0u, 0u, 0u, 0u};
@@ -430,12 +677,21 @@ __device__ __forceinline__ void segment_role(const KParams& p, Smem<C>& sm, int 
             kr0[jj] = ldsr128(rowp + 16 * rot<C::CPR>(ch, krow));
             if constexpr (C::EB == 2) kr1[jj] = ldsr128(rowp + 16 * rot<C::CPR>((cbyte >> 4) + 1, krow));
           }
-          // ---- reference check of tile it-1 (its writes follow the score product) ----
+          // ---- reference check of tile g-1 (its writes follow the score product); at the first
+          //      tile of a request: publish the previous request's sums, switch the query ----
           lds_wait_n<cmin15(C::NCODE + C::NKR)>(tpart);
           bool rare = false;
           float alpha_f = 1.0f;
           bf16x4 pk_fix;
-          if (it >= 1) fix_decide(tpart, rare, alpha_f, pk_fix);
+          if (g >= 1) fix_decide(tpart, rare, alpha_f, pk_fix);
+          if (ts == 0) {
+            if (g >= 1 && (fl_prev & SEG_LAST)) publish_fin(ks - 1);
+            if (s_fl & SEG_FIRST) {
+              mref = kNegInf;
+              lpart = 0.f;
+              set_q();
+            }
+          }
           // ---- S^T = K . Q^T as the K rows arrive ----
           f32x4 s2a = f32x4{0.f, 0.f, 0.f, 0.f}, s2b = s2a, s2c = s2a, s2d = s2a;
           static_for<0, C::KP>([&](auto jc) {
@@ -520,33 +776,35 @@ __device__ __forceinline__ void segment_role(const KParams& p, Smem<C>& sm, int 
             ps += e;
             pk[i] = (__bf16)e;
           }
-          *reinterpret_cast<bf16x4*>(&sm.p[it % 3][r][(16 * tb + 4 * lg) * 2]) = pk;
-          if (lg == 0) sm.tmax[it & 1][tb][r] = tm;
-          if (it >= 1) fix_publish(it - 1, rare, alpha_f, pk_fix);
+          *reinterpret_cast<bf16x4*>(&sm.p[g % 3][r][(16 * tb + 4 * lg) * 2]) = pk;
+          if (lg == 0) sm.tmax[g & 1][tb][r] = tm;
+          if (g >= 1) fix_publish(g - 1, rare, alpha_f, pk_fix);
           scp = sc;
           tmp = tm;
           ps_pend = ps;
-        } else if (it == nt && nt >= 1) {
-          // reference check of the last tile
-          float tpart = ldsr32f(&sm.tmax[(it + 1) & 1][tb ^ 1][r]);
+          if (++ts == s_nt) {
+            ts = 0;
+            fl_prev = s_fl;
+            ++ks;
+          }
+        } else if (g == ntot) {
+          // reference check of the window's last tile
+          float tpart = ldsr32f(&sm.tmax[(g + 1) & 1][tb ^ 1][r]);
           lds_wait_n<0>(tpart);
           bool rare = false;
           float alpha_f = 1.0f;
           bf16x4 pk_fix;
           fix_decide(tpart, rare, alpha_f, pk_fix);
-          fix_publish(it - 1, rare, alpha_f, pk_fix);
-        }
-        if constexpr (ISSUER) {
-          if (it + C::A < nt) issue(it + C::A);
-          if (it + 1 < nt) wait_tile(it + 1, it + C::A < nt - 1 ? it + C::A : nt - 1);
+          fix_publish(g - 1, rare, alpha_f, pk_fix);
+          if (fl_prev & SEG_LAST) publish_fin(ks - 1);
         }
       } else {
-        if constexpr (ISSUER && C::ISS >= 1) {
-          if (it + C::A < nt) issue(it + C::A);
+        if constexpr (C::ISS == 1) {
+          if (g + C::A < ntot) issue(g + C::A);
         }
-        if (it >= 2) {
-          // ---- P . V for tile j = it-2 over columns VC*vw .. +VC ----
-          const int j = it - 2, pj = j % 3;
+        if (g >= 2) {
+          // ---- P . V for tile j = g-2 over columns VC*vw .. +VC ----
+          const int j = g - 2, pj = j % 3;
           const char* kvs = sm.kv[j % C::S];
           i32x2 fl = ldsr64(&sm.flag[pj][0]);
           i32x4 pr[2];
@@ -601,66 +859,28 @@ __device__ __forceinline__ void segment_role(const KParams& p, Smem<C>& sm, int 
 #pragma unroll
             for (int mb = 0; mb < 2; ++mb) acc[mb][cb] = mfma16(pf[mb], vf, acc[mb][cb]);
           });
+          if (++tv == v_nt) {
+            // the request's last tile: its sums were published at the previous step
+            if (v_fl & SEG_LAST) finalize(kv, v_req, v_fl);
+            tv = 0;
+            if (++kv < nseg) {
+              const SegD d = read_seg(kv);
+              v_req = d.req;
+              v_nt = d.nt;
+              v_fl = d.fl;
+            }
+          }
         }
-        if constexpr (ISSUER) {
-          if (C::ISS == 0 && it + C::A < nt) issue(it + C::A);
-          if (it + 1 < nt) wait_tile(it + 1, it + C::A < nt - 1 ? it + C::A : nt - 1);
+        if constexpr (C::ISS == 0) {
+          if (g + C::A < ntot) issue(g + C::A);
         }
+        if (g + 1 < ntot) wait_tile(g + 1, g + C::A < ntot - 1 ? g + C::A : ntot - 1);
       }
       lds_barrier();
     }
+    wait_vmcnt<0>();
+    if (!more) break;
   }
-  wait_vmcnt<0>();
-
-  // ---- epilogue: score waves publish (reference max, sum) per row and token block; value waves
-  //      normalize their columns and write the output (final or partial) and natural-log lse ----
-  if constexpr (ROLE == SCORE) {
-    const float l = sum_lg(lpart);
-    if (lg == 0) {
-      sm.fin[0][tb][r] = mref;
-      sm.fin[1][tb][r] = l;
-    }
-  }
-  lds_barrier();
-  if constexpr (ROLE == VALUE) {
-#pragma unroll
-    for (int mb = 0; mb < 2; ++mb)
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int rr = 16 * mb + 4 * lg + i;
-        if (rr >= nrows) continue;
-        const float m = sm.fin[0][0][rr];
-        const float l = sm.fin[1][0][rr] + sm.fin[1][1][rr];
-        const int jq = rr / hpg, h = rr - jq * hpg;
-        const float inv = l > 0.f ? kscale / l : 0.f;   // fp8 values were accumulated unscaled
-        const float lse_v = l > 0.f ? (m + fast_log2(l)) * kLn2 : kNegInf;
-        const int col = C::VC * vw + ln16;
-        if (so.final_out) {
-          const int64_t ob = (int64_t)(row0 + jq) * p.o_sr + (int64_t)h * p.o_sh + col;
-#pragma unroll
-          for (int cb = 0; cb < C::CB; ++cb) store_out(p.out, p.out_dt, ob + 16 * cb, acc[mb][cb][i] * inv);
-          if (vw == 0 && ln16 == 0 && p.lse) store_out(p.lse, p.lse_dt, (int64_t)(row0 + jq) * p.lse_sr + h, lse_v);
-        } else {
-          float* ob = so.po + (int64_t)jq * so.po_sr + (int64_t)h * so.po_sh + col;
-#pragma unroll
-          for (int cb = 0; cb < C::CB; ++cb) ob[16 * cb] = acc[mb][cb][i] * inv;
-          if (vw == 0 && ln16 == 0) {
-            if (so.plse) so.plse[(int64_t)jq * so.plse_sr + h] = lse_v;
-            else so.po[(int64_t)jq * so.po_sr + (int64_t)h * so.po_sh + C::DCG] = lse_v;
-          }
-        }
-      }
-  }
-  lds_barrier();   // LDS free for the next range
-}
-
-template <class C>
-__device__ __forceinline__ void segment(const KParams& p, Smem<C>& sm, int req, int ta, int te, int L,
-                                        const SegOut& so, float kscale) {
-  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  if (w < 4) segment_role<C, SCORE>(p, sm, req, ta, te, L, so, kscale);
-  else if (!C::DW || w < 8) segment_role<C, VALUE>(p, sm, req, ta, te, L, so, kscale);
-  else if constexpr (C::DW) segment_role<C, DMA>(p, sm, req, ta, te, L, so, kscale);
 }
 
 template <class C>
@@ -668,9 +888,16 @@ __global__ __launch_bounds__(C::NTHR, 1) void ws_kernel(const KParams p) {
   static_assert(sizeof(Smem<C>) <= 163840, "LDS budget of a workgroup");
   __shared__ __attribute__((aligned(16))) Smem<C> sm;
   const float kscale = (C::EB == 1 && p.k_scale) ? *p.k_scale : 1.0f;
-  for_each_segment<C::DCG>(p, [&](int req, int a, int e, int L, const SegOut& so) {
-    segment<C>(p, sm, req, a, e, L, so, kscale);
-  });
+  const bool fixed = p.num_splits > 0;
+  int lo = 0, hi = 0;
+  if (!fixed) {
+    const int chunk = p.plan[0], total = p.plan[1];
+    lo = (int)blockIdx.x * chunk;
+    hi = lo + chunk < total ? lo + chunk : total;
+    if (lo >= hi) return;
+  }
+  if (__builtin_amdgcn_readfirstlane(threadIdx.x >> 6) < 4) role_main<C, SCORE>(p, sm, kscale, fixed, lo, hi);
+  else role_main<C, VALUE>(p, sm, kscale, fixed, lo, hi);
 }
 
 struct Inst {
