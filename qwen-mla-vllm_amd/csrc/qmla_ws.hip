@@ -119,19 +119,22 @@ __device__ __forceinline__ int lanes_below(uint64_t m) {
 
 // Compile-time shape: EB cache element bytes (1 fp8, 2 bf16), RMS tail format, DCG latent columns,
 // A tiles in flight ahead of the score waves, CPR 16-byte chunks staged per row, CAP tanh logit
-// cap, RTR rms codes read transposed (query rows are the heads of one token), ISS when the value
-// waves issue a tile's DMA: 1 before their step, 0 after it.
+// cap, RTR rms codes read transposed (query rows are the heads of one token), ISS who issues a
+// tile's DMA and when: 0 the value waves after their step, 1 before it, 3 between issuing their
+// LDS reads and waiting for them, 2 all eight waves (value waves before their step, score waves
+// after theirs).
 template <int EB_, int RMS_, int DCG_, int A_, int CPR_, bool CAP_, bool RTR_, int ISS_>
 struct WS {
   static constexpr int EB = EB_, RMS = RMS_, DCG = DCG_, A = A_, S = A_ + 3, CPR = CPR_;
   static constexpr bool CAP = CAP_, RTR = RTR_;
   static constexpr int ISS = ISS_;
   static constexpr int NW = 8, NTHR = 64 * NW;
+  static constexpr int NIW = ISS == 2 ? 8 : 4;        // waves sharing a tile's DMA instructions
   static constexpr int RB = 16 * CPR;                 // staged row bytes
   static constexpr int STAGE = TILE * RB;
   static constexpr int NCH = TILE * CPR;              // 16-byte chunks per tile
   static constexpr int NI = (NCH + 63) / 64;          // DMA instructions per tile
-  static constexpr int DPW = (NI + 3) / 4;            // ... per value wave (at most)
+  static constexpr int DPW = (NI + NIW - 1) / NIW;    // ... per issuing wave (at most)
   static constexpr int KQ = (DCG + 64) / 32;          // k-steps of the score product (latent + rope 64)
   static constexpr int KP = KQ / 2;                   // 16-byte K reads per lane and tile
   static constexpr int VC = DCG / 4;                  // latent columns per value wave
@@ -177,9 +180,9 @@ __device__ __forceinline__ int lbyte(int r, int b) {
   return r * (16 * CPR) + 16 * rot<CPR>(b >> 4, r) + (b & 15);
 }
 
-// DMA instructions value wave d issues per tile (instructions d, d+4, ... < NI)
+// DMA instructions issuing wave d issues per tile (instructions d, d+NIW, ... < NI)
 template <class C>
-__device__ __forceinline__ constexpr int dpw(int d) { return (C::NI - d + 3) / 4; }
+__device__ __forceinline__ constexpr int dpw(int d) { return (C::NI - d + C::NIW - 1) / C::NIW; }
 
 // vmcnt <= ahead * D (ahead tiles of D loads each issued after the awaited one), ahead <= K
 template <int D, int K>
@@ -315,12 +318,14 @@ __device__ __forceinline__ void role_main(const KParams& p, Smem<C>& sm, float k
   constexpr bool F8 = C::EB == 1;
   constexpr int NB = C::DCG / 128;       // latent blocks of the fp8 product
   constexpr bool QS = ROLE == SCORE;
-  constexpr int ND = ROLE == VALUE ? C::DPW : 1;
+  constexpr bool ISSUER = ROLE == VALUE || C::ISS == 2;
+  constexpr int ND = ISSUER ? C::DPW : 1;
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int tb = (w >> 1) & 1, smb = w & 1;   // score wave: token block, row block
-  const int vw = w & 3;                        // value wave: column slice and DMA instruction lane
+  const int vw = w & 3;                        // value wave: column slice
+  const int dw = C::NIW == 8 ? w : vw;         // issuing wave: first DMA instruction of a tile
   const int ln16 = lane & 15, lg = lane >> 4;
   const int qrows = p.qrows, hpg = p.hpg;
   const int nrows = qrows * hpg;
@@ -424,10 +429,10 @@ __device__ __forceinline__ void role_main(const KParams& p, Smem<C>& sm, float k
   //      row q / CPR, position q % CPR, i.e. row chunk (position - (row & 15)) mod CPR ----
   uint32_t doff[ND];
   int drow[ND];
-  if constexpr (ROLE == VALUE) {
+  if constexpr (ISSUER) {
 #pragma unroll
     for (int j = 0; j < ND; ++j) {
-      int q = (vw + 4 * j) * 64 + lane;
+      int q = (dw + C::NIW * j) * 64 + lane;
       q = q < C::NCH ? q : C::NCH - 1;
       const int rr = q / C::CPR, pp = q - rr * C::CPR;
       int c = pp - (rr & 15);
@@ -436,7 +441,7 @@ __device__ __forceinline__ void role_main(const KParams& p, Smem<C>& sm, float k
       drow[j] = rr;
     }
   }
-  const bool big = dpw<C>(vw) == C::DPW;
+  const bool big = dpw<C>(dw) == C::DPW;
 
   // reads one piece descriptor (asm reads: no wait on the LDS-DMA in flight); its fields are
   // wave-uniform, so they live in scalar registers (the DMA's buffer resources are built from them)
@@ -568,26 +573,29 @@ __device__ __forceinline__ void role_main(const KParams& p, Smem<C>& sm, float k
       ioff = d.ta % P;
     };
     // issues tile g (the cursor's) into ring stage g % S and advances the cursor
-    auto issue = [&](int g) {
+    // (pid_landed: the page id was read before the last barrier, so no LDS read issued since needs
+    // to complete before it is used)
+    auto issue = [&](int g, bool pid_landed) {
       const int tok0 = i_ta + ti * TILE;
       const int nvalid = i_te - tok0 < TILE ? i_te - tok0 : TILE;
       char* dst = sm.kv[g % C::S];
       if (contig && ioff + TILE <= P) {
         // the tile's rows are consecutive in one page; rows past the piece end read as zeros
-        lds_wait_n<0>(pidv);
+        if (pid_landed) lds_wait_n<15>(pidv);
+        else lds_wait_n<0>(pidv);
         const int pg = __builtin_amdgcn_readfirstlane(pidv);
         const char* base = p.kv + (int64_t)pg * p.page_stride_b + (int64_t)ioff * p.token_stride_b;
         const __amdgpu_buffer_rsrc_t rs = make_rsrc(base, (uint32_t)(nvalid * C::RB));
 #pragma unroll
         for (int j = 0; j < ND; ++j) {
-          const int i = vw + 4 * j;
+          const int i = dw + C::NIW * j;
           if (i < C::NI && (i * 64 + 64 <= C::NCH || i * 64 + lane < C::NCH)) dma16_buf(rs, doff[j], dst + i * 1024);
         }
       } else {
         // per-lane page lookup; rows past the piece end repeat its last row
 #pragma unroll
         for (int j = 0; j < ND; ++j) {
-          const int i = vw + 4 * j;
+          const int i = dw + C::NIW * j;
           if (i < C::NI && (i * 64 + 64 <= C::NCH || i * 64 + lane < C::NCH)) {
             const int rr = drow[j] < nvalid ? drow[j] : nvalid - 1;
             const int tok = tok0 + rr;
@@ -615,20 +623,22 @@ __device__ __forceinline__ void role_main(const KParams& p, Smem<C>& sm, float k
     auto wait_tile = [&](int t, int last) {
       const int ahead = last - t;
       if (big) wait_tiles<C::DPW, C::A - 1>(ahead);
-      else wait_tiles<(C::NI % 4 == 0 ? C::DPW : C::DPW - 1), C::A - 1>(ahead);
+      else wait_tiles<(C::NI % C::NIW == 0 ? C::DPW : C::DPW - 1), C::A - 1>(ahead);
     };
     // score: piece ks, tile ts; value: piece kv, tile tv
     int ks = 0, ts = 0, s_ta = 0, s_nt = 0, s_fl = 0, fl_prev = 0;
     int kv = 0, tv = 0, v_req = 0, v_nt = 0, v_fl = 0;
     if constexpr (ROLE == VALUE) {
-      enter_i();
-      pidv = ldsr32(&sm.pid[ipg]);
       const SegD d = read_seg(0);
       v_req = d.req;
       v_nt = d.nt;
       v_fl = d.fl;
+    }
+    if constexpr (ISSUER) {
+      enter_i();
+      pidv = ldsr32(&sm.pid[ipg]);
       // prologue: tiles 0 .. A-1 in flight, tile 0 landed
-      for (int t = 0; t < C::A && t < ntot; ++t) issue(t);
+      for (int t = 0; t < C::A && t < ntot; ++t) issue(t, false);
       wait_tile(0, (C::A < ntot ? C::A : ntot) - 1);
     }
     lds_barrier();
@@ -798,19 +808,24 @@ __device__ __forceinline__ void role_main(const KParams& p, Smem<C>& sm, float k
           fix_publish(g - 1, rare, alpha_f, pk_fix);
           if (fl_prev & SEG_LAST) publish_fin(ks - 1);
         }
-      } else {
-        if constexpr (C::ISS == 1) {
-          if (g + C::A < ntot) issue(g + C::A);
+        if constexpr (C::ISS == 2) {
+          if (g + C::A < ntot) issue(g + C::A, false);
+          if (g + 1 < ntot) wait_tile(g + 1, g + C::A < ntot - 1 ? g + C::A : ntot - 1);
         }
+      } else {
+        if constexpr (C::ISS == 1 || C::ISS == 2) {
+          if (g + C::A < ntot) issue(g + C::A, false);
+        }
+        // ---- P . V for tile j = g-2 over columns VC*vw .. +VC: reads first ----
+        const int j = g - 2, pj = (g + 1) % 3;
+        i32x2 fl = {0, 0};
+        i32x4 pr[2];
+        i32x2 vraw[C::CB][C::EB];
         if (g >= 2) {
-          // ---- P . V for tile j = g-2 over columns VC*vw .. +VC ----
-          const int j = g - 2, pj = j % 3;
           const char* kvs = sm.kv[j % C::S];
-          i32x2 fl = ldsr64(&sm.flag[pj][0]);
-          i32x4 pr[2];
+          fl = ldsr64(&sm.flag[pj][0]);
 #pragma unroll
           for (int mb = 0; mb < 2; ++mb) pr[mb] = ldsr128(&sm.p[pj][16 * mb + ln16][(8 * lg) * 2]);
-          i32x2 vraw[C::CB][C::EB];
 #pragma unroll
           for (int cb = 0; cb < C::CB; ++cb) {
             const int col0 = C::VC * vw + 16 * cb;
@@ -824,6 +839,12 @@ __device__ __forceinline__ void role_main(const KParams& p, Smem<C>& sm, float k
               vraw[cb][C::EB - 1] = lds_read_tr16_async(kvs + lbyte<C::CPR>(vr + 4, vb));
             }
           }
+        }
+        // the DMA issue stalls while the memory pipeline is full: let the reads land meanwhile
+        if constexpr (C::ISS == 3) {
+          if (g + C::A < ntot) issue(g + C::A, true);
+        }
+        if (g >= 2) {
           lds_wait_n<cmin15(2 + C::NVR)>(fl);
           const int f0 = __builtin_amdgcn_readfirstlane(fl[0]), f1 = __builtin_amdgcn_readfirstlane(fl[1]);
           if (f0 | f1) {
@@ -872,7 +893,7 @@ __device__ __forceinline__ void role_main(const KParams& p, Smem<C>& sm, float k
           }
         }
         if constexpr (C::ISS == 0) {
-          if (g + C::A < ntot) issue(g + C::A);
+          if (g + C::A < ntot) issue(g + C::A, false);
         }
         if (g + 1 < ntot) wait_tile(g + 1, g + C::A < ntot - 1 ? g + C::A : ntot - 1);
       }
