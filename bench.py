@@ -277,7 +277,10 @@ def main():
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "bf16",
-        "storage": ("e4m3 latent/rope + u8 log8 rms; bf16 MFMA operands, fp32 accumulate and softmax"
+        "storage": (("e4m3 latent/rope + u8 log8 rms; scores on the fp8 MFMAs (cache bytes as stored, query as "
+                     "e4m3 hi+lo, 8 significant bits), bf16 P.V, fp32 accumulate and softmax")
+                    if case.kv == "fp8" and case.groups == 1 and case.qrows * case.heads <= 32 else
+                    "e4m3 latent/rope + u8 log8 rms; bf16 MFMA operands, fp32 accumulate and softmax"
                     if case.kv == "fp8" else "bf16 cache; bf16 MFMA operands, fp32 accumulate and softmax"),
         "data": "synthetic",
         "config": {"workload": f"mla_decode_{args.workload}", "batch": n_req, "rows": rows, "heads": H,
