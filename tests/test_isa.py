@@ -1,0 +1,70 @@
+"""The warp-specialized decode waits for its LDS reads with counted `s_waitcnt lgkmcnt(N)`: LDS
+operations complete in order, but scalar memory loads share that counter and complete out of
+order, so the counts are only right while no scalar load is in flight. The compiler may place
+scalar loads (kernel arguments it reloads) anywhere; this test compiles the kernel to gfx950
+assembly exactly as the library is built and checks that every scalar load is drained
+(`lgkmcnt(0)`) before the next LDS operation or counted wait. CPU only (hipcc cross-compiles).
+"""
+import pathlib
+import re
+import subprocess
+import sys
+
+import pytest
+
+REPO = pathlib.Path(__file__).resolve().parent.parent
+sys.path.insert(0, str(REPO / "qwen-mla-vllm_amd"))
+
+
+def _assembly(tmp_path, source):
+    import build as qbuild
+    try:
+        hipcc = qbuild.hipcc()
+    except RuntimeError:
+        pytest.skip("hipcc not available")
+    extra = dict((s.name, e) for s, e in qbuild.SOURCES)[source]
+    out = tmp_path / (source + ".s")
+    cmd = [hipcc, *qbuild.COMMON_FLAGS, *extra, f"-I{REPO / 'include'}", f"-I{qbuild.CSRC}", "--cuda-device-only",
+           "-S", str(qbuild.CSRC / source), "-o", str(out)]
+    r = subprocess.run(cmd, capture_output=True, text=True, timeout=600)
+    assert r.returncode == 0, r.stderr[-2000:]
+    return out.read_text().splitlines()
+
+
+def _kernels(lines, pattern):
+    starts = [i for i, l in enumerate(lines) if re.match(pattern, l)]
+    for s in starts:
+        e = next(i for i in range(s, len(lines)) if "s_endpgm" in lines[i])
+        yield lines[s].split(":")[0], lines[s:e]
+
+
+def _hazards(body):
+    found = []
+    for i, line in enumerate(body):
+        if not re.search(r"\bs_(buffer_)?load_", line):
+            continue
+        for j in range(i + 1, len(body)):
+            t = body[j]
+            if "s_waitcnt" in t and "lgkmcnt(0)" in t:
+                break
+            if re.search(r"\bds_(read|write)", t) or re.search(r"lgkmcnt\([1-9]", t):
+                found.append((i, j, t.strip()))
+                break
+    return found
+
+
+def test_ws_scalar_loads_drained_before_lds(tmp_path):
+    lines = _assembly(tmp_path, "qmla_ws.hip")
+    n = 0
+    for name, body in _kernels(lines, r"^_ZN4qmla2ws9ws_kernel\S*:"):
+        n += 1
+        hz = _hazards(body)
+        assert not hz, f"{name}: scalar load in flight at an LDS operation: {hz[:3]}"
+        assert any("lgkmcnt(" in l and "lgkmcnt(0)" not in l for l in body), "counted waits expected"
+    assert n >= 1
+
+
+def test_hazard_check_sees_a_planted_overlap():
+    body = ["s_load_dword s4, s[0:1], 0x10", "ds_read_b128 v[0:3], v4", "s_waitcnt lgkmcnt(0)"]
+    assert _hazards(body)
+    assert not _hazards(["s_load_dword s4, s[0:1], 0x10", "s_waitcnt lgkmcnt(0)", "ds_read_b128 v[0:3], v4"])
