@@ -156,6 +156,35 @@ int qmla_plan(const qmla_decode_params* p, void* stream);
 int qmla_decode_partial(const qmla_decode_params* p, void* stream);
 int qmla_combine(const qmla_decode_params* p, void* stream);
 
+/* ---- cache-row writer ---------------------------------------------------------------------
+ * Replaces QwenMLATritonImpl.do_kv_cache_update (qwen_mla/mla_impl.py:309-342) and, for the rows it
+ * hands to vLLM (bf16 caches; FP8 caches whose rms is stored as e4m3), vLLM's concat_and_cache_mla:
+ * one new token per input row, written at its flat cache slot as
+ *   FP8:  [latent e4m3 | rope e4m3 | rms tail | (pad untouched)] with e4m3 = RNE of
+ *         clamp(x * (1/k_scale), -448, 448) in fp32; rms tail = log8 code per head
+ *         (round-half-even of (log2(max(r, 1e-30)) + 3) * 42.5, clamped to [0, 255]), or the rms
+ *         as 2 bf16 bytes per head, or e4m3 like the rope, or nothing;
+ *   bf16: [latent | rope | rms (rms_heads elements, or none)] copied.
+ * Slot -1 (padding) is redirected to slot 0 (vLLM's never-read null block) as the reference does;
+ * slots >= num_slots are skipped. Inputs are bf16. Asynchronous on `stream`, allocates nothing. */
+typedef struct qmla_cache_write_params {
+  const void* kv_c;               /* [n, d_c] bf16 */
+  int64_t kv_c_stride;            /* elements between rows */
+  const void* k_pe;               /* [n, rope_w + rms tail] bf16: rope, then the per-head rms */
+  int64_t k_pe_stride;
+  const int64_t* slots;           /* [n] page * page_size + token */
+  int32_t n, d_c, rope_w, rms_heads;
+  int32_t kv_dtype;               /* QMLA_KV_FP8 or QMLA_KV_BF16 */
+  int32_t rms_mode;               /* FP8: QMLA_RMS_LOG8, _BF16_BYTES, _E4M3, _NONE; bf16: _BF16, _NONE */
+  const float* k_scale;           /* FP8: device scalar (per-layer scale) */
+  void* cache;                    /* [num_pages, page_size, (1,) row] */
+  int64_t page_stride, token_stride;   /* bytes */
+  int32_t page_size;
+  int64_t num_slots;              /* num_pages * page_size */
+} qmla_cache_write_params;
+
+int qmla_cache_write(const qmla_cache_write_params* p, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -1041,8 +1041,9 @@ extern "C" {
 int qmla_version(void) { return QMLA_ABI_VERSION; }
 
 const char* qmla_build_info(void) {
-  return "qmla gfx950: LDS-DMA paged rows, MFMA 16x16x32 bf16 QK/PV, tr8/tr16 value reads, "
-         "fixed and balanced split-K + LSE combine, column-split single-pass wide latent (d_c 1792)";
+  return "qmla gfx950: warp-specialized FP8 decode (fp8 MFMA scores, query as e4m3 hi+lo), segment decode "
+         "(bf16 MFMA QK/PV) for bf16 / verify / GLA, column-split single-pass wide latent (d_c 1792); "
+         "LDS-DMA paged rows, tr8/tr16 value reads, fixed and balanced split-K + LSE combine; cache-row writer";
 }
 
 size_t qmla_workspace_bytes(const qmla_decode_params* p) {

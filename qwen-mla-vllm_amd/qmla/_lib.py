@@ -82,8 +82,33 @@ class DecodeParams(ctypes.Structure):
     ]
 
 
+class CacheWriteParams(ctypes.Structure):
+    """Mirror of `qmla_cache_write_params` (include/qmla.h); field order and types must match."""
+
+    _fields_ = [
+        ("kv_c", ctypes.c_void_p),
+        ("kv_c_stride", ctypes.c_int64),
+        ("k_pe", ctypes.c_void_p),
+        ("k_pe_stride", ctypes.c_int64),
+        ("slots", ctypes.c_void_p),
+        ("n", ctypes.c_int32),
+        ("d_c", ctypes.c_int32),
+        ("rope_w", ctypes.c_int32),
+        ("rms_heads", ctypes.c_int32),
+        ("kv_dtype", ctypes.c_int32),
+        ("rms_mode", ctypes.c_int32),
+        ("k_scale", ctypes.c_void_p),
+        ("cache", ctypes.c_void_p),
+        ("page_stride", ctypes.c_int64),
+        ("token_stride", ctypes.c_int64),
+        ("page_size", ctypes.c_int32),
+        ("num_slots", ctypes.c_int64),
+    ]
+
+
 # every function include/qmla.h declares, with its ctypes signature
 _P = ctypes.POINTER(DecodeParams)
+_W = ctypes.POINTER(CacheWriteParams)
 SIGNATURES = {
     "qmla_version": (ctypes.c_int, []),
     "qmla_build_info": (ctypes.c_char_p, []),
@@ -92,6 +117,7 @@ SIGNATURES = {
     "qmla_plan": (ctypes.c_int, [_P, ctypes.c_void_p]),
     "qmla_decode_partial": (ctypes.c_int, [_P, ctypes.c_void_p]),
     "qmla_combine": (ctypes.c_int, [_P, ctypes.c_void_p]),
+    "qmla_cache_write": (ctypes.c_int, [_W, ctypes.c_void_p]),
 }
 
 _lib = None

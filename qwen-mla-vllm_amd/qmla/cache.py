@@ -1,0 +1,87 @@
+"""Cache-row writer: the new token's latent, rope and rms tail into its paged slot.
+
+Mirrors QwenMLATritonImpl.do_kv_cache_update (qwen_mla/mla_impl.py:309-342): FP8 caches get
+`[latent e4m3 | rope e4m3 | rms tail]` with e4m3 = RNE of clamp(x * (1/k_scale), -448, 448) and the
+tail a log8 code per head (mode "log8"), the rms as two bf16 bytes per head ("bf16"), or e4m3 like
+the rope ("e4m3", the bytes vLLM's concat_and_cache_mla writes for the plugin in that mode); bf16
+caches get the row copied. Padding slots (-1) go to slot 0, vLLM's never-read null block. Runs as one
+HIP kernel on the current stream (libqmla.so, `qmla_cache_write`); there is no CPU path.
+"""
+from __future__ import annotations
+
+import ctypes
+
+import torch
+
+from . import _lib
+
+_RMS_WRITE = {"log8": _lib.RMS_LOG8, "bf16": _lib.RMS_BF16_BYTES, "e4m3": _lib.RMS_E4M3}
+
+
+def _stream() -> int:
+    return torch.cuda.current_stream().cuda_stream
+
+
+def cache_write(kv_c: torch.Tensor, k_pe: torch.Tensor, kv_cache: torch.Tensor, slot_mapping: torch.Tensor, *,
+                d_c: int | None = None, rope_w: int, rms_heads: int, kv_fp8: bool | None = None,
+                rms: str = "log8", k_scale: torch.Tensor | None = None) -> None:
+    """Write len(slot_mapping) rows: kv_c [>= n, d_c] and k_pe [>= n, rope_w + rms tail] (bf16) into
+    kv_cache [num_pages, page_size, (1,) row] at the flat slots (page * page_size + token).
+
+    rms: "log8" | "bf16" | "e4m3" | "none" for FP8 caches, "bf16" | "none" for bf16 caches.
+    """
+    slots = slot_mapping.reshape(-1)
+    n = slots.shape[0]
+    if kv_fp8 is None:
+        kv_fp8 = kv_cache.dtype in (torch.uint8, torch.float8_e4m3fn)
+    if d_c is None:
+        d_c = kv_c.shape[-1]
+    for t in (kv_c, k_pe, kv_cache, slots):
+        if not t.is_cuda:
+            raise ValueError("cache_write: every tensor must live on the GPU")
+    if kv_c.dtype != torch.bfloat16 or k_pe.dtype != torch.bfloat16:
+        raise TypeError("cache_write: kv_c and k_pe must be bf16")
+    kv_c2 = kv_c.reshape(kv_c.shape[0], -1)
+    k_pe2 = k_pe.reshape(k_pe.shape[0], -1)
+    if kv_c2.shape[0] < n or k_pe2.shape[0] < n:
+        raise ValueError("cache_write: fewer input rows than slots")
+    if kv_c2.stride(-1) != 1 or k_pe2.stride(-1) != 1:
+        raise ValueError("cache_write: rows must be contiguous in their last dimension")
+    slots = slots.to(torch.int64)
+    p = _lib.CacheWriteParams()
+    p.kv_c, p.kv_c_stride = kv_c2.data_ptr(), kv_c2.stride(0)
+    p.k_pe, p.k_pe_stride = k_pe2.data_ptr(), k_pe2.stride(0)
+    p.slots = slots.data_ptr()
+    p.n, p.d_c, p.rope_w, p.rms_heads = n, d_c, rope_w, rms_heads
+    if kv_fp8:
+        p.kv_dtype = _lib.KV_FP8
+        p.rms_mode = _lib.RMS_NONE if rms == "none" else _RMS_WRITE[rms]
+        if k_scale is None:
+            raise ValueError("cache_write: FP8 caches need k_scale")
+        ks = k_scale.reshape(-1)[:1].to(device=kv_cache.device, dtype=torch.float32).contiguous()
+        p.k_scale = ks.data_ptr()
+    else:
+        p.kv_dtype = _lib.KV_BF16
+        p.rms_mode = {"bf16": _lib.RMS_BF16, "none": _lib.RMS_NONE}[rms]
+    esz = kv_cache.element_size()
+    p.cache = kv_cache.data_ptr()
+    p.page_stride, p.token_stride = kv_cache.stride(0) * esz, kv_cache.stride(1) * esz
+    p.page_size = kv_cache.shape[1]
+    p.num_slots = kv_cache.shape[0] * kv_cache.shape[1]
+    _lib.check("qmla_cache_write", _lib.lib().qmla_cache_write(ctypes.byref(p), _stream()))
+    if kv_fp8:
+        ks.record_stream(torch.cuda.current_stream())
+
+
+def do_kv_cache_update(kv_c_normed: torch.Tensor, k_pe: torch.Tensor, kv_cache: torch.Tensor,
+                       slot_mapping: torch.Tensor, kv_cache_dtype: str, k_scale: torch.Tensor, *,
+                       packed_rope: int, n_heads: int, rms_mode: str = "log8") -> None:
+    """The reference method's signature (mla_impl.py:309) with the layer attributes it reads
+    (`mla_packed_rope`, `mla_local_heads`, `mla_fp8_rms_mode()`) as keywords. kv_cache_dtype
+    "fp8*" writes FP8 rows, anything else bf16 rows with the rms tail copied."""
+    if kv_cache.numel() == 0:
+        return
+    fp8 = str(kv_cache_dtype).startswith("fp8")
+    d_c = kv_c_normed.shape[-1]
+    cache_write(kv_c_normed, k_pe, kv_cache, slot_mapping, d_c=d_c, rope_w=packed_rope, rms_heads=n_heads,
+                kv_fp8=fp8, rms=(rms_mode if fp8 else "bf16"), k_scale=k_scale)

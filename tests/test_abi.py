@@ -24,7 +24,7 @@ def _declared_functions() -> list[str]:
 
 def test_header_functions_exported_and_bound():
     names = _declared_functions()
-    assert "qmla_decode" in names and len(names) >= 7
+    assert "qmla_decode" in names and "qmla_cache_write" in names and len(names) >= 8
     lib = _lib.lib()
     for n in names:
         assert hasattr(lib, n), n
@@ -163,3 +163,50 @@ def test_product_path_refuses_cpu_tensors():
         qmla.forward(case_q, torch.zeros(1, 24, 64, dtype=torch.bfloat16),
                      torch.zeros(1, 64, 1, 608, dtype=torch.uint8), torch.zeros(1, 1, dtype=torch.int32),
                      torch.ones(1, dtype=torch.int32), page_size=64, sm_scale=0.1, kv_fp8=True)
+
+
+def test_cache_write_struct_mirror_matches_header():
+    text = HEADER.read_text()
+    body = text[text.index("typedef struct qmla_cache_write_params"):text.index("} qmla_cache_write_params;")]
+    body = re.sub(r"/\*.*?\*/", "", body, flags=re.S)
+    fields = []
+    for decl in body.split("{", 1)[1].split(";"):
+        decl = decl.strip()
+        if not decl:
+            continue
+        parts = decl.split(",")
+        fields.append(re.findall(r"(\w+)\s*$", parts[0])[0])
+        fields.extend(re.sub(r"[\*\s]", "", x) for x in parts[1:])
+    assert fields == [f[0] for f in _lib.CacheWriteParams._fields_]
+
+
+def _write_params(**over) -> _lib.CacheWriteParams:
+    p = _lib.CacheWriteParams()
+    base = 0x10000
+    p.kv_c, p.kv_c_stride, p.k_pe, p.k_pe_stride = base, 512, base + 0x100000, 96
+    p.slots, p.n, p.d_c, p.rope_w, p.rms_heads = base + 0x200000, 8, 512, 64, 24
+    p.kv_dtype, p.rms_mode, p.k_scale = _lib.KV_FP8, _lib.RMS_LOG8, base + 0x300000
+    p.cache, p.page_stride, p.token_stride, p.page_size, p.num_slots = base + 0x400000, 64 * 608, 608, 64, 6400
+    for k, v in over.items():
+        setattr(p, k, v)
+    return p
+
+
+@pytest.mark.parametrize("over,code", [
+    (dict(kv_c=None), _lib.ERR_NULL),
+    (dict(k_scale=None), _lib.ERR_NULL),
+    (dict(kv_dtype=5), _lib.ERR_MODE),
+    (dict(rms_mode=_lib.RMS_BF16), _lib.ERR_MODE),                          # bf16 element in an fp8 row
+    (dict(kv_dtype=_lib.KV_BF16, rms_mode=_lib.RMS_LOG8), _lib.ERR_MODE),
+    (dict(d_c=508), _lib.ERR_SHAPE),
+    (dict(token_stride=592, page_stride=64 * 592), _lib.ERR_SHAPE),        # 600 bytes do not fit
+    (dict(rms_mode=_lib.RMS_BF16_BYTES), _lib.ERR_SHAPE),                   # 624 bytes do not fit 608
+    (dict(k_pe_stride=80), _lib.ERR_SHAPE),                                 # rope + 24 codes do not fit
+    (dict(kv_c=0x10008), _lib.ERR_ALIGN),
+    (dict(kv_c_stride=516), _lib.ERR_ALIGN),
+    (dict(n=0), _lib.OK),
+])
+def test_cache_write_error_codes(over, code):
+    p = _write_params(**over)
+    assert _lib.lib().qmla_cache_write(ctypes.byref(p), None) == code
+    assert _lib.lib().qmla_cache_write(None, None) == _lib.ERR_NULL
