@@ -185,6 +185,38 @@ typedef struct qmla_cache_write_params {
 
 int qmla_cache_write(const qmla_cache_write_params* p, void* stream);
 
+/* ---- prefill context gather -----------------------------------------------------------------
+ * Replaces gather_cache_torch (qwen_mla/ops/mla_gather.py:28-76), the plugin's stand-in for vLLM's
+ * gather_and_maybe_dequant_cache on the chunked-context prefill path. Destination row j reads
+ *   s = token_to_seq[j], tok = j - cu_seq_lens[s] (+ seq_starts[s]), page block_table[s, tok / P],
+ * slot tok % P. bf16 caches: the row is copied (row_elems elements). FP8 caches: dst[j, :rms_offset]
+ * = e4m3 * scale (fp32 product, rounded to dst's dtype), then one element per head at rms_offset:
+ * 2^(-3 + code*6/255) (log8), the raw bf16 (two bytes per head), or e4m3 * scale (e4m3 mode);
+ * columns past rms_offset + rms_heads are not written. Rows whose metadata points outside
+ * [0, num_seqs), [0, bt_cols) or [0, num_pages) are not written. Asynchronous, allocates nothing. */
+typedef struct qmla_gather_params {
+  const void* cache;              /* [num_pages, page_size, (1,) row] */
+  int64_t page_stride, token_stride;   /* bytes */
+  int32_t page_size, num_pages;
+  int32_t kv_dtype;               /* QMLA_KV_FP8 or QMLA_KV_BF16 */
+  int32_t rms_mode;               /* FP8: QMLA_RMS_LOG8, _BF16_BYTES, _E4M3 */
+  int32_t rms_offset, rms_heads;  /* FP8: latent + rope columns, heads of the rms tail */
+  int32_t row_elems;              /* bf16: elements copied per row */
+  const float* scale;             /* FP8: device scalar */
+  const int32_t* block_table;     /* [num_seqs, bt_cols] */
+  int64_t bt_stride;
+  int32_t num_seqs, bt_cols;
+  const int32_t* cu_seq_lens;     /* [num_seqs + 1] first destination row of each sequence */
+  const int32_t* token_to_seq;    /* [>= num_tokens] */
+  const int32_t* seq_starts;      /* [num_seqs] or NULL: first sequence token of this chunk */
+  int32_t num_tokens;
+  void* dst;                      /* [>= num_tokens, >= width] */
+  int64_t dst_stride;             /* elements between rows */
+  int32_t dst_dtype;              /* QMLA_DT_BF16 or QMLA_DT_F16 */
+} qmla_gather_params;
+
+int qmla_gather(const qmla_gather_params* p, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -1,4 +1,5 @@
-// qmla_write.hip -- gfx950 cache-row writer: one new token per input row into its paged cache slot.
+// qmla_write.hip -- gfx950 cache-row kernels: the writer (one new token per input row into its paged
+// cache slot) and the prefill context gather (paged rows back into a dense bf16 workspace).
 //
 // Reference: qwen_mla/mla_impl.py:309-342 (QwenMLATritonImpl.do_kv_cache_update, the FP8 writer
 // with log8 or bf16-byte rms tails) and vLLM's concat_and_cache_mla for the rows the plugin hands
@@ -158,6 +159,177 @@ extern "C" int qmla_cache_write(const qmla_cache_write_params* p, void* stream) 
   void* args[] = {&k};
   const unsigned grid = (unsigned)((p->n + wr::ROWS_PER_WG - 1) / wr::ROWS_PER_WG);
   const hipError_t e = hipLaunchKernel((const void*)wr::write_kernel, dim3(grid), dim3(64 * wr::ROWS_PER_WG), args,
+                                       0, (hipStream_t)stream);
+  return e == hipSuccess ? QMLA_OK : QMLA_ERR_LAUNCH;
+}
+
+// ---- prefill context gather (qwen_mla/ops/mla_gather.py:28-76) -----------------------------------
+// One wave per destination row: the row's sequence, token and page from the chunk metadata, then the
+// cached row copied (bf16 caches) or dequantized into the destination dtype (FP8 caches).
+namespace qmla {
+namespace ga {
+
+constexpr int ROWS_PER_WG = 4;
+
+struct GParams {
+  const char* cache;
+  int64_t page_stride, token_stride;
+  int page_size, num_pages, kv_dtype, rms_mode, rms_offset, rms_heads, row_elems;
+  const float* scale;
+  const int32_t* block_table;
+  int64_t bt_stride;
+  int num_seqs, bt_cols;
+  const int32_t* cu_seq_lens;
+  const int32_t* token_to_seq;
+  const int32_t* seq_starts;
+  int num_tokens;
+  char* dst;
+  int64_t dst_stride;
+  int dst_dtype;
+};
+
+// one e4m3 byte (byte k of w) -> fp32; the conversion returns +0 for the negative zero 0x80, so the
+// sign bit is put back (torch decodes 0x80 as -0.0, which survives the scale and the rounding)
+__device__ __forceinline__ float e4m3_f32(int w, int k) {
+  float f;
+  switch (k) {
+    case 0: f = __builtin_amdgcn_cvt_f32_fp8(w, 0); break;
+    case 1: f = __builtin_amdgcn_cvt_f32_fp8(w, 1); break;
+    case 2: f = __builtin_amdgcn_cvt_f32_fp8(w, 2); break;
+    default: f = __builtin_amdgcn_cvt_f32_fp8(w, 3); break;
+  }
+  return __uint_as_float(__float_as_uint(f) | (((uint32_t)w >> (8 * k + 7)) & 1u) << 31);
+}
+
+// fp32 -> the destination dtype, round to nearest even; the sign bit is carried over explicitly so a
+// negative zero stays negative whatever instruction the conversion compiles to
+__device__ __forceinline__ uint16_t to_out(float x, int dt) {
+  const uint16_t sign = (uint16_t)((__float_as_uint(x) >> 16) & 0x8000u);
+  if (dt == QMLA_DT_F16) return (uint16_t)(__builtin_bit_cast(uint16_t, (_Float16)x) | sign);
+  return (uint16_t)(__builtin_bit_cast(uint16_t, (__bf16)x) | sign);
+}
+
+__global__ __launch_bounds__(64 * ROWS_PER_WG) void gather_kernel(const GParams p) {
+  const int lane = threadIdx.x & 63;
+  const int j = (int)blockIdx.x * ROWS_PER_WG + (int)(threadIdx.x >> 6);
+  if (j >= p.num_tokens) return;
+  const int s = p.token_to_seq[j];
+  if (s < 0 || s >= p.num_seqs) return;
+  int64_t tok = (int64_t)j - p.cu_seq_lens[s];
+  if (p.seq_starts) tok += p.seq_starts[s];
+  if (tok < 0) return;
+  const int64_t pi = tok / p.page_size;
+  if (pi >= p.bt_cols) return;
+  const int blk = p.block_table[(int64_t)s * p.bt_stride + pi];
+  if (blk < 0 || blk >= p.num_pages) return;
+  const char* row = p.cache + (int64_t)blk * p.page_stride + (tok - pi * p.page_size) * p.token_stride;
+  uint16_t* out = reinterpret_cast<uint16_t*>(p.dst) + (int64_t)j * p.dst_stride;
+
+  if (p.kv_dtype == QMLA_KV_BF16) {
+    const uint16_t* src = reinterpret_cast<const uint16_t*>(row);
+    if (p.dst_dtype == QMLA_DT_BF16) {
+      const int nv = p.row_elems / 8;
+      for (int c = lane; c < nv; c += 64)
+        reinterpret_cast<uint4*>(out)[c] = reinterpret_cast<const uint4*>(src)[c];
+      for (int c = 8 * nv + lane; c < p.row_elems; c += 64) out[c] = src[c];
+    } else {
+      for (int c = lane; c < p.row_elems; c += 64) out[c] = to_out(__uint_as_float((uint32_t)src[c] << 16), p.dst_dtype);
+    }
+    return;
+  }
+  const float sc = *p.scale;
+  // latent + rope: e4m3 * scale in fp32, rounded to the destination dtype
+  for (int c = 8 * lane; c < p.rms_offset; c += 512) {
+    const uint2 raw = *reinterpret_cast<const uint2*>(row + c);
+    const uint32_t w[2] = {raw.x, raw.y};
+    uint32_t o[4];
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const int wv = (int)w[h];
+      const float f0 = e4m3_f32(wv, 0) * sc, f1 = e4m3_f32(wv, 1) * sc;
+      const float f2 = e4m3_f32(wv, 2) * sc, f3 = e4m3_f32(wv, 3) * sc;
+      o[2 * h] = (uint32_t)to_out(f0, p.dst_dtype) | ((uint32_t)to_out(f1, p.dst_dtype) << 16);
+      o[2 * h + 1] = (uint32_t)to_out(f2, p.dst_dtype) | ((uint32_t)to_out(f3, p.dst_dtype) << 16);
+    }
+    *reinterpret_cast<uint4*>(out + c) = make_uint4(o[0], o[1], o[2], o[3]);
+  }
+  // the rms tail: one element per head at rms_offset
+  const unsigned char* tail = reinterpret_cast<const unsigned char*>(row) + p.rms_offset;
+  for (int h = lane; h < p.rms_heads; h += 64) {
+    float v;
+    if (p.rms_mode == QMLA_RMS_LOG8) {
+      v = (float)exp2(-3.0 + (double)tail[h] * (6.0 / 255.0));   // 2^(-3 + code*6/255)
+    } else if (p.rms_mode == QMLA_RMS_BF16_BYTES) {
+      const uint32_t bits = (uint32_t)tail[2 * h] | ((uint32_t)tail[2 * h + 1] << 8);
+      if (p.dst_dtype == QMLA_DT_BF16) {
+        out[p.rms_offset + h] = (uint16_t)bits;
+        continue;
+      }
+      v = __uint_as_float(bits << 16);
+    } else {
+      v = e4m3_f32((int)tail[h], 0) * sc;
+    }
+    out[p.rms_offset + h] = to_out(v, p.dst_dtype);
+  }
+}
+
+}  // namespace ga
+}  // namespace qmla
+
+extern "C" int qmla_gather(const qmla_gather_params* p, void* stream) {
+  using namespace qmla;
+  if (!p) return QMLA_ERR_NULL;
+  if (p->num_tokens == 0) return QMLA_OK;
+  if (!p->cache || !p->block_table || !p->cu_seq_lens || !p->token_to_seq || !p->dst) return QMLA_ERR_NULL;
+  if (p->num_tokens < 0 || p->page_size <= 0 || p->num_pages <= 0 || p->num_seqs <= 0 || p->bt_cols <= 0 ||
+      p->bt_stride < p->bt_cols)
+    return QMLA_ERR_SHAPE;
+  if (p->dst_dtype != QMLA_DT_BF16 && p->dst_dtype != QMLA_DT_F16) return QMLA_ERR_MODE;
+  const bool fp8 = p->kv_dtype == QMLA_KV_FP8;
+  if (!fp8 && p->kv_dtype != QMLA_KV_BF16) return QMLA_ERR_MODE;
+  int64_t width;
+  if (fp8) {
+    if (p->rms_mode != QMLA_RMS_LOG8 && p->rms_mode != QMLA_RMS_BF16_BYTES && p->rms_mode != QMLA_RMS_E4M3)
+      return QMLA_ERR_MODE;
+    if (!p->scale) return QMLA_ERR_NULL;
+    if (p->rms_offset <= 0 || p->rms_offset % 8 || p->rms_heads < 0) return QMLA_ERR_SHAPE;
+    const int64_t rb = p->rms_mode == QMLA_RMS_BF16_BYTES ? 2 : 1;
+    if (p->rms_offset + rb * p->rms_heads > p->token_stride) return QMLA_ERR_SHAPE;
+    width = (int64_t)p->rms_offset + p->rms_heads;
+  } else {
+    if (p->row_elems <= 0 || 2 * (int64_t)p->row_elems > p->token_stride) return QMLA_ERR_SHAPE;
+    width = p->row_elems;
+  }
+  if (p->dst_stride < width || p->page_stride < p->token_stride * p->page_size) return QMLA_ERR_SHAPE;
+  if (((uintptr_t)p->cache | (uintptr_t)p->dst) % 16 || p->token_stride % 16 || p->page_stride % 16 ||
+      (p->dst_stride * 2) % 16)
+    return QMLA_ERR_ALIGN;
+  ga::GParams k;
+  k.cache = static_cast<const char*>(p->cache);
+  k.page_stride = p->page_stride;
+  k.token_stride = p->token_stride;
+  k.page_size = p->page_size;
+  k.num_pages = p->num_pages;
+  k.kv_dtype = p->kv_dtype;
+  k.rms_mode = p->rms_mode;
+  k.rms_offset = p->rms_offset;
+  k.rms_heads = p->rms_heads;
+  k.row_elems = p->row_elems;
+  k.scale = p->scale;
+  k.block_table = p->block_table;
+  k.bt_stride = p->bt_stride;
+  k.num_seqs = p->num_seqs;
+  k.bt_cols = p->bt_cols;
+  k.cu_seq_lens = p->cu_seq_lens;
+  k.token_to_seq = p->token_to_seq;
+  k.seq_starts = p->seq_starts;
+  k.num_tokens = p->num_tokens;
+  k.dst = static_cast<char*>(p->dst);
+  k.dst_stride = p->dst_stride;
+  k.dst_dtype = p->dst_dtype;
+  void* args[] = {&k};
+  const unsigned grid = (unsigned)((p->num_tokens + ga::ROWS_PER_WG - 1) / ga::ROWS_PER_WG);
+  const hipError_t e = hipLaunchKernel((const void*)ga::gather_kernel, dim3(grid), dim3(64 * ga::ROWS_PER_WG), args,
                                        0, (hipStream_t)stream);
   return e == hipSuccess ? QMLA_OK : QMLA_ERR_LAUNCH;
 }

@@ -106,9 +106,39 @@ class CacheWriteParams(ctypes.Structure):
     ]
 
 
+class GatherParams(ctypes.Structure):
+    """Mirror of `qmla_gather_params` (include/qmla.h); field order and types must match."""
+
+    _fields_ = [
+        ("cache", ctypes.c_void_p),
+        ("page_stride", ctypes.c_int64),
+        ("token_stride", ctypes.c_int64),
+        ("page_size", ctypes.c_int32),
+        ("num_pages", ctypes.c_int32),
+        ("kv_dtype", ctypes.c_int32),
+        ("rms_mode", ctypes.c_int32),
+        ("rms_offset", ctypes.c_int32),
+        ("rms_heads", ctypes.c_int32),
+        ("row_elems", ctypes.c_int32),
+        ("scale", ctypes.c_void_p),
+        ("block_table", ctypes.c_void_p),
+        ("bt_stride", ctypes.c_int64),
+        ("num_seqs", ctypes.c_int32),
+        ("bt_cols", ctypes.c_int32),
+        ("cu_seq_lens", ctypes.c_void_p),
+        ("token_to_seq", ctypes.c_void_p),
+        ("seq_starts", ctypes.c_void_p),
+        ("num_tokens", ctypes.c_int32),
+        ("dst", ctypes.c_void_p),
+        ("dst_stride", ctypes.c_int64),
+        ("dst_dtype", ctypes.c_int32),
+    ]
+
+
 # every function include/qmla.h declares, with its ctypes signature
 _P = ctypes.POINTER(DecodeParams)
 _W = ctypes.POINTER(CacheWriteParams)
+_G = ctypes.POINTER(GatherParams)
 SIGNATURES = {
     "qmla_version": (ctypes.c_int, []),
     "qmla_build_info": (ctypes.c_char_p, []),
@@ -118,6 +148,7 @@ SIGNATURES = {
     "qmla_decode_partial": (ctypes.c_int, [_P, ctypes.c_void_p]),
     "qmla_combine": (ctypes.c_int, [_P, ctypes.c_void_p]),
     "qmla_cache_write": (ctypes.c_int, [_W, ctypes.c_void_p]),
+    "qmla_gather": (ctypes.c_int, [_G, ctypes.c_void_p]),
 }
 
 _lib = None

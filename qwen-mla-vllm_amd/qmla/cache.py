@@ -1,4 +1,5 @@
-"""Cache-row writer: the new token's latent, rope and rms tail into its paged slot.
+"""Cache rows: the writer (the new token's latent, rope and rms tail into its paged slot) and the
+prefill context gather (paged rows back into the dense bf16 workspace the prefill path reads).
 
 Mirrors QwenMLATritonImpl.do_kv_cache_update (qwen_mla/mla_impl.py:309-342): FP8 caches get
 `[latent e4m3 | rope e4m3 | rms tail]` with e4m3 = RNE of clamp(x * (1/k_scale), -448, 448) and the
@@ -85,3 +86,62 @@ def do_kv_cache_update(kv_c_normed: torch.Tensor, k_pe: torch.Tensor, kv_cache: 
     d_c = kv_c_normed.shape[-1]
     cache_write(kv_c_normed, k_pe, kv_cache, slot_mapping, d_c=d_c, rope_w=packed_rope, rms_heads=n_heads,
                 kv_fp8=fp8, rms=(rms_mode if fp8 else "bf16"), k_scale=k_scale)
+
+
+_RMS_GATHER = {"log8": _lib.RMS_LOG8, "bf16": _lib.RMS_BF16_BYTES, "e4m3": _lib.RMS_E4M3}
+
+
+def gather_cache(*, src_cache: torch.Tensor, dst: torch.Tensor, block_table: torch.Tensor,
+                 cu_seq_lens: torch.Tensor, token_to_seq: torch.Tensor, num_tokens: int,
+                 kv_cache_dtype: str, scale: torch.Tensor, seq_starts: torch.Tensor | None = None,
+                 mla_rms=None) -> None:
+    """gather_cache_torch (qwen_mla/ops/mla_gather.py:28-76) on the device, same keywords.
+
+    Destination row j: s = token_to_seq[j], tok = j - cu_seq_lens[s] (+ seq_starts[s]); the cached
+    row at block_table[s, tok // P], slot tok % P. bf16 caches copy the row; FP8 caches (mla_rms =
+    (rms_offset, heads[, "log8" | "bf16" | "e4m3"])) write bf16(e4m3 * scale) for the first rms_offset
+    columns and one decoded rms element per head after them.
+    """
+    fp8 = str(kv_cache_dtype).startswith("fp8")
+    if not fp8 and kv_cache_dtype not in ("auto", "bfloat16", "float16"):
+        raise NotImplementedError(f"MLA gather has no dequant path for kv_cache_dtype={kv_cache_dtype}")
+    if fp8 and mla_rms is None:
+        raise NotImplementedError("FP8 MLA gather needs the row layout (rms offset, heads)")
+    if num_tokens <= 0:
+        return
+    for t in (src_cache, dst, block_table, cu_seq_lens, token_to_seq):
+        if not t.is_cuda:
+            raise ValueError("gather_cache: every tensor must live on the GPU")
+    if dst.dtype not in (torch.bfloat16, torch.float16):
+        raise TypeError("gather_cache: dst must be bf16 or fp16")
+    dst2 = dst.reshape(dst.shape[0], -1)
+    if dst2.stride(-1) != 1 or dst2.shape[0] < num_tokens:
+        raise ValueError("gather_cache: dst rows must be contiguous and cover num_tokens")
+    i32 = lambda t: t.to(torch.int32).contiguous()
+    bt, cu, t2s = i32(block_table), i32(cu_seq_lens), i32(token_to_seq)
+    ss = i32(seq_starts) if seq_starts is not None else None
+    p = _lib.GatherParams()
+    esz = src_cache.element_size()
+    p.cache = src_cache.data_ptr()
+    p.page_stride, p.token_stride = src_cache.stride(0) * esz, src_cache.stride(1) * esz
+    p.page_size, p.num_pages = src_cache.shape[1], src_cache.shape[0]
+    if fp8:
+        off, nh = mla_rms[:2]
+        mode = mla_rms[2] if len(mla_rms) > 2 else "bf16"
+        p.kv_dtype, p.rms_mode, p.rms_offset, p.rms_heads = _lib.KV_FP8, _RMS_GATHER[mode], off, nh
+        sc = scale.reshape(-1)[:1].to(device=dst.device, dtype=torch.float32).contiguous()
+        p.scale = sc.data_ptr()
+    else:
+        p.kv_dtype, p.row_elems = _lib.KV_BF16, src_cache.reshape(src_cache.shape[0], src_cache.shape[1], -1).shape[-1]
+    p.block_table, p.bt_stride = bt.data_ptr(), bt.stride(0)
+    p.num_seqs, p.bt_cols = bt.shape[0], bt.shape[1]
+    p.cu_seq_lens, p.token_to_seq = cu.data_ptr(), t2s.data_ptr()
+    p.seq_starts = ss.data_ptr() if ss is not None else None
+    p.num_tokens = num_tokens
+    p.dst, p.dst_stride = dst2.data_ptr(), dst2.stride(0)
+    p.dst_dtype = _lib.DT_BF16 if dst.dtype == torch.bfloat16 else _lib.DT_F16
+    _lib.check("qmla_gather", _lib.lib().qmla_gather(ctypes.byref(p), _stream()))
+    cur = torch.cuda.current_stream()
+    for t in (bt, cu, t2s, ss, sc if fp8 else None):
+        if t is not None:
+            t.record_stream(cur)

@@ -24,7 +24,7 @@ def _declared_functions() -> list[str]:
 
 def test_header_functions_exported_and_bound():
     names = _declared_functions()
-    assert "qmla_decode" in names and "qmla_cache_write" in names and len(names) >= 8
+    assert "qmla_decode" in names and "qmla_cache_write" in names and "qmla_gather" in names and len(names) >= 9
     lib = _lib.lib()
     for n in names:
         assert hasattr(lib, n), n
@@ -165,9 +165,11 @@ def test_product_path_refuses_cpu_tensors():
                      torch.ones(1, dtype=torch.int32), page_size=64, sm_scale=0.1, kv_fp8=True)
 
 
-def test_cache_write_struct_mirror_matches_header():
+@pytest.mark.parametrize("name,mirror", [("qmla_cache_write_params", _lib.CacheWriteParams),
+                                         ("qmla_gather_params", _lib.GatherParams)])
+def test_cache_struct_mirrors_match_header(name, mirror):
     text = HEADER.read_text()
-    body = text[text.index("typedef struct qmla_cache_write_params"):text.index("} qmla_cache_write_params;")]
+    body = text[text.index("typedef struct " + name):text.index("} " + name + ";")]
     body = re.sub(r"/\*.*?\*/", "", body, flags=re.S)
     fields = []
     for decl in body.split("{", 1)[1].split(";"):
@@ -177,7 +179,7 @@ def test_cache_write_struct_mirror_matches_header():
         parts = decl.split(",")
         fields.append(re.findall(r"(\w+)\s*$", parts[0])[0])
         fields.extend(re.sub(r"[\*\s]", "", x) for x in parts[1:])
-    assert fields == [f[0] for f in _lib.CacheWriteParams._fields_]
+    assert fields == [f[0] for f in mirror._fields_]
 
 
 def _write_params(**over) -> _lib.CacheWriteParams:
@@ -210,3 +212,36 @@ def test_cache_write_error_codes(over, code):
     p = _write_params(**over)
     assert _lib.lib().qmla_cache_write(ctypes.byref(p), None) == code
     assert _lib.lib().qmla_cache_write(None, None) == _lib.ERR_NULL
+
+
+def _gather_params(**over) -> _lib.GatherParams:
+    p = _lib.GatherParams()
+    base = 0x10000
+    p.cache, p.page_stride, p.token_stride, p.page_size, p.num_pages = base, 64 * 608, 608, 64, 100
+    p.kv_dtype, p.rms_mode, p.rms_offset, p.rms_heads, p.scale = _lib.KV_FP8, _lib.RMS_LOG8, 576, 24, base + 0x100000
+    p.block_table, p.bt_stride, p.num_seqs, p.bt_cols = base + 0x200000, 16, 4, 16
+    p.cu_seq_lens, p.token_to_seq, p.num_tokens = base + 0x300000, base + 0x400000, 100
+    p.dst, p.dst_stride, p.dst_dtype = base + 0x500000, 608, _lib.DT_BF16
+    for k, v in over.items():
+        setattr(p, k, v)
+    return p
+
+
+@pytest.mark.parametrize("over,code", [
+    (dict(cache=None), _lib.ERR_NULL),
+    (dict(scale=None), _lib.ERR_NULL),
+    (dict(dst_dtype=_lib.DT_F32), _lib.ERR_MODE),
+    (dict(rms_mode=_lib.RMS_NONE), _lib.ERR_MODE),
+    (dict(kv_dtype=_lib.KV_BF16, row_elems=0), _lib.ERR_SHAPE),
+    (dict(kv_dtype=_lib.KV_BF16, row_elems=600), _lib.ERR_SHAPE),        # 1200 bytes > 608-byte rows
+    (dict(rms_offset=572), _lib.ERR_SHAPE),
+    (dict(dst_stride=500), _lib.ERR_SHAPE),
+    (dict(bt_stride=8), _lib.ERR_SHAPE),
+    (dict(dst=0x500008), _lib.ERR_ALIGN),
+    (dict(dst_stride=604), _lib.ERR_ALIGN),
+    (dict(num_tokens=0), _lib.OK),
+])
+def test_gather_error_codes(over, code):
+    p = _gather_params(**over)
+    assert _lib.lib().qmla_gather(ctypes.byref(p), None) == code
+    assert _lib.lib().qmla_gather(None, None) == _lib.ERR_NULL
