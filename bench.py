@@ -12,7 +12,8 @@ at one layer; `roofline` reports the decode kernel's algorithmic bytes over its 
 duration (HIP events on the stream it runs on); `cpu_baseline` times the CPU oracle on a fixed
 sample of the same workload on this host's cores.
 
-    python bench.py [--steps K] [--warmup W] [--workload fp8_b128|bf16_b64|gla_b48] [--no-cpu]
+    python bench.py [--steps K] [--warmup W] [--workload fp8_b128|bf16_b64|gla_b48|wide_b32] [--no-cpu]
+    python bench.py --path write_n16384|gather_n16384|prep_b128     (the kernels beside the decode)
 """
 from __future__ import annotations
 
@@ -153,6 +154,159 @@ def cpu_baseline(case, sample_every: int, budget_s: float):
                       f"({t:.2f} s each), scaled per request"}
 
 
+# ------------------------------------------------------------------------------------------------
+# the kernels either side of the decode: cache-row writer, prefill context gather, decode prep
+# ------------------------------------------------------------------------------------------------
+ADJACENT = {
+    # FP8 log8 rows for a 16384-token prefill chunk written to random free slots
+    "write_n16384": dict(n=16384, heads=24, d_c=512, rope_w=64, page_size=64, seed=5),
+    # 4 x 4096 cached tokens of FP8 log8 rows gathered into a bf16 workspace
+    "gather_n16384": dict(n=16384, seqs=4, heads=24, d_c=512, rope_w=64, page_size=64, seed=6),
+    # the decode step's q / k_pe prep at B=128: 24 heads of 256, rope 64 in 4 groups, d_c 512
+    "prep_b128": dict(n=128, heads=24, head_dim=256, rd=64, kv_heads=4, rope_group=6, d_c=512, declared=296,
+                      max_pos=65536, seed=7),
+}
+
+
+def _time_launches(fn, steps, warmup):
+    import torch
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    st = torch.cuda.current_stream()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t = time.perf_counter()
+    e0.record(st)
+    for _ in range(steps):
+        fn()
+    e1.record(st)
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) / steps, time.perf_counter() - t
+
+
+def _cpu_time(fn, budget_s):
+    times, t_all = [], time.perf_counter()
+    while True:
+        t0 = time.perf_counter()
+        fn()
+        times.append(time.perf_counter() - t0)
+        if time.perf_counter() - t_all > budget_s or len(times) >= 5:
+            return statistics.median(times), len(times)
+
+
+def adjacent(args):
+    """One JSON line for a kernel either side of the decode: rows per second of one launch with
+    inputs resident in HBM, algorithmic bytes over its average duration (HIP events on the stream it
+    runs on) against the HBM peak, and the oracle on the same rows on this host's cores."""
+    import numpy as np
+    import torch
+    import qmla
+    from oracle import mla_oracle as ora
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    w = ADJACENT[args.path_workload]
+    g = torch.Generator().manual_seed(w["seed"])
+    kind = args.path_workload.split("_")[0]
+    if kind == "write":
+        n, H, d_c, W, P = w["n"], w["heads"], w["d_c"], w["rope_w"], w["page_size"]
+        kv_c = (torch.randn(n, d_c, generator=g) * 4).to(torch.bfloat16)
+        k_pe = torch.empty(n, W + H, dtype=torch.bfloat16)
+        k_pe[:, :W] = (torch.randn(n, W, generator=g) * 4).to(torch.bfloat16)
+        k_pe[:, W:] = torch.exp(torch.randn(n, H, generator=g) * 0.6).to(torch.bfloat16)
+        pages = n // P * 2
+        slots = torch.randperm(pages * P, generator=g)[:n]
+        cache = torch.zeros(pages, P, 1, 608, dtype=torch.uint8, device=dev)
+        ks = torch.tensor(kv_c.float().abs().max().item() / 448.0, device=dev)
+        a = (kv_c.to(dev), k_pe.to(dev), cache, slots.to(dev))
+        fn = lambda: qmla.cache_write(*a, rope_w=W, rms_heads=H, kv_fp8=True, rms="log8", k_scale=ks)
+        alg = n * ((d_c + W + H) * 2 + (d_c + W + H) + 8)          # bf16 inputs + fp8 row + slot id
+        kc, kp = kv_c.float().numpy(), k_pe.float().numpy()
+        ksf = float(ks.cpu())
+        cpu_fn = lambda: ora.fp8_row_bytes(kc, kp, packed_rope=W, n_heads=H, k_scale=ksf, rms_mode=ora.RMS_LOG8)
+        cpu_rows, sample = n, f"all {n} rows, numpy oracle (fp8_row_bytes)"
+        cfg = {"workload": f"mla_cache_write_{args.path_workload}", "tokens": n, "heads": H, "d_c": d_c, "d_r": W,
+               "kv": "fp8", "rms": "log8", "row_bytes": 608}
+        metric, dtype = "MLA FP8 cache-row writer rows/s + achieved HBM GB/s", "bf16->e4m3"
+    elif kind == "gather":
+        from qmla.synth import make_case
+        n, S, H, P = w["n"], w["seqs"], w["heads"], w["page_size"]
+        c = make_case(batch=S, heads=H, d_c=w["d_c"], rope_w=w["rope_w"], page_size=P, lens=[n // S] * S, kv="fp8",
+                      rms_mode="log8", seed=w["seed"], device=dev, rms="spread")
+        lens = torch.full((S,), n // S, dtype=torch.int64)
+        cu = torch.zeros(S + 1, dtype=torch.int32)
+        cu[1:] = torch.cumsum(lens, 0).to(torch.int32)
+        t2s = torch.repeat_interleave(torch.arange(S, dtype=torch.int32), lens)
+        dst = torch.empty(n, c.row, dtype=torch.bfloat16, device=dev)
+        cud, t2sd = cu.to(dev), t2s.to(dev)
+        mla_rms = (c.rms_offset, H, "log8")
+        fn = lambda: qmla.gather_cache(src_cache=c.cache, dst=dst, block_table=c.block_table, cu_seq_lens=cud,
+                                       token_to_seq=t2sd, num_tokens=n, kv_cache_dtype="fp8", scale=c.k_scale,
+                                       mla_rms=mla_rms)
+        width = c.rms_offset + H
+        alg = n * (width + 2 * width + 4) + S * (n // S // P) * 4 + (S + 1) * 4
+        cb = c.cache.cpu().contiguous().view(torch.uint8).reshape(c.cache.shape[0], P, -1).numpy()
+        btn, ks = c.block_table.cpu().numpy(), float(c.k_scale.cpu())
+        cpu_fn = lambda: ora.gather_context(cb, btn, cu.numpy(), t2s.numpy(), n, None, kv="fp8", scale=ks,
+                                            rms_offset=c.rms_offset, n_heads=H, rms_mode=ora.RMS_LOG8)
+        cpu_rows, sample = n, f"all {n} rows, numpy oracle (gather_context)"
+        cfg = {"workload": f"mla_gather_{args.path_workload}", "tokens": n, "seqs": S, "heads": H, "d_c": w["d_c"],
+               "d_r": w["rope_w"], "page_size": P, "kv": "fp8", "rms": "log8", "dst": "bf16"}
+        metric, dtype = "MLA prefill context gather rows/s + achieved HBM GB/s", "e4m3->bf16"
+    else:
+        n, H, hd, rd, kvh, d_c, decl = (w[k] for k in ("n", "heads", "head_dim", "rd", "kv_heads", "d_c", "declared"))
+        nope = hd - rd
+        q = torch.randn(n, H, hd, generator=g).to(torch.bfloat16)
+        lat = torch.randn(n, d_c, generator=g).to(torch.bfloat16)
+        kr = torch.randn(n, kvh * rd, generator=g).to(torch.bfloat16)
+        ku = (torch.randn(H * nope, d_c, generator=g) * d_c ** -0.5).to(torch.bfloat16)
+        wn = (torch.randn(hd, generator=g) * 0.1).to(torch.bfloat16)
+        tab = torch.from_numpy(ora.partial_rope_table(list(range(rd // 2)), rd, 1e7, w["max_pos"])).to(torch.bfloat16)
+        pos = torch.randint(0, w["max_pos"], (n,), generator=g)
+        a = [t.to(dev) for t in (pos, q, lat, kr, ku)]
+        gain = qmla.k_gain(wn.to(dev), rd)
+        tabd = tab.to(dev)
+        q_out = torch.empty(n, H, nope + decl, dtype=torch.bfloat16, device=dev)
+        k_pe = torch.empty(n, decl, dtype=torch.bfloat16, device=dev)
+        fn = lambda: qmla.mla_decode_prep(*a, gain, tabd, head_offset=0, rope_group=w["rope_group"], rope_first=0,
+                                          rope_span=kvh, declared_rope=decl, eps=1e-6, q_out=q_out, k_pe=k_pe)
+        alg = (n * H * hd * 2 + n * d_c * 2 + n * kvh * rd * 2 + H * nope * d_c * 2 + rd * 4 + n * 8 + n * rd * 2
+               + n * H * (nope + decl) * 2 + n * decl * 2)
+        qn, ln, krn, kun, wnn, tabn = (t.float().numpy() for t in (q, lat, kr, ku, wn, tab))
+        krn = krn.reshape(n, kvh, rd)
+        posn = pos.numpy()
+        cpu_fn = lambda: ora.mla_decode_prep(qn, ln, krn, kun, wnn, tabn, posn, head_offset=0,
+                                             rope_group=w["rope_group"], rope_first=0, rope_span=kvh,
+                                             declared_rope=decl, eps=1e-6)
+        cpu_rows, sample = n, f"all {n} tokens, numpy oracle (mla_decode_prep, float64 up-projection)"
+        cfg = {"workload": f"mla_decode_prep_{args.path_workload}", "tokens": n, "heads": H, "head_dim": hd,
+               "rope_dim": rd, "rope_groups": kvh, "d_c": d_c, "declared_rope": decl}
+        metric, dtype = "MLA decode q/k_pe prep tokens/s + achieved HBM GB/s", "bf16"
+    ms, wall = _time_launches(fn, args.steps, args.warmup)
+    if args.copy_calib_mib:
+        src = torch.empty(args.copy_calib_mib << 20, dtype=torch.uint8, device=dev).fill_(1)
+        dst_c = torch.empty_like(src)
+        for _ in range(3):
+            dst_c.copy_(src)
+        torch.cuda.synchronize()
+    n_rows = w["n"]
+    gbps = alg / (ms / 1e3) / 1e9
+    cpu = None
+    if not args.no_cpu:
+        from threadpoolctl import threadpool_limits
+        with threadpool_limits(1):                      # numpy / BLAS on one thread: cores = 1
+            t, k = _cpu_time(cpu_fn, min(args.cpu_budget, 10.0))
+        cpu = {"value": round(cpu_rows / t, 1), "unit": "tokens/s", "cores": 1, "kind": "port",
+               "cpu": cpu_model(), "sample": f"{sample}, median of {k} runs ({t:.3f} s each)"}
+    print(json.dumps({
+        "metric": metric, "value": round(n_rows / (ms / 1e3), 1), "unit": "tokens/s", "n_gpus": 1,
+        "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms, 5), "higher_is_better": True,
+        "scaling": "weak", "vs_baseline": None, "dtype": dtype, "data": "synthetic", "config": cfg,
+        "kernel_us": round(ms * 1e3, 3), "wall_s_timed": round(wall, 3),
+        "roofline": {"bound": "hbm", "achieved": round(gbps, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
+                     "frac": round(gbps / HBM_PEAK_GBPS, 4), "traffic": None, "algorithmic_bytes_per_launch": alg},
+        "cpu_baseline": cpu}), flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -164,12 +318,17 @@ def main():
     ap.add_argument("--cpu-budget", type=float, default=20.0)
     ap.add_argument("--copy-calib-mib", type=int, default=0,
                     help="also run a plain device copy of this many MiB (FETCH/WRITE_SIZE calibration)")
+    ap.add_argument("--path", dest="path_workload", default=None, choices=sorted(ADJACENT),
+                    help="time a kernel either side of the decode instead (writer, gather, prep)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(json.dumps({"error": "this build measures one GPU only: the decode shards by request "
                                    "(no collectives); run with --gpus 1"}))
         sys.exit(2)
 
+    if args.path_workload:
+        adjacent(args)
+        return
     import torch
     import qmla
     from qmla import _lib

@@ -217,6 +217,47 @@ typedef struct qmla_gather_params {
 
 int qmla_gather(const qmla_gather_params* p, void* stream);
 
+/* ---- decode q / k_pe prep --------------------------------------------------------------------
+ * Replaces the per-token prep of the absorbed-MLA attention module between its projections and the
+ * attention call (qwen_mla/qwen3_5_mla.py:262-301, rotation as in :341-354, rope table from
+ * qwen_mla/partial_rope.py:52-76), fused into one launch:
+ *   rms[t,h]   = sqrt((sum_j bf16(latent[t] . k_up[h*nope + j])^2 + sum_i k_rope[t, g*rd + i]^2)
+ *                     / head_dim + eps),  g = (head_offset + h) / rope_group  (fp32)
+ *   q_out[t,h] = [ q[t,h, rd:head_dim] | q_pe ],  q_pe (declared_rope wide) zero except the slot
+ *                (g - rope_first)*rd .. +rd, which holds rot(q[t,h, :rd])
+ *   k_pe[t]    = [ rot(bf16(k_rope[t, g*rd + i] * k_gain[i])) for g in rope_first.. +rope_span |
+ *                  bf16(rms[t, :]) | zeros up to declared_rope ]
+ * rot is the neox rotation in bf16 arithmetic (each product and sum rounded to bf16) with the
+ * cos/sin table row of the token's position rounded to bf16: x1*cos - x2*sin | x2*cos + x1*sin.
+ * With pos_rows == 3 (M-RoPE) frequency i takes its position from row rope_sec[i]. Positions
+ * outside [0, max_pos) give NaN in the rotated elements. Asynchronous, allocates nothing. */
+typedef struct qmla_prep_params {
+  const void* q;                  /* bf16 [n, heads, head_dim], the normed query, rope dims first */
+  int64_t q_token_stride, q_head_stride;          /* elements */
+  const void* latent;             /* bf16 [n, d_c], the cached latent c */
+  int64_t latent_stride;
+  const void* k_rope;             /* bf16 [n, kv_heads * rope_dim], the raw rope key */
+  int64_t k_rope_stride;
+  const void* k_up;               /* bf16 [heads * nope, d_c], the raw (unscaled) key up-projection */
+  const float* k_gain;            /* fp32 [rope_dim]: 1 + k_norm.weight[:rope_dim] */
+  const void* cos_sin;            /* [max_pos, rope_dim] = cos | sin, dtype cos_sin_dtype */
+  int32_t cos_sin_dtype;          /* QMLA_DT_BF16, QMLA_DT_F32 or QMLA_DT_F16 */
+  int64_t max_pos;
+  const int64_t* positions;       /* [pos_rows, n] */
+  int64_t pos_row_stride;
+  int32_t pos_rows;               /* 1, or 3 for M-RoPE */
+  const int32_t* rope_sec;        /* M-RoPE: [rope_dim / 2] position row (0..2) per frequency */
+  int32_t n, heads, head_dim, rope_dim, kv_heads, d_c;
+  int32_t head_offset, rope_group, rope_first, rope_span, declared_rope;
+  float eps;
+  void* q_out;                    /* bf16 [n, heads, nope + declared_rope] */
+  int64_t q_out_token_stride, q_out_head_stride;
+  void* k_pe;                     /* bf16 [n, declared_rope] */
+  int64_t k_pe_stride;
+} qmla_prep_params;
+
+int qmla_prep(const qmla_prep_params* p, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

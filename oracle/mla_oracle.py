@@ -19,7 +19,9 @@ It restates, on the CPU, the arithmetic of the reference plugin's decode path:
 * spec-verify row flattening (mla_impl.py:628-662) and the grouped-latent (GLA) head/column mapping
   (mla_impl.py:182-194, qwen3_5_mla.py:58-73);
 * the FP8 cache-row writer (mla_impl.py:309-342) and the prefill context gather
-  (ops/mla_gather.py:28-76).
+  (ops/mla_gather.py:28-76);
+* the decode q / k_pe prep of the attention module (qwen3_5_mla.py:232-301, :341-354) and the
+  partial-rope cos/sin table (partial_rope.py:66-76).
 
 Floating-point work runs in float32 torch on the CPU; byte work (e4m3fn and log8 codes) is numpy
 bit arithmetic. Every function is pinned by tests against closed forms, brute force on tiny
@@ -381,3 +383,98 @@ def gather_context(cache_u8: np.ndarray, block_table: np.ndarray, cu_seq_lens: n
         raw = rows[:, rms_offset:rms_offset + 2 * n_heads].copy().view(np.uint16)
         out[:, rms_offset:rms_offset + n_heads] = raw
     return out
+
+
+# ------------------------------------------------------------------------------------------------
+# decode q / k_pe prep (the attention module's per-token work before the attention call)
+# ------------------------------------------------------------------------------------------------
+def partial_rope_table(keep, model_rope_dim: int, theta: float, max_pos: int) -> np.ndarray:
+    """cos/sin table of the kept rope subspaces (partial_rope.py:66-76): subspace keep[i] rotates
+    at its ORIGINAL frequency theta^(-2*keep[i]/model_rope_dim); the angles t*inv are float32
+    products; row t = [cos(angles) | sin(angles)] as float32 [max_pos, 2*len(keep)]. cos and sin
+    are evaluated on the float32 angle in float64 and rounded once."""
+    k = np.asarray(keep, dtype=np.float32)
+    expo = (np.float32(2.0) * k / np.float32(model_rope_dim)).astype(np.float32)
+    inv = (1.0 / np.power(np.float64(np.float32(theta)), expo.astype(np.float64))).astype(np.float32)
+    ang = (np.arange(max_pos, dtype=np.float32)[:, None] * inv[None, :]).astype(np.float32)
+    a64 = ang.astype(np.float64)
+    return np.concatenate([np.cos(a64), np.sin(a64)], axis=1).astype(np.float32)
+
+
+def _bf16(x: np.ndarray) -> np.ndarray:
+    """float32 -> nearest-even bf16 value, as float32."""
+    return bf16_bits_to_f32(f32_to_bf16_bits(np.asarray(x, np.float32)))
+
+
+def neox_rotate_bf16(x: np.ndarray, cos: np.ndarray, sin: np.ndarray) -> np.ndarray:
+    """Neox rotation in bf16 arithmetic (qwen3_5_mla.py:346-353, the rotation vLLM's rotary applies
+    with is_neox_style): x [..., rd] holds bf16 values, cos/sin [..., rd/2] are rounded to bf16
+    first (the table is cast to the query dtype, :346); each product and each sum is rounded to
+    bf16: [x1*cos - x2*sin | x2*cos + x1*sin]. Returns float32 values that are bf16."""
+    half = x.shape[-1] // 2
+    x = np.asarray(x, np.float32)
+    c, s = _bf16(cos), _bf16(sin)
+    x1, x2 = x[..., :half], x[..., half:]
+    o1 = _bf16(_bf16(x1 * c) - _bf16(x2 * s))
+    o2 = _bf16(_bf16(x2 * c) + _bf16(x1 * s))
+    return np.concatenate([o1, o2], axis=-1)
+
+
+def rope_rows(table: np.ndarray, positions: np.ndarray, rope_sec=None) -> tuple[np.ndarray, np.ndarray]:
+    """(cos, sin) [n, rd/2] for each token. positions [n], or [3, n] with rope_sec[i] in 0..2
+    naming the position row of frequency i (M-RoPE, qwen3_5_mla.py:346-348)."""
+    half = table.shape[1] // 2
+    pos = np.asarray(positions, np.int64)
+    if pos.ndim == 1:
+        rows = table[pos]
+        return rows[:, :half], rows[:, half:]
+    sec = np.asarray(rope_sec, np.int64)
+    f = np.arange(half)
+    p = pos[sec[f]]                                     # [half, n]
+    return table[p.T, f[None, :]], table[p.T, half + f[None, :]]
+
+
+def mla_decode_prep(q: np.ndarray, latent: np.ndarray, k_rope: np.ndarray, k_up: np.ndarray,
+                    k_norm_weight: np.ndarray, table: np.ndarray, positions: np.ndarray, *,
+                    head_offset: int, rope_group: int, rope_first: int, rope_span: int,
+                    declared_rope: int, eps: float, rope_sec=None):
+    """The decode prep of qwen3_5_mla.py:232-301 on bf16 inputs (float32 arrays holding bf16
+    values): q [n, H, hd] (normed, rope dims first), latent [n, d_c], k_rope [n, kv_heads, rd] (raw),
+    k_up [H*nope, d_c] (raw), k_norm_weight [hd], table [max_pos, rd] cos|sin.
+
+      g(h)   = (head_offset + h) // rope_group                                      (:239-240)
+      k_nope = bf16(latent @ k_up^T)   (the bf16 GEMM output; accumulated here in float64)  (:262)
+      rms    = sqrt((sum bf16(k_nope)^2 + sum k_rope[:, g]^2) / hd + eps)   float32  (:263-265)
+      q_rot  = rot(q[..., :rd]);  k_rot = rot(bf16(k_rope * (1 + w[:rd])))          (:274-283)
+      q_out  = [q[..., rd:] | q_pe],  q_pe zero but slot (g - rope_first)*rd          (:289-292, :303)
+      k_pe   = [k_rot[:, rope_first:rope_first+rope_span] | bf16(rms) | 0]          (:293-301)
+
+    Returns (q_out [n, H, nope + declared_rope], k_pe [n, declared_rope], rms float32 [n, H]);
+    the first two as bf16-valued float32.
+    """
+    n, H, hd = q.shape
+    rd = table.shape[1]
+    nope = hd - rd
+    kv_heads = k_rope.shape[1]
+    g = (head_offset + np.arange(H)) // rope_group
+    k_nope = _bf16((latent.astype(np.float64) @ k_up.astype(np.float64).T).astype(np.float32))
+    k_nope = k_nope.reshape(n, H, nope).astype(np.float64)
+    kr = k_rope.astype(np.float64)
+    sumsq = (k_nope ** 2).sum(-1) + (kr ** 2).sum(-1)[:, g]
+    rms = np.sqrt((sumsq / hd).astype(np.float32) + np.float32(eps)).astype(np.float32)
+    cos, sin = rope_rows(table, positions, rope_sec)
+    q_rot = neox_rotate_bf16(q[..., :rd], cos[:, None, :], sin[:, None, :])
+    gain = (np.float32(1.0) + np.asarray(k_norm_weight, np.float32))[:rd]
+    k_in = _bf16(k_rope.astype(np.float32) * gain)
+    k_rot = neox_rotate_bf16(k_in, cos[:, None, :], sin[:, None, :])
+    q_out = np.zeros((n, H, nope + declared_rope), np.float32)
+    q_out[..., :nope] = q[..., rd:]
+    for h in range(H):
+        s0 = nope + (g[h] - rope_first) * rd
+        q_out[:, h, s0:s0 + rd] = q_rot[:, h]
+    packed = rope_span * rd
+    assert rope_first + rope_span <= kv_heads and declared_rope >= packed + H
+    k_pe = np.zeros((n, declared_rope), np.float32)
+    k_pe[:, :packed] = k_rot[:, rope_first:rope_first + rope_span].reshape(n, packed)
+    k_pe[:, packed:packed + H] = _bf16(rms)
+    return q_out, k_pe, rms

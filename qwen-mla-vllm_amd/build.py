@@ -32,6 +32,7 @@ SOURCES = [
     (CSRC / "qmla_cs.hip", ["-mllvm", "-amdgpu-mfma-vgpr-form"]),
     (CSRC / "qmla_ws.hip", ["-mllvm", "-amdgpu-mfma-vgpr-form"]),
     (CSRC / "qmla_write.hip", []),
+    (CSRC / "qmla_prep.hip", []),
 ]
 
 

@@ -135,10 +135,51 @@ class GatherParams(ctypes.Structure):
     ]
 
 
+class PrepParams(ctypes.Structure):
+    """Mirror of `qmla_prep_params` (include/qmla.h); field order and types must match."""
+
+    _fields_ = [
+        ("q", ctypes.c_void_p),
+        ("q_token_stride", ctypes.c_int64),
+        ("q_head_stride", ctypes.c_int64),
+        ("latent", ctypes.c_void_p),
+        ("latent_stride", ctypes.c_int64),
+        ("k_rope", ctypes.c_void_p),
+        ("k_rope_stride", ctypes.c_int64),
+        ("k_up", ctypes.c_void_p),
+        ("k_gain", ctypes.c_void_p),
+        ("cos_sin", ctypes.c_void_p),
+        ("cos_sin_dtype", ctypes.c_int32),
+        ("max_pos", ctypes.c_int64),
+        ("positions", ctypes.c_void_p),
+        ("pos_row_stride", ctypes.c_int64),
+        ("pos_rows", ctypes.c_int32),
+        ("rope_sec", ctypes.c_void_p),
+        ("n", ctypes.c_int32),
+        ("heads", ctypes.c_int32),
+        ("head_dim", ctypes.c_int32),
+        ("rope_dim", ctypes.c_int32),
+        ("kv_heads", ctypes.c_int32),
+        ("d_c", ctypes.c_int32),
+        ("head_offset", ctypes.c_int32),
+        ("rope_group", ctypes.c_int32),
+        ("rope_first", ctypes.c_int32),
+        ("rope_span", ctypes.c_int32),
+        ("declared_rope", ctypes.c_int32),
+        ("eps", ctypes.c_float),
+        ("q_out", ctypes.c_void_p),
+        ("q_out_token_stride", ctypes.c_int64),
+        ("q_out_head_stride", ctypes.c_int64),
+        ("k_pe", ctypes.c_void_p),
+        ("k_pe_stride", ctypes.c_int64),
+    ]
+
+
 # every function include/qmla.h declares, with its ctypes signature
 _P = ctypes.POINTER(DecodeParams)
 _W = ctypes.POINTER(CacheWriteParams)
 _G = ctypes.POINTER(GatherParams)
+_R = ctypes.POINTER(PrepParams)
 SIGNATURES = {
     "qmla_version": (ctypes.c_int, []),
     "qmla_build_info": (ctypes.c_char_p, []),
@@ -149,6 +190,7 @@ SIGNATURES = {
     "qmla_combine": (ctypes.c_int, [_P, ctypes.c_void_p]),
     "qmla_cache_write": (ctypes.c_int, [_W, ctypes.c_void_p]),
     "qmla_gather": (ctypes.c_int, [_G, ctypes.c_void_p]),
+    "qmla_prep": (ctypes.c_int, [_R, ctypes.c_void_p]),
 }
 
 _lib = None

@@ -24,7 +24,8 @@ def _declared_functions() -> list[str]:
 
 def test_header_functions_exported_and_bound():
     names = _declared_functions()
-    assert "qmla_decode" in names and "qmla_cache_write" in names and "qmla_gather" in names and len(names) >= 9
+    assert "qmla_decode" in names and "qmla_cache_write" in names and "qmla_gather" in names and "qmla_prep" in names
+    assert len(names) >= 10
     lib = _lib.lib()
     for n in names:
         assert hasattr(lib, n), n
@@ -166,7 +167,8 @@ def test_product_path_refuses_cpu_tensors():
 
 
 @pytest.mark.parametrize("name,mirror", [("qmla_cache_write_params", _lib.CacheWriteParams),
-                                         ("qmla_gather_params", _lib.GatherParams)])
+                                         ("qmla_gather_params", _lib.GatherParams),
+                                         ("qmla_prep_params", _lib.PrepParams)])
 def test_cache_struct_mirrors_match_header(name, mirror):
     text = HEADER.read_text()
     body = text[text.index("typedef struct " + name):text.index("} " + name + ";")]
@@ -245,3 +247,49 @@ def test_gather_error_codes(over, code):
     p = _gather_params(**over)
     assert _lib.lib().qmla_gather(ctypes.byref(p), None) == code
     assert _lib.lib().qmla_gather(None, None) == _lib.ERR_NULL
+
+
+def _prep_params(**over) -> _lib.PrepParams:
+    """A valid description of 24 heads x 256 (rope 64 first), 4 rope groups, d_c 512 (never launched:
+    every case below fails validation or has no tokens)."""
+    p = _lib.PrepParams()
+    base = 0x10000
+    p.q, p.q_token_stride, p.q_head_stride = base, 24 * 512, 512
+    p.latent, p.latent_stride = base + 0x100000, 512
+    p.k_rope, p.k_rope_stride = base + 0x200000, 256
+    p.k_up, p.k_gain = base + 0x300000, base + 0x400000
+    p.cos_sin, p.cos_sin_dtype, p.max_pos = base + 0x500000, _lib.DT_BF16, 4096
+    p.positions, p.pos_row_stride, p.pos_rows, p.rope_sec = base + 0x600000, 0, 1, None
+    p.n, p.heads, p.head_dim, p.rope_dim, p.kv_heads, p.d_c = 8, 24, 256, 64, 4, 512
+    p.head_offset, p.rope_group, p.rope_first, p.rope_span, p.declared_rope = 0, 6, 0, 4, 296
+    p.eps = 1e-6
+    p.q_out, p.q_out_token_stride, p.q_out_head_stride = base + 0x700000, 24 * 488, 488
+    p.k_pe, p.k_pe_stride = base + 0x800000, 296
+    for k, v in over.items():
+        setattr(p, k, v)
+    return p
+
+
+@pytest.mark.parametrize("over,code", [
+    (dict(q=None), _lib.ERR_NULL),
+    (dict(k_gain=None), _lib.ERR_NULL),
+    (dict(pos_rows=3, pos_row_stride=8), _lib.ERR_NULL),                  # M-RoPE without rope_sec
+    (dict(pos_rows=2), _lib.ERR_SHAPE),
+    (dict(cos_sin_dtype=7), _lib.ERR_MODE),
+    (dict(d_c=448), _lib.ERR_SHAPE),                                      # K halves of 64-wide blocks
+    (dict(head_dim=64), _lib.ERR_SHAPE),                                  # no nope part
+    (dict(rope_first=1), _lib.ERR_SHAPE),                                 # head 0's group not cached
+    (dict(rope_span=5), _lib.ERR_SHAPE),                                  # more groups than k_rope holds
+    (dict(declared_rope=272), _lib.ERR_SHAPE),                            # rope 256 + 24 rms do not fit
+    (dict(head_offset=12, rope_first=2, rope_span=1), _lib.ERR_SHAPE),    # heads 12..35 span 4 groups
+    (dict(q_out_head_stride=480), _lib.ERR_SHAPE),
+    (dict(k_pe_stride=200), _lib.ERR_SHAPE),
+    (dict(latent=0x100008 + 0x10000), _lib.ERR_ALIGN),
+    (dict(latent_stride=516), _lib.ERR_ALIGN),
+    (dict(q_head_stride=513, q_token_stride=24 * 513), _lib.ERR_ALIGN),
+    (dict(n=0), _lib.OK),
+])
+def test_prep_error_codes(over, code):
+    p = _prep_params(**over)
+    assert _lib.lib().qmla_prep(ctypes.byref(p), None) == code
+    assert _lib.lib().qmla_prep(None, None) == _lib.ERR_NULL
