@@ -196,14 +196,17 @@ def _cpu_time(fn, budget_s):
 
 def adjacent(args):
     """One JSON line for a kernel either side of the decode: rows per second of one launch with
-    inputs resident in HBM, algorithmic bytes over its average duration (HIP events on the stream it
-    runs on) against the HBM peak, and the oracle on the same rows on this host's cores."""
+    inputs resident in HBM (the C entry point called with prebuilt parameters, K launches back to
+    back), algorithmic bytes over its average duration (HIP events on the stream it runs on) against
+    the HBM peak, and the oracle on the same rows on this host's cores."""
     import numpy as np
     import torch
     import qmla
     from oracle import mla_oracle as ora
+    import ctypes
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
+    lib, st = qmla.lib(), torch.cuda.current_stream().cuda_stream
     w = ADJACENT[args.path_workload]
     g = torch.Generator().manual_seed(w["seed"])
     kind = args.path_workload.split("_")[0]
@@ -218,13 +221,15 @@ def adjacent(args):
         cache = torch.zeros(pages, P, 1, 608, dtype=torch.uint8, device=dev)
         ks = torch.tensor(kv_c.float().abs().max().item() / 448.0, device=dev)
         a = (kv_c.to(dev), k_pe.to(dev), cache, slots.to(dev))
-        fn = lambda: qmla.cache_write(*a, rope_w=W, rms_heads=H, kv_fp8=True, rms="log8", k_scale=ks)
+        from qmla.cache import cache_write_params
+        prm, keep = cache_write_params(*a, rope_w=W, rms_heads=H, kv_fp8=True, rms="log8", k_scale=ks)
+        fn = lambda: lib.qmla_cache_write(ctypes.byref(prm), st)
         alg = n * ((d_c + W + H) * 2 + (d_c + W + H) + 8)          # bf16 inputs + fp8 row + slot id
         kc, kp = kv_c.float().numpy(), k_pe.float().numpy()
         ksf = float(ks.cpu())
         cpu_fn = lambda: ora.fp8_row_bytes(kc, kp, packed_rope=W, n_heads=H, k_scale=ksf, rms_mode=ora.RMS_LOG8)
         cpu_rows, sample = n, f"all {n} rows, numpy oracle (fp8_row_bytes)"
-        cfg = {"workload": f"mla_cache_write_{args.path_workload}", "tokens": n, "heads": H, "d_c": d_c, "d_r": W,
+        cfg = {"workload": "mla_cache_write_n16384", "tokens": n, "heads": H, "d_c": d_c, "d_r": W,
                "kv": "fp8", "rms": "log8", "row_bytes": 608}
         metric, dtype = "MLA FP8 cache-row writer rows/s + achieved HBM GB/s", "bf16->e4m3"
     elif kind == "gather":
@@ -239,9 +244,11 @@ def adjacent(args):
         dst = torch.empty(n, c.row, dtype=torch.bfloat16, device=dev)
         cud, t2sd = cu.to(dev), t2s.to(dev)
         mla_rms = (c.rms_offset, H, "log8")
-        fn = lambda: qmla.gather_cache(src_cache=c.cache, dst=dst, block_table=c.block_table, cu_seq_lens=cud,
-                                       token_to_seq=t2sd, num_tokens=n, kv_cache_dtype="fp8", scale=c.k_scale,
-                                       mla_rms=mla_rms)
+        from qmla.cache import gather_params
+        prm, keep = gather_params(src_cache=c.cache, dst=dst, block_table=c.block_table, cu_seq_lens=cud,
+                                  token_to_seq=t2sd, num_tokens=n, kv_cache_dtype="fp8", scale=c.k_scale,
+                                  mla_rms=mla_rms)
+        fn = lambda: lib.qmla_gather(ctypes.byref(prm), st)
         width = c.rms_offset + H
         alg = n * (width + 2 * width + 4) + S * (n // S // P) * 4 + (S + 1) * 4
         cb = c.cache.cpu().contiguous().view(torch.uint8).reshape(c.cache.shape[0], P, -1).numpy()
@@ -249,7 +256,7 @@ def adjacent(args):
         cpu_fn = lambda: ora.gather_context(cb, btn, cu.numpy(), t2s.numpy(), n, None, kv="fp8", scale=ks,
                                             rms_offset=c.rms_offset, n_heads=H, rms_mode=ora.RMS_LOG8)
         cpu_rows, sample = n, f"all {n} rows, numpy oracle (gather_context)"
-        cfg = {"workload": f"mla_gather_{args.path_workload}", "tokens": n, "seqs": S, "heads": H, "d_c": w["d_c"],
+        cfg = {"workload": "mla_gather_n16384", "tokens": n, "seqs": S, "heads": H, "d_c": w["d_c"],
                "d_r": w["rope_w"], "page_size": P, "kv": "fp8", "rms": "log8", "dst": "bf16"}
         metric, dtype = "MLA prefill context gather rows/s + achieved HBM GB/s", "e4m3->bf16"
     else:
@@ -267,8 +274,10 @@ def adjacent(args):
         tabd = tab.to(dev)
         q_out = torch.empty(n, H, nope + decl, dtype=torch.bfloat16, device=dev)
         k_pe = torch.empty(n, decl, dtype=torch.bfloat16, device=dev)
-        fn = lambda: qmla.mla_decode_prep(*a, gain, tabd, head_offset=0, rope_group=w["rope_group"], rope_first=0,
-                                          rope_span=kvh, declared_rope=decl, eps=1e-6, q_out=q_out, k_pe=k_pe)
+        from qmla.prep import prep_params
+        prm, keep, _, _ = prep_params(*a, gain, tabd, head_offset=0, rope_group=w["rope_group"], rope_first=0,
+                                      rope_span=kvh, declared_rope=decl, eps=1e-6, q_out=q_out, k_pe=k_pe)
+        fn = lambda: lib.qmla_prep(ctypes.byref(prm), st)
         alg = (n * H * hd * 2 + n * d_c * 2 + n * kvh * rd * 2 + H * nope * d_c * 2 + rd * 4 + n * 8 + n * rd * 2
                + n * H * (nope + decl) * 2 + n * decl * 2)
         qn, ln, krn, kun, wnn, tabn = (t.float().numpy() for t in (q, lat, kr, ku, wn, tab))
@@ -278,10 +287,15 @@ def adjacent(args):
                                              rope_group=w["rope_group"], rope_first=0, rope_span=kvh,
                                              declared_rope=decl, eps=1e-6)
         cpu_rows, sample = n, f"all {n} tokens, numpy oracle (mla_decode_prep, float64 up-projection)"
-        cfg = {"workload": f"mla_decode_prep_{args.path_workload}", "tokens": n, "heads": H, "head_dim": hd,
+        cfg = {"workload": "mla_decode_prep_b128", "tokens": n, "heads": H, "head_dim": hd,
                "rope_dim": rd, "rope_groups": kvh, "d_c": d_c, "declared_rope": decl}
         metric, dtype = "MLA decode q/k_pe prep tokens/s + achieved HBM GB/s", "bf16"
-    ms, wall = _time_launches(fn, args.steps, args.warmup)
+    def launch():
+        rc = fn()
+        if rc != 0:
+            raise RuntimeError(f"{kind} launch failed: {rc}")
+
+    ms, wall = _time_launches(launch, args.steps, args.warmup)
     if args.copy_calib_mib:
         src = torch.empty(args.copy_calib_mib << 20, dtype=torch.uint8, device=dev).fill_(1)
         dst_c = torch.empty_like(src)
@@ -290,6 +304,12 @@ def adjacent(args):
         torch.cuda.synchronize()
     n_rows = w["n"]
     gbps = alg / (ms / 1e3) / 1e9
+    traffic = None
+    f = REPO / "profiles" / f"traffic_{cfg['workload']}.md"
+    if f.exists():
+        for line in f.read_text().splitlines():
+            if line.startswith("hbm_bytes_per_launch:"):
+                traffic = int(line.split(":", 1)[1])
     cpu = None
     if not args.no_cpu:
         from threadpoolctl import threadpool_limits
@@ -303,7 +323,7 @@ def adjacent(args):
         "scaling": "weak", "vs_baseline": None, "dtype": dtype, "data": "synthetic", "config": cfg,
         "kernel_us": round(ms * 1e3, 3), "wall_s_timed": round(wall, 3),
         "roofline": {"bound": "hbm", "achieved": round(gbps, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
-                     "frac": round(gbps / HBM_PEAK_GBPS, 4), "traffic": None, "algorithmic_bytes_per_launch": alg},
+                     "frac": round(gbps / HBM_PEAK_GBPS, 4), "traffic": traffic, "algorithmic_bytes_per_launch": alg},
         "cpu_baseline": cpu}), flush=True)
 
 

@@ -31,6 +31,19 @@ def cache_write(kv_c: torch.Tensor, k_pe: torch.Tensor, kv_cache: torch.Tensor, 
 
     rms: "log8" | "bf16" | "e4m3" | "none" for FP8 caches, "bf16" | "none" for bf16 caches.
     """
+    p, keep = cache_write_params(kv_c, k_pe, kv_cache, slot_mapping, d_c=d_c, rope_w=rope_w, rms_heads=rms_heads,
+                                 kv_fp8=kv_fp8, rms=rms, k_scale=k_scale)
+    _lib.check("qmla_cache_write", _lib.lib().qmla_cache_write(ctypes.byref(p), _stream()))
+    cur = torch.cuda.current_stream()
+    for t in keep:
+        t.record_stream(cur)
+
+
+def cache_write_params(kv_c: torch.Tensor, k_pe: torch.Tensor, kv_cache: torch.Tensor, slot_mapping: torch.Tensor,
+                       *, d_c: int | None = None, rope_w: int, rms_heads: int, kv_fp8: bool | None = None,
+                       rms: str = "log8", k_scale: torch.Tensor | None = None):
+    """The `qmla_cache_write_params` of a `cache_write` call, and the tensors it points into that the
+    caller must keep alive (converted copies). For callers that launch the same write repeatedly."""
     slots = slot_mapping.reshape(-1)
     n = slots.shape[0]
     if kv_fp8 is None:
@@ -69,9 +82,7 @@ def cache_write(kv_c: torch.Tensor, k_pe: torch.Tensor, kv_cache: torch.Tensor, 
     p.page_stride, p.token_stride = kv_cache.stride(0) * esz, kv_cache.stride(1) * esz
     p.page_size = kv_cache.shape[1]
     p.num_slots = kv_cache.shape[0] * kv_cache.shape[1]
-    _lib.check("qmla_cache_write", _lib.lib().qmla_cache_write(ctypes.byref(p), _stream()))
-    if kv_fp8:
-        ks.record_stream(torch.cuda.current_stream())
+    return p, ((slots, ks) if kv_fp8 else (slots,))
 
 
 def do_kv_cache_update(kv_c_normed: torch.Tensor, k_pe: torch.Tensor, kv_cache: torch.Tensor,
@@ -102,13 +113,29 @@ def gather_cache(*, src_cache: torch.Tensor, dst: torch.Tensor, block_table: tor
     (rms_offset, heads[, "log8" | "bf16" | "e4m3"])) write bf16(e4m3 * scale) for the first rms_offset
     columns and one decoded rms element per head after them.
     """
+    if num_tokens <= 0:
+        if not str(kv_cache_dtype).startswith("fp8") and kv_cache_dtype not in ("auto", "bfloat16", "float16"):
+            raise NotImplementedError(f"MLA gather has no dequant path for kv_cache_dtype={kv_cache_dtype}")
+        return
+    p, keep = gather_params(src_cache=src_cache, dst=dst, block_table=block_table, cu_seq_lens=cu_seq_lens,
+                            token_to_seq=token_to_seq, num_tokens=num_tokens, kv_cache_dtype=kv_cache_dtype,
+                            scale=scale, seq_starts=seq_starts, mla_rms=mla_rms)
+    _lib.check("qmla_gather", _lib.lib().qmla_gather(ctypes.byref(p), _stream()))
+    cur = torch.cuda.current_stream()
+    for t in keep:
+        t.record_stream(cur)
+
+
+def gather_params(*, src_cache: torch.Tensor, dst: torch.Tensor, block_table: torch.Tensor,
+                  cu_seq_lens: torch.Tensor, token_to_seq: torch.Tensor, num_tokens: int,
+                  kv_cache_dtype: str, scale: torch.Tensor, seq_starts: torch.Tensor | None = None, mla_rms=None):
+    """The `qmla_gather_params` of a `gather_cache` call (num_tokens > 0), and the converted tensors it
+    points into that the caller must keep alive."""
     fp8 = str(kv_cache_dtype).startswith("fp8")
     if not fp8 and kv_cache_dtype not in ("auto", "bfloat16", "float16"):
         raise NotImplementedError(f"MLA gather has no dequant path for kv_cache_dtype={kv_cache_dtype}")
     if fp8 and mla_rms is None:
         raise NotImplementedError("FP8 MLA gather needs the row layout (rms offset, heads)")
-    if num_tokens <= 0:
-        return
     for t in (src_cache, dst, block_table, cu_seq_lens, token_to_seq):
         if not t.is_cuda:
             raise ValueError("gather_cache: every tensor must live on the GPU")
@@ -140,8 +167,4 @@ def gather_cache(*, src_cache: torch.Tensor, dst: torch.Tensor, block_table: tor
     p.num_tokens = num_tokens
     p.dst, p.dst_stride = dst2.data_ptr(), dst2.stride(0)
     p.dst_dtype = _lib.DT_BF16 if dst.dtype == torch.bfloat16 else _lib.DT_F16
-    _lib.check("qmla_gather", _lib.lib().qmla_gather(ctypes.byref(p), _stream()))
-    cur = torch.cuda.current_stream()
-    for t in (bt, cu, t2s, ss, sc if fp8 else None):
-        if t is not None:
-            t.record_stream(cur)
+    return p, tuple(t for t in (bt, cu, t2s, ss, sc if fp8 else None) if t is not None)

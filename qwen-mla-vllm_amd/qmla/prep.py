@@ -54,6 +54,21 @@ def mla_decode_prep(positions: torch.Tensor, q: torch.Tensor, latent: torch.Tens
     Returns (q_out [n, H, nope + declared_rope], k_pe [n, declared_rope]), both bf16, written into
     the given tensors when passed. Positions outside the table give NaN in the rotated elements.
     """
+    p, keep, q_out, k_pe = prep_params(positions, q, latent, k_rope, k_up_raw, k_gain, cos_sin_cache,
+                                       head_offset=head_offset, rope_group=rope_group, rope_first=rope_first,
+                                       rope_span=rope_span, declared_rope=declared_rope, eps=eps, rope_sec=rope_sec,
+                                       q_out=q_out, k_pe=k_pe)
+    _lib.check("qmla_prep", _lib.lib().qmla_prep(ctypes.byref(p), torch.cuda.current_stream().cuda_stream))
+    s = torch.cuda.current_stream()
+    for t in keep:
+        t.record_stream(s)
+    return q_out, k_pe
+
+
+def prep_params(positions, q, latent, k_rope, k_up_raw, k_gain, cos_sin_cache, *, head_offset, rope_group,
+                rope_first, rope_span, declared_rope, eps, rope_sec=None, q_out=None, k_pe=None):
+    """The `qmla_prep_params` of a `mla_decode_prep` call, the converted tensors it points into (keep
+    them alive), and the two outputs."""
     if q.dim() != 3:
         raise ValueError("mla_decode_prep: q must be [n, heads, head_dim]")
     n, H, hd = q.shape
@@ -123,8 +138,4 @@ def mla_decode_prep(positions: torch.Tensor, q: torch.Tensor, latent: torch.Tens
     p.declared_rope, p.eps = declared_rope, eps
     p.q_out, p.q_out_token_stride, p.q_out_head_stride = q_out.data_ptr(), q_out.stride(0), q_out.stride(1)
     p.k_pe, p.k_pe_stride = kp.data_ptr(), kp.stride(0)
-    _lib.check("qmla_prep", _lib.lib().qmla_prep(ctypes.byref(p), torch.cuda.current_stream().cuda_stream))
-    s = torch.cuda.current_stream()
-    for t in (ku, gain, pos) + ((sec,) if sec is not None else ()):
-        t.record_stream(s)
-    return q_out, k_pe
+    return p, (ku, gain, pos) + ((sec,) if sec is not None else ()), q_out, k_pe
