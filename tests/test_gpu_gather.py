@@ -125,3 +125,15 @@ def test_fp16_destination(gpu):
     assert bad.size == 0, [(float(lat[r, k]), hex(got[r, k]), hex(exp[r, k])) for r, k in bad[:6]] + [len(bad)]
     rms = torch.from_numpy(ora.log8_decode(rows[:, c.rms_offset:c.rms_offset + c.heads])).to(torch.float16)
     assert np.array_equal(got[:n, c.rms_offset:c.rms_offset + c.heads], rms.view(torch.int16).numpy().view(np.uint16))
+
+
+def test_wide_latent_gather(gpu):
+    """d_c 1792 FP8 rows (rms offset 1856, the per-row kernel): bit-exact against the oracle."""
+    lens = [300, 77]
+    c = make_case(batch=2, heads=24, d_c=1792, rope_w=64, page_size=16, lens=lens, kv="fp8", rms_mode="log8",
+                  seed=26, device=gpu, rms="spread")
+    cu, t2s, ss, n = _meta(lens)
+    got = _run(gpu, c, "fp8", (c.rms_offset, c.heads, "log8"), cu, t2s, ss, n, c.row)
+    exp = _oracle(c, cu, t2s, ss, n, "fp8", ora.RMS_LOG8)
+    k = c.rms_offset + c.heads
+    assert np.array_equal(got[:n, :k], exp[:, :k]) and np.all(got[:n, k:] == SENT)

@@ -178,3 +178,25 @@ def test_written_cache_decodes_like_the_oracle(gpu):
                             rms_mode=ora.RMS_LOG8, k_scale=k_scale, sm_scale=sm, rms_heads=H, groups=1)
     err = ((o.float().cpu() - ro).abs() - 2.0 ** -7 * ro.abs()).max().item()
     assert err < 3e-2 and (lse.cpu() - rl).abs().max().item() < 1e-2
+
+
+def test_wide_latent_rows_bit_exact(gpu):
+    """d_c 1792 (the per-row kernel rather than the multi-row one): the same bytes as the oracle."""
+    import qmla
+    n, d_c, width = 70, 1792, 1888
+    g = torch.Generator().manual_seed(8)
+    kv_c = (torch.randn(n, d_c, generator=g) * 4).to(torch.bfloat16)
+    k_pe = torch.empty(n, ROPE + H, dtype=torch.bfloat16)
+    k_pe[:, :ROPE] = (torch.randn(n, ROPE, generator=g) * 4).to(torch.bfloat16)
+    k_pe[:, ROPE:] = torch.exp(torch.randn(n, H, generator=g)).to(torch.bfloat16)
+    slots = torch.randperm(20 * 16, generator=g)[:n]
+    cache = torch.full((20, 16, 1, width), 0xAB, dtype=torch.uint8, device=gpu)
+    ks = torch.tensor(0.021, device=gpu)
+    qmla.cache_write(kv_c.to(gpu), k_pe.to(gpu), cache, slots.to(gpu), rope_w=ROPE, rms_heads=H, kv_fp8=True,
+                     rms="log8", k_scale=ks)
+    torch.cuda.synchronize()
+    got = cache.cpu().view(-1, width).numpy()
+    exp = ora.fp8_row_bytes(kv_c.float().numpy(), k_pe.float().numpy(), packed_rope=ROPE, n_heads=H, k_scale=0.021,
+                            rms_mode=ora.RMS_LOG8)
+    nb = exp.shape[1]
+    assert np.array_equal(got[slots.numpy(), :nb], exp) and np.all(got[slots.numpy(), nb:] == 0xAB)
