@@ -6,6 +6,7 @@
 #include <stdint.h>
 
 #include "qmla.h"
+#include "qmla_device.h"
 
 namespace qmla {
 
@@ -43,7 +44,19 @@ struct KParams {
   int* plan;        // [0] = chunk (tiles per workgroup), [1] = total tiles, [2 + b] = prefix C_b
   float* part_o;    // [(nwg + n_req), qrows*heads, Dv]
   float* part_lse;  // [(nwg + n_req), qrows*heads]
+  int q_vec;        // query rows and strides 16-byte aligned: 16-byte query loads (else element loads)
 };
+
+// 8 consecutive query elements: one 16-byte load when the caller's query rows are 16-byte aligned,
+// else eight element loads (queries are read once per request or segment, so this costs nothing
+// that shows). `vec` is the same for every lane.
+__device__ __forceinline__ bf16x8 load_q8(const __bf16* ptr, bool vec) {
+  if (vec) return *reinterpret_cast<const bf16x8*>(ptr);
+  bf16x8 v;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) v[e] = ptr[e];
+  return v;
+}
 
 __device__ __forceinline__ void store_out(void* base, int dt, int64_t idx, float v) {
   if (dt == QMLA_DT_BF16) reinterpret_cast<__bf16*>(base)[idx] = (__bf16)v;

@@ -186,19 +186,25 @@ __device__ __forceinline__ void segment(const KParams& p, Smem<C>& sm, int req, 
     const __bf16* qn = p.q_nope + (int64_t)(row0 + jq) * p.qn_sr + (int64_t)head * p.qn_sh + c * C::DCW + 8 * lg;
 #pragma unroll
     for (int ks = 0; ks < C::KS; ++ks) {
-      bf16x8 v = *reinterpret_cast<const bf16x8*>(qn + 32 * ks);
+      bf16x8 v = load_q8(qn + 32 * ks, p.q_vec);
       if (!ok) v = bf16x8{};
       qf[ks][mb] = v;
     }
     const __bf16* qp = p.q_pe + (int64_t)(row0 + jq) * p.qp_sr + (int64_t)head * p.qp_sh + rope_col;
     if constexpr (C::RW == 16) {
-      s16x4 v = *reinterpret_cast<const s16x4*>(qp + 4 * lg);
+      s16x4 v;
+      if (p.q_vec) {
+        v = *reinterpret_cast<const s16x4*>(qp + 4 * lg);
+      } else {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) v[e] = reinterpret_cast<const short*>(qp + 4 * lg)[e];
+      }
       if (!ok || !has_rope) v = s16x4{};
       qr4[mb] = v;
     } else {
 #pragma unroll
       for (int k = 0; k < RKS; ++k) {
-        bf16x8 v = *reinterpret_cast<const bf16x8*>(qp + 32 * k + 8 * lg);
+        bf16x8 v = load_q8(qp + 32 * k + 8 * lg, p.q_vec);
         if (!ok) v = bf16x8{};
         qr8[k][mb] = v;
       }

@@ -238,11 +238,11 @@ __device__ __forceinline__ void process_segment(const KParams& p, Smem<C>& sm, i
         if (rv) {
           const int col = kcol + 8 * half;
           if (col < C::DCG) {
-            v = *reinterpret_cast<const bf16x8*>(qn + col);
+            v = load_q8(qn + col, p.q_vec);
           } else {
             const int pc = col - C::DCG;
             if (pc + 8 <= p.rope_w) {
-              v = *reinterpret_cast<const bf16x8*>(qp + pc);
+              v = load_q8(qp + pc, p.q_vec);
             } else if (pc < p.rope_w) {
 #pragma unroll
               for (int e = 0; e < 8; ++e) {
@@ -704,11 +704,12 @@ __global__ __launch_bounds__(256) void combine_kernel(const KParams p, int dv) {
 
 // LSE-weighted combine, balanced mode: one 256-thread workgroup per (query row, block of CH_HB
 // heads). Request b's partials sit in slots w + b for the workgroups w0..w1 that touched it; a
-// request covered by one workgroup was finished by the partial pass and is skipped here. All
-// segment LSEs are fetched at once into LDS and turned into weights; the partial outputs are
-// then read in unrolled batches so the loads of a batch are in flight together.
+// request covered by one workgroup was finished by the partial pass and is skipped here. Every
+// thread owns two adjacent output columns of the CH_HB heads and combines the segments CH_NS at a
+// time with a running maximum: the segment LSEs (the same for all threads) and the partial outputs
+// of a batch are loaded together, so a batch costs one memory round trip and no barrier.
 constexpr int CH_HB = 8;
-constexpr int CH_SEG = 32;   // segments whose weights are staged per pass
+constexpr int CH_NS = 4;   // segments per batch of loads
 __global__ __launch_bounds__(256) void combine_bal_kernel(const KParams p, int dv) {
   const int hblk = blockIdx.x, row = blockIdx.y;
   const int tid = threadIdx.x;
@@ -717,8 +718,6 @@ __global__ __launch_bounds__(256) void combine_bal_kernel(const KParams p, int d
   const int nh = p.heads - h0 < CH_HB ? p.heads - h0 : CH_HB;
   const int chunk = p.plan[0];
   const int c0 = p.plan[2 + req], c1 = p.plan[3 + req];
-  __shared__ float s_lse[CH_SEG][CH_HB];
-  __shared__ float s_m[CH_HB], s_inv[CH_HB];
   if (c1 <= c0) {  // empty request: zero output, -inf lse
     for (int h = 0; h < nh; ++h)
       for (int c = tid; c < dv; c += 256)
@@ -731,64 +730,55 @@ __global__ __launch_bounds__(256) void combine_bal_kernel(const KParams p, int d
   const int nseg = w1 - w0 + 1;
   const int64_t nrow = (int64_t)p.qrows * p.heads;
   const int rl0 = jq * p.heads + h0;
-  // pass 1: max and sum of exp over all segments, per head
-  float m = kNegInf, l = 0.f;
-  for (int s0 = 0; s0 < nseg; s0 += CH_SEG) {
-    const int ns = nseg - s0 < CH_SEG ? nseg - s0 : CH_SEG;
-    if (tid < ns * CH_HB) {
-      const int sg = tid / CH_HB, h = tid - sg * CH_HB;
-      s_lse[sg][h] = h < nh ? p.part_lse[((int64_t)w0 + s0 + sg + req) * nrow + rl0 + h] : kNegInf;
-    }
-    __syncthreads();
-    if (tid < nh) {
-      float mm = m;
-      for (int sg = 0; sg < ns; ++sg) mm = fmaxf(mm, s_lse[sg][tid]);
-      if (mm != kNegInf) {
-        l = m == kNegInf ? 0.f : l * __expf(m - mm);
-        for (int sg = 0; sg < ns; ++sg) l += __expf(s_lse[sg][tid] - mm);
-        m = mm;
-      }
-    }
-    __syncthreads();
-  }
-  if (tid < nh) {
-    s_m[tid] = m;
-    s_inv[tid] = l > 0.f ? 1.0f / l : 0.f;
-    if (p.lse) store_out(p.lse, p.lse_dt, (int64_t)row * p.lse_sr + h0 + tid, l > 0.f ? m + __logf(l) : kNegInf);
-  }
-  __syncthreads();
-  // pass 2: weighted sum of the partial outputs, 4 segments per unrolled batch
-  for (int c = tid; c < dv; c += 256) {
-    float acc[CH_HB];
+  for (int cb = 2 * tid; cb < dv; cb += 512) {
+    float m[CH_HB], l[CH_HB], a0[CH_HB], a1[CH_HB];
 #pragma unroll
-    for (int h = 0; h < CH_HB; ++h) acc[h] = 0.f;
-    for (int s0 = 0; s0 < nseg; s0 += 4) {
-      float v[4][CH_HB], ls[4][CH_HB];
+    for (int h = 0; h < CH_HB; ++h) m[h] = kNegInf, l[h] = 0.f, a0[h] = 0.f, a1[h] = 0.f;
+    for (int s0 = 0; s0 < nseg; s0 += CH_NS) {
+      float ls[CH_NS][CH_HB];
+      float2 v[CH_NS][CH_HB];
 #pragma unroll
-      for (int k = 0; k < 4; ++k) {
-        const int sg = s0 + k < nseg ? s0 + k : nseg - 1;
+      for (int k = 0; k < CH_NS; ++k) {
+        const int sg = s0 + k < nseg ? s0 + k : nseg - 1;   // past the end: a valid slot, weight 0
         const int64_t slot = (int64_t)w0 + sg + req;
         const float* pl = p.part_lse + slot * nrow + rl0;
-        const float* po = p.part_o + (slot * nrow + rl0) * (int64_t)dv + c;
+        const float* po = p.part_o + (slot * nrow + rl0) * (int64_t)dv + cb;
 #pragma unroll
         for (int h = 0; h < CH_HB; ++h) {
           const int hh = h < nh ? h : 0;
-          v[k][h] = po[(int64_t)hh * dv];
           ls[k][h] = s0 + k < nseg ? pl[hh] : kNegInf;
+          v[k][h] = *reinterpret_cast<const float2*>(po + (int64_t)hh * dv);
         }
       }
 #pragma unroll
-      for (int k = 0; k < 4; ++k)
+      for (int h = 0; h < CH_HB; ++h) {
+        float mm = m[h];
 #pragma unroll
-        for (int h = 0; h < CH_HB; ++h) {
-          const float wgt = ls[k][h] == kNegInf ? 0.f : __expf(ls[k][h] - s_m[h]);
-          acc[h] += wgt * v[k][h];
+        for (int k = 0; k < CH_NS; ++k) mm = fmaxf(mm, ls[k][h]);
+        if (mm == kNegInf) continue;
+        const float sc = m[h] == kNegInf ? 0.f : __expf(m[h] - mm);
+        l[h] *= sc;
+        a0[h] *= sc;
+        a1[h] *= sc;
+#pragma unroll
+        for (int k = 0; k < CH_NS; ++k) {
+          const float wgt = ls[k][h] == kNegInf ? 0.f : __expf(ls[k][h] - mm);
+          l[h] += wgt;
+          a0[h] += wgt * v[k][h].x;
+          a1[h] += wgt * v[k][h].y;
         }
+        m[h] = mm;
+      }
     }
 #pragma unroll
-    for (int h = 0; h < CH_HB; ++h)
-      if (h < nh)
-        store_out(p.out, p.out_dt, (int64_t)row * p.o_sr + (int64_t)(h0 + h) * p.o_sh + c, acc[h] * s_inv[h]);
+    for (int h = 0; h < CH_HB; ++h) {
+      if (h >= nh) continue;
+      const float inv = l[h] > 0.f ? 1.0f / l[h] : 0.f;
+      const int64_t ob = (int64_t)row * p.o_sr + (int64_t)(h0 + h) * p.o_sh + cb;
+      store_out(p.out, p.out_dt, ob, a0[h] * inv);
+      if (cb + 1 < dv) store_out(p.out, p.out_dt, ob + 1, a1[h] * inv);
+      if (cb == 0 && p.lse) store_out(p.lse, p.lse_dt, (int64_t)row * p.lse_sr + h0 + h, l[h] > 0.f ? m[h] + __logf(l[h]) : kNegInf);
+    }
   }
 }
 
@@ -826,6 +816,21 @@ static const Inst kInst[] = {
     QMLA_INST(2, QMLA_RMS_NONE, 512, 64, 2, 1, 2, 72, false, 64, 1, 4),
     // GLA-g2: two latent groups of 256, 12 heads each, 4 verify tokens -> 48 rows per group
     QMLA_INST(1, QMLA_RMS_LOG8, 256, 64, 3, 2, 3, 38, false, 64, 1, 4),
+    // the plugin's deployed fp8 layouts (tests/test_fp8_kv.py): partial rope of 4 groups x 58 = 232
+    // with 24 heads (one GPU) or 2 x 58 = 116 with 12 heads (rank-local at TP 2), latent ranks 256
+    // and 768; rows [latent | rope | rms (1 byte, or 2 for raw bf16) | pad to 16 bytes]
+    QMLA_INST(1, QMLA_RMS_LOG8, 256, 256, 2, 1, 3, 32, false, 64, 1, 4),
+    QMLA_INST(1, QMLA_RMS_E4M3, 256, 256, 2, 1, 3, 32, false, 64, 1, 4),
+    QMLA_INST(1, QMLA_RMS_BF16_BYTES, 256, 256, 2, 1, 3, 34, false, 64, 1, 4),
+    QMLA_INST(1, QMLA_RMS_LOG8, 768, 256, 2, 1, 3, 64, false, 32, 1, 4),
+    QMLA_INST(1, QMLA_RMS_E4M3, 768, 256, 2, 1, 3, 64, false, 32, 1, 4),
+    QMLA_INST(1, QMLA_RMS_BF16_BYTES, 768, 256, 2, 1, 3, 66, false, 32, 1, 4),
+    QMLA_INST(1, QMLA_RMS_LOG8, 256, 128, 1, 1, 3, 24, false, 64, 1, 4),
+    QMLA_INST(1, QMLA_RMS_E4M3, 256, 128, 1, 1, 3, 24, false, 64, 1, 4),
+    QMLA_INST(1, QMLA_RMS_BF16_BYTES, 256, 128, 1, 1, 3, 25, false, 64, 1, 4),
+    QMLA_INST(1, QMLA_RMS_LOG8, 768, 128, 1, 1, 2, 56, false, 64, 1, 4),
+    QMLA_INST(1, QMLA_RMS_E4M3, 768, 128, 1, 1, 2, 56, false, 64, 1, 4),
+    QMLA_INST(1, QMLA_RMS_BF16_BYTES, 768, 128, 1, 1, 2, 57, false, 64, 1, 4),
 };
 
 static int g_cu_count[64];
@@ -896,10 +901,8 @@ static int validate(const qmla_decode_params* p) {
   const int eb = elem_bytes(p->kv_dtype);
   if (!aligned16(p->kv_cache) || (p->page_stride * eb) % 16 || (p->token_stride * eb) % 16) return QMLA_ERR_ALIGN;
   if (needed_row_bytes(p) > p->token_stride * eb && p->page_size > 1) return QMLA_ERR_SHAPE;
-  if (!aligned16(p->q_nope) || (p->q_nope_stride_row * 2) % 16 || (p->q_nope_stride_head * 2) % 16)
-    return QMLA_ERR_ALIGN;
-  if (p->rope_w > 0 && (!aligned16(p->q_pe) || (p->q_pe_stride_row * 2) % 16 || (p->q_pe_stride_head * 2) % 16))
-    return QMLA_ERR_ALIGN;
+  // queries: element alignment (16-byte aligned rows take the vector loads)
+  if ((uintptr_t)p->q_nope % 2 || (p->rope_w > 0 && (uintptr_t)p->q_pe % 2)) return QMLA_ERR_ALIGN;
   return QMLA_OK;
 }
 
@@ -952,6 +955,9 @@ static BalancedLayout balanced_layout(const qmla_decode_params* p) {
 static KParams make_kparams(const qmla_decode_params* p) {
   KParams k;
   const int eb = elem_bytes(p->kv_dtype);
+  k.q_vec = aligned16(p->q_nope) && (p->q_nope_stride_row * 2) % 16 == 0 && (p->q_nope_stride_head * 2) % 16 == 0 &&
+            (p->rope_w == 0 || (aligned16(p->q_pe) && (p->q_pe_stride_row * 2) % 16 == 0 &&
+                                (p->q_pe_stride_head * 2) % 16 == 0));
   k.q_nope = reinterpret_cast<const __bf16*>(p->q_nope);
   k.qn_sr = p->q_nope_stride_row;
   k.qn_sh = p->q_nope_stride_head;
@@ -1018,6 +1024,7 @@ static int run_partial(const qmla_decode_params* p, const Inst* in, KParams& k, 
 static int run_combine(const qmla_decode_params* p, KParams& k, hipStream_t st) {
   int dv = p->d_c / p->groups;
   void* args[] = {&k, &dv};
+  if (p->num_splits == 0 && (dv & 1)) return QMLA_ERR_SHAPE;   // the balanced combine reads column pairs
   if (p->num_splits == 0)
     return launch((const void*)&combine_bal_kernel, dim3((p->heads + CH_HB - 1) / CH_HB, p->rows, 1),
                   dim3(256, 1, 1), args, st);

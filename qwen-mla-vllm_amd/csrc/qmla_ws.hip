@@ -359,8 +359,7 @@ __device__ __forceinline__ void role_main(const KParams& p, Smem<C>& sm, float k
     for (int k = 0; k < C::KQ; ++k) {
       const int col = !F8 ? 64 * (k >> 1) + 16 * lg + 8 * (k & 1)
                           : k < 4 * NB ? 128 * (k >> 2) + 32 * lg + 8 * (k & 3) : C::DCG + 16 * lg + 8 * (k - 4 * NB);
-      bf16x8 v = col < C::DCG ? *reinterpret_cast<const bf16x8*>(qnp + col)
-                              : *reinterpret_cast<const bf16x8*>(qpp + (col - C::DCG));
+      bf16x8 v = load_q8(col < C::DCG ? qnp + col : qpp + (col - C::DCG), p.q_vec);
       if (!rok) v = bf16x8{};
       qn[k] = v;
     }

@@ -95,7 +95,7 @@ def _valid_params(**over) -> _lib.DecodeParams:
     (dict(out_dtype=9), _lib.ERR_MODE),
     (dict(kv_cache=0x200008), _lib.ERR_ALIGN),
     (dict(token_stride=600), _lib.ERR_ALIGN),
-    (dict(q_nope_stride_head=500), _lib.ERR_ALIGN),
+    (dict(q_nope=0x100001), _lib.ERR_ALIGN),                 # queries need element alignment
     (dict(rows=9, qrows=2), _lib.ERR_SHAPE),
     (dict(heads=24, groups=5), _lib.ERR_SHAPE),
     (dict(token_stride=512, page_stride=64 * 512), _lib.ERR_SHAPE),   # row narrower than latent+rope

@@ -1,0 +1,77 @@
+"""The plugin's deployed FP8 layouts, built the way its own FP8 test builds them
+(tests/test_fp8_kv.py:23-31, :79-100): latent x2 with four outlier channels x8, rope x1.5, rms
+exp(N(0, 0.6)), query x0.05, per-layer scale = max|x| / 448, rows [latent | rope | rms | pad to 16],
+784-token pages behind a permuted block table, ragged lengths ctx - (37 b) % 784, 32 fixed splits,
+sm_scale 1/16, called through the reference's entry signature (decode_attention_fwd). Layouts: 24
+heads with rope 232 (one GPU) and 12 heads with rope 116 (rank-local at TP 2); latent ranks 256 and
+768; rms as log8 codes, raw bf16 bytes or e4m3.
+
+The kernel is checked against the oracle on the same cache bytes (max-abs 3e-2, the FP8 bar, and
+the reference test's own bar: max-rel < 2e-2 against the dequantized reference, :127).
+"""
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from tests.mla_cases import ora
+
+pytestmark = pytest.mark.gpu
+
+PAGE = 784
+F8 = torch.float8_e4m3fn
+ORA_MODE = {"log8": ora.RMS_LOG8, "bf16": ora.RMS_BF16_BYTES, "e4m3": ora.RMS_E4M3}
+
+
+def _case(batch, heads, ctx, rank, rope, mode, seed):
+    g = torch.Generator().manual_seed(seed)
+    pps = (ctx + PAGE - 1) // PAGE
+    lat = torch.randn(batch * pps, PAGE, rank, generator=g) * 2.0
+    lat[..., :4] *= 8
+    rp = torch.randn(batch * pps, PAGE, rope, generator=g) * 1.5
+    rms = torch.exp(torch.randn(batch * pps, PAGE, heads, generator=g) * 0.6)
+    q = (torch.randn(batch, heads, rank + rope, generator=g) * 0.05).to(torch.bfloat16)
+    scale = float(max(lat.abs().max(), rp.abs().max())) / 448
+    if mode == "bf16":
+        rb = rms.to(torch.bfloat16).contiguous().view(torch.uint8)
+    elif mode == "e4m3":
+        rb = (rms / scale).clamp(-448, 448).to(F8).view(torch.uint8)
+    else:
+        rb = ((rms.log2() + 3.0) * (255.0 / 6.0)).round().clamp(0, 255).to(torch.uint8)
+    row = torch.cat([(lat / scale).clamp(-448, 448).to(F8).view(torch.uint8),
+                     (rp / scale).clamp(-448, 448).to(F8).view(torch.uint8), rb], -1)
+    width = rank + rope + (2 if mode == "bf16" else 1) * heads
+    width += (-width) % 16
+    cache = torch.zeros(batch * pps, PAGE, 1, width, dtype=torch.uint8)
+    cache[:, :, 0, :row.shape[-1]] = row
+    bt = torch.randperm(batch * pps, generator=torch.Generator().manual_seed(1)).reshape(batch, pps).to(torch.int32)
+    lens = torch.tensor([ctx - (37 * b) % PAGE for b in range(batch)], dtype=torch.int32)
+    return q, cache, bt, lens, scale, width
+
+
+@pytest.mark.parametrize("mode", ["log8", "bf16", "e4m3"])
+@pytest.mark.parametrize("heads,rope", [(24, 232), (12, 116)])
+@pytest.mark.parametrize("rank", [256, 768])
+def test_deployed_fp8_layouts(gpu, mode, heads, rope, rank):
+    import qmla
+    batch, ctx = 4, 3000
+    q, cache, bt, lens, scale, width = _case(batch, heads, ctx, rank, rope, mode, seed=rank + heads)
+    cd = cache.to(gpu).view(F8)
+    o = torch.zeros(batch, heads, rank, dtype=torch.bfloat16, device=gpu)
+    lse = torch.zeros(batch, heads, dtype=torch.bfloat16, device=gpu)
+    logits = torch.zeros(batch, heads, 32, rank + 1, dtype=torch.float32, device=gpu)
+    ks = torch.tensor(scale, device=gpu)
+    qmla.decode_attention_fwd(q.to(gpu), cd, cd[..., :rank], o, lse, bt.to(gpu), lens.to(gpu), logits, 32, 1 / 16.0,
+                              PAGE, k_scale=ks, v_scale=ks, is_mla=True, rms_offset=rank + rope,
+                              rms_bf16=mode == "bf16", rms_log8=mode == "log8")
+    torch.cuda.synchronize()
+    ro, rl = ora.mla_decode(q[..., :rank].float(), q[..., rank:].float(), cache.view(batch * bt.shape[1], PAGE, width),
+                            bt, lens, page_size=PAGE, d_c=rank, rope_w=rope, rms_offset=rank + rope, kv="fp8",
+                            rms_mode=ORA_MODE[mode], k_scale=scale, sm_scale=1 / 16.0, rms_heads=heads, groups=1)
+    got = o.float().cpu()
+    err = (got - ro).abs().max().item()
+    rel = err / ro.abs().max().item()
+    assert err < 3e-2 and rel < 2e-2, (err, rel)
+    assert ((lse.float().cpu() - rl).abs() - 2.0 ** -7 * rl.abs()).max().item() < 1e-2   # lse is stored as bf16
+    assert np.isfinite(got.numpy()).all()
