@@ -831,6 +831,10 @@ static const Inst kInst[] = {
     QMLA_INST(1, QMLA_RMS_LOG8, 768, 128, 1, 1, 2, 56, false, 64, 1, 4),
     QMLA_INST(1, QMLA_RMS_E4M3, 768, 128, 1, 1, 2, 56, false, 64, 1, 4),
     QMLA_INST(1, QMLA_RMS_BF16_BYTES, 768, 128, 1, 1, 2, 57, false, 64, 1, 4),
+    // the same layouts on bf16 caches (tests/test_fi_partial_rope.py): one bf16 rms per head
+    QMLA_INST(2, QMLA_RMS_BF16, 256, 256, 2, 1, 3, 64, false, 32, 1, 4),
+    QMLA_INST(2, QMLA_RMS_BF16, 256, 128, 1, 1, 2, 48, false, 64, 1, 4),
+    QMLA_INST(2, QMLA_RMS_BF16, 768, 128, 2, 1, 2, 112, false, 32, 1, 4),
 };
 
 static int g_cu_count[64];

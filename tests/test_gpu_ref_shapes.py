@@ -75,3 +75,41 @@ def test_deployed_fp8_layouts(gpu, mode, heads, rope, rank):
     assert err < 3e-2 and rel < 2e-2, (err, rel)
     assert ((lse.float().cpu() - rl).abs() - 2.0 ** -7 * rl.abs()).max().item() < 1e-2   # lse is stored as bf16
     assert np.isfinite(got.numpy()).all()
+
+
+def _bf16_case(batch, heads, ctx, rank, rope, page, seed):
+    """tests/test_fi_partial_rope.py:27-46 with --shuffle --ragged --rms-spread: bf16 rows
+    [latent | rope | one rms per head | pad to 16 bytes], rms exp(N(0,1)) per (key, head)."""
+    g = torch.Generator().manual_seed(seed)
+    entry = rank + rope + heads + (-(rope + heads)) % 8
+    pps = (ctx + page - 1) // page
+    cache = (torch.randn(batch * pps, page, 1, entry, generator=g) * 0.05).to(torch.bfloat16)
+    cache[..., rank + rope:] = torch.exp(torch.randn(batch * pps, page, 1, entry - rank - rope, generator=g)).to(torch.bfloat16)
+    q = (torch.randn(batch, heads, rank + rope, generator=g) * 0.05).to(torch.bfloat16)
+    gb = torch.Generator().manual_seed(1)
+    bt = torch.randperm(batch * pps, generator=gb).reshape(batch, pps).to(torch.int32)
+    lens = torch.tensor([ctx - (int(torch.randint(0, page + 37, (1,), generator=gb)) if b else 0) for b in range(batch)],
+                        dtype=torch.int32)
+    return cache, q, bt, lens, entry
+
+
+@pytest.mark.parametrize("rank,heads,rope", [(256, 24, 232), (256, 12, 116), (768, 12, 116)])
+def test_deployed_bf16_layouts(gpu, rank, heads, rope):
+    import qmla
+    batch, ctx, page = 4, 2048, 400
+    cache, q, bt, lens, entry = _bf16_case(batch, heads, ctx, rank, rope, page, seed=rank + heads)
+    cd = cache.to(gpu)
+    o = torch.zeros(batch, heads, rank, dtype=torch.bfloat16, device=gpu)
+    lse = torch.zeros(batch, heads, dtype=torch.bfloat16, device=gpu)
+    logits = torch.zeros(batch, heads, 64, rank + 1, dtype=torch.float32, device=gpu)
+    qmla.decode_attention_fwd(q.to(gpu), cd, cd[..., :rank], o, lse, bt.to(gpu), lens.to(gpu), logits, 64,
+                              1.0 / 256 ** 0.5, page, is_mla=True, rms_offset=rank + rope)
+    torch.cuda.synchronize()
+    cu8 = cache.view(torch.uint8).view(cache.shape[0], page, entry * 2)
+    ro, rl = ora.mla_decode(q[..., :rank].float(), q[..., rank:].float(), cu8, bt, lens, page_size=page, d_c=rank,
+                            rope_w=rope, rms_offset=rank + rope, kv="bf16", rms_mode=ora.RMS_BF16,
+                            sm_scale=1.0 / 256 ** 0.5, rms_heads=heads, groups=1)
+    got = o.float().cpu()
+    err = ((got - ro).abs() - 2.0 ** -7 * ro.abs()).max().item()   # bf16 output rounding allowed
+    assert err < 1e-2, err
+    assert ((lse.float().cpu() - rl).abs() - 2.0 ** -7 * rl.abs()).max().item() < 1e-2
