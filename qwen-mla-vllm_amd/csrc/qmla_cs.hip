@@ -74,15 +74,6 @@ __device__ __forceinline__ uint32_t ldsr16(const char* p) {
   return r;
 }
 
-// 4 fp8 bytes -> bf16x4 (exact). Assembled from whole 32-bit words: element-wise bit casts of the
-// packed results have been compiled into a permute that duplicated the low half.
-__device__ __forceinline__ s16x4 fp8x4_to_bf16(int raw) {
-  const bf16x2 a = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(raw, 1.0f, false);
-  const bf16x2 b = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(raw, 1.0f, true);
-  const i32x2 r = {__builtin_bit_cast(int, a), __builtin_bit_cast(int, b)};
-  return __builtin_bit_cast(s16x4, r);
-}
-
 // Compile-time shape of one instance.
 //   EB   cache element bytes (1 = fp8 e4m3fn, 2 = bf16);  RMS  QMLA_RMS_* tail format
 //   DCG  latent columns per group, G latent groups;  NCG column slices per group
@@ -90,19 +81,23 @@ __device__ __forceinline__ s16x4 fp8x4_to_bf16(int raw) {
 //   MB   16-row blocks per latent group (rows per group = qrows*heads/G <= 16*MB)
 //   S    LDS ring stages;  CRM 16-byte chunks of the rms tail staged per token;  CAP tanh logit cap
 //   RTR  rms codes read transposed (rows are the heads of one token: G = 1 and qrows = 1)
+//   WP   rope columns staged per row: 64 (exactly the rope), or the padded window 128 / 256 of a
+//        partial rope (116 / 232 wide), spread over all NCG waves; columns past rope_w are zeroed
+//        in both operands (the row bytes there are rms codes, which may read as fp8 NaN)
 template <int EB_, int RMS_, int DCG_, int G_, int NCG_, int NTG_, int NTB_, int MB_, int S_, int CRM_,
-          bool CAP_, bool RTR_>
+          bool CAP_, bool RTR_, int WP_>
 struct CS {
   static constexpr int EB = EB_, RMS = RMS_, DCG = DCG_, G = G_, NCG = NCG_, NTG = NTG_, NTB = NTB_;
-  static constexpr int MB = MB_, S = S_, CRM = CRM_;
+  static constexpr int MB = MB_, S = S_, CRM = CRM_, WP = WP_;
   static constexpr bool CAP = CAP_, RTR = RTR_;
+  static constexpr bool PR = WP != 64;                   // partial rope: mask columns >= rope_w
   static constexpr int NW = G * NCG * NTG, NTHR = 64 * NW;
   static constexpr int T = 16 * NTB, TT = NTG * T;
   static constexpr int DC = G * DCG;
   static constexpr int DCW = DCG / NCG;                  // latent columns per wave
   static constexpr int KS = DCW / 32;                    // 32-column k-steps
   static constexpr int CB = DCW / 16;                    // 16-column output blocks
-  static constexpr int RW = NCG >= 4 ? 16 : 64 / NCG;    // rope columns per wave (NCG 8: waves c < 4)
+  static constexpr int RW = PR ? WP / NCG : (NCG >= 4 ? 16 : 64 / NCG);   // rope columns per wave (WP 64, NCG 8: waves c < 4)
   static constexpr int CL = DCW * EB / 16;               // latent chunks of a row slice
   static constexpr int CR = RW * EB / 16;                // rope chunks
   static constexpr int CPW = (CL + CR) | 1;              // odd 16-byte count: conflict-free rows
@@ -119,6 +114,7 @@ struct CS {
   static_assert(NTB == 1 || NTB == 2, "score tiles per token group");
   static_assert(EB == 2 || NTB == 2, "fp8 values are read 8 tokens at a time");
   static_assert(RW == 16 || RW == 32 || RW == 64, "rope slice");
+  static_assert(!PR || (WP % NCG == 0 && (WP == 128 || WP == 256)), "padded rope window");
   static_assert((S - 1) * (NI + NRI) < 64, "vmcnt range");
   static_assert(!RTR || CRM * 16 >= RB * ROWS, "transposed rms reads cover all row heads");
 };
@@ -155,11 +151,16 @@ __device__ __forceinline__ void segment(const KParams& p, Smem<C>& sm, int req, 
   const int g = (w / C::NCG) % C::G;
   const int c = w % C::NCG;
   const bool rms_wave = (C::CRM > 0) && (w % (C::G * C::NCG)) == 0;   // (g 0, c 0) of each token group
-  const bool has_rope = C::NCG < 8 || c < 4;
-  const int rope_col = C::NCG >= 4 ? 16 * (c & 3) : C::RW * c;
+  const bool has_rope = C::PR || C::NCG < 8 || c < 4;
+  const int rope_col = (C::NCG >= 4 && !C::PR) ? 16 * (c & 3) : C::RW * c;
+  // the rms tail is staged from the 16-byte boundary at or below its offset
+  const int roff_al = p.rms_off_b & ~15, rdelta = p.rms_off_b & 15;
   const int ln16 = lane & 15, lg = lane >> 4;
   const int hpg = p.hpg;
   const int rows_pg = p.qrows * hpg;
+  // rows (verify token x head of the group) [rbase, rbase + 16*MB) of the request: requests with
+  // more rows than one workgroup holds are split over gridDim.z workgroups (each reads the rows)
+  const int rbase = (int)blockIdx.z * C::ROWS;
   const int row0 = req * p.qrows;
   const int P = p.page_size;
   const int64_t TS = p.token_stride_b, PS = p.page_stride_b;
@@ -170,19 +171,22 @@ __device__ __forceinline__ void segment(const KParams& p, Smem<C>& sm, int req, 
   // ---- query fragments (B operands) for this wave's columns; zero for padding rows ----
   bf16x8 qf[C::KS][C::MB];
   constexpr int RKS = C::RW == 64 ? 2 : 1;
-  bf16x8 qr8[RKS][C::MB];   // RW 32/64: 16x16x32 steps
-  s16x4 qr4[C::MB];         // RW 16: one 16x16x16 step
+  // rope: 16x16x32 steps. A 16-column slice is one step with the upper half zero (lanes lg 0-1
+  // carry columns 8lg..8lg+7, lanes 2-3 zeros in both operands), so every product of the score
+  // chain has the same MFMA shape: a 16x16x16 step accumulating onto a 16x16x32 result right
+  // behind it reads the accumulator before it is complete
+  bf16x8 qr8[RKS][C::MB];
   int lim[C::MB], hb[C::MB];
 #pragma unroll
   for (int mb = 0; mb < C::MB; ++mb) {
-    const int r = ln16 + 16 * mb;
+    const int r = rbase + ln16 + 16 * mb;
     const bool ok = r < rows_pg;
     const int jq = ok ? r / hpg : 0, hh = ok ? r - jq * hpg : 0;
     const int head = g * hpg + hh;
     // verify row jq of the request sees its first L - (qrows-1-jq) tokens (mla_impl.py:628-662)
     const int lr = L - (p.qrows - 1 - jq);
     lim[mb] = ok ? (lr < te ? lr : te) : 0;
-    hb[mb] = ok ? head * C::RB : 0;
+    hb[mb] = (ok ? head * C::RB : 0) + rdelta;
     const __bf16* qn = p.q_nope + (int64_t)(row0 + jq) * p.qn_sr + (int64_t)head * p.qn_sh + c * C::DCW + 8 * lg;
 #pragma unroll
     for (int ks = 0; ks < C::KS; ++ks) {
@@ -191,23 +195,47 @@ __device__ __forceinline__ void segment(const KParams& p, Smem<C>& sm, int req, 
       qf[ks][mb] = v;
     }
     const __bf16* qp = p.q_pe + (int64_t)(row0 + jq) * p.qp_sr + (int64_t)head * p.qp_sh + rope_col;
-    if constexpr (C::RW == 16) {
-      s16x4 v;
-      if (p.q_vec) {
-        v = *reinterpret_cast<const s16x4*>(qp + 4 * lg);
-      } else {
+    const bool lane_rope = C::RW != 16 || lg < 2;
+    if constexpr (C::PR) {
+      // element loads of the real rope columns only; the window past rope_w is zero
 #pragma unroll
-        for (int e = 0; e < 4; ++e) v[e] = reinterpret_cast<const short*>(qp + 4 * lg)[e];
+      for (int k = 0; k < RKS; ++k) {
+        bf16x8 v;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const int col = (C::RW == 16 ? 8 * (lg & 1) : 32 * k + 8 * lg) + e;
+          v[e] = (ok && lane_rope && rope_col + col < p.rope_w) ? qp[col] : (__bf16)0.0f;
+        }
+        qr8[k][mb] = v;
       }
-      if (!ok || !has_rope) v = s16x4{};
-      qr4[mb] = v;
     } else {
 #pragma unroll
       for (int k = 0; k < RKS; ++k) {
-        bf16x8 v = load_q8(qp + 32 * k + 8 * lg, p.q_vec);
-        if (!ok) v = bf16x8{};
+        bf16x8 v = load_q8(qp + (C::RW == 16 ? 8 * (lg & 1) : 32 * k + 8 * lg), p.q_vec);
+        if (!ok || !has_rope || !lane_rope) v = bf16x8{};
         qr8[k][mb] = v;
       }
+    }
+  }
+  // key masks of a padded rope window: word j of k-step k covers the lane's elements
+  // [4j/EB, 4(j+1)/EB); elements at columns >= rope_w (rms codes, possibly fp8 NaN bytes) and the
+  // zero half of a 16-column step are cleared. Without a window no mask is needed: the zero query
+  // lanes meet rope bytes of the same row (a 16-column step's upper lanes read its lower half)
+  constexpr bool KMASK = C::PR;
+  uint32_t kmw[RKS][4];
+#pragma unroll
+  for (int k = 0; k < RKS; ++k) {
+    const int col0 = rope_col + (C::RW == 16 ? 8 * (lg & 1) : 32 * k + 8 * lg);
+    const bool lane_ok = has_rope && (C::RW != 16 || lg < 2);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      uint32_t m = 0;
+#pragma unroll
+      for (int b = 0; b < 4 / C::EB; ++b) {
+        const int e = j * (4 / C::EB) + b;
+        if (lane_ok && (!C::PR || col0 + e < p.rope_w)) m |= (C::EB == 1 ? 0xFFu : 0xFFFFu) << (8 * C::EB * b);
+      }
+      kmw[k][j] = m;
     }
   }
   // smallest row limit: tiles below it need no masking
@@ -278,7 +306,7 @@ __device__ __forceinline__ void segment(const KParams& p, Smem<C>& sm, int req, 
             const int j = 64 * k + ln;
             const int row = j / (C::CRM > 0 ? C::CRM : 1);
             if (64 * k + 64 <= C::T * C::CRM || j < C::T * C::CRM)
-              dma16_buf(rs, (uint32_t)((tb0 + row) * (int)TS + p.rms_off_b + 16 * (j - row * C::CRM)), rdst + k * 1024);
+              dma16_buf(rs, (uint32_t)((tb0 + row) * (int)TS + roff_al + 16 * (j - row * C::CRM)), rdst + k * 1024);
           }
         }
       } else {
@@ -307,7 +335,7 @@ __device__ __forceinline__ void segment(const KParams& p, Smem<C>& sm, int req, 
               const int tok = nv > 0 ? tb0 + rr : se - 1;
               const int q = tok / P;
               const int pg = sm.pid[q - pbase];
-              dma16(p.kv + (int64_t)pg * PS + (int64_t)(tok - q * P) * TS + p.rms_off_b + 16 * (j - row * C::CRM),
+              dma16(p.kv + (int64_t)pg * PS + (int64_t)(tok - q * P) * TS + roff_al + 16 * (j - row * C::CRM),
                     rdst + k * 1024);
             }
           }
@@ -334,39 +362,27 @@ __device__ __forceinline__ void segment(const KParams& p, Smem<C>& sm, int req, 
           i32x2 kv[C::KS];
 #pragma unroll
           for (int ks = 0; ks < C::KS; ++ks) kv[ks] = ldsr64(kr + 32 * ks + 8 * lg);
-          if constexpr (C::RW == 16) {
-            int rv = ldsr32(kr + 16 * C::CL + 4 * lg);
+          i32x2 rv[RKS];
 #pragma unroll
-            for (int ks = 0; ks < C::KS; ++ks) {
-              lds_wait(kv[ks]);
-              const bf16x8 kf = fp8x8_to_bf16(kv[ks]);
+          for (int k = 0; k < RKS; ++k)
+            rv[k] = ldsr64(kr + 16 * C::CL + (C::RW == 16 ? 8 * (lg & 1) : 32 * k + 8 * lg));
 #pragma unroll
-              for (int mb = 0; mb < C::MB; ++mb) sp[tb][mb] = mfma16(kf, qf[ks][mb], sp[tb][mb]);
+          for (int ks = 0; ks < C::KS; ++ks) {
+            lds_wait(kv[ks]);
+            const bf16x8 kf = fp8x8_to_bf16(kv[ks]);
+#pragma unroll
+            for (int mb = 0; mb < C::MB; ++mb) sp[tb][mb] = mfma16(kf, qf[ks][mb], sp[tb][mb]);
+          }
+#pragma unroll
+          for (int k = 0; k < RKS; ++k) {
+            lds_wait(rv[k]);
+            if constexpr (KMASK) {
+              rv[k][0] &= (int)kmw[k][0];
+              rv[k][1] &= (int)kmw[k][1];
             }
-            lds_wait(rv);
-            if (has_rope) {
-              const s16x4 rf = fp8x4_to_bf16(rv);
+            const bf16x8 rf = fp8x8_to_bf16(rv[k]);
 #pragma unroll
-              for (int mb = 0; mb < C::MB; ++mb) sp[tb][mb] = mfma16k16(rf, qr4[mb], sp[tb][mb]);
-            }
-          } else {
-            i32x2 rv[RKS];
-#pragma unroll
-            for (int k = 0; k < RKS; ++k) rv[k] = ldsr64(kr + 16 * C::CL + 32 * k + 8 * lg);
-#pragma unroll
-            for (int ks = 0; ks < C::KS; ++ks) {
-              lds_wait(kv[ks]);
-              const bf16x8 kf = fp8x8_to_bf16(kv[ks]);
-#pragma unroll
-              for (int mb = 0; mb < C::MB; ++mb) sp[tb][mb] = mfma16(kf, qf[ks][mb], sp[tb][mb]);
-            }
-#pragma unroll
-            for (int k = 0; k < RKS; ++k) {
-              lds_wait(rv[k]);
-              const bf16x8 rf = fp8x8_to_bf16(rv[k]);
-#pragma unroll
-              for (int mb = 0; mb < C::MB; ++mb) sp[tb][mb] = mfma16(rf, qr8[k][mb], sp[tb][mb]);
-            }
+            for (int mb = 0; mb < C::MB; ++mb) sp[tb][mb] = mfma16(rf, qr8[k][mb], sp[tb][mb]);
           }
         } else {
           constexpr int KB = 4;   // k-steps per batch of LDS reads
@@ -385,23 +401,17 @@ __device__ __forceinline__ void segment(const KParams& p, Smem<C>& sm, int req, 
                 for (int mb = 0; mb < C::MB; ++mb) sp[tb][mb] = mfma16(kf, qf[k0 + j][mb], sp[tb][mb]);
               }
           }
-          if constexpr (C::RW == 16) {
-            i32x2 rv = ldsr64(kr + 16 * C::CL + 8 * lg);
+#pragma unroll
+          for (int k = 0; k < RKS; ++k) {
+            i32x4 rv = ldsr128(kr + 16 * C::CL + (C::RW == 16 ? 16 * (lg & 1) : 64 * k + 16 * lg));
             lds_wait(rv);
-            if (has_rope) {
-              const s16x4 rf = __builtin_bit_cast(s16x4, rv);
+            if constexpr (KMASK) {
 #pragma unroll
-              for (int mb = 0; mb < C::MB; ++mb) sp[tb][mb] = mfma16k16(rf, qr4[mb], sp[tb][mb]);
+              for (int j = 0; j < 4; ++j) rv[j] &= (int)kmw[k][j];
             }
-          } else {
+            const bf16x8 rf = __builtin_bit_cast(bf16x8, rv);
 #pragma unroll
-            for (int k = 0; k < RKS; ++k) {
-              i32x4 rv = ldsr128(kr + 16 * C::CL + 64 * k + 16 * lg);
-              lds_wait(rv);
-              const bf16x8 rf = __builtin_bit_cast(bf16x8, rv);
-#pragma unroll
-              for (int mb = 0; mb < C::MB; ++mb) sp[tb][mb] = mfma16(rf, qr8[k][mb], sp[tb][mb]);
-            }
+            for (int mb = 0; mb < C::MB; ++mb) sp[tb][mb] = mfma16(rf, qr8[k][mb], sp[tb][mb]);
           }
         }
       }
@@ -452,11 +462,11 @@ __device__ __forceinline__ void segment(const KParams& p, Smem<C>& sm, int req, 
         const char* rs = sm.rms[t % (C::S + 1)][tg];
         uint32_t code[C::NTB][C::MB][4];
         if constexpr (C::RTR && C::RB == 1) {
-          // one tr_b8 read per 16 rows: lane (n, q) gets head 16mb+n of the 8 tokens vtok(q, 0..7)
+          // one tr_b8 read per 16 rows: lane (n, q) gets head rbase+16mb+n of the 8 tokens vtok(q, 0..7)
           i32x2 raw[C::MB];
           const int rr = vtok(lg, ln16 >> 1);
 #pragma unroll
-          for (int mb = 0; mb < C::MB; ++mb) raw[mb] = lds_read_tr8_async(rs + rr * C::RRS + 16 * mb + 8 * (ln16 & 1));
+          for (int mb = 0; mb < C::MB; ++mb) raw[mb] = lds_read_tr8_async(rs + rr * C::RRS + rbase + 16 * mb + 8 * (ln16 & 1));
 #pragma unroll
           for (int mb = 0; mb < C::MB; ++mb) {
             lds_wait(raw[mb]);
@@ -467,14 +477,14 @@ __device__ __forceinline__ void segment(const KParams& p, Smem<C>& sm, int req, 
             }
           }
         } else if constexpr (C::RTR && C::RB == 2) {
-          // tr_b16: lanes 4r..4r+3 of a 16-lane block supply token row r; lane n gets head 16mb+n
+          // tr_b16: lanes 4r..4r+3 of a 16-lane block supply token row r; lane n gets head rbase+16mb+n
 #pragma unroll
           for (int tb = 0; tb < C::NTB; ++tb) {
             i32x2 raw[C::MB];
             const int rr = tok_of(tb, 4 * lg + (ln16 >> 2));
 #pragma unroll
             for (int mb = 0; mb < C::MB; ++mb)
-              raw[mb] = lds_read_tr16_async(rs + rr * C::RRS + 32 * mb + 8 * (ln16 & 3));
+              raw[mb] = lds_read_tr16_async(rs + rr * C::RRS + 2 * rbase + 32 * mb + 8 * (ln16 & 3));
 #pragma unroll
             for (int mb = 0; mb < C::MB; ++mb) {
               lds_wait(raw[mb]);
@@ -715,7 +725,7 @@ __device__ __forceinline__ void segment(const KParams& p, Smem<C>& sm, int req, 
     for (int i = 0; i < 4; ++i) iv[i] = __shfl(inv, 4 * lg + i);
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      const int r = 16 * mb + 4 * lg + i;
+      const int r = rbase + 16 * mb + 4 * lg + i;
       if (r >= rows_pg) continue;
       const int jq = r / hpg, hh = r - jq * hpg;
       const int head = g * hpg + hh;
@@ -742,7 +752,7 @@ __device__ __forceinline__ void segment(const KParams& p, Smem<C>& sm, int req, 
       }
     }
     // lse from the score layout (row ln16 + 16mb), one lane per row
-    const int r = ln16 + 16 * mb;
+    const int r = rbase + ln16 + 16 * mb;
     if (c == 0 && lg == 0 && r < rows_pg) {
       const int jq = r / hpg, hh = r - jq * hpg;
       const int head = g * hpg + hh;
@@ -773,44 +783,65 @@ __global__ __launch_bounds__(C::NTHR, 1) void cs_kernel(const KParams p) {
 }
 
 struct Inst {
-  int eb, rms, dcg, g, mb, crm, nthr;
+  int eb, rms, dcg, g, mb, crm, wp, nthr;
   bool cap, rtr;
   void (*fn)(const KParams);
 };
 
-#define QMLA_CS(EB, RMS, DCG, G, NCG, NTG, NTB, MB, S, CRM, CAP, RTR)                                \
-  {EB, RMS, DCG, G, MB, CRM, CS<EB, RMS, DCG, G, NCG, NTG, NTB, MB, S, CRM, CAP, RTR>::NTHR, CAP, RTR, \
-   &cs_kernel<CS<EB, RMS, DCG, G, NCG, NTG, NTB, MB, S, CRM, CAP, RTR>>}
+#define QMLA_CS(EB, RMS, DCG, G, NCG, NTG, NTB, MB, S, CRM, CAP, RTR, WP)                                    \
+  {EB, RMS, DCG, G, MB, CRM, WP, CS<EB, RMS, DCG, G, NCG, NTG, NTB, MB, S, CRM, CAP, RTR, WP>::NTHR, CAP, RTR, \
+   &cs_kernel<CS<EB, RMS, DCG, G, NCG, NTG, NTB, MB, S, CRM, CAP, RTR, WP>>}
 
-// One entry per compiled shape (rope 64; rows [latent | rope | rms | pad]).
+// One entry per compiled shape; rows [latent | rope | rms | pad].
 static const Inst kInst[] = {
     // bf16 cache, d_c 1792 (the reference's two-pass widths): 8 column slices, 16-token tiles
-    QMLA_CS(2, QMLA_RMS_BF16, 1792, 1, 8, 1, 1, 2, 2, 4, false, true),
-    QMLA_CS(2, QMLA_RMS_NONE, 1792, 1, 8, 1, 1, 2, 2, 0, false, false),
+    QMLA_CS(2, QMLA_RMS_BF16, 1792, 1, 8, 1, 1, 2, 2, 4, false, true, 64),
+    QMLA_CS(2, QMLA_RMS_NONE, 1792, 1, 8, 1, 1, 2, 2, 0, false, false, 64),
+    // fp8 cache, d_c 1792: 32-token tiles, 16 rows per workgroup (32 rows of 1792 accumulator and
+    // query columns exceed the register file), more heads split over gridDim.z.
+    // Rope 64, log8 codes (transposed rms reads: 2 chunks cover the heads of two row blocks):
+    QMLA_CS(1, QMLA_RMS_LOG8, 1792, 1, 8, 1, 2, 1, 2, 2, false, true, 64),
+    // the plugin's deployed fp8 layouts at rank 1792 (tests/test_fp8_kv.py:136-138): rope 116 with
+    // 12 heads (window 128) and rope 232 with 24 heads (window 256); log8 / e4m3 / bf16-byte rms
+    // tails at offsets that are not 16-byte aligned (general rms reads)
+    QMLA_CS(1, QMLA_RMS_LOG8, 1792, 1, 8, 1, 2, 1, 2, 1, false, false, 128),
+    QMLA_CS(1, QMLA_RMS_E4M3, 1792, 1, 8, 1, 2, 1, 2, 1, false, false, 128),
+    QMLA_CS(1, QMLA_RMS_BF16_BYTES, 1792, 1, 8, 1, 2, 1, 2, 2, false, false, 128),
+    QMLA_CS(1, QMLA_RMS_LOG8, 1792, 1, 8, 1, 2, 1, 2, 2, false, false, 256),
+    QMLA_CS(1, QMLA_RMS_E4M3, 1792, 1, 8, 1, 2, 1, 2, 2, false, false, 256),
+    QMLA_CS(1, QMLA_RMS_BF16_BYTES, 1792, 1, 8, 1, 2, 1, 2, 4, false, false, 256),
 };
+
+// workgroups per request along z: its rows in blocks of 16*MB
+static int row_splits(const Inst& in, const qmla_decode_params* p) {
+  const int rows_pg = p->qrows * (p->heads / p->groups);
+  return (rows_pg + 16 * in.mb - 1) / (16 * in.mb);
+}
 
 }  // namespace cs
 
 int cs_select(const qmla_decode_params* p) {
-  if (p->rope_w != 64) return -1;
   const int eb = p->kv_dtype == QMLA_KV_FP8 ? 1 : 2;
   const int dcg = p->d_c / p->groups;
-  const int hpg = p->heads / p->groups;
-  const int rows_pg = p->qrows * hpg;
   const bool cap = p->logit_cap > 0.f;
   const int64_t ts = p->token_stride * eb;
   for (int i = 0; i < (int)(sizeof(cs::kInst) / sizeof(cs::kInst[0])); ++i) {
     const cs::Inst& in = cs::kInst[i];
     if (in.eb != eb || in.rms != p->rms_mode || in.dcg != dcg || in.g != p->groups || in.cap != cap) continue;
-    if (rows_pg > 16 * in.mb) continue;
+    const int hs = cs::row_splits(in, p);
+    if (hs > 4) continue;   // at most 4 workgroups read each token range
     if (in.rtr && (p->qrows != 1 || p->groups != 1)) continue;
-    if ((int64_t)p->d_c * eb + 64 * eb > ts) continue;     // latent + rope inside the row
+    // rope 64 exactly, or a partial rope inside the instance's padded window
+    if (in.wp == 64 ? p->rope_w != 64 : (p->rope_w < 1 || p->rope_w > in.wp)) continue;
+    if ((int64_t)p->d_c * eb + (int64_t)in.wp * eb > ts) continue;   // latent + rope window inside the row
     if (in.crm > 0) {
       const int rb = (p->rms_mode == QMLA_RMS_BF16 || p->rms_mode == QMLA_RMS_BF16_BYTES) ? 2 : 1;
       const int64_t roff = (int64_t)p->rms_offset * eb;
-      const int need = in.rtr ? 16 * in.mb * rb : p->heads * rb;   // transposed reads cover 16*MB heads
-      if (need > 16 * in.crm || roff % 16 || roff + 16 * in.crm > ts) continue;
-      if (!in.rtr && p->rms_heads * rb > 16 * in.crm) continue;
+      const int64_t delta = roff % 16;   // staged from the 16-byte boundary below the tail
+      if (in.rtr && delta) continue;     // transposed reads need an aligned tail
+      const int64_t need = in.rtr ? 16 * in.mb * hs * rb : delta + (int64_t)p->heads * rb;   // transposed reads cover 16*MB*hs heads
+      if (need > 16 * in.crm || roff - delta + 16 * in.crm > ts) continue;
+      if (!in.rtr && delta + (int64_t)p->rms_heads * rb > 16 * in.crm) continue;
     }
     return i;
   }
@@ -820,7 +851,8 @@ int cs_select(const qmla_decode_params* p) {
 int cs_launch(int inst, const qmla_decode_params* p, const KParams& k, int nwg, hipStream_t st) {
   KParams kk = k;
   void* args[] = {&kk};
-  dim3 grid = p->num_splits > 0 ? dim3(p->num_splits, k.n_req, 1) : dim3(nwg, 1, 1);
+  const int hs = cs::row_splits(cs::kInst[inst], p);
+  dim3 grid = p->num_splits > 0 ? dim3(p->num_splits, k.n_req, hs) : dim3(nwg, 1, hs);
   if (grid.x == 0 || grid.y == 0) return QMLA_OK;
   hipError_t e = hipLaunchKernel((const void*)cs::kInst[inst].fn, grid, dim3(cs::kInst[inst].nthr, 1, 1), args, 0, st);
   return e == hipSuccess ? QMLA_OK : QMLA_ERR_LAUNCH;

@@ -3,8 +3,8 @@
 exp(N(0, 0.6)), query x0.05, per-layer scale = max|x| / 448, rows [latent | rope | rms | pad to 16],
 784-token pages behind a permuted block table, ragged lengths ctx - (37 b) % 784, 32 fixed splits,
 sm_scale 1/16, called through the reference's entry signature (decode_attention_fwd). Layouts: 24
-heads with rope 232 (one GPU) and 12 heads with rope 116 (rank-local at TP 2); latent ranks 256 and
-768; rms as log8 codes, raw bf16 bytes or e4m3.
+heads with rope 232 (one GPU) and 12 heads with rope 116 (rank-local at TP 2); latent ranks 256, 768
+and 1792 (:137); rms as log8 codes, raw bf16 bytes or e4m3.
 
 The kernel is checked against the oracle on the same cache bytes (max-abs 3e-2, the FP8 bar, and
 the reference test's own bar: max-rel < 2e-2 against the dequantized reference, :127).
@@ -52,7 +52,7 @@ def _case(batch, heads, ctx, rank, rope, mode, seed):
 
 @pytest.mark.parametrize("mode", ["log8", "bf16", "e4m3"])
 @pytest.mark.parametrize("heads,rope", [(24, 232), (12, 116)])
-@pytest.mark.parametrize("rank", [256, 768])
+@pytest.mark.parametrize("rank", [256, 768, 1792])
 def test_deployed_fp8_layouts(gpu, mode, heads, rope, rank):
     import qmla
     batch, ctx = 4, 3000

@@ -1,8 +1,11 @@
-"""GPU parity of the wide-latent decode (d_c = 1792, bf16 cache, rope 64, 24 heads) against the CPU
-oracle: the reference routes these widths to its two-pass path (ops/mla_decode_attention.py:778-849);
-the library computes them in one pass, with the same partial layout and split bounds.
+"""GPU parity of the wide-latent decode (d_c = 1792, rope 64, 24 heads) against the CPU oracle: the
+reference routes these widths to its two-pass path (ops/mla_decode_attention.py:778-849); the library
+computes them in one pass, with the same partial layout and split bounds. bf16 caches (one workgroup
+holds the 24 heads), FP8 caches with log8 codes (16 rows per workgroup: the heads are split over two
+workgroups that read the same tokens), and 4-token verify rows (96 rows over three workgroups).
 
-Tolerance: max-abs 1e-2 on the output (bf16 cache) beyond the output's own bf16 rounding, lse 1e-2.
+Tolerance: max-abs 1e-2 (bf16 cache) / 3e-2 (FP8 cache) on the output beyond the output's own bf16
+rounding, lse 1e-2.
 """
 import pytest
 import torch
@@ -86,4 +89,46 @@ def test_wide_no_rms(gpu):
     torch.cuda.synchronize()
     ro, rl = run_oracle(c)
     err, lerr = _report("wide no-rms", o, lse, ro, rl)
+    assert err < TOL and lerr < 1e-2
+
+
+@pytest.mark.parametrize("page_size,splits", [(64, 16), (40, 0)])
+def test_wide_fp8(gpu, page_size, splits):
+    """FP8 rows with log8 codes: fixed splits on 64-token pages and the balanced mode on 40-token
+    pages (pages change inside a 32-token tile)."""
+    import qmla
+    lens = [1, 2100, 5000, 333]
+    c = make_case(batch=len(lens), heads=24, d_c=DC, rope_w=64, page_size=page_size, lens=lens, kv="fp8",
+                  rms_mode="log8", seed=21, device=gpu, rms="spread", amp=4.0)
+    o, lse = qmla.forward(c.q_nope, c.q_pe, c.cache, c.block_table, c.seq_lens, page_size=page_size,
+                          sm_scale=c.sm_scale, kv_fp8=True, fp8_rms="log8", k_scale=c.k_scale, num_splits=splits,
+                          num_workgroups=0 if splits else 11)
+    torch.cuda.synchronize()
+    ro, rl = run_oracle(c)
+    err, lerr = _report(f"wide fp8 P={page_size} S={splits}", o, lse, ro, rl)
+    assert err < 3e-2 and lerr < 1e-2
+
+
+def test_wide_verify_rows(gpu):
+    """4 verify tokens per request (row j sees L - 3 + j tokens) x 24 heads, no rms tail, passed to the
+    C entry unfolded (96 rows per request: three workgroups per token range), balanced mode."""
+    import qmla
+    from qmla import _lib
+    from qmla.decode import Workspace, build_params, workspace_bytes
+    lens = [5, 1500, 3333]
+    c = make_case(batch=len(lens), heads=24, d_c=DC, rope_w=64, page_size=64, lens=lens, kv="bf16",
+                  rms_mode="none", seed=22, device=gpu, qrows=4)
+    rows = c.q_nope.shape[0]
+    out = torch.empty(rows, 24, DC, dtype=torch.bfloat16, device=gpu)
+    lse = torch.empty(rows, 24, dtype=torch.float32, device=gpu)
+    a = dict(q_nope=c.q_nope, q_pe=c.q_pe, kv_cache=c.cache, block_table=c.block_table, seq_lens=c.seq_lens,
+             out=out, lse=lse, d_c=DC, rope_w=64, rms_offset=-1, rms_mode=_lib.RMS_NONE, kv=_lib.KV_BF16,
+             page_size=64, sm_scale=c.sm_scale, qrows=4, groups=1, num_splits=0, num_workgroups=5)
+    ws = Workspace().reserve(workspace_bytes(build_params(**a)), gpu)
+    p = build_params(workspace=ws, **a)
+    rc = qmla.lib().qmla_decode(p, torch.cuda.current_stream().cuda_stream)
+    assert rc == 0, rc
+    torch.cuda.synchronize()
+    ro, rl = run_oracle(c)
+    err, lerr = _report("wide verify x4", out, lse, ro, rl)
     assert err < TOL and lerr < 1e-2
