@@ -797,6 +797,11 @@ static const Inst kInst[] = {
     // bf16 cache, d_c 1792 (the reference's two-pass widths): 8 column slices, 16-token tiles
     QMLA_CS(2, QMLA_RMS_BF16, 1792, 1, 8, 1, 1, 2, 2, 4, false, true, 64),
     QMLA_CS(2, QMLA_RMS_NONE, 1792, 1, 8, 1, 1, 2, 2, 0, false, false, 64),
+    // bf16 cache, rank 768 with a rope window of 256 (the plugin's 24-head rope 232 layout,
+    // tests/test_fi_partial_rope.py:105-110, and full rope 256): 8 slices of 96 columns; the
+    // per-group kernel's fragments for 24 heads exceed the register file
+    QMLA_CS(2, QMLA_RMS_BF16, 768, 1, 8, 1, 1, 2, 4, 3, false, false, 256),
+    QMLA_CS(2, QMLA_RMS_BF16, 768, 1, 8, 1, 1, 1, 4, 2, false, false, 256),   // 12 heads, rope 256
     // fp8 cache, d_c 1792: 32-token tiles, 16 rows per workgroup (32 rows of 1792 accumulator and
     // query columns exceed the register file), more heads split over gridDim.z.
     // Rope 64, log8 codes (transposed rms reads: 2 chunks cover the heads of two row blocks):

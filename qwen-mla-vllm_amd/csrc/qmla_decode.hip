@@ -834,6 +834,10 @@ static const Inst kInst[] = {
     // the same layouts on bf16 caches (tests/test_fi_partial_rope.py): one bf16 rms per head
     QMLA_INST(2, QMLA_RMS_BF16, 256, 256, 2, 1, 3, 64, false, 32, 1, 4),
     QMLA_INST(2, QMLA_RMS_BF16, 256, 128, 1, 1, 2, 48, false, 64, 1, 4),
+    // full rope 256 (the reference test's tp1full / tp2full layouts, :105): rms tails end at bytes
+    // 1072 (24 heads) and 1048 (12 heads), past the 1024 bytes of latent + rope
+    QMLA_INST(2, QMLA_RMS_BF16, 256, 256, 2, 1, 3, 67, false, 32, 1, 4),
+    QMLA_INST(2, QMLA_RMS_BF16, 256, 256, 1, 1, 2, 66, false, 64, 1, 4),
     QMLA_INST(2, QMLA_RMS_BF16, 768, 128, 2, 1, 2, 112, false, 32, 1, 4),
 };
 

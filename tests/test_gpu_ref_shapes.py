@@ -93,8 +93,11 @@ def _bf16_case(batch, heads, ctx, rank, rope, page, seed):
     return cache, q, bt, lens, entry
 
 
-@pytest.mark.parametrize("rank,heads,rope", [(256, 24, 232), (256, 12, 116), (768, 12, 116)])
+@pytest.mark.parametrize("rank,heads,rope", [(256, 24, 232), (256, 12, 116), (768, 24, 232), (768, 12, 116),
+                                             (256, 24, 256), (256, 12, 256), (768, 24, 256), (768, 12, 256)])
 def test_deployed_bf16_layouts(gpu, rank, heads, rope):
+    """The layouts of tests/test_fi_partial_rope.py:105 (tp1, tp2, and the full-rope tp1full / tp2full)
+    at its ranks 256 and 768 (:109)."""
     import qmla
     batch, ctx, page = 4, 2048, 400
     cache, q, bt, lens, entry = _bf16_case(batch, heads, ctx, rank, rope, page, seed=rank + heads)
