@@ -79,6 +79,23 @@ __device__ __forceinline__ uint32_t ldsr8(const void* p) {
   asm volatile("ds_read_u8 %0, %1" : "=v"(r) : "v"(lds_addr(static_cast<const char*>(p))));
   return r;
 }
+// Reads that may follow a scalar load the compiler placed (kernel arguments it reloads under
+// register pressure): one statement that drains the counter first and waits for its own reads, so
+// no counted wait is involved and nothing can be scheduled in between.
+__device__ __forceinline__ void ldsr32f3_drained(const void* a, const void* b, const void* c, float& x, float& y,
+                                                 float& z) {
+  asm volatile(
+      "s_waitcnt lgkmcnt(0)\n\tds_read_b32 %0, %3\n\tds_read_b32 %1, %4\n\tds_read_b32 %2, %5\n\t"
+      "s_waitcnt lgkmcnt(0)"
+      : "=v"(x), "=v"(y), "=v"(z)
+      : "v"(lds_addr(static_cast<const char*>(a))), "v"(lds_addr(static_cast<const char*>(b))),
+        "v"(lds_addr(static_cast<const char*>(c))));
+}
+__device__ __forceinline__ void ldsr128x2_drained(const void* a, const void* b, i32x4& x, i32x4& y) {
+  asm volatile("s_waitcnt lgkmcnt(0)\n\tds_read_b128 %0, %2\n\tds_read_b128 %1, %3\n\ts_waitcnt lgkmcnt(0)"
+               : "=v"(x), "=v"(y)
+               : "v"(lds_addr(static_cast<const char*>(a))), "v"(lds_addr(static_cast<const char*>(b))));
+}
 __device__ __forceinline__ uint32_t ldsr16(const void* p) {
   uint32_t r;
   asm volatile("ds_read_u16 %0, %1" : "=v"(r) : "v"(lds_addr(static_cast<const char*>(p))));
@@ -117,17 +134,28 @@ __device__ __forceinline__ int lanes_below(uint64_t m) {
   return __builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0));
 }
 
-// Compile-time shape: EB cache element bytes (1 fp8, 2 bf16), RMS tail format, DCG latent columns,
-// A tiles in flight ahead of the score waves, CPR 16-byte chunks staged per row, CAP tanh logit
-// cap, RTR rms codes read transposed (query rows are the heads of one token), ISS who issues a
+// Compile-time shape: EB cache element bytes (1 fp8, 2 bf16), RMS tail format, DCG latent columns
+// per group, A tiles in flight ahead of the score waves, CPR 16-byte chunks staged per row, CAP tanh
+// logit cap, RTR rms codes read transposed (query rows are the heads of one token), ISS who issues a
 // tile's DMA and when: 0 the value waves after their step, 1 before it, 3 between issuing their
 // LDS reads and waiting for them, 2 all eight waves (value waves before their step, score waves
-// after theirs).
-template <int EB_, int RMS_, int DCG_, int A_, int CPR_, bool CAP_, bool RTR_, int ISS_>
+// after theirs), G latent groups:
+//   G 1  up to 32 query rows (2 row blocks); score wave (tb, u) scores row block u over all 576
+//        columns, value wave v owns latent columns [128v, 128v+128) of every row;
+//   G 2  (GLA) up to 48 rows per group (3 row blocks each); score wave (tb, u) scores the 3 row
+//        blocks of group u over the group's 256 latent columns and the shared rope, value wave v
+//        owns columns [128(v&1), +128) of group v>>1 for the group's rows. fp8 rows only.
+template <int EB_, int RMS_, int DCG_, int A_, int CPR_, bool CAP_, bool RTR_, int ISS_, int G_>
 struct WS {
   static constexpr int EB = EB_, RMS = RMS_, DCG = DCG_, A = A_, S = A_ + 3, CPR = CPR_;
   static constexpr bool CAP = CAP_, RTR = RTR_;
-  static constexpr int ISS = ISS_;
+  static constexpr int ISS = ISS_, G = G_;
+  static constexpr int DC = G * DCG;                  // latent columns of a row
+  static constexpr int NRB = G == 1 ? 2 : 6;          // 16-row blocks of a request
+  static constexpr int MBG = NRB / 2;                 // row blocks per score wave
+  static constexpr int MBV = NRB / G;                 // row blocks per value wave (its group's)
+  static constexpr int ROWS = 16 * NRB;
+  static constexpr int VPG = 4 / G;                   // value waves per group
   static constexpr int NW = 8, NTHR = 64 * NW;
   static constexpr int NIW = ISS == 2 ? 8 : 4;        // waves sharing a tile's DMA instructions
   static constexpr int RB = 16 * CPR;                 // staged row bytes
@@ -137,14 +165,15 @@ struct WS {
   static constexpr int DPW = (NI + NIW - 1) / NIW;    // ... per issuing wave (at most)
   static constexpr int KQ = (DCG + 64) / 32;          // k-steps of the score product (latent + rope 64)
   static constexpr int KP = KQ / 2;                   // 16-byte K reads per lane and tile
-  static constexpr int VC = DCG / 4;                  // latent columns per value wave
+  static constexpr int VC = DCG / VPG;                // latent columns per value wave
   static constexpr int CB = VC / 16;
   static constexpr int RMS_EB = (RMS == QMLA_RMS_BF16 || RMS == QMLA_RMS_BF16_BYTES) ? 2 : 1;
   static constexpr int NCODE = RMS == QMLA_RMS_NONE ? 0 : (RTR && RMS_EB == 1) ? 1 : 4;   // rms reads
   static constexpr int NKR = KP * EB;                 // K reads of a score step
   static constexpr int NVR = CB * EB;                 // V reads of a value step
   static constexpr int PST = TILE * 2 + 16;           // P row stride in LDS (bytes)
-  static_assert(DCG % 64 == 0 && CPR * 16 >= (DCG + 64) * EB, "row slice");
+  static_assert(DCG % 64 == 0 && CPR * 16 >= (DC + 64) * EB, "row slice");
+  static_assert(G == 1 || (G == 2 && EB == 1 && !RTR), "latent groups: fp8 rows, rms codes read per row");
   static_assert(A >= 2 && A * DPW < 64, "lookahead / vmcnt range");
   static_assert(EB == 2 || DCG % 128 == 0, "fp8 latent in 128-column MFMA blocks");
 };
@@ -159,11 +188,11 @@ struct SegD {
 template <class C>
 struct Smem {
   char kv[C::S][C::STAGE];
-  alignas(16) char p[3][32][C::PST];   // P (bf16) of tiles g % 3
-  alignas(16) int flag[3][4];          // [g % 3][row block]: reference moved at tile g
-  alignas(16) float tmax[2][2][32];    // [g & 1][token block][row] tile max
-  alignas(16) float alpha[3][32];      // [g % 3][row] accumulator rescale at tile g
-  alignas(16) float fin[2][2][2][32];  // [piece & 1][max, sum][token block][row] of a finished request
+  alignas(16) char p[3][C::ROWS][C::PST];   // P (bf16) of tiles g % 3
+  alignas(16) int flag[3][C::G][4];         // [g % 3][group][row block of the group]: reference moved at tile g
+  alignas(16) float tmax[2][2][C::ROWS];    // [g & 1][token block][row] tile max
+  alignas(16) float alpha[3][C::ROWS];      // [g % 3][row] accumulator rescale at tile g
+  alignas(16) float fin[2][2][2][C::ROWS];  // [piece & 1][max, sum][token block][row] of a finished request
   alignas(16) SegD seg[NSEG];
   alignas(16) int pid[PIDN];
   int win[4];                          // pieces, tiles, pages of the window; another window follows
@@ -323,18 +352,30 @@ __device__ __forceinline__ void role_main(const KParams& p, Smem<C>& sm, float k
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int tb = (w >> 1) & 1, smb = w & 1;   // score wave: token block, row block
-  const int vw = w & 3;                        // value wave: column slice
+  const int tb = (w >> 1) & 1, su = w & 1;     // score wave: token block, row-block set
+  const int sg = su * C::MBG / C::MBV;         // score wave: latent group of its row blocks
+  const int vw = w & 3;                        // value wave
+  const int vg = vw / C::VPG, vh = vw % C::VPG;   // value wave: group, column slice of the group
   const int dw = C::NIW == 8 ? w : vw;         // issuing wave: first DMA instruction of a tile
   const int ln16 = lane & 15, lg = lane >> 4;
   const int qrows = p.qrows, hpg = p.hpg;
-  const int nrows = qrows * hpg;
+  const int nrows = qrows * hpg;               // rows per group
   const int P = p.page_size;
   const float c2b = p.sm_scale * kscale * kLog2e;
-  const int r = 16 * smb + ln16;   // score wave: the lane's row
-  const bool rok = r < nrows;
-  const int jq = rok ? r / hpg : 0, hh = rok ? r - jq * hpg : 0;
-  const int rms_b = p.rms_off_b + hh * C::RMS_EB;
+  // score wave: the lane's row in each of its row blocks (r indexes the workgroup's row arrays),
+  // its verify token and head
+  int r[C::MBG], jq[C::MBG], hd[C::MBG], rms_b[C::MBG];
+  bool rok[C::MBG];
+#pragma unroll
+  for (int m = 0; m < C::MBG; ++m) {
+    const int rb = su * C::MBG + m;
+    const int rg = 16 * (rb - sg * C::MBV) + ln16;   // row within the group
+    r[m] = 16 * rb + ln16;
+    rok[m] = rg < nrows;
+    jq[m] = rok[m] ? rg / hpg : 0;
+    hd[m] = sg * hpg + (rok[m] ? rg - jq[m] * hpg : 0);
+    rms_b[m] = p.rms_off_b + hd[m] * C::RMS_EB;
+  }
   const bool contig = p.token_stride_b == C::RB;
 
   // ---- score wave: query fragments (fp8 cache: e4m3 hi/lo parts scaled per row by a power of two
@@ -342,29 +383,41 @@ __device__ __forceinline__ void role_main(const KParams& p, Smem<C>& sm, float k
   //      128b + 32lg .. +32, the rope as two 16x16x32 k-steps over rope columns 16lg .. +16;
   //      bf16 cache: bf16, pair jj and lane group lg holding columns 64jj + 16lg .. +16) ----
   bf16x8 qf[!F8 && QS ? C::KQ : 1];
-  i32x8 qh8[F8 && QS ? NB : 1], ql8[F8 && QS ? NB : 1];
-  long qhr[2], qlr[2];
-  bf16x8 qn[QS ? C::KQ : 1];   // the query of a request, loaded at its first tile
-  float c2 = c2b;
-  float mref = kNegInf, lpart = 0.f;
-  float tmp = kNegInf, ps_pend = 0.f;    // own max and optimistic sum of the last scored tile
-  f32x4 scp = {0.f, 0.f, 0.f, 0.f};      // its scores (log2 domain, masked)
-  int lim = 0;
+  i32x8 qh8[C::MBG][F8 && QS ? NB : 1], ql8[C::MBG][F8 && QS ? NB : 1];
+  long qhr[C::MBG][2], qlr[C::MBG][2];
+  bf16x8 qn[QS ? C::KQ : 1];   // the query of one row block of a request, loaded at its first tile
+  // per row block: query scale, reference max, sum, own max / optimistic sum / scores (log2 domain,
+  // masked) of the last scored tile, verify limit
+  float c2[C::MBG], mref[C::MBG], lpart[C::MBG], tmp[C::MBG], ps_pend[C::MBG];
+  f32x4 scp[C::MBG];
+  int lim[C::MBG];
+#pragma unroll
+  for (int m = 0; m < C::MBG; ++m) {
+    c2[m] = c2b;
+    mref[m] = kNegInf;
+    lpart[m] = 0.f;
+    tmp[m] = kNegInf;
+    ps_pend[m] = 0.f;
+    scp[m] = f32x4{0.f, 0.f, 0.f, 0.f};
+    lim[m] = 0;
+  }
 
-  auto load_q = [&](int req) {
-    const int row = req * qrows + jq;
-    const __bf16* qnp = p.q_nope + (int64_t)row * p.qn_sr + (int64_t)hh * p.qn_sh;
-    const __bf16* qpp = p.q_pe + (int64_t)row * p.qp_sr + (int64_t)hh * p.qp_sh;
+  // query row block m of request req into qn (group-local latent columns, then the rope)
+  auto load_q = [&](int req, int m) {
+    const int row = req * qrows + jq[m];
+    const __bf16* qnp = p.q_nope + (int64_t)row * p.qn_sr + (int64_t)hd[m] * p.qn_sh;
+    const __bf16* qpp = p.q_pe + (int64_t)row * p.qp_sr + (int64_t)hd[m] * p.qp_sh;
 #pragma unroll
     for (int k = 0; k < C::KQ; ++k) {
       const int col = !F8 ? 64 * (k >> 1) + 16 * lg + 8 * (k & 1)
                           : k < 4 * NB ? 128 * (k >> 2) + 32 * lg + 8 * (k & 3) : C::DCG + 16 * lg + 8 * (k - 4 * NB);
       bf16x8 v = load_q8(col < C::DCG ? qnp + col : qpp + (col - C::DCG), p.q_vec);
-      if (!rok) v = bf16x8{};
+      if (!rok[m]) v = bf16x8{};
       qn[k] = v;
     }
   };
-  auto set_q = [&]() {
+  // qn -> the MFMA operands of row block m
+  auto set_q = [&](int m) {
     if constexpr (F8) {
       float mx = 0.f;
 #pragma unroll
@@ -375,7 +428,7 @@ __device__ __forceinline__ void role_main(const KParams& p, Smem<C>& sm, float k
       // |q| * qs in (112, 448]: e4m3 keeps 4 significant bits in hi and 4 more in lo
       const float ex = mx > 0.f ? fminf(floorf(fast_log2(224.0f / mx)), 126.0f) : 0.0f;
       const float qs = fast_exp2(ex);
-      c2 = c2b * fast_exp2(-ex);
+      c2[m] = c2b * fast_exp2(-ex);
       int hq[2 * C::KQ], lq[2 * C::KQ];
 #pragma unroll
       for (int k = 0; k < C::KQ; ++k) {
@@ -400,13 +453,13 @@ __device__ __forceinline__ void role_main(const KParams& p, Smem<C>& sm, float k
       for (int b = 0; b < NB; ++b)
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
-          qh8[b][e] = hq[8 * b + e];
-          ql8[b][e] = lq[8 * b + e];
+          qh8[m][b][e] = hq[8 * b + e];
+          ql8[m][b][e] = lq[8 * b + e];
         }
 #pragma unroll
       for (int t = 0; t < 2; ++t) {
-        qhr[t] = __builtin_bit_cast(long, i32x2{hq[8 * NB + 2 * t], hq[8 * NB + 2 * t + 1]});
-        qlr[t] = __builtin_bit_cast(long, i32x2{lq[8 * NB + 2 * t], lq[8 * NB + 2 * t + 1]});
+        qhr[m][t] = __builtin_bit_cast(long, i32x2{hq[8 * NB + 2 * t], hq[8 * NB + 2 * t + 1]});
+        qlr[m][t] = __builtin_bit_cast(long, i32x2{lq[8 * NB + 2 * t], lq[8 * NB + 2 * t + 1]});
       }
     } else {
 #pragma unroll
@@ -414,11 +467,11 @@ __device__ __forceinline__ void role_main(const KParams& p, Smem<C>& sm, float k
     }
   };
 
-  // ---- value wave: accumulator of rows (16mb + 4lg + i) x columns VC*vw + 16cb + ln16 ----
-  f32x4 acc[2][ROLE == VALUE ? C::CB : 1];
+  // ---- value wave: accumulator of the group's rows (16mb + 4lg + i) x its columns VC*vh + 16cb + ln16 ----
+  f32x4 acc[C::MBV][ROLE == VALUE ? C::CB : 1];
   auto zero_acc = [&]() {
 #pragma unroll
-    for (int mb = 0; mb < 2; ++mb)
+    for (int mb = 0; mb < C::MBV; ++mb)
 #pragma unroll
       for (int cb = 0; cb < (ROLE == VALUE ? C::CB : 1); ++cb) acc[mb][cb] = f32x4{0.f, 0.f, 0.f, 0.f};
   };
@@ -445,10 +498,15 @@ __device__ __forceinline__ void role_main(const KParams& p, Smem<C>& sm, float k
   // reads one piece descriptor (asm reads: no wait on the LDS-DMA in flight); its fields are
   // wave-uniform, so they live in scalar registers (the DMA's buffer resources are built from them)
   auto read_seg = [&](int k) {
-    i32x4 a = ldsr128(&sm.seg[k].req);
-    i32x4 b = ldsr128(&sm.seg[k].nt);
-    lds_wait_n<1>(a);
-    lds_wait_n<0>(b);
+    i32x4 a, b;
+    if constexpr (C::G == 1) {
+      a = ldsr128(&sm.seg[k].req);
+      b = ldsr128(&sm.seg[k].nt);
+      lds_wait_n<1>(a);
+      lds_wait_n<0>(b);
+    } else {
+      ldsr128x2_drained(&sm.seg[k].req, &sm.seg[k].nt, a, b);
+    }
     SegD d;
     d.req = __builtin_amdgcn_readfirstlane(a[0]);
     d.ta = __builtin_amdgcn_readfirstlane(a[1]);
@@ -462,40 +520,40 @@ __device__ __forceinline__ void role_main(const KParams& p, Smem<C>& sm, float k
   };
 
   // score step helpers: reference check of the previous tile and its publication
-  auto fix_decide = [&](float tpart, bool& rare, float& alpha_f, bf16x4& pk_fix) {
-    const float gm = fmaxf(tmp, tpart);
-    const bool ch = gm > mref + SHIFT;
+  auto fix_decide = [&](int m, float tpart, bool& rare, float& alpha_f, bf16x4& pk_fix) {
+    const float gm = fmaxf(tmp[m], tpart);
+    const bool ch = gm > mref[m] + SHIFT;
     rare = __builtin_amdgcn_ballot_w64(ch) != 0;
     if (!rare) {
-      lpart += ps_pend;
+      lpart[m] += ps_pend[m];
       return;
     }
-    const float mn = ch ? gm : mref;
-    alpha_f = ch ? (mref == kNegInf ? 0.f : fast_exp2(mref - mn)) : 1.0f;
-    mref = mn;
-    const float mu = mref == kNegInf ? 0.f : mref;
+    const float mn = ch ? gm : mref[m];
+    alpha_f = ch ? (mref[m] == kNegInf ? 0.f : fast_exp2(mref[m] - mn)) : 1.0f;
+    mref[m] = mn;
+    const float mu = mref[m] == kNegInf ? 0.f : mref[m];
     float ps2 = 0.f;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      const float e = fast_exp2(scp[i] - mu);
+      const float e = fast_exp2(scp[m][i] - mu);
       ps2 += e;
       pk_fix[i] = (__bf16)e;
     }
-    lpart = lpart * alpha_f + ps2;
+    lpart[m] = lpart[m] * alpha_f + ps2;
   };
-  auto fix_publish = [&](int g, bool rare, float alpha_f, const bf16x4& pk_fix) {
+  auto fix_publish = [&](int m, int g, bool rare, float alpha_f, const bf16x4& pk_fix) {
     const int pt = g % 3;
     if (rare) {
-      *reinterpret_cast<bf16x4*>(&sm.p[pt][r][(16 * tb + 4 * lg) * 2]) = pk_fix;
-      if (tb == 0 && lg == 0) sm.alpha[pt][r] = alpha_f;
+      *reinterpret_cast<bf16x4*>(&sm.p[pt][r[m]][(16 * tb + 4 * lg) * 2]) = pk_fix;
+      if (tb == 0 && lg == 0) sm.alpha[pt][r[m]] = alpha_f;
     }
-    if (tb == 0 && lane == 0) sm.flag[pt][smb] = rare ? 1 : 0;
+    if (tb == 0 && lane == 0) sm.flag[pt][sg][su * C::MBG + m - sg * C::MBV] = rare ? 1 : 0;
   };
-  auto publish_fin = [&](int k) {
-    const float l = sum_lg(lpart);
+  auto publish_fin = [&](int k, int m) {
+    const float l = sum_lg(lpart[m]);
     if (lg == 0) {
-      sm.fin[k & 1][0][tb][r] = mref;
-      sm.fin[k & 1][1][tb][r] = l;
+      sm.fin[k & 1][0][tb][r[m]] = mref[m];
+      sm.fin[k & 1][1][tb][r[m]] = l;
     }
   };
   // value wave: normalize and write the output of request req, whose sums are in fin[k & 1]
@@ -503,32 +561,38 @@ __device__ __forceinline__ void role_main(const KParams& p, Smem<C>& sm, float k
     const SegOut so = seg_out<C::DCG>(p, req, (fl & SEG_FINAL) != 0);
     const int row0 = req * qrows;
 #pragma unroll
-    for (int mb = 0; mb < 2; ++mb)
+    for (int mb = 0; mb < C::MBV; ++mb)
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        const int rr = 16 * mb + 4 * lg + i;
-        float m = ldsr32f(&sm.fin[k & 1][0][0][rr]);
-        float l0 = ldsr32f(&sm.fin[k & 1][1][0][rr]);
-        float l1 = ldsr32f(&sm.fin[k & 1][1][1][rr]);
-        lds_wait_n<2>(m);
-        lds_wait_n<1>(l0);
-        lds_wait_n<0>(l1);
+        const int rr = 16 * mb + 4 * lg + i;        // row within the group
+        const int rw = 16 * C::MBV * vg + rr;       // row of the workgroup's arrays
+        float m, l0, l1;
+        if constexpr (C::G == 1) {
+          m = ldsr32f(&sm.fin[k & 1][0][0][rw]);
+          l0 = ldsr32f(&sm.fin[k & 1][1][0][rw]);
+          l1 = ldsr32f(&sm.fin[k & 1][1][1][rw]);
+          lds_wait_n<2>(m);
+          lds_wait_n<1>(l0);
+          lds_wait_n<0>(l1);
+        } else {
+          ldsr32f3_drained(&sm.fin[k & 1][0][0][rw], &sm.fin[k & 1][1][0][rw], &sm.fin[k & 1][1][1][rw], m, l0, l1);
+        }
         if (rr >= nrows) continue;
         const float l = l0 + l1;
-        const int jr = rr / hpg, h = rr - jr * hpg;
+        const int jr = rr / hpg, h = vg * hpg + rr - jr * hpg;
         const float inv = l > 0.f ? kscale / l : 0.f;   // fp8 values were accumulated unscaled
         const float lse_v = l > 0.f ? (m + fast_log2(l)) * kLn2 : kNegInf;
-        const int col = C::VC * vw + ln16;
+        const int col = C::VC * vh + ln16;
         if (so.final_out) {
           const int64_t ob = (int64_t)(row0 + jr) * p.o_sr + (int64_t)h * p.o_sh + col;
 #pragma unroll
           for (int cb = 0; cb < C::CB; ++cb) store_out(p.out, p.out_dt, ob + 16 * cb, acc[mb][cb][i] * inv);
-          if (vw == 0 && ln16 == 0 && p.lse) store_out(p.lse, p.lse_dt, (int64_t)(row0 + jr) * p.lse_sr + h, lse_v);
+          if (vh == 0 && ln16 == 0 && p.lse) store_out(p.lse, p.lse_dt, (int64_t)(row0 + jr) * p.lse_sr + h, lse_v);
         } else {
           float* ob = so.po + (int64_t)jr * so.po_sr + (int64_t)h * so.po_sh + col;
 #pragma unroll
           for (int cb = 0; cb < C::CB; ++cb) ob[16 * cb] = acc[mb][cb][i] * inv;
-          if (vw == 0 && ln16 == 0) {
+          if (vh == 0 && ln16 == 0) {
             if (so.plse) so.plse[(int64_t)jr * so.plse_sr + h] = lse_v;
             else so.po[(int64_t)jr * so.po_sr + (int64_t)h * so.po_sh + C::DCG] = lse_v;
           }
@@ -653,144 +717,224 @@ __device__ __forceinline__ void role_main(const KParams& p, Smem<C>& sm, float k
             s_ta = d.ta;
             s_nt = d.nt;
             s_fl = d.fl;
-            if (d.fl & SEG_FIRST) load_q(d.req);   // in flight during the reads below, converted after them
-            const int lr = d.L - (qrows - 1 - jq);
-            lim = rok ? (lr < d.te ? lr : d.te) : 0;
+            if (d.fl & SEG_FIRST) {
+              if constexpr (C::G == 1) {
+                load_q(d.req, 0);   // in flight during the reads below, converted after them
+              } else {
+                // three row blocks: the query switches here, before this tile's reads (the previous
+                // request's softmax state does not depend on the query or its scale)
+#pragma unroll
+                for (int m = 0; m < C::MBG; ++m) {
+                  load_q(d.req, m);
+                  set_q(m);
+                }
+              }
+            }
+#pragma unroll
+            for (int m = 0; m < C::MBG; ++m) {
+              const int lr = d.L - (qrows - 1 - jq[m]);
+              lim[m] = rok[m] ? (lr < d.te ? lr : d.te) : 0;
+            }
           }
           const char* kvs = sm.kv[g % C::S];
           const int tok0 = s_ta + ts * TILE;
-          // ---- LDS reads, in this order: partner max of tile g-1, rms codes, K rows ----
-          float tpart = ldsr32f(&sm.tmax[(g + 1) & 1][tb ^ 1][r]);   // unused at g == 0
+          // ---- LDS reads, in this order: partner maxima of tile g-1, rms codes, K rows ----
+          float tpart[C::MBG];   // unused at g == 0
+#pragma unroll
+          for (int m = 0; m < C::MBG; ++m) tpart[m] = ldsr32f(&sm.tmax[(g + 1) & 1][tb ^ 1][r[m]]);
           const int krow = 16 * tb + ln16;
           const char* rowp = kvs + krow * C::RB;
-          uint32_t code[4] = {0u, 0u, 0u, 0u};
+          uint32_t code[C::MBG][4];
+#pragma unroll
+          for (int m = 0; m < C::MBG; ++m)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) code[m][i] = 0u;
           i32x2 craw = {0, 0};
           if constexpr (C::RMS != QMLA_RMS_NONE) {
             if constexpr (C::RTR && C::RMS_EB == 1) {
-              // tr_b8: lanes 2r', 2r'+1 of block lg supply token row 16tb + 4lg + (r' & 3); lane n gets head 16smb + n
+              // tr_b8: lanes 2r', 2r'+1 of block lg supply token row 16tb + 4lg + (r' & 3); lane n gets head 16su + n
               const int rr = 16 * tb + 4 * lg + ((ln16 >> 1) & 3);
-              craw = lds_read_tr8_async(kvs + lbyte<C::CPR>(rr, p.rms_off_b + 16 * smb + 8 * (ln16 & 1)));
+              craw = lds_read_tr8_async(kvs + lbyte<C::CPR>(rr, p.rms_off_b + 16 * su + 8 * (ln16 & 1)));
             } else {
 #pragma unroll
-              for (int i = 0; i < 4; ++i) {
-                const char* a = kvs + lbyte<C::CPR>(16 * tb + 4 * lg + i, rms_b);
-                code[i] = C::RMS_EB == 1 ? ldsr8(a) : ldsr16(a);
-              }
+              for (int m = 0; m < C::MBG; ++m)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                  const char* a = kvs + lbyte<C::CPR>(16 * tb + 4 * lg + i, rms_b[m]);
+                  code[m][i] = C::RMS_EB == 1 ? ldsr8(a) : ldsr16(a);
+                }
             }
           }
           i32x4 kr0[C::KP], kr1[C::EB == 2 ? C::KP : 1];
 #pragma unroll
           for (int jj = 0; jj < C::KP; ++jj) {
             const int cbyte = (64 * jj + 16 * lg) * C::EB;
-            const int ch = !F8 ? cbyte >> 4 : jj < 2 * NB ? 8 * (jj >> 1) + 2 * lg + (jj & 1) : C::DCG / 16 + lg;
+            // fp8: latent block jj/2 of the wave's group, then the rope after the whole latent
+            const int ch = !F8 ? cbyte >> 4
+                               : jj < 2 * NB ? sg * (C::DCG / 16) + 8 * (jj >> 1) + 2 * lg + (jj & 1) : C::DC / 16 + lg;
             kr0[jj] = ldsr128(rowp + 16 * rot<C::CPR>(ch, krow));
             if constexpr (C::EB == 2) kr1[jj] = ldsr128(rowp + 16 * rot<C::CPR>((cbyte >> 4) + 1, krow));
           }
           // ---- reference check of tile g-1 (its writes follow the score product); at the first
           //      tile of a request: publish the previous request's sums, switch the query ----
-          lds_wait_n<cmin15(C::NCODE + C::NKR)>(tpart);
-          bool rare = false;
-          float alpha_f = 1.0f;
-          bf16x4 pk_fix;
-          if (g >= 1) fix_decide(tpart, rare, alpha_f, pk_fix);
+#pragma unroll
+          for (int m = 0; m < C::MBG; ++m) lds_wait_n<cmin15(C::MBG * C::NCODE + C::NKR)>(tpart[m]);
+          bool rare[C::MBG];
+          float alpha_f[C::MBG];
+          bf16x4 pk_fix[C::MBG];
+#pragma unroll
+          for (int m = 0; m < C::MBG; ++m) {
+            rare[m] = false;
+            alpha_f[m] = 1.0f;
+            if (g >= 1) fix_decide(m, tpart[m], rare[m], alpha_f[m], pk_fix[m]);
+          }
           if (ts == 0) {
-            if (g >= 1 && (fl_prev & SEG_LAST)) publish_fin(ks - 1);
+            if (g >= 1 && (fl_prev & SEG_LAST)) {
+#pragma unroll
+              for (int m = 0; m < C::MBG; ++m) publish_fin(ks - 1, m);
+            }
             if (s_fl & SEG_FIRST) {
-              mref = kNegInf;
-              lpart = 0.f;
-              set_q();
+#pragma unroll
+              for (int m = 0; m < C::MBG; ++m) {
+                mref[m] = kNegInf;
+                lpart[m] = 0.f;
+              }
+              if constexpr (C::G == 1) set_q(0);
             }
           }
           // ---- S^T = K . Q^T as the K rows arrive ----
-          f32x4 s2a = f32x4{0.f, 0.f, 0.f, 0.f}, s2b = s2a, s2c = s2a, s2d = s2a;
-          static_for<0, C::KP>([&](auto jc) {
-            constexpr int jj = decltype(jc)::value;
-            if constexpr (F8) {
+          f32x4 sc[C::MBG];
+          if constexpr (C::G == 1) {
+            f32x4 s2a = f32x4{0.f, 0.f, 0.f, 0.f}, s2b = s2a, s2c = s2a, s2d = s2a;
+            static_for<0, C::KP>([&](auto jc) {
+              constexpr int jj = decltype(jc)::value;
+              if constexpr (F8) {
+                if constexpr (jj < 2 * NB && (jj & 1)) {
+                  // latent block jj/2: 32 bytes per lane from reads jj-1, jj
+                  lds_wait_n<cmin15(C::KP - 1 - jj)>(kr0[jj]);
+                  lds_wait_n<cmin15(C::KP - jj)>(kr0[jj - 1]);
+                  const i32x8 ka = {kr0[jj - 1][0], kr0[jj - 1][1], kr0[jj - 1][2], kr0[jj - 1][3],
+                                    kr0[jj][0], kr0[jj][1], kr0[jj][2], kr0[jj][3]};
+                  s2a = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(ka, qh8[0][jj >> 1], s2a, 0, 0, 0, 127, 0, 127);
+                  s2b = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(ka, ql8[0][jj >> 1], s2b, 0, 0, 0, 127, 0, 127);
+                } else if constexpr (jj == 2 * NB) {
+                  lds_wait_n<cmin15(C::KP - 1 - jj)>(kr0[jj]);
+                  const long k0 = __builtin_bit_cast(long, i32x2{kr0[jj][0], kr0[jj][1]});
+                  const long k1 = __builtin_bit_cast(long, i32x2{kr0[jj][2], kr0[jj][3]});
+                  s2c = __builtin_amdgcn_mfma_f32_16x16x32_fp8_fp8(k0, qhr[0][0], s2c, 0, 0, 0);
+                  s2d = __builtin_amdgcn_mfma_f32_16x16x32_fp8_fp8(k0, qlr[0][0], s2d, 0, 0, 0);
+                  s2c = __builtin_amdgcn_mfma_f32_16x16x32_fp8_fp8(k1, qhr[0][1], s2c, 0, 0, 0);
+                  s2d = __builtin_amdgcn_mfma_f32_16x16x32_fp8_fp8(k1, qlr[0][1], s2d, 0, 0, 0);
+                }
+              } else {
+                lds_wait_n<cmin15(2 * (C::KP - 1 - jj) + 1)>(kr0[jj]);
+                lds_wait_n<cmin15(2 * (C::KP - 1 - jj))>(kr1[jj]);
+                const bf16x8 ka = __builtin_bit_cast(bf16x8, kr0[jj]);
+                const bf16x8 kb = __builtin_bit_cast(bf16x8, kr1[jj]);
+                if constexpr (jj & 1) {
+                  s2b = mfma16(ka, qf[2 * jj], s2b);
+                  s2b = mfma16(kb, qf[2 * jj + 1], s2b);
+                } else {
+                  s2a = mfma16(ka, qf[2 * jj], s2a);
+                  s2a = mfma16(kb, qf[2 * jj + 1], s2a);
+                }
+              }
+            });
+            sc[0] = (s2a + s2c) + (s2b + s2d);
+          } else {
+            // latent groups (fp8): per row block one 16x16x128 chain (hi and lo parts) and one
+            // 16x16x32 chain for the rope; the row blocks' chains are independent of each other
+            f32x4 sl[C::MBG], sr[C::MBG];
+#pragma unroll
+            for (int m = 0; m < C::MBG; ++m) sl[m] = sr[m] = f32x4{0.f, 0.f, 0.f, 0.f};
+            static_for<0, C::KP>([&](auto jc) {
+              constexpr int jj = decltype(jc)::value;
               if constexpr (jj < 2 * NB && (jj & 1)) {
-                // latent block jj/2: 32 bytes per lane from reads jj-1, jj
                 lds_wait_n<cmin15(C::KP - 1 - jj)>(kr0[jj]);
                 lds_wait_n<cmin15(C::KP - jj)>(kr0[jj - 1]);
                 const i32x8 ka = {kr0[jj - 1][0], kr0[jj - 1][1], kr0[jj - 1][2], kr0[jj - 1][3],
                                   kr0[jj][0], kr0[jj][1], kr0[jj][2], kr0[jj][3]};
-                s2a = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(ka, qh8[jj >> 1], s2a, 0, 0, 0, 127, 0, 127);
-                s2b = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(ka, ql8[jj >> 1], s2b, 0, 0, 0, 127, 0, 127);
+#pragma unroll
+                for (int m = 0; m < C::MBG; ++m)
+                  sl[m] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(ka, qh8[m][jj >> 1], sl[m], 0, 0, 0, 127, 0, 127);
+#pragma unroll
+                for (int m = 0; m < C::MBG; ++m)
+                  sl[m] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(ka, ql8[m][jj >> 1], sl[m], 0, 0, 0, 127, 0, 127);
               } else if constexpr (jj == 2 * NB) {
                 lds_wait_n<cmin15(C::KP - 1 - jj)>(kr0[jj]);
                 const long k0 = __builtin_bit_cast(long, i32x2{kr0[jj][0], kr0[jj][1]});
                 const long k1 = __builtin_bit_cast(long, i32x2{kr0[jj][2], kr0[jj][3]});
-                s2c = __builtin_amdgcn_mfma_f32_16x16x32_fp8_fp8(k0, qhr[0], s2c, 0, 0, 0);
-                s2d = __builtin_amdgcn_mfma_f32_16x16x32_fp8_fp8(k0, qlr[0], s2d, 0, 0, 0);
-                s2c = __builtin_amdgcn_mfma_f32_16x16x32_fp8_fp8(k1, qhr[1], s2c, 0, 0, 0);
-                s2d = __builtin_amdgcn_mfma_f32_16x16x32_fp8_fp8(k1, qlr[1], s2d, 0, 0, 0);
+#pragma unroll
+                for (int m = 0; m < C::MBG; ++m) sr[m] = __builtin_amdgcn_mfma_f32_16x16x32_fp8_fp8(k0, qhr[m][0], sr[m], 0, 0, 0);
+#pragma unroll
+                for (int m = 0; m < C::MBG; ++m) sr[m] = __builtin_amdgcn_mfma_f32_16x16x32_fp8_fp8(k0, qlr[m][0], sr[m], 0, 0, 0);
+#pragma unroll
+                for (int m = 0; m < C::MBG; ++m) sr[m] = __builtin_amdgcn_mfma_f32_16x16x32_fp8_fp8(k1, qhr[m][1], sr[m], 0, 0, 0);
+#pragma unroll
+                for (int m = 0; m < C::MBG; ++m) sr[m] = __builtin_amdgcn_mfma_f32_16x16x32_fp8_fp8(k1, qlr[m][1], sr[m], 0, 0, 0);
               }
-            } else {
-              lds_wait_n<cmin15(2 * (C::KP - 1 - jj) + 1)>(kr0[jj]);
-              lds_wait_n<cmin15(2 * (C::KP - 1 - jj))>(kr1[jj]);
-              const bf16x8 ka = __builtin_bit_cast(bf16x8, kr0[jj]);
-              const bf16x8 kb = __builtin_bit_cast(bf16x8, kr1[jj]);
-              if constexpr (jj & 1) {
-                s2b = mfma16(ka, qf[2 * jj], s2b);
-                s2b = mfma16(kb, qf[2 * jj + 1], s2b);
-              } else {
-                s2a = mfma16(ka, qf[2 * jj], s2a);
-                s2a = mfma16(kb, qf[2 * jj + 1], s2a);
-              }
-            }
-          });
+            });
+#pragma unroll
+            for (int m = 0; m < C::MBG; ++m) sc[m] = sl[m] + sr[m];
+          }
           if constexpr (C::RMS != QMLA_RMS_NONE) {
             if constexpr (C::RTR && C::RMS_EB == 1) {
               lds_wait_n<0>(craw);   // landed before the K rows
 #pragma unroll
-              for (int i = 0; i < 4; ++i) code[i] = ((uint32_t)craw[0] >> (8 * i)) & 0xFF;
+              for (int i = 0; i < 4; ++i) code[0][i] = ((uint32_t)craw[0] >> (8 * i)) & 0xFF;
             } else {
 #pragma unroll
-              for (int i = 0; i < 4; ++i) lds_wait_n<0>(code[i]);
-            }
-          }
-          f32x4 sc = (s2a + s2c) + (s2b + s2d);
-          // ---- rms divide, scale, cap, mask ----
-          float tm = kNegInf;
+              for (int m = 0; m < C::MBG; ++m)
 #pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            float rinv = 1.0f;
-            if constexpr (C::RMS == QMLA_RMS_LOG8) {
-              rinv = fast_exp2(fmaf((float)code[i], -6.0f / 255.0f, 3.0f));   // 1 / 2^(-3 + c*6/255)
-            } else if constexpr (C::RMS == QMLA_RMS_E4M3) {
-              const float rv = fp8_to_f32(code[i]) * kscale;
-              rinv = rv > 0.f ? __builtin_amdgcn_rcpf(rv) : 1.0f;
-            } else if constexpr (C::RMS == QMLA_RMS_BF16 || C::RMS == QMLA_RMS_BF16_BYTES) {
-              const float rv = bf16_bits_to_f32(code[i]);
-              rinv = rv > 0.f ? __builtin_amdgcn_rcpf(rv) : 1.0f;
+                for (int i = 0; i < 4; ++i) lds_wait_n<0>(code[m][i]);
             }
-            float v;
-            if constexpr (C::CAP) {
-              const float sn = sc[i] * (c2 * kLn2) * rinv;
-              const float th = 1.0f - 2.0f / (fast_exp2(2.0f * kLog2e * (sn / p.logit_cap)) + 1.0f);
-              v = p.logit_cap * th * kLog2e;
-            } else {
-              v = sc[i] * c2 * rinv;
-            }
-            v = tok0 + 16 * tb + 4 * lg + i < lim ? v : kNegInf;
-            sc[i] = v;
-            tm = fmaxf(tm, v);
           }
-          tm = max_lg(tm);
-          // ---- optimistic P against the current reference ----
-          const float mu = mref == kNegInf ? 0.f : mref;
-          bf16x4 pk;
-          float ps = 0.f;
 #pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            const float e = fast_exp2(sc[i] - mu);
-            ps += e;
-            pk[i] = (__bf16)e;
+          for (int m = 0; m < C::MBG; ++m) {
+            // ---- rms divide, scale, cap, mask ----
+            float tm = kNegInf;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+              float rinv = 1.0f;
+              if constexpr (C::RMS == QMLA_RMS_LOG8) {
+                rinv = fast_exp2(fmaf((float)code[m][i], -6.0f / 255.0f, 3.0f));   // 1 / 2^(-3 + c*6/255)
+              } else if constexpr (C::RMS == QMLA_RMS_E4M3) {
+                const float rv = fp8_to_f32(code[m][i]) * kscale;
+                rinv = rv > 0.f ? __builtin_amdgcn_rcpf(rv) : 1.0f;
+              } else if constexpr (C::RMS == QMLA_RMS_BF16 || C::RMS == QMLA_RMS_BF16_BYTES) {
+                const float rv = bf16_bits_to_f32(code[m][i]);
+                rinv = rv > 0.f ? __builtin_amdgcn_rcpf(rv) : 1.0f;
+              }
+              float v;
+              if constexpr (C::CAP) {
+                const float sn = sc[m][i] * (c2[m] * kLn2) * rinv;
+                const float th = 1.0f - 2.0f / (fast_exp2(2.0f * kLog2e * (sn / p.logit_cap)) + 1.0f);
+                v = p.logit_cap * th * kLog2e;
+              } else {
+                v = sc[m][i] * c2[m] * rinv;
+              }
+              v = tok0 + 16 * tb + 4 * lg + i < lim[m] ? v : kNegInf;
+              sc[m][i] = v;
+              tm = fmaxf(tm, v);
+            }
+            tm = max_lg(tm);
+            // ---- optimistic P against the current reference ----
+            const float mu = mref[m] == kNegInf ? 0.f : mref[m];
+            bf16x4 pk;
+            float ps = 0.f;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+              const float e = fast_exp2(sc[m][i] - mu);
+              ps += e;
+              pk[i] = (__bf16)e;
+            }
+            *reinterpret_cast<bf16x4*>(&sm.p[g % 3][r[m]][(16 * tb + 4 * lg) * 2]) = pk;
+            if (lg == 0) sm.tmax[g & 1][tb][r[m]] = tm;
+            if (g >= 1) fix_publish(m, g - 1, rare[m], alpha_f[m], pk_fix[m]);
+            scp[m] = sc[m];
+            tmp[m] = tm;
+            ps_pend[m] = ps;
           }
-          *reinterpret_cast<bf16x4*>(&sm.p[g % 3][r][(16 * tb + 4 * lg) * 2]) = pk;
-          if (lg == 0) sm.tmax[g & 1][tb][r] = tm;
-          if (g >= 1) fix_publish(g - 1, rare, alpha_f, pk_fix);
-          scp = sc;
-          tmp = tm;
-          ps_pend = ps;
           if (++ts == s_nt) {
             ts = 0;
             fl_prev = s_fl;
@@ -798,14 +942,22 @@ __device__ __forceinline__ void role_main(const KParams& p, Smem<C>& sm, float k
           }
         } else if (g == ntot) {
           // reference check of the window's last tile
-          float tpart = ldsr32f(&sm.tmax[(g + 1) & 1][tb ^ 1][r]);
-          lds_wait_n<0>(tpart);
-          bool rare = false;
-          float alpha_f = 1.0f;
-          bf16x4 pk_fix;
-          fix_decide(tpart, rare, alpha_f, pk_fix);
-          fix_publish(g - 1, rare, alpha_f, pk_fix);
-          if (fl_prev & SEG_LAST) publish_fin(ks - 1);
+          float tpart[C::MBG];
+#pragma unroll
+          for (int m = 0; m < C::MBG; ++m) tpart[m] = ldsr32f(&sm.tmax[(g + 1) & 1][tb ^ 1][r[m]]);
+#pragma unroll
+          for (int m = 0; m < C::MBG; ++m) {
+            lds_wait_n<0>(tpart[m]);
+            bool rare = false;
+            float alpha_f = 1.0f;
+            bf16x4 pk_fix;
+            fix_decide(m, tpart[m], rare, alpha_f, pk_fix);
+            fix_publish(m, g - 1, rare, alpha_f, pk_fix);
+          }
+          if (fl_prev & SEG_LAST) {
+#pragma unroll
+            for (int m = 0; m < C::MBG; ++m) publish_fin(ks - 1, m);
+          }
         }
         if constexpr (C::ISS == 2) {
           if (g + C::A < ntot) issue(g + C::A, false);
@@ -817,20 +969,23 @@ __device__ __forceinline__ void role_main(const KParams& p, Smem<C>& sm, float k
         }
         // ---- P . V for tile j = g-2 over columns VC*vw .. +VC: reads first ----
         const int j = g - 2, pj = (g + 1) % 3;
-        i32x2 fl = {0, 0};
-        i32x4 pr[2];
+        const int vr0 = 16 * C::MBV * vg;   // the group's first row in the workgroup's arrays
+        i32x2 fl = {0, 0};                  // one group: the two row blocks' flags
+        i32x4 fl4 = {0, 0, 0, 0};           // latent groups: the group's row blocks' flags
+        i32x4 pr[C::MBV];
         i32x2 vraw[C::CB][C::EB];
         if (g >= 2) {
           const char* kvs = sm.kv[j % C::S];
-          fl = ldsr64(&sm.flag[pj][0]);
+          if constexpr (C::G == 1) fl = ldsr64(&sm.flag[pj][0][0]);
+          else fl4 = ldsr128(&sm.flag[pj][vg][0]);
 #pragma unroll
-          for (int mb = 0; mb < 2; ++mb) pr[mb] = ldsr128(&sm.p[pj][16 * mb + ln16][(8 * lg) * 2]);
+          for (int mb = 0; mb < C::MBV; ++mb) pr[mb] = ldsr128(&sm.p[pj][vr0 + 16 * mb + ln16][(8 * lg) * 2]);
 #pragma unroll
           for (int cb = 0; cb < C::CB; ++cb) {
-            const int col0 = C::VC * vw + 16 * cb;
+            const int col0 = C::VC * vh + 16 * cb;
             if constexpr (C::EB == 1) {
               const int vr = 8 * lg + (ln16 >> 1);
-              vraw[cb][0] = lds_read_tr8_async(kvs + lbyte<C::CPR>(vr, col0 + 8 * (ln16 & 1)));
+              vraw[cb][0] = lds_read_tr8_async(kvs + lbyte<C::CPR>(vr, vg * C::DCG + col0 + 8 * (ln16 & 1)));
             } else {
               const int vr = 8 * lg + (ln16 >> 2);
               const int vb = (col0 + 4 * (ln16 & 3)) * 2;
@@ -844,26 +999,42 @@ __device__ __forceinline__ void role_main(const KParams& p, Smem<C>& sm, float k
           if (g + C::A < ntot) issue(g + C::A, true);
         }
         if (g >= 2) {
-          lds_wait_n<cmin15(2 + C::NVR)>(fl);
-          const int f0 = __builtin_amdgcn_readfirstlane(fl[0]), f1 = __builtin_amdgcn_readfirstlane(fl[1]);
-          if (f0 | f1) {
-            // the reference of some row moved at tile j: rescale before adding it
-            i32x4 a0 = ldsr128(&sm.alpha[pj][4 * lg]), a1 = ldsr128(&sm.alpha[pj][16 + 4 * lg]);
-            lds_wait_n<0>(a0);
-            lds_wait_n<0>(a1);
-            const f32x4 al[2] = {__builtin_bit_cast(f32x4, a0), __builtin_bit_cast(f32x4, a1)};
+          int fm[C::MBV];
+          if constexpr (C::G == 1) {
+            lds_wait_n<cmin15(C::MBV + C::NVR)>(fl);
 #pragma unroll
-            for (int mb = 0; mb < 2; ++mb) {
-              if ((mb == 0 ? f0 : f1) == 0) continue;
+            for (int mb = 0; mb < C::MBV; ++mb) fm[mb] = __builtin_amdgcn_readfirstlane(fl[mb]);
+          } else {
+            lds_wait_n<cmin15(C::MBV + C::NVR)>(fl4);
+#pragma unroll
+            for (int mb = 0; mb < C::MBV; ++mb) fm[mb] = __builtin_amdgcn_readfirstlane(fl4[mb]);
+          }
+          int fany = 0;
+#pragma unroll
+          for (int mb = 0; mb < C::MBV; ++mb) fany |= fm[mb];
+          if (fany) {
+            // the reference of some row moved at tile j: rescale before adding it
+            i32x4 ar[C::MBV];
+#pragma unroll
+            for (int mb = 0; mb < C::MBV; ++mb) ar[mb] = ldsr128(&sm.alpha[pj][vr0 + 16 * mb + 4 * lg]);
+#pragma unroll
+            for (int mb = 0; mb < C::MBV; ++mb) lds_wait_n<0>(ar[mb]);
+#pragma unroll
+            for (int mb = 0; mb < C::MBV; ++mb) {
+              if (fm[mb] == 0) continue;
+              const f32x4 al = __builtin_bit_cast(f32x4, ar[mb]);
 #pragma unroll
               for (int i = 0; i < 4; ++i)
 #pragma unroll
-                for (int cb = 0; cb < C::CB; ++cb) acc[mb][cb][i] *= al[mb][i];
+                for (int cb = 0; cb < C::CB; ++cb) acc[mb][cb][i] *= al[i];
             }
           }
-          lds_wait_n<cmin15(C::NVR)>(pr[0]);
-          lds_wait_n<cmin15(C::NVR)>(pr[1]);
-          const bf16x8 pf[2] = {__builtin_bit_cast(bf16x8, pr[0]), __builtin_bit_cast(bf16x8, pr[1])};
+          bf16x8 pf[C::MBV];
+#pragma unroll
+          for (int mb = 0; mb < C::MBV; ++mb) {
+            lds_wait_n<cmin15(C::NVR)>(pr[mb]);
+            pf[mb] = __builtin_bit_cast(bf16x8, pr[mb]);
+          }
           static_for<0, C::CB>([&](auto cc) {
             constexpr int cb = decltype(cc)::value;
             bf16x8 vf;
@@ -877,7 +1048,7 @@ __device__ __forceinline__ void role_main(const KParams& p, Smem<C>& sm, float k
               vf = __builtin_bit_cast(bf16x8, w4);
             }
 #pragma unroll
-            for (int mb = 0; mb < 2; ++mb) acc[mb][cb] = mfma16(pf[mb], vf, acc[mb][cb]);
+            for (int mb = 0; mb < C::MBV; ++mb) acc[mb][cb] = mfma16(pf[mb], vf, acc[mb][cb]);
           });
           if (++tv == v_nt) {
             // the request's last tile: its sums were published at the previous step
@@ -921,33 +1092,39 @@ __global__ __launch_bounds__(C::NTHR, 1) void ws_kernel(const KParams p) {
 }
 
 struct Inst {
-  int eb, rms, dcg, cpr;
+  int eb, rms, dcg, cpr, g;
   bool cap, rtr;
   int nthr;
   void (*fn)(const KParams);
 };
 
-#define QMLA_WS(EB, RMS, DCG, A, CPR, CAP, RTR, ISS) \
-  {EB, RMS, DCG, CPR, CAP, RTR, WS<EB, RMS, DCG, A, CPR, CAP, RTR, ISS>::NTHR, &ws_kernel<WS<EB, RMS, DCG, A, CPR, CAP, RTR, ISS>>}
+#define QMLA_WS(EB, RMS, DCG, A, CPR, CAP, RTR, ISS, G)                                   \
+  {EB, RMS, DCG, CPR, G, CAP, RTR, WS<EB, RMS, DCG, A, CPR, CAP, RTR, ISS, G>::NTHR, \
+   &ws_kernel<WS<EB, RMS, DCG, A, CPR, CAP, RTR, ISS, G>>}
 
 static const Inst kInst[] = {
     // fp8 e4m3 + log8 codes, d_c 512, rope 64, 24 heads: 608-byte rows, 32-token tiles 3 ahead (6 stages)
-    QMLA_WS(1, QMLA_RMS_LOG8, 512, 3, 38, false, true, 1),
-    QMLA_WS(1, QMLA_RMS_LOG8, 512, 3, 38, false, false, 1),
+    QMLA_WS(1, QMLA_RMS_LOG8, 512, 3, 38, false, true, 1, 1),
+    QMLA_WS(1, QMLA_RMS_LOG8, 512, 3, 38, false, false, 1, 1),
     // ... up to 16 heads (592-byte rows), rms codes read per row
-    QMLA_WS(1, QMLA_RMS_LOG8, 512, 3, 37, false, false, 1),
+    QMLA_WS(1, QMLA_RMS_LOG8, 512, 3, 37, false, false, 1, 1),
+    // GLA-g2: two latent groups of 256 columns, up to 48 rows per group (12 heads x 4 verify tokens)
+    QMLA_WS(1, QMLA_RMS_LOG8, 256, 3, 38, false, false, 1, 2),
 };
 
 }  // namespace ws
 
 int ws_select(const qmla_decode_params* p) {
-  if (p->rope_w != 64 || p->groups != 1 || p->qrows * p->heads > 32) return -1;
+  if (p->rope_w != 64 || (p->groups != 1 && p->groups != 2)) return -1;
+  // rows per group: 2 row blocks with one group, 3 per group with two
+  if (p->qrows * (p->heads / p->groups) > (p->groups == 1 ? 32 : 48)) return -1;
   const int eb = p->kv_dtype == QMLA_KV_FP8 ? 1 : 2;
   const bool cap = p->logit_cap > 0.f;
   const int64_t ts = p->token_stride * eb;
   for (int i = 0; i < (int)(sizeof(ws::kInst) / sizeof(ws::kInst[0])); ++i) {
     const ws::Inst& in = ws::kInst[i];
-    if (in.eb != eb || in.rms != p->rms_mode || in.dcg != p->d_c || in.cap != cap) continue;
+    if (in.g != p->groups || in.eb != eb || in.rms != p->rms_mode || in.dcg != p->d_c / p->groups || in.cap != cap)
+      continue;
     if (in.rtr && (p->qrows != 1 || p->heads > 32)) continue;
     if ((int64_t)in.cpr * 16 > ts) continue;   // never read past a row
     if (p->rms_mode != QMLA_RMS_NONE) {
