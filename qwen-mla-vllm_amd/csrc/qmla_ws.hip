@@ -81,19 +81,21 @@ __device__ __forceinline__ uint32_t ldsr8(const void* p) {
 }
 // Reads that may follow a scalar load the compiler placed (kernel arguments it reloads under
 // register pressure): one statement that drains the counter first and waits for its own reads, so
-// no counted wait is involved and nothing can be scheduled in between.
+// no counted wait is involved and nothing can be scheduled in between. The destinations are
+// early-clobber: a read's result may land while a later read of the statement still waits to issue,
+// so no destination may share a register with an address.
 __device__ __forceinline__ void ldsr32f3_drained(const void* a, const void* b, const void* c, float& x, float& y,
                                                  float& z) {
   asm volatile(
       "s_waitcnt lgkmcnt(0)\n\tds_read_b32 %0, %3\n\tds_read_b32 %1, %4\n\tds_read_b32 %2, %5\n\t"
       "s_waitcnt lgkmcnt(0)"
-      : "=v"(x), "=v"(y), "=v"(z)
+      : "=&v"(x), "=&v"(y), "=&v"(z)
       : "v"(lds_addr(static_cast<const char*>(a))), "v"(lds_addr(static_cast<const char*>(b))),
         "v"(lds_addr(static_cast<const char*>(c))));
 }
 __device__ __forceinline__ void ldsr128x2_drained(const void* a, const void* b, i32x4& x, i32x4& y) {
   asm volatile("s_waitcnt lgkmcnt(0)\n\tds_read_b128 %0, %2\n\tds_read_b128 %1, %3\n\ts_waitcnt lgkmcnt(0)"
-               : "=v"(x), "=v"(y)
+               : "=&v"(x), "=&v"(y)
                : "v"(lds_addr(static_cast<const char*>(a))), "v"(lds_addr(static_cast<const char*>(b))));
 }
 __device__ __forceinline__ uint32_t ldsr16(const void* p) {

@@ -1,0 +1,62 @@
+"""GLA-g2 (two latent groups of 256 columns, 12 heads per group, fp8 + log8) on the warp-specialized
+decode, against the CPU oracle (tolerances of tests/test_gpu_ws.py): fixed splits, 1, 2 and 4 verify
+tokens (12 / 24 / 48 rows per group), pages that change inside a tile, hundreds of short and empty
+requests over two workgroups (several planning windows), and long requests split into many pieces.
+The reference runs GLA as its TP = 2 rank-local decode (mla_impl.py:628-662 for the verify rows).
+"""
+import pytest
+import torch
+
+from tests.mla_cases import make_case
+from tests.test_gpu_ws import _check
+
+pytestmark = pytest.mark.gpu
+
+
+def _case(gpu, lens, qrows=4, page_size=64, seed=50):
+    return make_case(batch=len(lens), heads=24, d_c=512, rope_w=64, page_size=page_size, lens=lens, kv="fp8",
+                     rms_mode="log8", seed=seed, device=gpu, qrows=qrows, groups=2, rms="spread", amp=4.0)
+
+
+def _forward(c, **kw):
+    import qmla
+    o, lse = qmla.forward(c.q_nope, c.q_pe, c.cache, c.block_table, c.seq_lens, d_c=c.d_c, page_size=c.page_size,
+                          sm_scale=c.sm_scale, kv_fp8=True, fp8_rms="log8", k_scale=c.k_scale, qrows=c.qrows,
+                          groups=2, **kw)
+    torch.cuda.synchronize()
+    return o, lse
+
+
+def test_gla_fixed_splits(gpu):
+    c = _case(gpu, [1, 900, 4097, 2500, 33], seed=51)
+    o, lse = _forward(c, num_splits=8)
+    _check("gla fixed 8 splits", c, o, lse)
+
+
+@pytest.mark.parametrize("qrows", [1, 2])
+def test_gla_verify_tokens(gpu, qrows):
+    c = _case(gpu, [2, 777, 3001, 64, 1500], qrows=qrows, seed=52 + qrows)
+    o, lse = _forward(c, num_workgroups=5)
+    _check(f"gla q{qrows}", c, o, lse)
+
+
+@pytest.mark.parametrize("page_size", [16, 1])
+def test_gla_small_pages(gpu, page_size):
+    c = _case(gpu, [5, 333, 1200], page_size=page_size, seed=55)
+    o, lse = _forward(c, num_workgroups=4)
+    _check(f"gla pages of {page_size}", c, o, lse)
+
+
+def test_gla_many_short_requests(gpu):
+    g = torch.Generator().manual_seed(56)
+    lens = [int(x) for x in torch.randint(0, 90, (200,), generator=g)]
+    lens[::13] = [0] * len(lens[::13])
+    c = _case(gpu, lens, seed=56)
+    o, lse = _forward(c, num_workgroups=2)
+    _check("gla 200 short requests, 2 workgroups", c, o, lse)
+
+
+def test_gla_long_requests(gpu):
+    c = _case(gpu, [40000, 31001], seed=57)
+    o, lse = _forward(c, num_workgroups=64)
+    _check("gla 2 long requests over 64 workgroups", c, o, lse)

@@ -3,7 +3,11 @@ operations complete in order, but scalar memory loads share that counter and com
 order, so the counts are only right while no scalar load is in flight. The compiler may place
 scalar loads (kernel arguments it reloads) anywhere; this test compiles the kernel to gfx950
 assembly exactly as the library is built and checks that every scalar load is drained
-(`lgkmcnt(0)`) before the next LDS operation or counted wait. CPU only (hipcc cross-compiles).
+(`lgkmcnt(0)`) before the next LDS operation or counted wait.
+
+Inline-assembly statements that issue several LDS reads in a row must not give one read's
+destination a register that a later read of the same statement uses as its address: the first
+result may land while the later read still waits to issue. CPU only (hipcc cross-compiles).
 """
 import pathlib
 import re
@@ -68,3 +72,47 @@ def test_hazard_check_sees_a_planted_overlap():
     body = ["s_load_dword s4, s[0:1], 0x10", "ds_read_b128 v[0:3], v4", "s_waitcnt lgkmcnt(0)"]
     assert _hazards(body)
     assert not _hazards(["s_load_dword s4, s[0:1], 0x10", "s_waitcnt lgkmcnt(0)", "ds_read_b128 v[0:3], v4"])
+
+
+def _vregs(text):
+    out = set()
+    for m in re.finditer(r"v\[(\d+):(\d+)\]", text):
+        out |= set(range(int(m.group(1)), int(m.group(2)) + 1))
+    for m in re.finditer(r"\bv(\d+)\b", text):
+        out.add(int(m.group(1)))
+    return out
+
+
+def _asm_read_overlaps(body):
+    """(destination, later read) pairs inside one inline-asm statement whose registers overlap."""
+    found = []
+    block = None
+    for line in body:
+        t = line.strip()
+        if t == ";;#ASMSTART":
+            block = []
+        elif t == ";;#ASMEND":
+            reads = [x for x in (block or []) if x.startswith("ds_read")]
+            for a in range(len(reads)):
+                dst = _vregs(reads[a].split(None, 1)[1].split(",")[0])
+                for b in range(a + 1, len(reads)):
+                    if dst & _vregs(reads[b].split(None, 1)[1].split(",", 1)[1]):
+                        found.append((reads[a], reads[b]))
+            block = None
+        elif block is not None:
+            block.append(t)
+    return found
+
+
+def test_ws_multi_read_statements_keep_addresses(tmp_path):
+    lines = _assembly(tmp_path, "qmla_ws.hip")
+    for name, body in _kernels(lines, r"^_ZN4qmla2ws9ws_kernel\S*:"):
+        ov = _asm_read_overlaps(body)
+        assert not ov, f"{name}: a read's destination is a later read's address: {ov[:2]}"
+
+
+def test_overlap_check_sees_a_planted_overlap():
+    body = [";;#ASMSTART", "s_waitcnt lgkmcnt(0)", "ds_read_b32 v1, v2", "ds_read_b32 v3, v1", ";;#ASMEND"]
+    assert _asm_read_overlaps(body)
+    body[3] = "ds_read_b32 v3, v4"
+    assert not _asm_read_overlaps(body)
