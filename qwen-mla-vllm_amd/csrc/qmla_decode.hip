@@ -814,8 +814,6 @@ static const Inst kInst[] = {
     QMLA_INST(2, QMLA_RMS_BF16, 512, 64, 2, 1, 2, 75, false, 64, 1, 4),
     QMLA_INST(2, QMLA_RMS_BF16, 512, 64, 2, 1, 2, 75, true, 64, 1, 4),
     QMLA_INST(2, QMLA_RMS_NONE, 512, 64, 2, 1, 2, 72, false, 64, 1, 4),
-    // GLA-g2: two latent groups of 256, 12 heads each, 4 verify tokens -> 48 rows per group
-    QMLA_INST(1, QMLA_RMS_LOG8, 256, 64, 3, 2, 3, 38, false, 64, 1, 4),
     // the plugin's deployed fp8 layouts (tests/test_fp8_kv.py): partial rope of 4 groups x 58 = 232
     // with 24 heads (one GPU) or 2 x 58 = 116 with 12 heads (rank-local at TP 2), latent ranks 256
     // and 768; rows [latent | rope | rms (1 byte, or 2 for raw bf16) | pad to 16 bytes]
