@@ -111,6 +111,42 @@ def test_error_codes(over, code):
         assert lib.qmla_combine(ctypes.byref(p), None) == code
 
 
+def _layout(kv, d_c, rope, heads, rms, qrows=1, groups=1):
+    """Parameter block for one cache layout (fake pointers). With 4 fixed splits and no workspace the
+    entry returns ERR_WORKSPACE once it has an instance for the shape and ERR_NOKERNEL otherwise: the
+    routing is checked without a launch."""
+    eb = 1 if kv == _lib.KV_FP8 else 2
+    rb = 2 if rms in (_lib.RMS_BF16, _lib.RMS_BF16_BYTES) else 1
+    row_bytes = d_c * eb + rope * eb + heads * rb
+    row_bytes += (-row_bytes) % 16
+    ts = row_bytes // eb
+    dcg = d_c // groups
+    return _valid_params(kv_dtype=kv, d_c=d_c, rope_w=rope, heads=heads, rms_heads=heads, rms_mode=rms,
+                         rms_offset=d_c + rope, token_stride=ts, page_stride=64 * ts, qrows=qrows, groups=groups,
+                         rows=2 * qrows, q_nope_stride_row=heads * dcg, q_nope_stride_head=dcg,
+                         q_pe_stride_row=heads * rope, q_pe_stride_head=rope, out_stride_row=heads * dcg,
+                         out_stride_head=dcg, workspace=None, num_splits=4)
+
+
+@pytest.mark.parametrize("kv,d_c,rope,heads,rms,qrows,groups,code", [
+    # the plugin's deployed FP8 layouts at rank 1792 (column-split kernel, padded rope windows)
+    (_lib.KV_FP8, 1792, 232, 24, _lib.RMS_LOG8, 1, 1, _lib.ERR_WORKSPACE),
+    (_lib.KV_FP8, 1792, 232, 24, _lib.RMS_BF16_BYTES, 1, 1, _lib.ERR_WORKSPACE),
+    (_lib.KV_FP8, 1792, 116, 12, _lib.RMS_E4M3, 1, 1, _lib.ERR_WORKSPACE),
+    (_lib.KV_FP8, 1792, 64, 24, _lib.RMS_LOG8, 1, 1, _lib.ERR_WORKSPACE),
+    # bf16 rank 768 with a 256-column window; bf16 rank 1792 with a partial rope has no instance
+    (_lib.KV_BF16, 768, 232, 24, _lib.RMS_BF16, 1, 1, _lib.ERR_WORKSPACE),
+    (_lib.KV_BF16, 1792, 232, 24, _lib.RMS_BF16, 1, 1, _lib.ERR_NOKERNEL),
+    # GLA-g2 with 4 verify tokens: FP8 + log8 only
+    (_lib.KV_FP8, 512, 64, 24, _lib.RMS_LOG8, 4, 2, _lib.ERR_WORKSPACE),
+    (_lib.KV_BF16, 512, 64, 24, _lib.RMS_BF16, 4, 2, _lib.ERR_NOKERNEL),
+])
+def test_routing_without_launch(kv, d_c, rope, heads, rms, qrows, groups, code):
+    lib = _lib.lib()
+    p = _layout(kv, d_c, rope, heads, rms, qrows, groups)
+    assert lib.qmla_decode(ctypes.byref(p), None) == code
+
+
 def test_null_params_and_balanced_workspace_errors():
     lib = _lib.lib()
     assert lib.qmla_decode(None, None) == _lib.ERR_NULL
