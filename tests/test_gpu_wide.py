@@ -2,7 +2,9 @@
 reference routes these widths to its two-pass path (ops/mla_decode_attention.py:778-849); the library
 computes them in one pass, with the same partial layout and split bounds. bf16 caches (one workgroup
 holds the 24 heads), FP8 caches with log8 codes (16 rows per workgroup: the heads are split over two
-workgroups that read the same tokens), and 4-token verify rows (96 rows over three workgroups).
+workgroups that read the same tokens), 4-token verify rows (96 rows over three workgroups), and the
+plugin's deployed FP8 layouts (rope 232 / 116 in padded windows) in balanced mode and with verify
+rows.
 
 Tolerance: max-abs 1e-2 (bf16 cache) / 3e-2 (FP8 cache) on the output beyond the output's own bf16
 rounding, lse 1e-2.
@@ -132,3 +134,28 @@ def test_wide_verify_rows(gpu):
     ro, rl = run_oracle(c)
     err, lerr = _report("wide verify x4", out, lse, ro, rl)
     assert err < TOL and lerr < 1e-2
+
+
+@pytest.mark.parametrize("heads,rope,rms,qrows,splits", [
+    (24, 232, "log8", 1, 0),          # deployed layout, balanced mode, 784-token pages
+    (12, 116, "e4m3", 4, 0),          # 4 verify tokens, folded in pairs: 24 rows over two workgroups along z
+    (12, 116, "bf16_bytes", 2, 8),    # 2 verify tokens, fixed splits
+])
+def test_wide_fp8_partial_rope(gpu, heads, rope, rms, qrows, splits):
+    """The plugin's deployed FP8 layouts at rank 1792 (padded rope windows, unaligned rms tails)
+    through `forward`: balanced and fixed splits, verify rows."""
+    import qmla
+    lens = [3, 1500, 4100, 790]
+    c = make_case(batch=len(lens), heads=heads, d_c=DC, rope_w=rope, page_size=784, lens=lens, kv="fp8",
+                  rms_mode=rms, seed=23 + heads + qrows, device=gpu, rms="spread", amp=4.0, qrows=qrows)
+    o, lse = qmla.forward(c.q_nope, c.q_pe, c.cache, c.block_table, c.seq_lens, page_size=784, sm_scale=c.sm_scale,
+                          kv_fp8=True, fp8_rms={"bf16_bytes": "bf16"}.get(rms, rms), k_scale=c.k_scale,
+                          qrows=qrows, num_splits=splits, num_workgroups=0 if splits else 9)
+    torch.cuda.synchronize()
+    ro, rl = run_oracle(c)
+    lg = lse.float().cpu()
+    empty = torch.isneginf(rl)
+    assert torch.equal(torch.isneginf(lg), empty)
+    err, _ = _report(f"wide fp8 rope {rope} {rms} q{qrows} S={splits}", o, lse, ro, rl)
+    lerr = (lg[~empty] - rl[~empty]).abs().max().item()
+    assert err < 3e-2 and lerr < 1e-2
