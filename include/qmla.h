@@ -142,7 +142,9 @@ const char* qmla_build_info(void);
 size_t qmla_workspace_bytes(const qmla_decode_params* p);
 
 /* Decode: scores, online softmax and P.V over the paged latent rows (split-K partials where the
- * split mode needs them) followed by the LSE combine, all on `stream` (a hipStream_t). */
+ * split mode needs them) followed by the LSE combine, all on `stream` (a hipStream_t). Rows that see
+ * no token get a zero output and lse -inf in every split mode (with num_splits == 1, where no
+ * combine runs, a small pass writes the rows of requests of length 0). */
 int qmla_decode(const qmla_decode_params* p, void* stream);
 
 /* The stages of qmla_decode, callable one by one on the same stream and params:
@@ -150,7 +152,8 @@ int qmla_decode(const qmla_decode_params* p, void* stream);
  *                        workspace (one small workgroup; no host involvement)
  *   qmla_decode_partial  the decode pass (stage 1, qwen_mla/ops/mla_decode_attention.py:297-586):
  *                        partials into attn_logits (fixed mode) or the balanced workspace, and the
- *                        final out / lse directly for requests a single workgroup covered
+ *                        final out / lse directly for requests a single workgroup covered (with
+ *                        num_splits == 1 all rows, those of requests of length 0 included)
  *   qmla_combine         the LSE merge (stage 2, qwen_mla/ops/mla_decode_attention.py:1064-1137) */
 int qmla_plan(const qmla_decode_params* p, void* stream);
 int qmla_decode_partial(const qmla_decode_params* p, void* stream);

@@ -1027,6 +1027,23 @@ static int run_partial(const qmla_decode_params* p, const Inst* in, KParams& k, 
   return launch((const void*)in->fn, dim3(k.nwg, 1, 1), dim3(in->nthr, 1, 1), args, st);
 }
 
+// One split: the decode kernels write final rows for the token ranges they own, and a request of
+// length 0 owns none. Its rows get what every combine writes for them: zero output, -inf lse.
+// Block (head, row); requests with tokens return at once.
+__global__ __launch_bounds__(64) void empty_rows_kernel(const KParams p, int dv) {
+  const int head = blockIdx.x, row = blockIdx.y;
+  if (req_len(p, row / p.qrows) > 0) return;
+  const int64_t obase = (int64_t)row * p.o_sr + (int64_t)head * p.o_sh;
+  for (int c = threadIdx.x; c < dv; c += 64) store_out(p.out, p.out_dt, obase + c, 0.f);
+  if (threadIdx.x == 0 && p.lse) store_out(p.lse, p.lse_dt, (int64_t)row * p.lse_sr + head, kNegInf);
+}
+
+static int run_empty_rows(const qmla_decode_params* p, KParams& k, hipStream_t st) {
+  int dv = p->d_c / p->groups;
+  void* args[] = {&k, &dv};
+  return launch((const void*)&empty_rows_kernel, dim3(p->heads, p->rows, 1), dim3(64, 1, 1), args, st);
+}
+
 static int run_combine(const qmla_decode_params* p, KParams& k, hipStream_t st) {
   int dv = p->d_c / p->groups;
   void* args[] = {&k, &dv};
@@ -1100,8 +1117,11 @@ int qmla_decode_partial(const qmla_decode_params* p, void* stream) {
     if (rc) return rc;
   }
   KParams k = make_kparams(p);
-  if (si >= 0) return ws_launch(si, p, k, k.nwg, (hipStream_t)stream);
-  return in ? run_partial(p, in, k, (hipStream_t)stream) : cs_launch(wi, p, k, k.nwg, (hipStream_t)stream);
+  hipStream_t st = (hipStream_t)stream;
+  rc = si >= 0 ? ws_launch(si, p, k, k.nwg, st) : in ? run_partial(p, in, k, st) : cs_launch(wi, p, k, k.nwg, st);
+  // one split writes the final rows here (the combine has nothing to do)
+  if (rc || p->num_splits != 1) return rc;
+  return run_empty_rows(p, k, st);
 }
 
 int qmla_combine(const qmla_decode_params* p, void* stream) {
@@ -1131,8 +1151,8 @@ int qmla_decode(const qmla_decode_params* p, void* stream) {
     if (p->num_splits > 1 && !p->workspace) return QMLA_ERR_WORKSPACE;
     KParams k = make_kparams(p);
     rc = si >= 0 ? ws_launch(si, p, k, 0, st) : in ? run_partial(p, in, k, st) : cs_launch(wi, p, k, 0, st);
-    if (rc || p->num_splits == 1) return rc;
-    return run_combine(p, k, st);
+    if (rc) return rc;
+    return p->num_splits == 1 ? run_empty_rows(p, k, st) : run_combine(p, k, st);
   }
   rc = check_balanced_ws(p);
   if (rc) return rc;

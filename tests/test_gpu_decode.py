@@ -110,3 +110,28 @@ def test_gla_verify(gpu):
     ro, rl = run_oracle(c)
     err, lerr = _report("gla-g2 verify", o, lse, ro, rl, 3e-2)
     assert err < 3e-2 and lerr < 1e-2
+
+
+@pytest.mark.parametrize("kv,rms,d_c,qrows", [("fp8", "log8", 512, 1), ("fp8", "e4m3", 512, 1), ("bf16", "bf16", 512, 4),
+                                              ("bf16", "bf16", 1792, 1)])
+def test_single_split_empty_requests(gpu, kv, rms, d_c, qrows):
+    """One split (final rows written by the decode kernel itself, no combine): requests of length 0
+    still get a zero output and -inf lse, as every combine writes them. Outputs start as NaN."""
+    import qmla
+    lens = [0, 700, 0, 3, 1]
+    c = make_case(batch=len(lens), heads=24, d_c=d_c, rope_w=64, page_size=64, lens=lens, kv=kv, rms_mode=rms,
+                  seed=61, device=gpu, qrows=qrows, rms="spread")
+    rows = c.q_nope.shape[0]
+    o = torch.full((rows, 24, d_c), float("nan"), dtype=torch.bfloat16, device=gpu)
+    lse = torch.full((rows, 24), float("nan"), dtype=torch.float32, device=gpu)
+    kw = dict(kv_fp8=True, fp8_rms=rms, k_scale=c.k_scale) if kv == "fp8" else {}
+    qmla.forward(c.q_nope, c.q_pe, c.cache, c.block_table, c.seq_lens, page_size=64, sm_scale=c.sm_scale, qrows=qrows,
+                 num_splits=1, out=o, lse=lse, **kw)
+    torch.cuda.synchronize()
+    ro, rl = run_oracle(c)
+    assert not torch.isnan(o.float()).any() and not torch.isnan(lse).any(), "unwritten rows"
+    err, _ = _report(f"one split {kv} {rms} d_c {d_c} q{qrows}", o, lse, ro, rl, TOL[kv])
+    lg = lse.cpu()
+    empty = torch.isneginf(rl)
+    assert torch.equal(torch.isneginf(lg), empty)
+    assert (lg[~empty] - rl[~empty]).abs().max().item() < 1e-2 and err < TOL[kv]
