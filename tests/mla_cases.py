@@ -25,7 +25,7 @@ def cache_bytes(case: Case) -> torch.Tensor:
     return c.view(torch.uint8).reshape(pages, P, -1)
 
 
-def run_oracle(case: Case, rows=None):
+def run_oracle(case: Case, rows=None, logit_cap: float = 0.0):
     """Oracle (o [rows, H, d_c/G], lse [rows, H]) in float32 on the CPU."""
     cb = cache_bytes(case)
     bt = case.block_table.cpu()
@@ -37,4 +37,5 @@ def run_oracle(case: Case, rows=None):
     ks = float(case.k_scale.cpu()) if case.k_scale is not None else 1.0
     return ora.mla_decode(qn, qp, cb, bt, sl, page_size=case.page_size, d_c=case.d_c, rope_w=case.rope_w,
                           rms_offset=case.rms_offset, kv=case.kv, rms_mode=ORACLE_RMS[case.rms_mode],
-                          k_scale=ks, sm_scale=case.sm_scale, rms_heads=case.heads, groups=case.groups)
+                          k_scale=ks, sm_scale=case.sm_scale, rms_heads=case.heads, groups=case.groups,
+                          logit_cap=logit_cap)

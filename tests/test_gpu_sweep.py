@@ -1,6 +1,7 @@
 """A seeded sweep over the supported decode families against the CPU oracle: every case draws a
-family, page size, batch, ragged lengths (empty requests included), verify tokens and split mode
-from its seed, so combinations no targeted test picks are covered too. Tolerances as in
+family (kernel family, cache format, rms format, latent rank, heads, rope width, logit cap), page
+size, batch, ragged lengths (empty requests included), verify tokens and split mode from its seed,
+so combinations no targeted test picks are covered too. Tolerances as in
 tests/test_gpu_decode.py (max-abs 1e-2 bf16 / 3e-2 fp8 beyond the output's own bf16 rounding; lse
 1e-2, -inf exactly where a row sees no token).
 """
@@ -14,23 +15,32 @@ from tests.mla_cases import make_case, run_oracle
 pytestmark = pytest.mark.gpu
 
 REL = 2.0 ** -7
-# (kv, rms mode, d_c, heads, verify tokens allowed, groups)
+# (kv, rms mode, d_c, heads, rope width, verify tokens allowed, groups, logit cap)
 FAMILIES = [
-    ("fp8", "log8", 512, 24, (1,), 1),           # warp-specialized, transposed rms reads
-    ("fp8", "log8", 512, 16, (1, 2), 1),         # warp-specialized, rms read per row
-    ("fp8", "log8", 512, 8, (1, 2, 4), 1),
-    ("fp8", "log8", 512, 24, (1, 2, 4), 2),      # GLA-g2
-    ("fp8", "e4m3", 512, 24, (1, 4), 1),         # per-group kernel
-    ("fp8", "bf16_bytes", 512, 24, (1,), 1),
-    ("bf16", "bf16", 512, 24, (1, 4), 1),
-    ("bf16", "bf16", 1792, 24, (1,), 1),         # column-split kernel
+    ("fp8", "log8", 512, 24, 64, (1,), 1, 0.0),            # warp-specialized, transposed rms reads
+    ("fp8", "log8", 512, 16, 64, (1, 2), 1, 0.0),          # warp-specialized, rms read per row
+    ("fp8", "log8", 512, 8, 64, (1, 2, 4), 1, 0.0),
+    ("fp8", "log8", 512, 24, 64, (1, 2, 4), 2, 0.0),       # GLA-g2
+    ("fp8", "e4m3", 512, 24, 64, (1, 4), 1, 0.0),          # per-group kernel
+    ("fp8", "bf16_bytes", 512, 24, 64, (1,), 1, 0.0),
+    ("bf16", "bf16", 512, 24, 64, (1, 4), 1, 0.0),
+    ("bf16", "bf16", 1792, 24, 64, (1,), 1, 0.0),          # column-split kernel
+    ("fp8", "log8", 512, 24, 64, (1,), 1, 30.0),           # tanh logit cap
+    ("bf16", "bf16", 512, 24, 64, (1,), 1, 30.0),
+    ("fp8", "log8", 256, 24, 232, (1,), 1, 0.0),           # the plugin's deployed partial-rope layouts
+    ("fp8", "e4m3", 768, 12, 116, (1,), 1, 0.0),
+    ("bf16", "bf16", 256, 12, 116, (1,), 1, 0.0),
+    ("bf16", "bf16", 768, 24, 232, (1,), 1, 0.0),          # ... rank 768 in the column-split kernel
+    ("fp8", "log8", 1792, 24, 232, (1,), 1, 0.0),          # ... rank 1792 (padded rope windows)
+    ("fp8", "bf16_bytes", 1792, 12, 116, (1, 2, 4), 1, 0.0),
+    ("fp8", "log8", 1792, 24, 64, (1,), 1, 0.0),           # FP8 wide latent, rows split over workgroups
 ]
 PAGES = (1, 16, 40, 64, 784)
 
 
 def _draw(seed):
     r = random.Random(seed)
-    kv, rms, d_c, heads, qopts, groups = FAMILIES[seed % len(FAMILIES)]
+    kv, rms, d_c, heads, rope, qopts, groups, cap = FAMILIES[seed % len(FAMILIES)]
     qrows = r.choice(qopts)
     page = r.choice(PAGES)
     batch = r.randint(1, 6)
@@ -39,25 +49,25 @@ def _draw(seed):
         lens[0] = 17
     splits = r.choice((0, 0, 1, 3, 16))
     nwg = r.choice((0, 2, 7, 33)) if splits == 0 else 0
-    return dict(kv=kv, rms=rms, d_c=d_c, heads=heads, qrows=qrows, groups=groups, page=page, lens=lens,
-                splits=splits, nwg=nwg)
+    return dict(kv=kv, rms=rms, d_c=d_c, heads=heads, rope=rope, qrows=qrows, groups=groups, cap=cap, page=page,
+                lens=lens, splits=splits, nwg=nwg)
 
 
-@pytest.mark.parametrize("seed", range(40))
+@pytest.mark.parametrize("seed", range(60))
 def test_sweep(gpu, seed):
     import qmla
     a = _draw(seed)
     print(f"[sweep {seed}] {a}", flush=True)
-    c = make_case(batch=len(a["lens"]), heads=a["heads"], d_c=a["d_c"], rope_w=64, page_size=a["page"], lens=a["lens"],
-                  kv=a["kv"], rms_mode=a["rms"], seed=1000 + seed, device=gpu, qrows=a["qrows"], groups=a["groups"],
-                  rms="spread", amp=2.0)
+    c = make_case(batch=len(a["lens"]), heads=a["heads"], d_c=a["d_c"], rope_w=a["rope"], page_size=a["page"],
+                  lens=a["lens"], kv=a["kv"], rms_mode=a["rms"], seed=1000 + seed, device=gpu, qrows=a["qrows"],
+                  groups=a["groups"], rms="spread", amp=2.0)
     kw = dict(kv_fp8=True, fp8_rms={"bf16_bytes": "bf16"}.get(a["rms"], a["rms"]), k_scale=c.k_scale) \
         if a["kv"] == "fp8" else {}
     o, lse = qmla.forward(c.q_nope, c.q_pe, c.cache, c.block_table, c.seq_lens, d_c=a["d_c"], page_size=a["page"],
                           sm_scale=c.sm_scale, qrows=a["qrows"], groups=a["groups"], num_splits=a["splits"],
-                          num_workgroups=a["nwg"], **kw)
+                          num_workgroups=a["nwg"], logit_cap=a["cap"], **kw)
     torch.cuda.synchronize()
-    ro, rl = run_oracle(c)
+    ro, rl = run_oracle(c, logit_cap=a["cap"])
     tol = 3e-2 if a["kv"] == "fp8" else 1e-2
     d = (o.float().cpu() - ro).abs()
     excess = (d - REL * ro.abs()).max().item()
