@@ -238,8 +238,11 @@ __global__ __launch_bounds__(64 * ROWS_PER_WG) void gather_kernel(const GParams 
     return;
   }
   const float sc = *p.scale;
-  // latent + rope: e4m3 * scale in fp32, rounded to the destination dtype
-  for (int c = 8 * lane; c < p.rms_offset; c += 512) {
+  // latent + rope: e4m3 * scale in fp32, rounded to the destination dtype; whole 8-byte groups as
+  // vectors, the 1-7 bytes before an rms tail that is not 8-aligned one by one (the plugin's 12-head
+  // rope-116 rows put the tail at 4 mod 8)
+  const int c8 = p.rms_offset & ~7;
+  for (int c = 8 * lane; c < c8; c += 512) {
     const uint2 raw = *reinterpret_cast<const uint2*>(row + c);
     const uint32_t w[2] = {raw.x, raw.y};
     uint32_t o[4];
@@ -252,6 +255,10 @@ __global__ __launch_bounds__(64 * ROWS_PER_WG) void gather_kernel(const GParams 
       o[2 * h + 1] = (uint32_t)to_out(f2, p.dst_dtype) | ((uint32_t)to_out(f3, p.dst_dtype) << 16);
     }
     *reinterpret_cast<uint4*>(out + c) = make_uint4(o[0], o[1], o[2], o[3]);
+  }
+  if (lane < p.rms_offset - c8) {
+    const int c = c8 + lane;
+    out[c] = to_out(e4m3_f32((int)(unsigned char)row[c], 0) * sc, p.dst_dtype);
   }
   // the rms tail: one element per head at rms_offset
   const unsigned char* tail = reinterpret_cast<const unsigned char*>(row) + p.rms_offset;
@@ -292,7 +299,7 @@ extern "C" int qmla_gather(const qmla_gather_params* p, void* stream) {
     if (p->rms_mode != QMLA_RMS_LOG8 && p->rms_mode != QMLA_RMS_BF16_BYTES && p->rms_mode != QMLA_RMS_E4M3)
       return QMLA_ERR_MODE;
     if (!p->scale) return QMLA_ERR_NULL;
-    if (p->rms_offset <= 0 || p->rms_offset % 8 || p->rms_heads < 0) return QMLA_ERR_SHAPE;
+    if (p->rms_offset <= 0 || p->rms_heads < 0) return QMLA_ERR_SHAPE;
     const int64_t rb = p->rms_mode == QMLA_RMS_BF16_BYTES ? 2 : 1;
     if (p->rms_offset + rb * p->rms_heads > p->token_stride) return QMLA_ERR_SHAPE;
     width = (int64_t)p->rms_offset + p->rms_heads;

@@ -272,7 +272,8 @@ def _gather_params(**over) -> _lib.GatherParams:
     (dict(rms_mode=_lib.RMS_NONE), _lib.ERR_MODE),
     (dict(kv_dtype=_lib.KV_BF16, row_elems=0), _lib.ERR_SHAPE),
     (dict(kv_dtype=_lib.KV_BF16, row_elems=600), _lib.ERR_SHAPE),        # 1200 bytes > 608-byte rows
-    (dict(rms_offset=572), _lib.ERR_SHAPE),
+    (dict(rms_offset=600), _lib.ERR_SHAPE),                           # 24 codes past the 608-byte row
+    (dict(rms_offset=0), _lib.ERR_SHAPE),
     (dict(dst_stride=500), _lib.ERR_SHAPE),
     (dict(bt_stride=8), _lib.ERR_SHAPE),
     (dict(dst=0x500008), _lib.ERR_ALIGN),
