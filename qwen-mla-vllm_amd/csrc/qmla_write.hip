@@ -85,8 +85,15 @@ __global__ __launch_bounds__(64 * ROWS_PER_WG) void write_kernel(const WParams p
     const float inv = 1.0f / *p.k_scale;
     for (int c = 8 * lane; c < p.d_c; c += 512)
       *reinterpret_cast<uint2*>(dst + c) = quant8(kc + c, inv);
-    for (int c = 8 * lane; c < p.rope_w; c += 512)
+    // the rope in 8-element groups, then the 1-7 elements before an rms tail that is not 8-aligned
+    // one by one (the plugin's rope 116): a group must not spill into the tail other lanes write
+    const int r8 = p.rope_w & ~7;
+    for (int c = 8 * lane; c < r8; c += 512)
       *reinterpret_cast<uint2*>(dst + p.d_c + c) = quant8(kp + c, inv);
+    if (lane < p.rope_w - r8) {
+      const int c = r8 + lane;
+      dst[p.d_c + c] = (char)(pack_e4m3(sat448(bf16_to_f32(kp[c]), inv), 0.f, 0.f, 0.f) & 0xFF);
+    }
     char* rt = dst + p.d_c + p.rope_w;
     for (int h = lane; h < p.rms_heads; h += 64) {
       const uint16_t rb = kp[p.rope_w + h];
@@ -127,7 +134,7 @@ extern "C" int qmla_cache_write(const qmla_cache_write_params* p, void* stream) 
       p->rms_mode != QMLA_RMS_NONE)
     return QMLA_ERR_MODE;
   if (!fp8 && p->rms_mode != QMLA_RMS_BF16 && p->rms_mode != QMLA_RMS_NONE) return QMLA_ERR_MODE;
-  if (fp8 && (p->rope_w % 8 || !p->k_scale)) return fp8 && !p->k_scale ? QMLA_ERR_NULL : QMLA_ERR_SHAPE;
+  if (fp8 && !p->k_scale) return QMLA_ERR_NULL;
   const int pe_elems = p->rope_w + (rb ? p->rms_heads : 0);
   if (p->k_pe_stride < pe_elems) return QMLA_ERR_SHAPE;
   // the written bytes must fit one token slot

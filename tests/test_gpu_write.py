@@ -200,3 +200,40 @@ def test_wide_latent_rows_bit_exact(gpu):
                             rms_mode=ora.RMS_LOG8)
     nb = exp.shape[1]
     assert np.array_equal(got[slots.numpy(), :nb], exp) and np.all(got[slots.numpy(), nb:] == 0xAB)
+
+
+@pytest.mark.parametrize("rms,mode", [("log8", ora.RMS_LOG8), ("bf16", ora.RMS_BF16_BYTES), ("e4m3", ora.RMS_E4M3)])
+@pytest.mark.parametrize("d_c,rope,heads", [(256, 232, 24), (768, 116, 12), (1792, 116, 12), (1792, 232, 24)])
+def test_fp8_rows_deployed_layouts(gpu, d_c, rope, heads, rms, mode):
+    """The plugin's deployed rows (tests/test_fp8_kv.py:105-120: rope 232 with 24 heads, 116 with 12;
+    rope 116 leaves the rms tail at 4 mod 8): the same bytes as the oracle, nothing past the row."""
+    import qmla
+    n, P, pages = 200, 16, 20
+    g = torch.Generator().manual_seed(d_c + rope + heads)
+    kv_c = (torch.randn(n, d_c, generator=g) * 4.0).to(torch.bfloat16)
+    k_pe = torch.empty(n, rope + heads, dtype=torch.bfloat16)
+    k_pe[:, :rope] = (torch.randn(n, rope, generator=g) * 4.0).to(torch.bfloat16)
+    k_pe[:, rope:] = torch.exp(torch.randn(n, heads, generator=g)).to(torch.bfloat16)
+    rb = 2 if rms == "bf16" else 1
+    width = d_c + rope + rb * heads
+    width += (-width) % 16
+    k_scale = 0.0217
+    slots = torch.randperm(pages * P, generator=g)[:n]
+    cache = torch.full((pages, P, 1, width), 0xAB, dtype=torch.uint8, device=gpu)
+    qmla.cache_write(kv_c.to(gpu), k_pe.to(gpu), cache, slots.to(gpu), rope_w=rope, rms_heads=heads, kv_fp8=True,
+                     rms=rms, k_scale=torch.tensor(k_scale, device=gpu))
+    torch.cuda.synchronize()
+    got = cache.cpu().view(pages * P, width).numpy()
+    kc, kp = kv_c.float().numpy(), k_pe.float().numpy()
+    if mode == ora.RMS_E4M3:
+        inv = np.float32(1.0) / np.float32(k_scale)
+        q = lambda x: ora.e4m3_encode(np.clip(x.astype(np.float32) * inv, -448.0, 448.0))
+        exp = np.concatenate([q(kc), q(kp[:, :rope]), q(kp[:, rope:])], axis=1)
+    else:
+        exp = ora.fp8_row_bytes(kc, kp, packed_rope=rope, n_heads=heads, k_scale=k_scale, rms_mode=mode)
+    nb = exp.shape[1]
+    s = slots.numpy()
+    bad = [(i, np.nonzero(got[s[i], :nb] != exp[i])[0][:6]) for i in range(n) if not np.array_equal(got[s[i], :nb], exp[i])]
+    assert not bad, bad[:3]
+    assert np.all(got[s, nb:] == 0xAB)
+    assert np.all(np.delete(got, s, axis=0) == 0xAB)
