@@ -1,0 +1,40 @@
+"""The balanced plan (qmla_plan) on its own, bit for bit: per-request exclusive prefix sums of
+64-token tile counts, the total and the per-workgroup chunk, against numpy. Batch sizes straddle the
+kernel's 1024-request batches; with verify rows the last row of a request carries its length. The
+plan stands in for FlashInfer's work-split plan (qwen_mla/fi_decode.py:210-233).
+"""
+import numpy as np
+import pytest
+import torch
+
+from tests.mla_cases import make_case
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.mark.parametrize("n_req,qrows,nwg", [(1, 1, 256), (128, 1, 256), (255, 1, 7), (1024, 1, 256), (1025, 1, 33),
+                                             (1000, 4, 256), (2049, 1, 1)])
+def test_plan_prefix_sums(gpu, n_req, qrows, nwg):
+    from qmla import _lib
+    from qmla.decode import _stream, build_params, workspace_bytes
+    c = make_case(batch=n_req, heads=24, d_c=512, rope_w=64, page_size=64, lens=[1] * n_req, kv="bf16",
+                  rms_mode="bf16", seed=9, device=gpu, qrows=qrows)
+    g = np.random.default_rng(n_req)
+    L = g.integers(0, 70000, n_req)
+    L[::7] = 0
+    rows = np.repeat(L, qrows) - np.tile(np.arange(qrows)[::-1], n_req)
+    sl = torch.tensor(np.maximum(rows, 0), dtype=torch.int32, device=gpu)
+    o = torch.empty(n_req * qrows, 24, 512, dtype=torch.bfloat16, device=gpu)
+    args = dict(q_nope=c.q_nope, q_pe=c.q_pe, kv_cache=c.cache, block_table=c.block_table, seq_lens=sl, out=o,
+                lse=None, d_c=512, rope_w=64, rms_offset=c.rms_offset, rms_mode=_lib.RMS_BF16, kv=_lib.KV_BF16,
+                page_size=64, sm_scale=c.sm_scale, qrows=qrows, num_splits=0, num_workgroups=nwg)
+    ws = torch.full((workspace_bytes(build_params(**args)) // 4,), -7, dtype=torch.int32, device=gpu)
+    p = build_params(workspace=ws, **args)
+    _lib.check("qmla_plan", _lib.lib().qmla_plan(p, _stream()))
+    torch.cuda.synchronize()
+    got = ws[:n_req + 3].cpu().numpy()
+    tiles = (L + 63) // 64
+    total = int(tiles.sum())
+    exp = np.concatenate([[max(-(-total // nwg), 1), total], np.cumsum(tiles) - tiles, [total]])
+    print(f"[plan n_req {n_req} qrows {qrows} nwg {nwg}] total {total} tiles", flush=True)
+    assert np.array_equal(got, exp), np.argwhere(got != exp)[:5].ravel().tolist()
