@@ -192,7 +192,7 @@ class RowLayout:
         return self.rope_w * eb + (self.n_rms * per if self.has_rms else 0)
 
 
-def baseline_layout(d_c: int = 512, rope_w: int = 64, heads: int = 24, fp8: bool = False,
+def rank_layout(d_c: int = 512, rope_w: int = 64, heads: int = 24, fp8: bool = False,
                     fp8_rms: str = "log8", groups: int = 1) -> RowLayout:
     """Row layout of a single-layer config: the padded width for one rank d_c, tail = rope + rms."""
     per = 2 if (fp8 and fp8_rms == "bf16") else 1

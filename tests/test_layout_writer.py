@@ -37,9 +37,9 @@ def test_row_width_known_answers():
     assert layout.effective_rope_dim(hk) == 58
     assert layout.mla_base_tail(hk, 1) == 256
     assert [layout.mla_padded_head_size(hk, r, 1) for r in (256, 768, 1792)] == [512, 1024, 2048]
-    assert layout.baseline_layout(512, 64, 24).row == 608
-    assert layout.baseline_layout(1792, 64, 24).row == 1888
-    assert layout.baseline_layout(512, 64, 24, fp8=True).row == 608
+    assert layout.rank_layout(512, 64, 24).row == 608
+    assert layout.rank_layout(1792, 64, 24).row == 1888
+    assert layout.rank_layout(512, 64, 24, fp8=True).row == 608
     # every width divides the largest one (pages of all layers unify)
     ws = [layout.mla_padded_head_size(hf, r, 1) for r in (256, 768, 1792)]
     assert all(max(ws) % w == 0 for w in ws)
