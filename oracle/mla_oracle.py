@@ -2,8 +2,8 @@
 
 TEST INFRASTRUCTURE ONLY. This module is the oracle the tests compare against, never the product:
 only the test suite (`tests/`), `__graft_entry__.smoke()` and the `cpu_baseline` leg of `bench.py`
-may import it. The
-product path (`qmla`) never calls it and fails loudly when its HIP library is missing.
+may import it. The product path (`qmla`) never calls it and fails loudly when its HIP library is
+missing.
 
 It restates, on the CPU, the arithmetic of the reference plugin's decode path:
 
