@@ -35,7 +35,7 @@ def _draw(seed):
     return dict(kv=kv, rms=rms, d_c=d_c, rope=rope, heads=heads, page=page, lens=lens, starts=starts, clen=clen)
 
 
-@pytest.mark.parametrize("seed", range(30))
+@pytest.mark.parametrize("seed", range(100))
 def test_gather_sweep(gpu, seed):
     a = _draw(seed)
     print(f"[gather sweep {seed}] {a['kv']} {a['rms']} d_c {a['d_c']} rope {a['rope']} heads {a['heads']} "

@@ -53,7 +53,7 @@ def _draw(seed):
                 lens=lens, splits=splits, nwg=nwg)
 
 
-@pytest.mark.parametrize("seed", range(60))
+@pytest.mark.parametrize("seed", range(200))
 def test_sweep(gpu, seed):
     import qmla
     a = _draw(seed)
