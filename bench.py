@@ -63,6 +63,35 @@ def make_workload(name, device):
     return make_case(lens=lens, device=device, rms="row", **w), spec
 
 
+def decode_call(case, splits, dev):
+    """The exact call the bench times: qmla_decode on prebuilt parameters, balanced split mode with a
+    reserved workspace, or `splits` fixed splits with the reference's attn_logits [B, H, S, Dv+1]
+    partials. Returns (params, out, lse, buffers to keep alive)."""
+    import torch
+    from qmla import _lib
+    from qmla.decode import Workspace, build_params, workspace_bytes
+    rows, H = case.q_nope.shape[0], case.heads
+    dv = case.d_c // case.groups
+    out = torch.empty(rows, H, dv, dtype=torch.bfloat16, device=dev)
+    lse = torch.empty(rows, H, dtype=torch.float32, device=dev)
+    kv = _lib.KV_FP8 if case.kv == "fp8" else _lib.KV_BF16
+    mode = {"bf16": _lib.RMS_BF16, "log8": _lib.RMS_LOG8, "bf16_bytes": _lib.RMS_BF16_BYTES,
+            "e4m3": _lib.RMS_E4M3, "none": _lib.RMS_NONE}[case.rms_mode]
+    args_p = dict(q_nope=case.q_nope, q_pe=case.q_pe, kv_cache=case.cache, block_table=case.block_table,
+                  seq_lens=case.seq_lens, out=out, lse=lse, d_c=case.d_c, rope_w=case.rope_w,
+                  rms_offset=case.rms_offset, rms_mode=mode, kv=kv, page_size=case.page_size,
+                  sm_scale=case.sm_scale, k_scale=case.k_scale, qrows=case.qrows, groups=case.groups,
+                  num_splits=0, split_align=0)
+    if splits:
+        logits = torch.empty(rows, H, splits, dv + 1, dtype=torch.float32, device=dev)
+        args_p.update(num_splits=splits, split_align=16 if case.page_size % 16 == 0 else 0)
+        p = build_params(workspace=logits, ws_strides=(logits.stride(0), logits.stride(1), logits.stride(2)),
+                         **args_p)
+        return p, out, lse, (logits,)
+    ws = Workspace().reserve(workspace_bytes(build_params(**args_p)), dev)
+    return build_params(workspace=ws, **args_p), out, lse, (ws,)
+
+
 def kernel_bytes(case) -> int:
     """Algorithmic bytes the decode kernel reads: cached rows (latent + rope + rms, padding
     excluded), queries, block-table entries and lengths."""
@@ -107,29 +136,13 @@ def cpu_baseline(case, sample_every: int, budget_s: float):
     from oracle import mla_oracle as ora
     cores = len(os.sched_getaffinity(0))
     torch.set_num_threads(cores)
+    from qmla.synth import compact_requests
     n_req = case.seq_lens.shape[0] // case.qrows
     picks = list(range(0, n_req, sample_every))
-    rows = [b * case.qrows + j for b in picks for j in range(case.qrows)]
-    # compact CPU copy of just the sampled requests' pages
+    cache, new_bt, sll, qn, qp, rows = compact_requests(case, picks)
     P = case.page_size
-    bt = case.block_table.cpu()
-    sl = case.seq_lens.cpu()
-    page_ids, new_bt = [], torch.zeros(len(rows), bt.shape[1], dtype=torch.int32)
-    for i, r in enumerate(rows):
-        n = max(1, -(-int(sl[r]) // P))
-        base = len(page_ids)
-        if i % case.qrows == 0:
-            page_ids.extend(int(x) for x in bt[r, :n])
-            first = base
-        new_bt[i, :n] = torch.arange(first, first + n, dtype=torch.int32)
-    idx = torch.tensor(page_ids, dtype=torch.long, device=case.cache.device)
-    cache = case.cache.index_select(0, idx).cpu().contiguous()
-    cache = cache.view(torch.uint8).reshape(cache.shape[0], P, -1)
     rms_map = {"bf16": ora.RMS_BF16, "log8": ora.RMS_LOG8, "bf16_bytes": ora.RMS_BF16_BYTES,
                "e4m3": ora.RMS_E4M3, "none": ora.RMS_NONE}
-    qn = case.q_nope.cpu().float()[rows]
-    qp = case.q_pe.cpu().float()[rows]
-    sll = sl[rows]
     ks = float(case.k_scale.cpu()) if case.k_scale is not None else 1.0
 
     def run():
@@ -334,6 +347,9 @@ def main():
     ap.add_argument("--warmup", type=int, default=300)
     ap.add_argument("--workload", default="fp8_b128", choices=sorted(WORKLOADS))
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-graph", action="store_true", help="skip the HIP-graph replay timing")
+    ap.add_argument("--settle-ms", type=float, default=250.0,
+                    help="run the call back to back this long before the warm-up steps (clock ramp)")
     ap.add_argument("--cpu-every", type=int, default=0, help="oracle on every k-th request (0: per workload)")
     ap.add_argument("--cpu-budget", type=float, default=20.0)
     ap.add_argument("--copy-calib-mib", type=int, default=0,
@@ -352,39 +368,28 @@ def main():
     import torch
     import qmla
     from qmla import _lib
-    from qmla.decode import Workspace, build_params, workspace_bytes
 
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
     case, spec = make_workload(args.workload, dev)
     rows, H = case.q_nope.shape[0], case.heads
-    dv = case.d_c // case.groups
-    out = torch.empty(rows, H, dv, dtype=torch.bfloat16, device=dev)
-    lse = torch.empty(rows, H, dtype=torch.float32, device=dev)
-    kv = _lib.KV_FP8 if case.kv == "fp8" else _lib.KV_BF16
-    mode = {"bf16": _lib.RMS_BF16, "log8": _lib.RMS_LOG8, "bf16_bytes": _lib.RMS_BF16_BYTES,
-            "e4m3": _lib.RMS_E4M3}[case.rms_mode]
-    args_p = dict(q_nope=case.q_nope, q_pe=case.q_pe, kv_cache=case.cache, block_table=case.block_table,
-                  seq_lens=case.seq_lens, out=out, lse=lse, d_c=case.d_c, rope_w=case.rope_w,
-                  rms_offset=case.rms_offset, rms_mode=mode, kv=kv, page_size=case.page_size,
-                  sm_scale=case.sm_scale, k_scale=case.k_scale, qrows=case.qrows, groups=case.groups,
-                  num_splits=0, split_align=0)
     splits = WORKLOADS[args.workload].get("splits", 0)
-    if splits:
-        # fixed splits with the reference's attn_logits [B, H, S, Dv+1] partials
-        logits = torch.empty(rows, H, splits, dv + 1, dtype=torch.float32, device=dev)
-        args_p.update(num_splits=splits, split_align=16 if case.page_size % 16 == 0 else 0)
-        p = build_params(workspace=logits, ws_strides=(logits.stride(0), logits.stride(1), logits.stride(2)),
-                         **args_p)
-    else:
-        ws = Workspace().reserve(workspace_bytes(build_params(**args_p)), dev)
-        p = build_params(workspace=ws, **args_p)
+    p, out, lse, keep = decode_call(case, splits, dev)
     lib = qmla.lib()
     st = torch.cuda.current_stream().cuda_stream
 
     def step():
         _lib.check("qmla_decode", lib.qmla_decode(p, st))
 
+    # clock settle: the GPU's clocks ramp over the first tens of milliseconds of load, so the call
+    # runs back to back for --settle-ms of wall time before the W warm-up steps
+    settle_calls = 0
+    t_settle = time.perf_counter()
+    while (time.perf_counter() - t_settle) * 1e3 < args.settle_ms:
+        for _ in range(20):
+            step()
+        settle_calls += 20
+        torch.cuda.synchronize()
     for _ in range(args.warmup):
         step()
     torch.cuda.synchronize()
@@ -416,6 +421,46 @@ def main():
     part_ms = statistics.mean(a.elapsed_time(b) for a, b, _ in evs)
     comb_ms = statistics.mean(b.elapsed_time(c) for _, b, c in evs)
 
+    # timed region 3: the call as the serving loop runs it, recorded once into a HIP graph and
+    # replayed K times back to back
+    graph_ms = None
+    if not args.no_graph:
+        g = torch.cuda.CUDAGraph()
+        cap = torch.cuda.Stream()
+        cap.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(cap):
+            step_on = lambda: _lib.check("qmla_decode", lib.qmla_decode(p, torch.cuda.current_stream().cuda_stream))
+            step_on()
+            torch.cuda.synchronize()
+            with torch.cuda.graph(g, stream=cap):
+                step_on()
+        torch.cuda.current_stream().wait_stream(cap)
+        for _ in range(5):
+            g.replay()
+        torch.cuda.synchronize()
+        g0, g1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        g0.record()
+        for _ in range(args.steps):
+            g.replay()
+        g1.record()
+        torch.cuda.synchronize()
+        graph_ms = g0.elapsed_time(g1) / args.steps
+        del g
+
+    # timed region 4: cold L2 / MALL -- 512 MiB written between calls, each call timed on its own
+    flush = torch.empty(512 << 20, dtype=torch.uint8, device=dev)
+    cold = []
+    for _ in range(args.steps):
+        flush.fill_(1)
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record()
+        step()
+        b.record()
+        cold.append((a, b))
+    torch.cuda.synchronize()
+    cold_ms = statistics.median(a.elapsed_time(b) for a, b in cold)
+    del flush
+
     if args.copy_calib_mib:
         n = args.copy_calib_mib << 20
         src = torch.empty(n, dtype=torch.uint8, device=dev).fill_(1)
@@ -434,6 +479,10 @@ def main():
     k_gbps = k_bytes / (part_ms / 1e3) / 1e9
     traffic = measured_traffic(args.workload)
 
+    # the warp-specialized kernel's fp8 score path serves fp8 + log8 rows, d_c 512, rope 64, one
+    # latent group and at most 32 rows per request, or GLA-g2 with at most 48 rows per group
+    ws_fp8 = (case.kv == "fp8" and case.rms_mode == "log8" and case.d_c // case.groups in (512, 256)
+              and case.rope_w == 64 and case.qrows * case.heads // case.groups <= (32 if case.groups == 1 else 48))
     cpu = None
     if not args.no_cpu:
         cpu = cpu_baseline(case, args.cpu_every or CPU_EVERY.get(args.workload, 2), args.cpu_budget)
@@ -455,10 +504,10 @@ def main():
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "bf16",
+        "dtype": "fp8+bf16" if ws_fp8 else "bf16",
         "storage": (("e4m3 latent/rope + u8 log8 rms; scores on the fp8 MFMAs (cache bytes as stored, query as "
                      "e4m3 hi+lo, 8 significant bits), bf16 P.V, fp32 accumulate and softmax")
-                    if case.kv == "fp8" and case.groups == 1 and case.qrows * case.heads <= 32 else
+                    if ws_fp8 else
                     "e4m3 latent/rope + u8 log8 rms; bf16 MFMA operands, fp32 accumulate and softmax"
                     if case.kv == "fp8" else "bf16 cache; bf16 MFMA operands, fp32 accumulate and softmax"),
         "data": "synthetic",
@@ -466,10 +515,15 @@ def main():
                    "d_c": case.d_c, "d_r": case.rope_w, "page_size": case.page_size, "kv": case.kv,
                    "rms": case.rms_mode, "ctx": ctx, "cached_tokens": toks_cached, "qrows": case.qrows,
                    "groups": case.groups, "split": f"fixed {splits} + combine" if splits else "balanced", "row_bytes": case.row * (1 if case.kv == "fp8" else 2)},
-        "gbps": round(gbps, 1),
-        "hbm_frac": round(gbps / HBM_PEAK_GBPS, 4),
+        # the whole call (plan + decode + combine) against the HBM peak: the metric's GB/s
+        "call_gbps": round(gbps, 1),
+        "call_hbm_frac": round(gbps / HBM_PEAK_GBPS, 4),
         "decode_kernel_us": round(part_ms * 1e3, 2),
         "combine_us": round(comb_ms * 1e3, 2),
+        "graph_ms_per_step": None if graph_ms is None else round(graph_ms, 4),
+        "graph_call_hbm_frac": None if graph_ms is None else round(call_bytes / (graph_ms / 1e3) / 1e9 / HBM_PEAK_GBPS, 4),
+        "cold_l2_ms_per_call": round(cold_ms, 4),
+        "settle_calls": settle_calls,
         "wall_s_timed": round(t_wall, 3),
         "roofline": {"bound": "hbm", "achieved": round(k_gbps, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
                      "frac": round(k_gbps / HBM_PEAK_GBPS, 4), "traffic": traffic,

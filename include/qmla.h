@@ -102,7 +102,9 @@ typedef struct qmla_decode_params {
   int32_t rows, heads, rms_heads;
   int32_t qrows;                  /* > 1: fold each run of qrows rows into one request so the
                                      cache is read once; row j of a request of length L sees
-                                     its first L - (qrows-1-j) tokens */
+                                     its first L - (qrows-1-j) tokens. A folded request takes L
+                                     and its page ids from its LAST row (seq_lens and block_table
+                                     row qrows*r + qrows-1), as the reference's folding does */
   int32_t groups;                 /* latent groups (1, or 2 for GLA-g2) */
 
   /* outputs: out [rows, heads, d_c/G] (out_dtype), lse [rows, heads] (lse_dtype, may be NULL),
@@ -117,7 +119,10 @@ typedef struct qmla_decode_params {
   /* split-K. num_splits > 0: the reference's fixed split count; split s of a request of length
    * L covers [s*per, min((s+1)*per, L)) with per = ceil(ceil(L/S)/split_align)*split_align
    * (split_align 0 = no rounding), and the partials live in the caller's workspace in the
-   * reference layout attn_logits[rows, heads, S, d_c/G + 1] (strides below, in floats).
+   * reference layout attn_logits[rows, heads, S, d_c/G + 1] (strides below, in floats). With
+   * S > 1 the call returns QMLA_ERR_WORKSPACE unless workspace_bytes >= qmla_workspace_bytes(),
+   * every stride is positive and the largest partial offset (rows-1)*ws_stride_row +
+   * (heads-1)*ws_stride_head + (S-1)*ws_stride_split + d_c/G lies inside workspace_bytes.
    * num_splits == 0: balanced mode. Every workgroup gets the same number of 64-token tiles
    * across request boundaries; partials go to the workspace at qmla_workspace_bytes() size and
    * the ws_stride_* fields are ignored. */

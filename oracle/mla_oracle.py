@@ -246,6 +246,83 @@ def mla_decode(q_lat: torch.Tensor, q_pe: torch.Tensor | None, cache_u8: torch.T
     return o, lse
 
 
+def _bf16_t(x: torch.Tensor) -> torch.Tensor:
+    """float32 tensor -> nearest-even bf16 values, as float32."""
+    return x.to(torch.bfloat16).float()
+
+
+def mla_decode_reference_rounding(q_lat: torch.Tensor, q_pe: torch.Tensor | None, cache_u8: torch.Tensor,
+                                  block_table: torch.Tensor, seq_lens: torch.Tensor, *, page_size: int,
+                                  d_c: int, rope_w: int, rms_offset: int, kv: str, rms_mode: str,
+                                  k_scale: float = 1.0, sm_scale: float, logit_cap: float = 0.0,
+                                  rms_heads: int | None = None, groups: int = 1, num_splits: int = 1,
+                                  align: int = 16, block_n: int = 16, partials: bool = False):
+    """The decode with the roundings the reference Triton kernel applies, so that its own error
+    against the float32 oracle can be measured (ops/mla_decode_attention.py:297-586, :1064-1137):
+
+    * fp8 keys are dequantized to bf16, `(k.float() * k_scale).to(bf16)` (:451-452, :463); the
+      latent is both key and value (`v = tl.trans(k)`, :547-551), so values carry the same rounding;
+    * scores `q.k` accumulate in fp32 from bf16 operands (:453-464), then `/ rms`, `* sm_scale`,
+      optional cap, mask (:466-514);
+    * per split (bounds of `split_bounds`, :383-396), an online softmax over tiles of `block_n`
+      tokens from the split start with natural `exp` against the running max (:553-560), P rounded
+      to bf16 before `P.V` while the sum uses the unrounded P (:557-559);
+    * the stage-2 LSE merge in fp32 (:1097-1132).
+
+    The running-max rescale `acc * exp(m_old - m_new)` is applied here in closed form: tile t's
+    `P.V` is weighted by `exp(m_t - m_last)`, which is the product of the rescale factors after it.
+    Returns (o float32 before the output cast, lse), like `mla_decode`; with `partials`, the split
+    partials in the workspace format of `mla_decode_partials` instead.
+    """
+    R, H, dcg = q_lat.shape
+    assert dcg * groups == d_c
+    n_rms = rms_heads if rms_heads is not None else H
+    hpg = H // groups
+    o = torch.zeros(R, H, dcg)
+    lse = torch.full((R, H), -math.inf)
+    att = torch.full((R, H, num_splits, dcg + 1), math.nan) if partials else None
+    for i in range(R):
+        L = int(seq_lens[i])
+        if L <= 0:
+            continue
+        rows = gather_rows(cache_u8, block_table, i, L, page_size)
+        c, r = dequant_rows(rows, d_c=d_c, rope_w=rope_w, kv=kv, k_scale=k_scale)
+        if kv == KV_FP8:
+            c, r = _bf16_t(c), _bf16_t(r)
+        rms = decode_rms(rows, rms_offset=rms_offset, n_heads=n_rms, kv=kv, mode=rms_mode, k_scale=k_scale)
+        live = [(si, a, e) for si, (a, e) in enumerate(split_bounds(L, num_splits, align)) if e > a]
+        for g in range(groups):
+            hs = slice(g * hpg, (g + 1) * hpg)
+            cg = c[:, g * dcg:(g + 1) * dcg]
+            s = _scores(_bf16_t(q_lat[i, hs].float()), None if q_pe is None else _bf16_t(q_pe[i, hs].float()), cg, r,
+                        rms[:, hs], sm_scale, logit_cap)                        # [hpg, L]
+            parts_o, parts_l = [], []
+            for si, a, e in live:
+                ss = s[:, a:e]
+                n = e - a
+                nt = -(-n // block_n)
+                pad = torch.full((ss.shape[0], nt * block_n), -math.inf)
+                pad[:, :n] = ss
+                tmax = pad.view(ss.shape[0], nt, block_n).max(-1).values        # [hpg, nt]
+                mrun = torch.cummax(tmax, dim=-1).values
+                mtok = mrun.repeat_interleave(block_n, dim=-1)[:, :n]
+                p = torch.exp(ss - mtok)
+                w = torch.exp(mtok - mrun[:, -1:])
+                acc = (w * _bf16_t(p)) @ cg[a:e]
+                esum = (w * p).sum(-1, keepdim=True)
+                parts_o.append(acc / esum)
+                parts_l.append(mrun[:, -1] + torch.log(esum.squeeze(-1)))
+                if partials:
+                    att[i, hs, si, :dcg] = parts_o[-1]
+                    att[i, hs, si, dcg] = parts_l[-1]
+            ls = torch.stack(parts_l, -1)                                       # [hpg, S']
+            m = ls.max(-1, keepdim=True).values
+            wt = torch.exp(ls - m)
+            o[i, hs] = (wt[..., None] * torch.stack(parts_o, 1)).sum(1) / wt.sum(-1, keepdim=True)
+            lse[i, hs] = (m + torch.log(wt.sum(-1, keepdim=True))).squeeze(-1)
+    return att if partials else (o, lse)
+
+
 def split_bounds(L: int, num_splits: int, align: int) -> list[tuple[int, int]]:
     """[start, end) of each split: per = ceil(ceil(L/S)/align)*align when align > 0, else
     ceil(L/S); empty splits have end <= start (ops/mla_decode_attention.py:389-396, :1101-1108)."""

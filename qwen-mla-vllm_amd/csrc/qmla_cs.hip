@@ -164,7 +164,8 @@ __device__ __forceinline__ void segment(const KParams& p, Smem<C>& sm, int req, 
   const int row0 = req * p.qrows;
   const int P = p.page_size;
   const int64_t TS = p.token_stride_b, PS = p.page_stride_b;
-  const int* btrow = p.bt + (int64_t)row0 * p.bt_stride;
+  // a folded request reads the block-table row of its last verify row, as its length does
+  const int* btrow = p.bt + (int64_t)(row0 + p.qrows - 1) * p.bt_stride;
   const float csc = p.sm_scale * kLog2e * kscale;
   const float cap2 = p.logit_cap * kLog2e;
 
@@ -557,25 +558,37 @@ __device__ __forceinline__ void segment(const KParams& p, Smem<C>& sm, int req, 
           }
         tmax[mb] = max_lg(m);
       }
-      // lazy reference max: it moves only when a tile max exceeds it by more than 8 (P <= 2^8)
-      bool need = false;
+      // reference max: it moves when a tile max exceeds it by more than ref_shift(the row's running
+      // sum), so a dominant token gets P = 1 exactly as under the reference's running max
+      // (ops/mla_decode_attention.py:553-560) and rounding P to bf16 before P.V costs no more
+      // than it does there; P <= 2^8
+      bool cand = false;
 #pragma unroll
-      for (int mb = 0; mb < C::MB; ++mb) need |= tmax[mb] > mref[mb] + 8.0f;
-      if (__builtin_amdgcn_ballot_w64(need)) {
+      for (int mb = 0; mb < C::MB; ++mb) cand |= tmax[mb] > mref[mb];
+      if (__builtin_amdgcn_ballot_w64(cand)) {
+        float shift[C::MB];
+        bool need = false;
 #pragma unroll
         for (int mb = 0; mb < C::MB; ++mb) {
-          const float mn = tmax[mb] > mref[mb] + 8.0f ? tmax[mb] : mref[mb];
-          const float alpha = mref[mb] == kNegInf ? 0.f : fast_exp2(mref[mb] - mn);
-          lpart[mb] *= alpha;
-          mref[mb] = mn;
-          // accumulator rows 4*lg + i live in lanes 4*lg + i of the score layout
-          float al[4];
+          shift[mb] = ref_shift(sum_lg(lpart[mb]), 8.0f);
+          need |= tmax[mb] > mref[mb] + shift[mb];
+        }
+        if (__builtin_amdgcn_ballot_w64(need)) {
 #pragma unroll
-          for (int i = 0; i < 4; ++i) al[i] = __shfl(alpha, 4 * lg + i);
+          for (int mb = 0; mb < C::MB; ++mb) {
+            const float mn = tmax[mb] > mref[mb] + shift[mb] ? tmax[mb] : mref[mb];
+            const float alpha = mref[mb] == kNegInf ? 0.f : fast_exp2(mref[mb] - mn);
+            lpart[mb] *= alpha;
+            mref[mb] = mn;
+            // accumulator rows 4*lg + i live in lanes 4*lg + i of the score layout
+            float al[4];
 #pragma unroll
-          for (int cb = 0; cb < C::CB; ++cb)
+            for (int i = 0; i < 4; ++i) al[i] = __shfl(alpha, 4 * lg + i);
 #pragma unroll
-            for (int i = 0; i < 4; ++i) acc[mb][cb][i] *= al[i];
+            for (int cb = 0; cb < C::CB; ++cb)
+#pragma unroll
+              for (int i = 0; i < 4; ++i) acc[mb][cb][i] *= al[i];
+          }
         }
       }
 

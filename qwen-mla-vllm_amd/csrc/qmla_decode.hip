@@ -430,9 +430,12 @@ __device__ __forceinline__ void process_segment(const KParams& p, Smem<C>& sm, i
     for (int mbl = 0; mbl < C::MBW; ++mbl) lmax[mbl] = max_lg(lmax[mbl]);
 
     // ---- optimistic softmax: P = exp2(s - mref) with the reference max of earlier tiles. A row
-    //      whose tile max exceeds its reference by more than 8 (P > 256) or that had no reference
-    //      yet raises the flag; then every wave rebuilds its P block against the new reference
-    //      (a second exchange) and the accumulator is rescaled. ----
+    //      whose tile max exceeds it by more than ref_shift(its running sum) (or that had no max
+    //      yet) raises the flag; then every wave rebuilds its P block against the rows' new maxima
+    //      (a second exchange) and the accumulator is rescaled. A dominant token thus gets P = 1
+    //      exactly, as the running max of the reference's online softmax gives it
+    //      (ops/mla_decode_attention.py:553-560), and the bf16 rounding of P before P.V costs no
+    //      more than it does there. ----
     float psum[C::MBW];
     auto write_p = [&]() {
 #pragma unroll
@@ -458,7 +461,7 @@ __device__ __forceinline__ void process_segment(const KParams& p, Smem<C>& sm, i
     };
     bool need = false;
 #pragma unroll
-    for (int mbl = 0; mbl < C::MBW; ++mbl) need |= lmax[mbl] > mref[mbl] + 8.0f;
+    for (int mbl = 0; mbl < C::MBW; ++mbl) need |= lmax[mbl] > mref[mbl] + ref_shift(l_run[mbl], 8.0f);
     const bool need_w = __builtin_amdgcn_ballot_w64(need) != 0;
     if (!need_w) write_p();
     if (lg == 0) {
@@ -1094,6 +1097,22 @@ static int check_balanced_ws(const qmla_decode_params* p) {
   return QMLA_OK;
 }
 
+// Fixed splits: attn_logits [rows, heads, S, dv + 1] fp32 at the caller's strides. The buffer must
+// hold the dense layout's bytes and the largest partial offset, (rows-1)*sr + (heads-1)*sh +
+// (S-1)*ss + dv, with positive strides; one split needs no workspace.
+static int check_fixed_ws(const qmla_decode_params* p) {
+  if (p->num_splits <= 1) return QMLA_OK;
+  if (!p->workspace) return QMLA_ERR_WORKSPACE;
+  if (p->workspace_bytes < qmla_workspace_bytes(p)) return QMLA_ERR_WORKSPACE;
+  if (p->ws_stride_row <= 0 || p->ws_stride_head <= 0 || p->ws_stride_split <= 0) return QMLA_ERR_WORKSPACE;
+  if ((uintptr_t)p->workspace % 4) return QMLA_ERR_ALIGN;
+  const int64_t dv = p->d_c / p->groups;
+  const int64_t last = (int64_t)(p->rows - 1) * p->ws_stride_row + (int64_t)(p->heads - 1) * p->ws_stride_head +
+                       (int64_t)(p->num_splits - 1) * p->ws_stride_split + dv;
+  if (p->rows > 0 && (last + 1) * 4 > (int64_t)p->workspace_bytes) return QMLA_ERR_WORKSPACE;
+  return QMLA_OK;
+}
+
 int qmla_plan(const qmla_decode_params* p, void* stream) {
   int rc = validate(p);
   if (rc) return rc;
@@ -1112,11 +1131,8 @@ int qmla_decode_partial(const qmla_decode_params* p, void* stream) {
   const int wi = si >= 0 ? -1 : cs_select(p);
   const Inst* in = (si >= 0 || wi >= 0) ? nullptr : find_inst(p);
   if (!in && wi < 0 && si < 0) return QMLA_ERR_NOKERNEL;
-  if (p->num_splits > 1 && !p->workspace) return QMLA_ERR_WORKSPACE;
-  if (p->num_splits == 0) {
-    rc = check_balanced_ws(p);
-    if (rc) return rc;
-  }
+  rc = p->num_splits == 0 ? check_balanced_ws(p) : check_fixed_ws(p);
+  if (rc) return rc;
   KParams k = make_kparams(p);
   hipStream_t st = (hipStream_t)stream;
   rc = si >= 0 ? ws_launch(si, p, k, k.nwg, st) : in ? run_partial(p, in, k, st) : cs_launch(wi, p, k, k.nwg, st);
@@ -1130,11 +1146,8 @@ int qmla_combine(const qmla_decode_params* p, void* stream) {
   if (rc) return rc;
   if (p->num_splits == 1) return QMLA_OK;
   if (p->d_c / p->groups > 2048) return QMLA_ERR_SHAPE;
-  if (p->num_splits > 1 && !p->workspace) return QMLA_ERR_WORKSPACE;
-  if (p->num_splits == 0) {
-    rc = check_balanced_ws(p);
-    if (rc) return rc;
-  }
+  rc = p->num_splits == 0 ? check_balanced_ws(p) : check_fixed_ws(p);
+  if (rc) return rc;
   KParams k = make_kparams(p);
   return run_combine(p, k, (hipStream_t)stream);
 }
@@ -1149,7 +1162,8 @@ int qmla_decode(const qmla_decode_params* p, void* stream) {
   if (!in && wi < 0 && si < 0) return QMLA_ERR_NOKERNEL;
   hipStream_t st = (hipStream_t)stream;
   if (p->num_splits > 0) {
-    if (p->num_splits > 1 && !p->workspace) return QMLA_ERR_WORKSPACE;
+    rc = check_fixed_ws(p);
+    if (rc) return rc;
     KParams k = make_kparams(p);
     rc = si >= 0 ? ws_launch(si, p, k, 0, st) : in ? run_partial(p, in, k, st) : cs_launch(wi, p, k, 0, st);
     if (rc) return rc;

@@ -24,6 +24,9 @@ typedef __attribute__((__vector_size__(2 * sizeof(int)))) int i32x2;
 typedef __attribute__((__vector_size__(4 * sizeof(int)))) int i32x4;
 typedef __attribute__((__vector_size__(8 * sizeof(int)))) int i32x8;
 typedef __attribute__((__vector_size__(4 * sizeof(short)))) short i16x4;
+typedef __attribute__((__vector_size__(8 * sizeof(_Float16)))) _Float16 f16x8;
+typedef __attribute__((__vector_size__(4 * sizeof(_Float16)))) _Float16 f16x4;
+typedef __attribute__((__vector_size__(2 * sizeof(_Float16)))) _Float16 f16x2;
 
 #define QMLA_LDS(T, p) ((__attribute__((address_space(3))) T*)(p))
 
@@ -33,6 +36,21 @@ constexpr float kNegInf = -__builtin_huge_valf();
 
 __device__ __forceinline__ f32x4 mfma16(const bf16x8& a, const bf16x8& b, const f32x4& c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+}
+
+__device__ __forceinline__ f32x4 mfma16(const f16x8& a, const f16x8& b, const f32x4& c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+}
+
+// 8 fp8 bytes -> f16x8, exact (every e4m3fn value is an fp16 value)
+__device__ __forceinline__ f16x8 fp8x8_to_f16(const i32x2& raw) {
+  f16x8 r;
+  f16x2 t;
+  t = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(raw[0], 1.0f, false); r[0] = t[0]; r[1] = t[1];
+  t = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(raw[0], 1.0f, true);  r[2] = t[0]; r[3] = t[1];
+  t = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(raw[1], 1.0f, false); r[4] = t[0]; r[5] = t[1];
+  t = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(raw[1], 1.0f, true);  r[6] = t[0]; r[7] = t[1];
+  return r;
 }
 
 // 16 fp8 e4m3fn bytes -> two bf16x8 (bytes 0-7, bytes 8-15), exact (scale 1.0 is a no-op).
@@ -168,5 +186,17 @@ __device__ __forceinline__ void lds_barrier() {
 
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 __device__ __forceinline__ float fast_log2(float x) { return __builtin_amdgcn_logf(x); }
+
+// How far a row's tile maximum may exceed its softmax reference before the reference moves, given
+// the row's running sum l (relative to the reference). A token that does not move it has
+// P <= 2^shift <= l / 32, so it holds at most 1/33 of the row's mass and the rounding of its P to
+// 16 bits before P.V moves the output by at most 1/33 of that rounding; a token above that share
+// moves the reference to itself and gets P = 1 exactly, as the running max of the reference's
+// online softmax does (qwen_mla/ops/mla_decode_attention.py:553-560). While a row has little mass
+// (its first tokens, a peaked softmax) the shift is 0, i.e. an exact running max; it grows to
+// `cap` as the mass accumulates, so the reference rarely moves in long rows.
+__device__ __forceinline__ float ref_shift(float l, float cap) {
+  return fminf(cap, fmaxf(0.f, fast_log2(l) - 5.0f));
+}
 
 }  // namespace qmla

@@ -12,12 +12,14 @@
 // Its 8 waves take two roles, one of each on every SIMD:
 //   score waves (0-3):  wave (tb, mb) scores 16 tokens x 16 rows over all 576 columns of a tile
 //                       (S^T = K . Q^T on MFMA, query fragments resident in VGPRs), divides by the
-//                       rms, applies the mask and the softmax shift, and writes P (bf16) into LDS.
+//                       rms, applies the mask and the softmax shift, and writes P into LDS (fp16
+//                       for fp8 rows, bf16 for bf16 rows).
 //                       With an fp8 cache the K bytes enter the MFMA as stored: the query is split
 //                       into two e4m3 parts (hi + lo, 8 significant bits, as bf16), the latent runs
 //                       on the 16x16x128 fp8 MFMA and the rope on the 16x16x32 one;
 //   value waves (4-7):  wave v accumulates P . V over latent columns [128v, 128v+128) for all rows,
-//                       two tiles behind the score waves, with V^T fragments from ds_read_b64_tr_b8,
+//                       two tiles behind the score waves, with V^T fragments from ds_read_b64_tr_b8
+//                       converted exactly to fp16 (fp8 rows; the MFMA is the fp16 one),
 //                       writes a request's output when its last tile is in, and streams the tiles
 //                       global -> LDS by LDS-DMA, A tiles ahead of the score waves, into a ring of
 //                       A+3 stages (each value wave waits only for its own loads).
@@ -50,7 +52,7 @@ namespace ws {
 constexpr int TILE = 32;          // tokens per tile
 constexpr int NSEG = 64;          // pieces per window (one per lane of the wave that plans it)
 constexpr int PIDN = 1024;        // page ids per window
-constexpr float SHIFT = 16.0f;    // P <= 2^16 before the reference max moves
+constexpr float SHIFT = 15.0f;    // P <= 2^15 before the reference max moves (fp16 P stays finite)
 enum Role { SCORE, VALUE };
 enum { SEG_FIRST = 1, SEG_LAST = 2, SEG_FINAL = 4 };
 
@@ -174,6 +176,12 @@ struct WS {
   static constexpr int NKR = KP * EB;                 // K reads of a score step
   static constexpr int NVR = CB * EB;                 // V reads of a value step
   static constexpr int PST = TILE * 2 + 16;           // P row stride in LDS (bytes)
+  // P.V operands: fp8 rows run it in fp16 (every e4m3 value is exact in fp16, and P keeps 11
+  // significant bits instead of bf16's 8, so its rounding before P.V is 8x smaller than the
+  // reference's bf16 P); bf16 rows in bf16
+  using PT = std::conditional_t<EB == 1, _Float16, __bf16>;
+  using PX4 = std::conditional_t<EB == 1, f16x4, bf16x4>;
+  using PX8 = std::conditional_t<EB == 1, f16x8, bf16x8>;
   static_assert(DCG % 64 == 0 && CPR * 16 >= (DC + 64) * EB, "row slice");
   static_assert(G == 1 || (G == 2 && EB == 1 && !RTR), "latent groups: fp8 rows, rms codes read per row");
   static_assert(A >= 2 && A * DPW < 64, "lookahead / vmcnt range");
@@ -190,7 +198,7 @@ struct SegD {
 template <class C>
 struct Smem {
   char kv[C::S][C::STAGE];
-  alignas(16) char p[3][C::ROWS][C::PST];   // P (bf16) of tiles g % 3
+  alignas(16) char p[3][C::ROWS][C::PST];   // P (C::PT) of tiles g % 3
   alignas(16) int flag[3][C::G][4];         // [g % 3][group][row block of the group]: reference moved at tile g
   alignas(16) float tmax[2][2][C::ROWS];    // [g & 1][token block][row] tile max
   alignas(16) float alpha[3][C::ROWS];      // [g % 3][row] accumulator rescale at tile g
@@ -522,7 +530,9 @@ __device__ __forceinline__ void role_main(const KParams& p, Smem<C>& sm, float k
   };
 
   // score step helpers: reference check of the previous tile and its publication
-  auto fix_decide = [&](int m, float tpart, bool& rare, float& alpha_f, bf16x4& pk_fix) {
+  using PX4 = typename C::PX4;
+  using PT = typename C::PT;
+  auto fix_decide = [&](int m, float tpart, bool& rare, float& alpha_f, PX4& pk_fix) {
     const float gm = fmaxf(tmp[m], tpart);
     const bool ch = gm > mref[m] + SHIFT;
     rare = __builtin_amdgcn_ballot_w64(ch) != 0;
@@ -539,14 +549,14 @@ __device__ __forceinline__ void role_main(const KParams& p, Smem<C>& sm, float k
     for (int i = 0; i < 4; ++i) {
       const float e = fast_exp2(scp[m][i] - mu);
       ps2 += e;
-      pk_fix[i] = (__bf16)e;
+      pk_fix[i] = (PT)e;
     }
     lpart[m] = lpart[m] * alpha_f + ps2;
   };
-  auto fix_publish = [&](int m, int g, bool rare, float alpha_f, const bf16x4& pk_fix) {
+  auto fix_publish = [&](int m, int g, bool rare, float alpha_f, const PX4& pk_fix) {
     const int pt = g % 3;
     if (rare) {
-      *reinterpret_cast<bf16x4*>(&sm.p[pt][r[m]][(16 * tb + 4 * lg) * 2]) = pk_fix;
+      *reinterpret_cast<PX4*>(&sm.p[pt][r[m]][(16 * tb + 4 * lg) * 2]) = pk_fix;
       if (tb == 0 && lg == 0) sm.alpha[pt][r[m]] = alpha_f;
     }
     if (tb == 0 && lane == 0) sm.flag[pt][sg][su * C::MBG + m - sg * C::MBV] = rare ? 1 : 0;
@@ -621,7 +631,8 @@ __device__ __forceinline__ void role_main(const KParams& p, Smem<C>& sm, float k
         else k1 = mid - 1;
       }
       const SegD& d = sm.seg[k0];
-      sm.pid[f] = p.bt[(int64_t)d.req * qrows * p.bt_stride + d.ta / P + (f - d.pf)];
+      // a folded request reads the block-table row of its last verify row, as its length does
+      sm.pid[f] = p.bt[((int64_t)d.req * qrows + qrows - 1) * p.bt_stride + d.ta / P + (f - d.pf)];
     }
     __syncthreads();
 
@@ -783,7 +794,7 @@ __device__ __forceinline__ void role_main(const KParams& p, Smem<C>& sm, float k
           for (int m = 0; m < C::MBG; ++m) lds_wait_n<cmin15(C::MBG * C::NCODE + C::NKR)>(tpart[m]);
           bool rare[C::MBG];
           float alpha_f[C::MBG];
-          bf16x4 pk_fix[C::MBG];
+          PX4 pk_fix[C::MBG];
 #pragma unroll
           for (int m = 0; m < C::MBG; ++m) {
             rare[m] = false;
@@ -922,15 +933,15 @@ __device__ __forceinline__ void role_main(const KParams& p, Smem<C>& sm, float k
             tm = max_lg(tm);
             // ---- optimistic P against the current reference ----
             const float mu = mref[m] == kNegInf ? 0.f : mref[m];
-            bf16x4 pk;
+            PX4 pk;
             float ps = 0.f;
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
               const float e = fast_exp2(sc[m][i] - mu);
               ps += e;
-              pk[i] = (__bf16)e;
+              pk[i] = (PT)e;
             }
-            *reinterpret_cast<bf16x4*>(&sm.p[g % 3][r[m]][(16 * tb + 4 * lg) * 2]) = pk;
+            *reinterpret_cast<PX4*>(&sm.p[g % 3][r[m]][(16 * tb + 4 * lg) * 2]) = pk;
             if (lg == 0) sm.tmax[g & 1][tb][r[m]] = tm;
             if (g >= 1) fix_publish(m, g - 1, rare[m], alpha_f[m], pk_fix[m]);
             scp[m] = sc[m];
@@ -952,7 +963,7 @@ __device__ __forceinline__ void role_main(const KParams& p, Smem<C>& sm, float k
             lds_wait_n<0>(tpart[m]);
             bool rare = false;
             float alpha_f = 1.0f;
-            bf16x4 pk_fix;
+            PX4 pk_fix;
             fix_decide(m, tpart[m], rare, alpha_f, pk_fix);
             fix_publish(m, g - 1, rare, alpha_f, pk_fix);
           }
@@ -1031,23 +1042,24 @@ __device__ __forceinline__ void role_main(const KParams& p, Smem<C>& sm, float k
                 for (int cb = 0; cb < C::CB; ++cb) acc[mb][cb][i] *= al[i];
             }
           }
-          bf16x8 pf[C::MBV];
+          using PX8 = typename C::PX8;
+          PX8 pf[C::MBV];
 #pragma unroll
           for (int mb = 0; mb < C::MBV; ++mb) {
             lds_wait_n<cmin15(C::NVR)>(pr[mb]);
-            pf[mb] = __builtin_bit_cast(bf16x8, pr[mb]);
+            pf[mb] = __builtin_bit_cast(PX8, pr[mb]);
           }
           static_for<0, C::CB>([&](auto cc) {
             constexpr int cb = decltype(cc)::value;
-            bf16x8 vf;
+            PX8 vf;
             if constexpr (C::EB == 1) {
               lds_wait_n<cmin15(C::CB - 1 - cb)>(vraw[cb][0]);
-              vf = fp8x8_to_bf16(vraw[cb][0]);
+              vf = fp8x8_to_f16(vraw[cb][0]);
             } else {
               lds_wait_n<cmin15(2 * (C::CB - 1 - cb) + 1)>(vraw[cb][0]);
               lds_wait_n<cmin15(2 * (C::CB - 1 - cb))>(vraw[cb][1]);
               const i32x4 w4 = {vraw[cb][0][0], vraw[cb][0][1], vraw[cb][1][0], vraw[cb][1][1]};
-              vf = __builtin_bit_cast(bf16x8, w4);
+              vf = __builtin_bit_cast(PX8, w4);
             }
 #pragma unroll
             for (int mb = 0; mb < C::MBV; ++mb) acc[mb][cb] = mfma16(pf[mb], vf, acc[mb][cb]);

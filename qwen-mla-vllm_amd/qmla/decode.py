@@ -87,11 +87,33 @@ def _fold_group(qrows: int, hpg: int, max_rows: int) -> int:
     return best
 
 
+def _check_layout(*, q_nope, q_pe, kv_cache, block_table, seq_lens, out, lse) -> None:
+    """The kernels read int32 metadata with unit strides along a row (block_table) and along the
+    batch (seq_lens), and every tensor row with a unit element stride. Anything else raises here:
+    converting would allocate, which a caller inside HIP-graph capture cannot do."""
+    if block_table.dtype != torch.int32:
+        raise TypeError(f"block_table must be int32, got {block_table.dtype}")
+    if seq_lens.dtype != torch.int32:
+        raise TypeError(f"seq_lens must be int32, got {seq_lens.dtype}")
+    if seq_lens.dim() != 1 or (seq_lens.numel() > 1 and seq_lens.stride(0) != 1):
+        raise ValueError("seq_lens must be a contiguous 1-D tensor")
+    if block_table.dim() != 2 or block_table.stride(-1) != 1:
+        raise ValueError("block_table must be 2-D with a unit column stride")
+    for name, t in (("q_nope", q_nope), ("q_pe", q_pe), ("kv_cache", kv_cache), ("out", out), ("lse", lse)):
+        if t is not None and t.numel() > 0 and t.stride(-1) != 1:
+            raise ValueError(f"{name} must have a unit stride in its last dimension")
+    if q_nope.dtype != torch.bfloat16 or (q_pe is not None and q_pe.dtype != torch.bfloat16):
+        raise TypeError("queries must be bfloat16")
+
+
 def build_params(*, q_nope, q_pe, kv_cache, block_table, seq_lens, out, lse, d_c, rope_w, rms_offset,
                  rms_mode, kv, page_size, sm_scale, k_scale=None, logit_cap=0.0, qrows=1, groups=1,
                  rms_heads=None, num_splits=0, split_align=0, workspace=None, ws_strides=(0, 0, 0),
                  num_workgroups=0) -> DecodeParams:
-    """Fill the C parameter block. Pure host work (no device access), so it is testable anywhere."""
+    """Fill the C parameter block. Pure host work (no device access), so it is testable anywhere.
+    Raises TypeError / ValueError for metadata or strides the kernels cannot read as given."""
+    _check_layout(q_nope=q_nope, q_pe=q_pe if (q_pe is not None and rope_w > 0) else None, kv_cache=kv_cache,
+                  block_table=block_table, seq_lens=seq_lens, out=out, lse=lse)
     rows, heads = q_nope.shape[0], q_nope.shape[1]
     page_stride, token_stride = _cache_strides(kv_cache, page_size)
     p = DecodeParams()

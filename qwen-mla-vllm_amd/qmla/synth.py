@@ -174,3 +174,28 @@ def algorithmic_bytes(case: Case) -> int:
     lse = rows * H * 4
     pages = int(((req_len + case.page_size - 1) // case.page_size).sum())
     return toks * per_tok + q + o + lse + pages * 4 + rows * 4
+
+
+def compact_requests(case: Case, reqs):
+    """The rows of the requests `reqs` (all qrows rows of each) with only their pages, as CPU tensors:
+    (cache bytes [pages, P, row_bytes], block table remapped onto those pages, seq_lens, q_nope,
+    q_pe, row indices). The pages are gathered on the case's device first, so a multi-GB cache is
+    never copied whole."""
+    P, qr = case.page_size, case.qrows
+    bt = case.block_table.cpu()
+    sl = case.seq_lens.cpu()
+    rows = [b * qr + j for b in reqs for j in range(qr)]
+    page_ids, new_bt = [], torch.zeros(len(rows), bt.shape[1], dtype=torch.int32)
+    first = 0
+    for i, r in enumerate(rows):
+        if i % qr == 0:
+            last = (int(reqs[i // qr]) + 1) * qr - 1          # the request's last row owns its pages
+            n = max(1, -(-int(sl[last]) // P))
+            first = len(page_ids)
+            page_ids.extend(int(x) for x in bt[last, :n])
+        n_r = max(1, -(-int(sl[r]) // P))
+        new_bt[i, :n_r] = torch.arange(first, first + n_r, dtype=torch.int32)
+    idx = torch.tensor(page_ids, dtype=torch.long, device=case.cache.device)
+    cache = case.cache.index_select(0, idx).cpu().contiguous()
+    cache = cache.view(torch.uint8).reshape(cache.shape[0], P, -1)
+    return cache, new_bt, sl[rows], case.q_nope.cpu().float()[rows], case.q_pe.cpu().float()[rows], rows

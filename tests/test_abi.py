@@ -111,6 +111,26 @@ def test_error_codes(over, code):
         assert lib.qmla_combine(ctypes.byref(p), None) == code
 
 
+DENSE_WS = 8 * 24 * 4 * 513 * 4   # rows x heads x splits x (d_c + 1) floats of _valid_params
+
+
+@pytest.mark.parametrize("over", [
+    dict(workspace_bytes=DENSE_WS - 4),                        # smaller than qmla_workspace_bytes()
+    dict(workspace_bytes=DENSE_WS, ws_stride_row=24 * 4 * 513 + 64),   # last partial past the end
+    dict(workspace_bytes=DENSE_WS, ws_stride_head=4 * 513 + 1),
+    dict(ws_stride_split=0),                                   # every stride must be positive
+    dict(ws_stride_head=-513),
+    dict(ws_stride_row=0),
+])
+def test_fixed_split_workspace_checked(over):
+    """Fixed splits write attn_logits [rows, heads, S, d_c + 1] at the caller's strides: an undersized
+    buffer or bad strides are rejected by every entry point before a launch."""
+    lib = _lib.lib()
+    p = _valid_params(**over)
+    for fn in (lib.qmla_decode, lib.qmla_decode_partial, lib.qmla_combine):
+        assert fn(ctypes.byref(p), None) == _lib.ERR_WORKSPACE, fn.__name__
+
+
 def _layout(kv, d_c, rope, heads, rms, qrows=1, groups=1):
     """Parameter block for one cache layout (fake pointers). With 4 fixed splits and no workspace the
     entry returns ERR_WORKSPACE once it has an instance for the shape and ERR_NOKERNEL otherwise: the
@@ -192,6 +212,34 @@ def test_build_params_reads_real_strides():
                       d_c=512, rope_w=64, rms_offset=576, rms_mode=_lib.RMS_LOG8, kv=_lib.KV_FP8, page_size=64,
                       sm_scale=0.1)
     assert (p3.page_stride, p3.token_stride) == (64 * 608, 608) and p3.lse is None
+
+
+def _bp_args(**over):
+    q = torch.empty(6, 24, 576, dtype=torch.bfloat16)
+    a = dict(q_nope=q[..., :512], q_pe=q[..., 512:], kv_cache=torch.empty(8, 64, 1, 608, dtype=torch.uint8),
+             block_table=torch.zeros(6, 40, dtype=torch.int32), seq_lens=torch.zeros(6, dtype=torch.int32),
+             out=torch.empty(6, 24, 512, dtype=torch.bfloat16), lse=torch.empty(6, 24), d_c=512, rope_w=64,
+             rms_offset=576, rms_mode=_lib.RMS_LOG8, kv=_lib.KV_FP8, page_size=64, sm_scale=0.1)
+    a.update(over)
+    return a
+
+
+@pytest.mark.parametrize("over,exc", [
+    (dict(block_table=torch.zeros(6, 40, dtype=torch.int64)), TypeError),
+    (dict(seq_lens=torch.zeros(6, dtype=torch.int64)), TypeError),
+    (dict(seq_lens=torch.zeros(12, dtype=torch.int32)[::2]), ValueError),          # strided lengths
+    (dict(block_table=torch.zeros(40, 6, dtype=torch.int32).t()), ValueError),      # column stride 6
+    (dict(out=torch.empty(6, 512, 24, dtype=torch.bfloat16).transpose(1, 2)), ValueError),
+    (dict(lse=torch.empty(24, 6).t()), ValueError),
+    (dict(kv_cache=torch.empty(8, 64, 1, 1216, dtype=torch.uint8)[..., ::2]), ValueError),
+    (dict(q_nope=torch.empty(6, 24, 1024, dtype=torch.bfloat16)[..., ::2]), ValueError),
+    (dict(q_nope=torch.empty(6, 24, 512, dtype=torch.float16)), TypeError),
+])
+def test_build_params_rejects_unreadable_layouts(over, exc):
+    """The kernels read int32 metadata and unit-stride rows; anything else raises rather than being
+    converted (a conversion would allocate inside graph capture) or silently misread."""
+    with pytest.raises(exc):
+        build_params(**_bp_args(**over))
 
 
 def test_product_path_refuses_cpu_tensors():

@@ -15,7 +15,7 @@ import numpy as np
 import pytest
 import torch
 
-from tests.mla_cases import ora
+from tests.mla_cases import C_REF, TOL, ora
 
 pytestmark = pytest.mark.gpu
 
@@ -73,7 +73,8 @@ def test_deployed_fp8_layouts(gpu, mode, heads, rope, rank):
     err = (got - ro).abs().max().item()
     rel = err / ro.abs().max().item()
     assert err < 3e-2 and rel < 2e-2, (err, rel)
-    assert ((lse.float().cpu() - rl).abs() - 2.0 ** -7 * rl.abs()).max().item() < 1e-2   # lse is stored as bf16
+    # lse is stored as bf16: its own rounding (2^-9 relative) is allowed
+    assert ((lse.float().cpu() - rl).abs() - 2.0 ** -8 * rl.abs()).max().item() < 1e-2
     assert np.isfinite(got.numpy()).all()
 
 
@@ -112,7 +113,14 @@ def test_deployed_bf16_layouts(gpu, rank, heads, rope):
     ro, rl = ora.mla_decode(q[..., :rank].float(), q[..., rank:].float(), cu8, bt, lens, page_size=page, d_c=rank,
                             rope_w=rope, rms_offset=rank + rope, kv="bf16", rms_mode=ora.RMS_BF16,
                             sm_scale=1.0 / 256 ** 0.5, rms_heads=heads, groups=1)
+    eo, _ = ora.mla_decode_reference_rounding(q[..., :rank].float(), q[..., rank:].float(), cu8, bt, lens,
+                                              page_size=page, d_c=rank, rope_w=rope, rms_offset=rank + rope, kv="bf16",
+                                              rms_mode=ora.RMS_BF16, sm_scale=1.0 / 256 ** 0.5, rms_heads=heads,
+                                              num_splits=64, align=16)
     got = o.float().cpu()
-    err = ((got - ro).abs() - 2.0 ** -7 * ro.abs()).max().item()   # bf16 output rounding allowed
-    assert err < 1e-2, err
-    assert ((lse.float().cpu() - rl).abs() - 2.0 ** -7 * rl.abs()).max().item() < 1e-2
+    err = (got - ro).abs().max().item()
+    ref_err = (eo.to(torch.bfloat16).float() - ro).abs().max().item()
+    print(f"[bf16 rank {rank} heads {heads} rope {rope}] max-abs {err:.3e} (reference roundings {ref_err:.3e})")
+    assert err < max(TOL["bf16"], C_REF * ref_err), err
+    # lse is stored as bf16: its own rounding (2^-9 relative) is allowed
+    assert ((lse.float().cpu() - rl).abs() - 2.0 ** -8 * rl.abs()).max().item() < 1e-2

@@ -2,20 +2,20 @@
 family (kernel family, cache format, rms format, latent rank, heads, rope width, logit cap), page
 size, batch, ragged lengths (empty requests included), verify tokens, split mode and the output
 element type (bf16, fp16 or fp32; outputs start as NaN) from its seed, so combinations no targeted
-test picks are covered too. Tolerances as in tests/test_gpu_decode.py (max-abs 1e-2 bf16 / 3e-2
-fp8 beyond the output's own bf16 rounding; lse 1e-2 beyond an fp16 lse's rounding, -inf exactly
-where a row sees no token).
+test picks are covered too. Bound: plain max-abs 1e-2 (bf16 cache) / 3e-2 (fp8 cache) against the
+float32 oracle, or, where the reference kernel's own roundings already exceed that on the same
+inputs, C_REF times their error; lse within 1e-2 (beyond an fp16 lse's rounding), -inf exactly
+where a row sees no token.
 """
 import random
 
 import pytest
 import torch
 
-from tests.mla_cases import make_case, run_oracle
+from tests.mla_cases import C_REF, TOL, make_case, run_oracle
 
 pytestmark = pytest.mark.gpu
 
-REL = 2.0 ** -7
 # (kv, rms mode, d_c, heads, rope width, verify tokens allowed, groups, logit cap)
 FAMILIES = [
     ("fp8", "log8", 512, 24, 64, (1,), 1, 0.0),            # warp-specialized, transposed rms reads
@@ -55,8 +55,10 @@ def _draw(seed):
                 lens=lens, splits=splits, nwg=nwg, odt=odt)
 
 
-@pytest.mark.parametrize("seed", range(200))
-def test_sweep(gpu, seed):
+def run_case(gpu, seed):
+    """Run sweep case `seed` on the GPU; returns its plain errors against the float32 oracle and the
+    error of the reference's own roundings (the oracle's emulation, output rounded to the same
+    element type) on the same inputs."""
     import qmla
     a = _draw(seed)
     print(f"[sweep {seed}] {a}", flush=True)
@@ -75,13 +77,25 @@ def test_sweep(gpu, seed):
                           num_workgroups=a["nwg"], logit_cap=a["cap"], out=o, lse=lse, **kw)
     torch.cuda.synchronize()
     ro, rl = run_oracle(c, logit_cap=a["cap"])
-    tol = 3e-2 if a["kv"] == "fp8" else 1e-2
-    d = (o.float().cpu() - ro).abs()
-    excess = (d - REL * ro.abs()).max().item()
+    eo, _ = run_oracle(c, logit_cap=a["cap"], reference_rounding=True, num_splits=max(a["splits"], 1),
+                       align=16 if a["page"] % 16 == 0 else 0)
     lg = lse.float().cpu()
     empty = torch.isneginf(rl)
-    assert torch.equal(torch.isneginf(lg), empty), "rows without tokens differ"
     lrel = 2.0 ** -11 if lse.dtype == torch.float16 else 0.0
     lerr = ((lg[~empty] - rl[~empty]).abs() - lrel * rl[~empty].abs()).max().item() if (~empty).any() else 0.0
-    print(f"   max-abs {d.max().item():.3e} beyond rounding {excess:.3e} (tol {tol}) lse {lerr:.3e}", flush=True)
-    assert excess < tol and lerr < 1e-2
+    return dict(kv=a["kv"], err=(o.float().cpu() - ro).abs().max().item(),
+                ref_err=(eo.to(dt).float() - ro).abs().max().item(), lerr=lerr,
+                empty_ok=torch.equal(torch.isneginf(lg), empty))
+
+
+# 1231: bf16 d_c 1792, one split, lengths [2102, 205, 2] on 784-token pages, inputs x2 -- the one
+# case of an earlier 2,800-seed sweep whose plain error (3.2e-2) exceeded the bound of its time
+@pytest.mark.parametrize("seed", list(range(200)) + [1231])
+def test_sweep(gpu, seed):
+    r = run_case(gpu, seed)
+    tol = TOL[r["kv"]]
+    bound = max(tol, C_REF * r["ref_err"])
+    print(f"   max-abs {r['err']:.3e} (tol {tol}, reference roundings {r['ref_err']:.3e}, bound {bound:.3e}) "
+          f"lse {r['lerr']:.3e}", flush=True)
+    assert r["empty_ok"], "rows without tokens differ"
+    assert r["err"] < bound and r["lerr"] < 1e-2
