@@ -152,6 +152,18 @@ size_t qmla_workspace_bytes(const qmla_decode_params* p);
  * combine runs, a small pass writes the rows of requests of length 0). */
 int qmla_decode(const qmla_decode_params* p, void* stream);
 
+/* qmla_decode without a caller workspace, for callers that cannot allocate device memory (code
+ * under HIP-graph capture, tight serving loops, harnesses that forbid it). No counterpart in the
+ * reference. The split-K scratch (balanced partials, or the fixed-split partials, which are then kept
+ * dense and p->ws_stride_* are ignored) lives in a library-owned device array of
+ * QMLA_STATIC_SCRATCH_BYTES per GPU, held until the process ends; p->workspace and
+ * p->workspace_bytes are ignored. Returns QMLA_ERR_WORKSPACE when qmla_workspace_bytes() of the call
+ * exceeds that size (the headline B = 128 decode needs about 19 MB). Allocates nothing. Every call on
+ * a GPU shares that GPU's array: calls that overlap on one GPU (two streams, two host threads) race;
+ * order them on one stream. Nothing in the array needs to start at zero. */
+#define QMLA_STATIC_SCRATCH_BYTES (64 << 20)
+int qmla_decode_static(const qmla_decode_params* p, void* stream);
+
 /* The stages of qmla_decode, callable one by one on the same stream and params:
  *   qmla_plan            balanced mode only: per-request tile counts and prefix sums into the
  *                        workspace (one small workgroup; no host involvement)

@@ -26,6 +26,8 @@
 #include <stdint.h>
 #include <string.h>
 
+#include <mutex>
+
 #include "qmla.h"
 #include "qmla_common.h"
 #include "qmla_device.h"
@@ -1150,6 +1152,52 @@ int qmla_combine(const qmla_decode_params* p, void* stream) {
   if (rc) return rc;
   KParams k = make_kparams(p);
   return run_combine(p, k, (hipStream_t)stream);
+}
+
+// ---- the decode without a caller workspace ------------------------------------------------------
+// Library-owned scratch for qmla_decode_static: one array per GPU (each device the library runs on
+// holds its own copy until the process ends). Host code never uses the array's name as an address:
+// its device address is fetched once per device with hipGetSymbolAddress and kept below.
+static __device__ __align__(256) char scratch[QMLA_STATIC_SCRATCH_BYTES];
+static void* g_scratch_ptr[64];
+static std::mutex g_scratch_mu;
+
+// Device address of this device's scratch (the current device), or nullptr on failure.
+static void* scratch_ptr() {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return nullptr;
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void* ptr = nullptr;
+    if (hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch)) != hipSuccess || !ptr) return nullptr;
+    g_scratch_ptr[dev] = ptr;
+  }
+  return g_scratch_ptr[dev];
+}
+
+int qmla_decode_static(const qmla_decode_params* p, void* stream) {
+  int rc = validate(p);
+  if (rc) return rc;
+  qmla_decode_params q = *p;
+  const int64_t dv = p->d_c / p->groups;
+  if (q.num_splits > 1) {
+    // the reference-layout partials, dense [rows, heads, S, dv + 1], in the scratch
+    q.ws_stride_split = dv + 1;
+    q.ws_stride_head = (int64_t)q.num_splits * (dv + 1);
+    q.ws_stride_row = (int64_t)q.heads * q.ws_stride_head;
+  }
+  const size_t need = qmla_workspace_bytes(&q);
+  if (need > (size_t)QMLA_STATIC_SCRATCH_BYTES) return QMLA_ERR_WORKSPACE;
+  if (need > 0) {
+    void* ptr = scratch_ptr();
+    if (!ptr) return QMLA_ERR_LAUNCH;
+    q.workspace = reinterpret_cast<float*>(ptr);
+    q.workspace_bytes = (size_t)QMLA_STATIC_SCRATCH_BYTES;
+  } else {
+    q.workspace = nullptr;
+    q.workspace_bytes = 0;
+  }
+  return qmla_decode(&q, stream);
 }
 
 int qmla_decode(const qmla_decode_params* p, void* stream) {

@@ -32,6 +32,7 @@ ERR_NAMES = {
 KV_BF16, KV_FP8 = 0, 1
 RMS_NONE, RMS_BF16, RMS_LOG8, RMS_BF16_BYTES, RMS_E4M3 = 0, 1, 2, 3, 4
 DT_BF16, DT_F32, DT_F16 = 0, 1, 2
+STATIC_SCRATCH_BYTES = 64 << 20   # QMLA_STATIC_SCRATCH_BYTES
 
 
 class DecodeParams(ctypes.Structure):
@@ -185,6 +186,7 @@ SIGNATURES = {
     "qmla_build_info": (ctypes.c_char_p, []),
     "qmla_workspace_bytes": (ctypes.c_size_t, [_P]),
     "qmla_decode": (ctypes.c_int, [_P, ctypes.c_void_p]),
+    "qmla_decode_static": (ctypes.c_int, [_P, ctypes.c_void_p]),
     "qmla_plan": (ctypes.c_int, [_P, ctypes.c_void_p]),
     "qmla_decode_partial": (ctypes.c_int, [_P, ctypes.c_void_p]),
     "qmla_combine": (ctypes.c_int, [_P, ctypes.c_void_p]),
