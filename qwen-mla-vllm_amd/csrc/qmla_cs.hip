@@ -815,6 +815,14 @@ static const Inst kInst[] = {
     // per-group kernel's fragments for 24 heads exceed the register file
     QMLA_CS(2, QMLA_RMS_BF16, 768, 1, 8, 1, 1, 2, 4, 3, false, false, 256),
     QMLA_CS(2, QMLA_RMS_BF16, 768, 1, 8, 1, 1, 1, 4, 2, false, false, 256),   // 12 heads, rope 256
+    // bf16 cache, rank 1792 with the plugin's partial-rope and full-rope-256 layouts
+    // (tests/test_two_pass_1792.py:12-19 on the rows of tests/test_fi_partial_rope.py:27-31): rope 232
+    // or 256 (window 256) and rope 116 (window 128, rms tail at 8 mod 16 bytes); 16 query rows per
+    // workgroup (32 rows with the 256-column window spill 72 registers), so 24 heads take two
+    // workgroups per token range; two stages of 16 tokens
+    QMLA_CS(2, QMLA_RMS_BF16, 1792, 1, 8, 1, 1, 1, 2, 3, false, false, 256),
+    QMLA_CS(2, QMLA_RMS_BF16, 1792, 1, 8, 1, 1, 1, 2, 2, false, false, 256),   // 12 heads: 32-byte tail
+    QMLA_CS(2, QMLA_RMS_BF16, 1792, 1, 8, 1, 1, 1, 2, 2, false, false, 128),
     // fp8 cache, d_c 1792: 32-token tiles, 16 rows per workgroup (32 rows of 1792 accumulator and
     // query columns exceed the register file), more heads split over gridDim.z.
     // Rope 64, log8 codes (transposed rms reads: 2 chunks cover the heads of two row blocks):
@@ -838,11 +846,14 @@ static int row_splits(const Inst& in, const qmla_decode_params* p) {
 
 }  // namespace cs
 
+// The instance that serves these params with the fewest workgroups per token range, then the
+// fewest row blocks (no idle rows), or -1.
 int cs_select(const qmla_decode_params* p) {
   const int eb = p->kv_dtype == QMLA_KV_FP8 ? 1 : 2;
   const int dcg = p->d_c / p->groups;
   const bool cap = p->logit_cap > 0.f;
   const int64_t ts = p->token_stride * eb;
+  int best = -1, best_hs = 0;
   for (int i = 0; i < (int)(sizeof(cs::kInst) / sizeof(cs::kInst[0])); ++i) {
     const cs::Inst& in = cs::kInst[i];
     if (in.eb != eb || in.rms != p->rms_mode || in.dcg != dcg || in.g != p->groups || in.cap != cap) continue;
@@ -861,9 +872,12 @@ int cs_select(const qmla_decode_params* p) {
       if (need > 16 * in.crm || roff - delta + 16 * in.crm > ts) continue;
       if (!in.rtr && delta + (int64_t)p->rms_heads * rb > 16 * in.crm) continue;
     }
-    return i;
+    if (best < 0 || hs < best_hs || (hs == best_hs && in.mb < cs::kInst[best].mb)) {
+      best = i;
+      best_hs = hs;
+    }
   }
-  return -1;
+  return best;
 }
 
 int cs_launch(int inst, const qmla_decode_params* p, const KParams& k, int nwg, hipStream_t st) {

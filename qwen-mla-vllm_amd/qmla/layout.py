@@ -24,6 +24,16 @@ RMS_LOG2_LO, RMS_LOG2_HI = -3.0, 3.0
 FP8_RMS_MODES = ("log8", "bf16", "e4m3")
 
 
+def mla_fp8_rms_mode() -> str:
+    """The FP8 rows' rms tail format from QWEN_MLA_FP8_RMS (qwen_mla/mla_impl.py:136-141): log8
+    (default), bf16 (two raw bytes per head) or e4m3."""
+    import os
+    m = os.environ.get("QWEN_MLA_FP8_RMS", "log8")
+    if m not in FP8_RMS_MODES:
+        raise ValueError(f"QWEN_MLA_FP8_RMS={m!r}: expected one of {FP8_RMS_MODES}")
+    return m
+
+
 def rope_keep_from_config(hf):
     """Kept rope subspace indices, or None for full rope (qwen_mla/partial_rope.py:20-27)."""
     keep = getattr(hf, "mla_rope_keep", None)
@@ -79,39 +89,42 @@ def mla_local_ranks(hf, tp_size: int = 1) -> dict[int, int]:
     return {int(k): int(v) // g for k, v in hf.mla_ranks.items()}
 
 
-def _pow2(x: int) -> int:
-    w = 1
-    while w < x:
-        w *= 2
-    return w
+def _next_pow2(x: int) -> int:
+    """Smallest power of two >= x (1 for x <= 1)."""
+    x = int(x)
+    return 1 if x <= 1 else 1 << (x - 1).bit_length()
+
+
+def _row_schemes(raw: dict[int, int]):
+    """The two row-width schemes whose pages vLLM can unify by block size, for raw widths
+    {rank: rank + tail}: each width rounded up to a power of two, or to a power-of-two multiple of
+    the smallest raw width rounded up to 16 elements (qwen_mla/mla_impl.py:230-266)."""
+    unit = -(-min(raw.values()) // 16) * 16
+    yield {r: _next_pow2(w) for r, w in raw.items()}
+    yield {r: unit * _next_pow2(-(-w // unit)) for r, w in raw.items()}
 
 
 def mla_padded_head_size(hf, kv_lora_rank: int, tp_size: int = 1, fp8: bool = False,
                          fp8_rms: str = "log8") -> int:
-    """Cache row width so every layer's page divides the largest: the cheaper (by mean row) of the
-    pow2 and base-multiple schemes whose rows all divide the maximum and are multiples of 16
-    (qwen_mla/mla_impl.py:203-275)."""
+    """Cache row width of a layer of rank `kv_lora_rank` (qwen_mla/mla_impl.py:203-275).
+
+    Of the two schemes of _row_schemes, the ones where every layer's row divides the largest and is
+    a multiple of 16 elements qualify; the one with the smaller total row width over the model's
+    layers wins (the pow2 scheme on a tie). A rank that no layer has gets its raw width rounded up
+    to a power of two."""
     tail = mla_base_tail(hf, tp_size, fp8, fp8_rms)
-    raw = kv_lora_rank + tail
-    counts: dict[int, int] = {}
-    for v in mla_local_ranks(hf, tp_size).values():
-        counts[int(v)] = counts.get(int(v), 0) + 1
-    ranks = sorted(counts)
-    base = ((min(r + tail for r in ranks) + 15) // 16) * 16
-    cand = []
-    for rows in ({r: _pow2(r + tail) for r in ranks},
-                 {r: base * _pow2(-(-(r + tail) // base)) for r in ranks}):
-        mx = max(rows.values())
-        if any(mx % v for v in rows.values()):
+    layer_ranks = [int(v) for v in mla_local_ranks(hf, tp_size).values()]
+    best_total, best = None, None
+    for rows in _row_schemes({r: r + tail for r in set(layer_ranks)}):
+        top = max(rows.values())
+        if any(top % w or w % 16 for w in rows.values()):
             continue
-        if any(v % 16 for v in rows.values()):
-            continue
-        cand.append((sum(rows[r] * counts[r] for r in ranks) / sum(counts.values()), rows))
-    if cand:
-        rows = min(cand, key=lambda t: t[0])[1]
-        if kv_lora_rank in rows:
-            return rows[kv_lora_rank]
-    return _pow2(raw)
+        total = sum(rows[r] for r in layer_ranks)
+        if best_total is None or total < best_total:
+            best_total, best = total, rows
+    if best is not None and kv_lora_rank in best:
+        return best[kv_lora_rank]
+    return _next_pow2(kv_lora_rank + tail)
 
 
 def mla_rank_by_head_size(hf, tp_size: int = 1, fp8: bool = False, fp8_rms: str = "log8") -> dict[int, int]:

@@ -154,9 +154,14 @@ def _layout(kv, d_c, rope, heads, rms, qrows=1, groups=1):
     (_lib.KV_FP8, 1792, 232, 24, _lib.RMS_BF16_BYTES, 1, 1, _lib.ERR_WORKSPACE),
     (_lib.KV_FP8, 1792, 116, 12, _lib.RMS_E4M3, 1, 1, _lib.ERR_WORKSPACE),
     (_lib.KV_FP8, 1792, 64, 24, _lib.RMS_LOG8, 1, 1, _lib.ERR_WORKSPACE),
-    # bf16 rank 768 with a 256-column window; bf16 rank 1792 with a partial rope has no instance
+    # bf16 rank 768 with a 256-column window; bf16 rank 1792 with the reference test's partial and
+    # full rope layouts (tests/test_two_pass_1792.py:12)
     (_lib.KV_BF16, 768, 232, 24, _lib.RMS_BF16, 1, 1, _lib.ERR_WORKSPACE),
-    (_lib.KV_BF16, 1792, 232, 24, _lib.RMS_BF16, 1, 1, _lib.ERR_NOKERNEL),
+    (_lib.KV_BF16, 1792, 232, 24, _lib.RMS_BF16, 1, 1, _lib.ERR_WORKSPACE),
+    (_lib.KV_BF16, 1792, 116, 12, _lib.RMS_BF16, 1, 1, _lib.ERR_WORKSPACE),
+    (_lib.KV_BF16, 1792, 256, 24, _lib.RMS_BF16, 1, 1, _lib.ERR_WORKSPACE),
+    (_lib.KV_BF16, 1792, 256, 12, _lib.RMS_BF16, 1, 1, _lib.ERR_WORKSPACE),
+    (_lib.KV_BF16, 1792, 300, 24, _lib.RMS_BF16, 1, 1, _lib.ERR_NOKERNEL),      # wider than any window
     # GLA-g2 with 4 verify tokens: FP8 + log8 only
     (_lib.KV_FP8, 512, 64, 24, _lib.RMS_LOG8, 4, 2, _lib.ERR_WORKSPACE),
     (_lib.KV_BF16, 512, 64, 24, _lib.RMS_BF16, 4, 2, _lib.ERR_NOKERNEL),

@@ -124,3 +124,40 @@ def test_deployed_bf16_layouts(gpu, rank, heads, rope):
     assert err < max(TOL["bf16"], C_REF * ref_err), err
     # lse is stored as bf16: its own rounding (2^-9 relative) is allowed
     assert ((lse.float().cpu() - rl).abs() - 2.0 ** -8 * rl.abs()).max().item() < 1e-2
+
+
+@pytest.mark.parametrize("ctx,batch", [(4096, 4), (16384, 6)])
+@pytest.mark.parametrize("heads,rope", [(24, 232), (12, 116), (24, 256), (12, 256)])
+def test_deployed_bf16_rank1792(gpu, heads, rope, ctx, batch):
+    """tests/test_two_pass_1792.py:10-19: rank 1792 on the bf16 rows of test_fi_partial_rope.py
+    (784-token pages, shuffled table, ragged lengths, rms exp(N(0,1)) per key and head), 24 heads with
+    rope 232 (TP 1), 12 with 116 (TP 2), and full rope 256; through decode_attention_fwd with fixed
+    splits and through forward in the balanced mode."""
+    import qmla
+    rank, page = 1792, 784
+    cache, q, bt, lens, entry = _bf16_case(batch, heads, ctx, rank, rope, page, seed=7 + heads + ctx)
+    cd = cache.to(gpu)
+    splits = 8 if ctx == 4096 else 16
+    o = torch.full((batch, heads, rank), float("nan"), dtype=torch.bfloat16, device=gpu)
+    lse = torch.zeros(batch, heads, dtype=torch.float32, device=gpu)
+    logits = torch.zeros(batch, heads, splits, rank + 1, dtype=torch.float32, device=gpu)
+    qd = q.to(gpu)
+    qmla.decode_attention_fwd(qd, cd, cd[..., :rank], o, lse, bt.to(gpu), lens.to(gpu), logits, splits,
+                              1.0 / 256 ** 0.5, page, is_mla=True, rms_offset=rank + rope)
+    ob, lb = qmla.forward(qd[..., :rank], qd[..., rank:], cd, bt.to(gpu), lens.to(gpu), d_c=rank, rope_w=rope,
+                          rms_offset=rank + rope, page_size=page, sm_scale=1.0 / 256 ** 0.5, rms_heads=heads)
+    torch.cuda.synchronize()
+    cu8 = cache.view(torch.uint8).view(cache.shape[0], page, entry * 2)
+    kw = dict(page_size=page, d_c=rank, rope_w=rope, rms_offset=rank + rope, kv="bf16", rms_mode=ora.RMS_BF16,
+              sm_scale=1.0 / 256 ** 0.5, rms_heads=heads)
+    ro, rl = ora.mla_decode(q[..., :rank].float(), q[..., rank:].float(), cu8, bt, lens, **kw)
+    eo, _ = ora.mla_decode_reference_rounding(q[..., :rank].float(), q[..., rank:].float(), cu8, bt, lens,
+                                              num_splits=splits, align=16, **kw)
+    ref_err = (eo.to(torch.bfloat16).float() - ro).abs().max().item()
+    bound = max(TOL["bf16"], C_REF * ref_err)
+    for name, out, l in (("fixed", o, lse), ("balanced", ob, lb)):
+        err = (out.float().cpu() - ro).abs().max().item()
+        lerr = (l.float().cpu() - rl).abs().max().item()
+        print(f"[bf16 rank 1792 heads {heads} rope {rope} ctx {ctx} {name}] max-abs {err:.3e} "
+              f"(reference roundings {ref_err:.3e}, bound {bound:.3e}) lse {lerr:.3e}", flush=True)
+        assert err < bound and lerr < 1e-2
