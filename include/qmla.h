@@ -166,7 +166,8 @@ int qmla_decode_static(const qmla_decode_params* p, void* stream);
 
 /* The stages of qmla_decode, callable one by one on the same stream and params:
  *   qmla_plan            balanced mode only: per-request tile counts and prefix sums into the
- *                        workspace (one small workgroup; no host involvement)
+ *                        workspace (one small workgroup; no host involvement). Optional: the
+ *                        decode pass derives the same plan itself and stores it for the combine
  *   qmla_decode_partial  the decode pass (stage 1, qwen_mla/ops/mla_decode_attention.py:297-586):
  *                        partials into attn_logits (fixed mode) or the balanced workspace, and the
  *                        final out / lse directly for requests a single workgroup covered (with

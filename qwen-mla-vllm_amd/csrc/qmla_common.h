@@ -79,6 +79,90 @@ __device__ __forceinline__ int req_len(const KParams& p, int req) {
   return L > 0 ? L : 0;
 }
 
+// ---- the balanced plan, computed by the decode kernels themselves ---------------------------------
+// Request b owns PLAN_TILE-token plan tiles [C_b, C_b + T_b) of the concatenated requests, with
+// T_b = ceil(L_b / PLAN_TILE) and C_b the exclusive prefix of the T's; workgroup w of nwg owns plan
+// tiles [w*chunk, min((w+1)*chunk, total)) with chunk = ceil(total / nwg). Every workgroup derives
+// its own range from seq_lens at its start (no planning launch: a launch of its own costs more
+// than the scan, and inside a HIP graph far more), and workgroup 0 also stores the plan for the
+// balanced combine.
+
+__device__ __forceinline__ int wave_incl_sum(int x) {
+  const int lane = threadIdx.x & 63;
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    const int y = __shfl_up(x, o, 64);
+    if (lane >= o) x += y;
+  }
+  return x;
+}
+
+__device__ __forceinline__ int plan_tiles(const KParams& p, int b) {
+  const int L = req_len(p, b);
+  return (L + PLAN_TILE - 1) / PLAN_TILE;
+}
+
+struct BalRange {
+  int lo, hi;      // plan tiles of this workgroup
+  int chunk, total;
+  int b0, c0;      // the last request with C_b <= lo, and its C_b
+};
+
+// One wave computes workgroup w's range (wave-uniform results; any wave may call it).
+__device__ inline BalRange balanced_range(const KParams& p, int w) {
+  const int lane = threadIdx.x & 63;
+  BalRange r;
+  int total = 0;
+  for (int base = 0; base < p.n_req; base += 64) {
+    const int b = base + lane;
+    total += __shfl(wave_incl_sum(b < p.n_req ? plan_tiles(p, b) : 0), 63, 64);
+  }
+  // wave-uniform values: scalar registers (shuffle results are vector registers to the compiler)
+  total = __builtin_amdgcn_readfirstlane(total);
+  r.total = total;
+  r.chunk = total > 0 ? (total + p.nwg - 1) / p.nwg : 1;
+  r.lo = w * r.chunk;
+  r.hi = r.lo + r.chunk < total ? r.lo + r.chunk : total;
+  r.b0 = 0;
+  r.c0 = 0;
+  if (r.lo >= r.hi) return r;
+  int run = 0;
+  for (int base = 0; base < p.n_req && run <= r.lo; base += 64) {
+    const int b = base + lane;
+    const int t = b < p.n_req ? plan_tiles(p, b) : 0;
+    const int incl = wave_incl_sum(t);
+    const int c = run + incl - t;
+    const uint64_t m = __builtin_amdgcn_ballot_w64(b < p.n_req && c <= r.lo);
+    if (m) {
+      const int x = 63 - __builtin_clzll(m);
+      r.b0 = base + x;
+      r.c0 = __shfl(c, x, 64);
+    }
+    run += __shfl(incl, 63, 64);
+  }
+  r.b0 = __builtin_amdgcn_readfirstlane(r.b0);
+  r.c0 = __builtin_amdgcn_readfirstlane(r.c0);
+  return r;
+}
+
+// One wave of one workgroup stores the plan the balanced combine reads: [0] chunk, [1] total,
+// [2 + b] = C_b for b <= n_req.
+__device__ inline void store_plan(const KParams& p) {
+  const int lane = threadIdx.x & 63;
+  int run = 0;
+  for (int base = 0; base <= p.n_req; base += 64) {
+    const int b = base + lane;
+    const int t = b < p.n_req ? plan_tiles(p, b) : 0;
+    const int incl = wave_incl_sum(t);
+    if (b <= p.n_req) p.plan[2 + b] = run + incl - t;
+    run += __shfl(incl, 63, 64);
+  }
+  if (lane == 0) {
+    p.plan[0] = run > 0 ? (run + p.nwg - 1) / p.nwg : 1;
+    p.plan[1] = run;
+  }
+}
+
 // Tokens per split in the fixed-split mode: ceil(ceil(L/S)/align)*align (mla_decode_attention.py:389-396).
 __device__ __forceinline__ int split_len(const KParams& p, int L) {
   int per = (L + p.num_splits - 1) / p.num_splits;
@@ -122,24 +206,17 @@ template <int DV, class F>
 __device__ __forceinline__ void for_each_segment(const KParams& p, F&& f) {
   // one call site of f, so the (large, inlined) segment body exists once per kernel
   const bool fixed = p.num_splits > 0;
-  int b_lo, b_hi, lo = 0, hi = 0;
-  const int* pref = p.plan + 2;
+  int b_lo, b_hi, lo = 0, hi = 0, c = 0;
   if (fixed) {
     b_lo = blockIdx.y;
     b_hi = b_lo + 1;
   } else {
-    const int w = blockIdx.x;
-    const int chunk = p.plan[0], total = p.plan[1];
-    lo = w * chunk;
-    hi = lo + chunk < total ? lo + chunk : total;
+    const BalRange r = balanced_range(p, blockIdx.x);
+    lo = r.lo;
+    hi = r.hi;
     if (lo >= hi) return;
-    // first request whose tile range [pref[b], pref[b+1]) contains lo
-    int b0 = 0, b1 = p.n_req - 1;
-    while (b0 < b1) {
-      const int mid = (b0 + b1 + 1) >> 1;
-      if (pref[mid] <= lo) b0 = mid; else b1 = mid - 1;
-    }
-    b_lo = b0;
+    b_lo = r.b0;   // the request whose tiles contain lo (or an empty one right before it)
+    c = r.c0;
     b_hi = p.n_req;
   }
   for (int b = b_lo; b < b_hi; ++b) {
@@ -152,7 +229,8 @@ __device__ __forceinline__ void for_each_segment(const KParams& p, F&& f) {
       e = a + per < L ? a + per : L;
       so = seg_out<DV>(p, b, p.num_splits == 1);
     } else {
-      const int c0 = pref[b], c1 = pref[b + 1];
+      const int c0 = c, c1 = c + (L + PLAN_TILE - 1) / PLAN_TILE;
+      c = c1;
       if (c0 >= hi) break;
       if (c1 <= lo) continue;
       const int t_lo = (lo > c0 ? lo : c0) - c0, t_hi = (hi < c1 ? hi : c1) - c0;

@@ -257,11 +257,14 @@ __device__ __forceinline__ void segment(const KParams& p, Smem<C>& sm, int req, 
     return off;
   };
 
-  float mref[C::MB], lpart[C::MB];
+  // mref: the softmax reference; mthr: mref + ref_shift of the running sum at its last evaluation
+  // (the sum only grows while mref stays, so a tile max at or below mthr cannot move mref)
+  float mref[C::MB], mthr[C::MB], lpart[C::MB];
   f32x4 acc[C::MB][C::CB];
 #pragma unroll
   for (int mb = 0; mb < C::MB; ++mb) {
     mref[mb] = kNegInf;
+    mthr[mb] = kNegInf;
     lpart[mb] = 0.f;
 #pragma unroll
     for (int cb = 0; cb < C::CB; ++cb) acc[mb][cb] = f32x4{0.f, 0.f, 0.f, 0.f};
@@ -564,22 +567,23 @@ __device__ __forceinline__ void segment(const KParams& p, Smem<C>& sm, int req, 
       // than it does there; P <= 2^8
       bool cand = false;
 #pragma unroll
-      for (int mb = 0; mb < C::MB; ++mb) cand |= tmax[mb] > mref[mb];
+      for (int mb = 0; mb < C::MB; ++mb) cand |= tmax[mb] > mthr[mb];
       if (__builtin_amdgcn_ballot_w64(cand)) {
-        float shift[C::MB];
         bool need = false;
 #pragma unroll
         for (int mb = 0; mb < C::MB; ++mb) {
-          shift[mb] = ref_shift(sum_lg(lpart[mb]), 8.0f);
-          need |= tmax[mb] > mref[mb] + shift[mb];
+          mthr[mb] = mref[mb] + ref_shift(sum_lg(lpart[mb]), 8.0f);
+          need |= tmax[mb] > mthr[mb];
         }
         if (__builtin_amdgcn_ballot_w64(need)) {
 #pragma unroll
           for (int mb = 0; mb < C::MB; ++mb) {
-            const float mn = tmax[mb] > mref[mb] + shift[mb] ? tmax[mb] : mref[mb];
+            const bool mv = tmax[mb] > mthr[mb];
+            const float mn = mv ? tmax[mb] : mref[mb];
             const float alpha = mref[mb] == kNegInf ? 0.f : fast_exp2(mref[mb] - mn);
             lpart[mb] *= alpha;
             mref[mb] = mn;
+            if (mv) mthr[mb] = mn;   // re-evaluated at the next tile max above the new reference
             // accumulator rows 4*lg + i live in lanes 4*lg + i of the score layout
             float al[4];
 #pragma unroll
@@ -789,6 +793,7 @@ __global__ __launch_bounds__(C::NTHR, 1) void cs_kernel(const KParams p) {
   // the per-layer scale dequantizes fp8 rows (and e4m3 rms codes); a bf16 cache ignores it, as
   // the reference does (mla_decode_attention.py:451-463)
   const float kscale = (C::EB == 1 && p.k_scale) ? *p.k_scale : 1.0f;
+  if (p.num_splits == 0 && blockIdx.x == 0 && blockIdx.z == 0 && threadIdx.x < 64) store_plan(p);   // for the combine
   for_each_segment<C::DCG>(p, [&](int req, int a, int e, int L, const SegOut& so) {
     segment<C>(p, sm, req, a, e, L, so, kscale);
     // the next range starts its sub-range set-up with a full barrier; nothing else to reset

@@ -597,6 +597,7 @@ __global__ __launch_bounds__(C::NTHR, C::WGPC) void partial_kernel(const KParams
   // the per-layer scale dequantizes fp8 rows (and e4m3 rms codes); a bf16 cache ignores it, as
   // the reference does (mla_decode_attention.py:451-463)
   const float kscale = (C::EB == 1 && p.k_scale) ? *p.k_scale : 1.0f;
+  if (p.num_splits == 0 && blockIdx.x == 0 && threadIdx.x < 64) store_plan(p);   // for the combine
   for_each_segment<C::DCG>(p, [&](int req, int a, int e, int L, const SegOut& so) {
     process_segment<C>(p, sm, req, a, e, L, so, kscale);
   });
@@ -1220,8 +1221,7 @@ int qmla_decode(const qmla_decode_params* p, void* stream) {
   rc = check_balanced_ws(p);
   if (rc) return rc;
   KParams k = make_kparams(p);
-  rc = run_plan(p, k, st);
-  if (rc) return rc;
+  // the decode kernels derive the balanced plan themselves (and store it for the combine)
   rc = si >= 0 ? ws_launch(si, p, k, k.nwg, st) : in ? run_partial(p, in, k, st) : cs_launch(wi, p, k, k.nwg, st);
   if (rc) return rc;
   return run_combine(p, k, st);

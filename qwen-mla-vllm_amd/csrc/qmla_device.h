@@ -189,14 +189,14 @@ __device__ __forceinline__ float fast_log2(float x) { return __builtin_amdgcn_lo
 
 // How far a row's tile maximum may exceed its softmax reference before the reference moves, given
 // the row's running sum l (relative to the reference). A token that does not move it has
-// P <= 2^shift <= l / 32, so it holds at most 1/33 of the row's mass and the rounding of its P to
-// 16 bits before P.V moves the output by at most 1/33 of that rounding; a token above that share
+// P <= 2^shift <= l / 4, so it holds at most 1/5 of the row's mass and the rounding of its P to
+// 16 bits before P.V moves the output by at most 1/5 of that rounding; a token above that share
 // moves the reference to itself and gets P = 1 exactly, as the running max of the reference's
 // online softmax does (qwen_mla/ops/mla_decode_attention.py:553-560). While a row has little mass
 // (its first tokens, a peaked softmax) the shift is 0, i.e. an exact running max; it grows to
 // `cap` as the mass accumulates, so the reference rarely moves in long rows.
 __device__ __forceinline__ float ref_shift(float l, float cap) {
-  return fminf(cap, fmaxf(0.f, fast_log2(l) - 5.0f));
+  return fminf(cap, fmaxf(0.f, fast_log2(l) - 2.0f));
 }
 
 }  // namespace qmla

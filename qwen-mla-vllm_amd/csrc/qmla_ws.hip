@@ -125,15 +125,6 @@ __device__ __forceinline__ void static_for(F&& f) {
   }
 }
 
-__device__ __forceinline__ int wave_incl_sum(int x) {
-  const int lane = threadIdx.x & 63;
-#pragma unroll
-  for (int o = 1; o < 64; o <<= 1) {
-    const int y = __shfl_up(x, o, 64);
-    if (lane >= o) x += y;
-  }
-  return x;
-}
 __device__ __forceinline__ int lanes_below(uint64_t m) {
   return __builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0));
 }
@@ -234,37 +225,24 @@ __device__ __forceinline__ void wait_tiles(int ahead) {
   }
 }
 
-// Wave-wide: the last request b in [0, n_req) whose first plan tile pref[b] <= lo (64-ary search;
-// pref is nondecreasing with pref[0] = 0).
-__device__ int find_first_req(const int* pref, int n_req, int lo) {
-  const int lane = threadIdx.x & 63;
-  int base = 0, len = n_req;
-  while (len > 1) {
-    const int step = (len + 63) >> 6;
-    const int idx = base + lane * step;
-    const bool ok = lane * step < len && pref[idx] <= lo;
-    const uint64_t m = __builtin_amdgcn_ballot_w64(ok);   // lane 0 always: pref[base] <= lo
-    const int last = 63 - __builtin_clzll(m);
-    base += last * step;
-    const int rem = len - last * step;
-    len = step < rem ? step : rem;
-  }
-  return base;
-}
-
 // Wave 0: the next window of pieces, from request cb at token ctok on, into sm.seg / sm.win.
 // Lane l looks at request cb + l; pieces are taken in request order while their pages fit PIDN (the
-// first piece that does not fit is cut at a page boundary).
+// first piece that does not fit is cut at a page boundary). Balanced mode: cp is the plan prefix
+// C_cb of the cursor's request, and the lanes' C_b follow from a scan of their tile counts.
 template <class C>
-__device__ void plan_window(const KParams& p, Smem<C>& sm, bool fixed, int lo, int hi, int& cb, int& ctok) {
+__device__ void plan_window(const KParams& p, Smem<C>& sm, bool fixed, int lo, int hi, int& cb, int& ctok,
+                            int& cp) {
   const int lane = threadIdx.x & 63;
   const int P = p.page_size;
-  const int* pref = p.plan + 2;
   int nseg = 0, ntot = 0, npg = 0;
   bool more = true;
   while (more && nseg == 0) {
     const int b = cb + lane;
     int a = 0, e = 0, L = 0, fl = 0;
+    // plan tiles [c0, c1) of request b (balanced mode)
+    const int tb = (!fixed && b < p.n_req) ? plan_tiles(p, b) : 0;
+    const int tincl = wave_incl_sum(tb);
+    const int c0 = cp + tincl - tb, c1 = cp + tincl;
     bool beyond;
     if (fixed) {
       beyond = lane != 0;
@@ -279,7 +257,6 @@ __device__ void plan_window(const KParams& p, Smem<C>& sm, bool fixed, int lo, i
     } else {
       beyond = b >= p.n_req;
       if (!beyond) {
-        const int c0 = pref[b], c1 = pref[b + 1];
         beyond = c0 >= hi;
         if (!beyond && c1 > lo) {
           L = req_len(p, b);
@@ -331,11 +308,13 @@ __device__ void plan_window(const KParams& p, Smem<C>& sm, bool fixed, int lo, i
       const int etx = __shfl(et, x, 64);
       const bool tookx = (tm >> x) & 1;
       cb += x;
+      cp = __shfl(c0, x, 64);
       ctok = tookx ? etx : 0;
     } else if (bm) {
       more = false;
     } else {
       cb += 64;
+      cp = __shfl(c1, 63, 64);
       ctok = 0;
     }
   }
@@ -352,7 +331,7 @@ __device__ void plan_window(const KParams& p, Smem<C>& sm, bool fixed, int lo, i
 // registers live (score waves the query fragments, value waves the accumulators).
 template <class C, int ROLE>
 __device__ __forceinline__ void role_main(const KParams& p, Smem<C>& sm, float kscale, bool fixed, int lo,
-                                          int hi) {
+                                          int hi, int b0, int c0) {
   constexpr int NTHR = C::NTHR;
   constexpr bool F8 = C::EB == 1;
   constexpr int NB = C::DCG / 128;       // latent blocks of the fp8 product
@@ -613,12 +592,11 @@ __device__ __forceinline__ void role_main(const KParams& p, Smem<C>& sm, float k
     zero_acc();
   };
 
-  // window planning cursor (wave 0 only)
-  int cb = 0, ctok = 0;
-  if (w == 0) cb = fixed ? (int)blockIdx.y : find_first_req(p.plan + 2, p.n_req, lo);
+  // window planning cursor (wave 0 only): request, token, plan prefix of the request
+  int cb = fixed ? (int)blockIdx.y : b0, ctok = 0, cp = c0;
 
   for (;;) {
-    if (w == 0) plan_window<C>(p, sm, fixed, lo, hi, cb, ctok);
+    if (w == 0) plan_window<C>(p, sm, fixed, lo, hi, cb, ctok, cp);
     __syncthreads();
     const int nseg = sm.win[0], ntot = sm.win[1], npg = sm.win[2], more = sm.win[3];
     if (nseg == 0) break;
@@ -1094,15 +1072,19 @@ __global__ __launch_bounds__(C::NTHR, 1) void ws_kernel(const KParams p) {
   __shared__ __attribute__((aligned(16))) Smem<C> sm;
   const float kscale = (C::EB == 1 && p.k_scale) ? *p.k_scale : 1.0f;
   const bool fixed = p.num_splits > 0;
-  int lo = 0, hi = 0;
+  const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  int lo = 0, hi = 0, b0 = 0, c0 = 0;
   if (!fixed) {
-    const int chunk = p.plan[0], total = p.plan[1];
-    lo = (int)blockIdx.x * chunk;
-    hi = lo + chunk < total ? lo + chunk : total;
+    if (blockIdx.x == 0 && wv == 1) store_plan(p);   // for the balanced combine
+    const BalRange r = balanced_range(p, blockIdx.x);
+    lo = r.lo;
+    hi = r.hi;
+    b0 = r.b0;
+    c0 = r.c0;
     if (lo >= hi) return;
   }
-  if (__builtin_amdgcn_readfirstlane(threadIdx.x >> 6) < 4) role_main<C, SCORE>(p, sm, kscale, fixed, lo, hi);
-  else role_main<C, VALUE>(p, sm, kscale, fixed, lo, hi);
+  if (wv < 4) role_main<C, SCORE>(p, sm, kscale, fixed, lo, hi, b0, c0);
+  else role_main<C, VALUE>(p, sm, kscale, fixed, lo, hi, b0, c0);
 }
 
 struct Inst {

@@ -38,3 +38,32 @@ def test_plan_prefix_sums(gpu, n_req, qrows, nwg):
     exp = np.concatenate([[max(-(-total // nwg), 1), total], np.cumsum(tiles) - tiles, [total]])
     print(f"[plan n_req {n_req} qrows {qrows} nwg {nwg}] total {total} tiles", flush=True)
     assert np.array_equal(got, exp), np.argwhere(got != exp)[:5].ravel().tolist()
+
+
+@pytest.mark.parametrize("kv,rms,d_c,n_req,nwg", [("fp8", "log8", 512, 300, 256), ("fp8", "log8", 512, 300, 7),
+                                                 ("bf16", "bf16", 512, 300, 64), ("bf16", "bf16", 1792, 90, 33)])
+def test_decode_kernels_store_the_plan(gpu, kv, rms, d_c, n_req, nwg):
+    """The decode kernels derive the balanced plan themselves; the first workgroup stores it for the
+    combine: the same words qmla_plan writes (warp-specialized, per-group and column-split kernels)."""
+    from qmla import _lib
+    from qmla.decode import _stream, build_params, workspace_bytes
+    g = np.random.default_rng(n_req + nwg)
+    L = g.integers(0, 3000, n_req)
+    L[::5] = 0
+    c = make_case(batch=n_req, heads=24, d_c=d_c, rope_w=64, page_size=64, lens=L.tolist(), kv=kv, rms_mode=rms,
+                  seed=10, device=gpu)
+    o = torch.empty(n_req, 24, d_c, dtype=torch.bfloat16, device=gpu)
+    lse = torch.empty(n_req, 24, dtype=torch.float32, device=gpu)
+    args = dict(q_nope=c.q_nope, q_pe=c.q_pe, kv_cache=c.cache, block_table=c.block_table, seq_lens=c.seq_lens, out=o,
+                lse=lse, d_c=d_c, rope_w=64, rms_offset=c.rms_offset,
+                rms_mode=_lib.RMS_LOG8 if kv == "fp8" else _lib.RMS_BF16, kv=_lib.KV_FP8 if kv == "fp8" else _lib.KV_BF16,
+                page_size=64, sm_scale=c.sm_scale, k_scale=c.k_scale, num_splits=0, num_workgroups=nwg)
+    ws = torch.full((workspace_bytes(build_params(**args)) // 4,), -7, dtype=torch.int32, device=gpu)
+    p = build_params(workspace=ws, **args)
+    _lib.check("qmla_decode_partial", _lib.lib().qmla_decode_partial(p, _stream()))
+    torch.cuda.synchronize()
+    got = ws[:n_req + 3].cpu().numpy()
+    tiles = (L + 63) // 64
+    total = int(tiles.sum())
+    exp = np.concatenate([[max(-(-total // nwg), 1), total], np.cumsum(tiles) - tiles, [total]])
+    assert np.array_equal(got, exp), np.argwhere(got != exp)[:5].ravel().tolist()
