@@ -42,6 +42,10 @@ WORKLOADS = {
                      amp=1.0, lens=("uniform", 4096, 32768)),
     "gla_b48": dict(batch=48, heads=24, d_c=512, rope_w=64, page_size=64, kv="fp8", rms_mode="log8", seed=4,
                     amp=1.0, lens=("uniform", 8192, 32768), qrows=4, groups=2),
+    # MTP verify on plain MLA: 64 requests x 4 query tokens x 24 heads (96 rows per request, folded
+    # so each cached row is read once from HBM: the heads split over 3 workgroups on one XCD)
+    "verify_b64x4": dict(batch=64, heads=24, d_c=512, rope_w=64, page_size=64, kv="fp8", rms_mode="log8", seed=5,
+                         amp=4.0, lens=("lognormal", 16384, 0.5, 1024, 65536), qrows=4),
     # wide latent: 16 fixed splits in the reference's attn_logits layout, then the combine
     "wide_b32": dict(batch=32, heads=24, d_c=1792, rope_w=64, page_size=1600, kv="bf16", rms_mode="bf16", seed=3,
                      amp=1.0, lens=("fixed", 65536), splits=16),

@@ -45,6 +45,8 @@ struct KParams {
   float* part_o;    // [(nwg + n_req), qrows*heads, Dv]
   float* part_lse;  // [(nwg + n_req), qrows*heads]
   int q_vec;        // query rows and strides 16-byte aligned: 16-byte query loads (else element loads)
+  int hsplit;       // warp-specialized kernel: workgroups sharing a request's token range, each with
+                    // heads/hsplit of its heads (balanced mode: nwg ranges x hsplit workgroups)
 };
 
 // 8 consecutive query elements: one 16-byte load when the caller's query rows are 16-byte aligned,
@@ -174,18 +176,19 @@ __device__ __forceinline__ int split_len(const KParams& p, int L) {
 // attn_logits row of split blockIdx.x; the balanced mode writes slot blockIdx.x + b of the partial
 // buffers; final_out (the workgroup covers the whole request) writes the normalized output directly.
 template <int DV>
-__device__ __forceinline__ SegOut seg_out(const KParams& p, int b, bool final_out) {
+__device__ __forceinline__ SegOut seg_out(const KParams& p, int b, bool final_out, int w = -1) {
+  if (w < 0) w = blockIdx.x;   // the workgroup's split (fixed) or range (balanced)
   SegOut so;
   so.final_out = final_out;
   if (p.num_splits > 0) {
-    so.po = p.ws + (int64_t)b * p.qrows * p.ws_sr + (int64_t)blockIdx.x * p.ws_ss;
+    so.po = p.ws + (int64_t)b * p.qrows * p.ws_sr + (int64_t)w * p.ws_ss;
     so.po_sr = p.ws_sr;
     so.po_sh = p.ws_sh;
     so.plse = nullptr;
     so.plse_sr = 0;
   } else {
     const int nrow = p.qrows * p.heads;
-    const int64_t slot = (int64_t)blockIdx.x + b;
+    const int64_t slot = (int64_t)w + b;
     so.po = p.part_o + slot * nrow * DV;
     so.po_sr = (int64_t)p.heads * DV;
     so.po_sh = DV;
@@ -245,6 +248,7 @@ __device__ __forceinline__ void for_each_segment(const KParams& p, F&& f) {
 
 // ---- host-side interface of the warp-specialized translation unit (qmla_ws.hip) ----
 int ws_select(const qmla_decode_params* p);
+int ws_head_split(const qmla_decode_params* p);
 int ws_launch(int inst, const qmla_decode_params* p, const KParams& k, int nwg, hipStream_t st);
 
 // ---- host-side interface of the column-split translation unit (qmla_cs.hip) ----

@@ -940,8 +940,19 @@ static const Inst* find_inst(const qmla_decode_params* p) {
 
 static const Inst* find_inst(const qmla_decode_params* p);
 
+// Token ranges of the balanced mode (workgroups, except that the warp-specialized kernel's head split
+// runs hsplit workgroups per range): one workgroup per compute unit; with a head split a multiple of
+// 8 ranges, so each range's workgroups share an XCD.
 static int balanced_nwg(const qmla_decode_params* p) {
   if (p->num_workgroups > 0) return p->num_workgroups;
+  if (ws_select(p) >= 0) {
+    const int hs = ws_head_split(p);
+    if (hs > 1) {
+      const int r = cu_count() / (8 * hs) * 8;
+      return r > 8 ? r : 8;
+    }
+    return cu_count();
+  }
   const Inst* in = find_inst(p);
   return cu_count() * (in ? in->wgpc : 1);
 }

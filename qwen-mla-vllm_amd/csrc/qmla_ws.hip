@@ -331,7 +331,7 @@ __device__ void plan_window(const KParams& p, Smem<C>& sm, bool fixed, int lo, i
 // registers live (score waves the query fragments, value waves the accumulators).
 template <class C, int ROLE>
 __device__ __forceinline__ void role_main(const KParams& p, Smem<C>& sm, float kscale, bool fixed, int lo,
-                                          int hi, int b0, int c0) {
+                                          int hi, int b0, int c0, int wr, int hz) {
   constexpr int NTHR = C::NTHR;
   constexpr bool F8 = C::EB == 1;
   constexpr int NB = C::DCG / 128;       // latent blocks of the fp8 product
@@ -348,7 +348,9 @@ __device__ __forceinline__ void role_main(const KParams& p, Smem<C>& sm, float k
   const int dw = C::NIW == 8 ? w : vw;         // issuing wave: first DMA instruction of a tile
   const int ln16 = lane & 15, lg = lane >> 4;
   const int qrows = p.qrows, hpg = p.hpg;
-  const int nrows = qrows * hpg;               // rows per group
+  // the workgroup's heads of each group: hpw of them from h0 (head split hz of p.hsplit)
+  const int hpw = hpg / p.hsplit, h0 = hz * hpw;
+  const int nrows = qrows * hpw;               // rows per group
   const int P = p.page_size;
   const float c2b = p.sm_scale * kscale * kLog2e;
   // score wave: the lane's row in each of its row blocks (r indexes the workgroup's row arrays),
@@ -361,8 +363,8 @@ __device__ __forceinline__ void role_main(const KParams& p, Smem<C>& sm, float k
     const int rg = 16 * (rb - sg * C::MBV) + ln16;   // row within the group
     r[m] = 16 * rb + ln16;
     rok[m] = rg < nrows;
-    jq[m] = rok[m] ? rg / hpg : 0;
-    hd[m] = sg * hpg + (rok[m] ? rg - jq[m] * hpg : 0);
+    jq[m] = rok[m] ? rg / hpw : 0;
+    hd[m] = sg * hpg + h0 + (rok[m] ? rg - jq[m] * hpw : 0);
     rms_b[m] = p.rms_off_b + hd[m] * C::RMS_EB;
   }
   const bool contig = p.token_stride_b == C::RB;
@@ -549,7 +551,7 @@ __device__ __forceinline__ void role_main(const KParams& p, Smem<C>& sm, float k
   };
   // value wave: normalize and write the output of request req, whose sums are in fin[k & 1]
   auto finalize = [&](int k, int req, int fl) {
-    const SegOut so = seg_out<C::DCG>(p, req, (fl & SEG_FINAL) != 0);
+    const SegOut so = seg_out<C::DCG>(p, req, (fl & SEG_FINAL) != 0, wr);
     const int row0 = req * qrows;
 #pragma unroll
     for (int mb = 0; mb < C::MBV; ++mb)
@@ -570,7 +572,7 @@ __device__ __forceinline__ void role_main(const KParams& p, Smem<C>& sm, float k
         }
         if (rr >= nrows) continue;
         const float l = l0 + l1;
-        const int jr = rr / hpg, h = vg * hpg + rr - jr * hpg;
+        const int jr = rr / hpw, h = vg * hpg + h0 + rr - jr * hpw;
         const float inv = l > 0.f ? kscale / l : 0.f;   // fp8 values were accumulated unscaled
         const float lse_v = l > 0.f ? (m + fast_log2(l)) * kLn2 : kNegInf;
         const int col = C::VC * vh + ln16;
@@ -1073,18 +1075,31 @@ __global__ __launch_bounds__(C::NTHR, 1) void ws_kernel(const KParams p) {
   const float kscale = (C::EB == 1 && p.k_scale) ? *p.k_scale : 1.0f;
   const bool fixed = p.num_splits > 0;
   const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  // head split: the p.hsplit workgroups of one token range are consecutive on one XCD (workgroup i
+  // runs on XCD i % 8), so their shared reads of the range's rows are served by that XCD's L2
+  int hz = fixed ? (int)blockIdx.z : 0, wr = blockIdx.x;
+  if (!fixed && p.hsplit > 1) {
+    if ((p.nwg & 7) == 0) {
+      const int slot = (int)blockIdx.x >> 3;
+      hz = slot % p.hsplit;
+      wr = (slot / p.hsplit) * 8 + ((int)blockIdx.x & 7);
+    } else {   // a caller's range count: the split's workgroups are at least adjacent in launch order
+      hz = (int)blockIdx.x % p.hsplit;
+      wr = (int)blockIdx.x / p.hsplit;
+    }
+  }
   int lo = 0, hi = 0, b0 = 0, c0 = 0;
   if (!fixed) {
-    if (blockIdx.x == 0 && wv == 1) store_plan(p);   // for the balanced combine
-    const BalRange r = balanced_range(p, blockIdx.x);
+    if (wr == 0 && hz == 0 && wv == 1) store_plan(p);   // for the balanced combine
+    const BalRange r = balanced_range(p, wr);
     lo = r.lo;
     hi = r.hi;
     b0 = r.b0;
     c0 = r.c0;
     if (lo >= hi) return;
   }
-  if (wv < 4) role_main<C, SCORE>(p, sm, kscale, fixed, lo, hi, b0, c0);
-  else role_main<C, VALUE>(p, sm, kscale, fixed, lo, hi, b0, c0);
+  if (wv < 4) role_main<C, SCORE>(p, sm, kscale, fixed, lo, hi, b0, c0, wr, hz);
+  else role_main<C, VALUE>(p, sm, kscale, fixed, lo, hi, b0, c0, wr, hz);
 }
 
 struct Inst {
@@ -1110,10 +1125,22 @@ static const Inst kInst[] = {
 
 }  // namespace ws
 
+// Workgroups per token range for a request's rows: one group holds 32 rows (2 row blocks) per
+// workgroup, so more rows split the heads over up to 4 workgroups (24 heads x 4 verify tokens: 3 of
+// 8 heads x 4 tokens); latent groups (GLA) hold 48 rows per group in one workgroup. 0: no fit.
+int ws_head_split(const qmla_decode_params* p) {
+  const int hpg = p->heads / p->groups, rows = p->qrows * hpg;
+  if (p->groups == 2) return rows <= 48 ? 1 : 0;
+  if (p->groups != 1) return 0;
+  for (int hs = 1; hs <= 4; ++hs)
+    if (hpg % hs == 0 && p->qrows * (hpg / hs) <= 32) return hs;
+  return 0;
+}
+
 int ws_select(const qmla_decode_params* p) {
   if (p->rope_w != 64 || (p->groups != 1 && p->groups != 2)) return -1;
-  // rows per group: 2 row blocks with one group, 3 per group with two
-  if (p->qrows * (p->heads / p->groups) > (p->groups == 1 ? 32 : 48)) return -1;
+  const int hs = ws_head_split(p);
+  if (hs == 0) return -1;
   const int eb = p->kv_dtype == QMLA_KV_FP8 ? 1 : 2;
   const bool cap = p->logit_cap > 0.f;
   const int64_t ts = p->token_stride * eb;
@@ -1121,7 +1148,7 @@ int ws_select(const qmla_decode_params* p) {
     const ws::Inst& in = ws::kInst[i];
     if (in.g != p->groups || in.eb != eb || in.rms != p->rms_mode || in.dcg != p->d_c / p->groups || in.cap != cap)
       continue;
-    if (in.rtr && (p->qrows != 1 || p->heads > 32)) continue;
+    if (in.rtr && (p->qrows != 1 || p->heads > 32 || hs != 1)) continue;
     if ((int64_t)in.cpr * 16 > ts) continue;   // never read past a row
     if (p->rms_mode != QMLA_RMS_NONE) {
       const int rb = (p->rms_mode == QMLA_RMS_BF16 || p->rms_mode == QMLA_RMS_BF16_BYTES) ? 2 : 1;
@@ -1137,8 +1164,9 @@ int ws_select(const qmla_decode_params* p) {
 
 int ws_launch(int inst, const qmla_decode_params* p, const KParams& k, int nwg, hipStream_t st) {
   KParams kk = k;
+  kk.hsplit = ws_head_split(p);
   void* args[] = {&kk};
-  dim3 grid = p->num_splits > 0 ? dim3(p->num_splits, k.n_req, 1) : dim3(nwg, 1, 1);
+  dim3 grid = p->num_splits > 0 ? dim3(p->num_splits, k.n_req, kk.hsplit) : dim3(nwg * kk.hsplit, 1, 1);
   if (grid.x == 0 || grid.y == 0) return QMLA_OK;
   hipError_t e = hipLaunchKernel((const void*)ws::kInst[inst].fn, grid, dim3(ws::kInst[inst].nthr, 1, 1), args, 0, st);
   return e == hipSuccess ? QMLA_OK : QMLA_ERR_LAUNCH;

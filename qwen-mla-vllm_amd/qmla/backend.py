@@ -29,7 +29,7 @@ from types import SimpleNamespace
 import torch
 
 from . import _lib
-from .decode import MAX_ROWS_PER_GROUP, Workspace, _fold_group, build_params, workspace_bytes
+from .decode import Workspace, _fold_rows, _ws_family, build_params, workspace_bytes
 from .layout import mla_fp8_rms_mode
 
 
@@ -111,7 +111,7 @@ def decode_params(impl, q, kv_c_and_k_pe_cache, attn_metadata, layer, out, lse):
     if qrows > 1:
         if q_nope.shape[0] % qrows:
             raise ValueError(f"{q_nope.shape[0]} decode rows are not whole requests of {qrows} query tokens")
-        qrows = _fold_group(qrows, q_nope.shape[1], MAX_ROWS_PER_GROUP[1])
+        qrows = _fold_rows(qrows, q_nope.shape[1], 1, _ws_family(kv, rms_mode, rank, rope_w, 1, 0.0))
     return build_params(q_nope=q_nope, q_pe=q_pe, kv_cache=cache, block_table=md.block_table, seq_lens=md.seq_lens,
                         out=out, lse=lse, d_c=rank, rope_w=rope_w, rms_offset=impl.rms_offset, rms_mode=rms_mode,
                         kv=kv, page_size=page_size, sm_scale=impl.scale, k_scale=k_scale,

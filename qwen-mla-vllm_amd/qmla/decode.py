@@ -166,6 +166,26 @@ def _check_device(*ts: torch.Tensor) -> None:
 
 # kernel row-tile capacity per latent group, per the compiled instances (MB * 16)
 MAX_ROWS_PER_GROUP = {1: 32, 2: 48}
+# the warp-specialized kernel (FP8 + log8 rows, d_c 512, rope 64, one latent group) also splits a
+# request's heads over up to 4 workgroups that share its token range: up to 128 rows
+MAX_ROWS_HEAD_SPLIT = 128
+
+
+def _ws_family(kv: int, rms_mode: int, d_c: int, rope_w: int, groups: int, logit_cap: float) -> bool:
+    return (kv == _lib.KV_FP8 and rms_mode == _lib.RMS_LOG8 and groups == 1 and d_c == 512 and rope_w == 64
+            and logit_cap <= 0)
+
+
+def _fold_rows(qrows: int, heads: int, groups: int, ws: bool) -> int:
+    """Verify tokens folded per kernel request (see _fold_group); with the warp-specialized kernel's
+    head split a fold must also leave whole heads per workgroup (heads % split == 0)."""
+    if not ws:
+        return _fold_group(qrows, heads // groups, MAX_ROWS_PER_GROUP.get(groups, 32))
+    best = 1
+    for d in range(1, qrows + 1):
+        if qrows % d == 0 and any(heads % hs == 0 and d * heads // hs <= 32 for hs in range(1, 5)):
+            best = d
+    return best
 
 
 def decode_attention_fwd(q, k_buffer, v_buffer, o, lse, req_to_token, b_seq_len, attn_logits,
@@ -189,7 +209,7 @@ def decode_attention_fwd(q, k_buffer, v_buffer, o, lse, req_to_token, b_seq_len,
     kv = _kv_code(k_buffer, None)
     mode = _rms_mode(kv, rms_offset, rms_bf16, rms_log8)
     if qrows > 1 and B % qrows == 0:
-        qrows = _fold_group(qrows, H, MAX_ROWS_PER_GROUP[1])
+        qrows = _fold_rows(qrows, H, 1, _ws_family(kv, mode, Lv, Lk - Lv, 1, logit_cap))
     else:
         qrows = 1
     if k_scale is not None and not torch.is_tensor(k_scale):
@@ -260,7 +280,7 @@ def forward(q_nope, q_rope, kv_cache, block_table, seq_lens, *, d_c=None, rope_w
     if qrows > 1:
         if rows % qrows:
             raise ValueError(f"rows {rows} not a multiple of qrows {qrows}")
-        qrows = _fold_group(qrows, H // groups, MAX_ROWS_PER_GROUP.get(groups, 32))
+        qrows = _fold_rows(qrows, H, groups, _ws_family(kv, mode, d_c, rope_w, groups, logit_cap))
     args = dict(q_nope=q_nope, q_pe=q_rope, kv_cache=kv_cache, block_table=block_table, seq_lens=seq_lens,
                 out=out, lse=lse, d_c=d_c, rope_w=rope_w, rms_offset=rms_offset, rms_mode=mode, kv=kv,
                 page_size=page_size, sm_scale=sm_scale, k_scale=k_scale, logit_cap=logit_cap, qrows=qrows,

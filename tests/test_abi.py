@@ -162,6 +162,9 @@ def _layout(kv, d_c, rope, heads, rms, qrows=1, groups=1):
     (_lib.KV_BF16, 1792, 256, 24, _lib.RMS_BF16, 1, 1, _lib.ERR_WORKSPACE),
     (_lib.KV_BF16, 1792, 256, 12, _lib.RMS_BF16, 1, 1, _lib.ERR_WORKSPACE),
     (_lib.KV_BF16, 1792, 300, 24, _lib.RMS_BF16, 1, 1, _lib.ERR_NOKERNEL),      # wider than any window
+    # 24 heads x 4 verify tokens, FP8 + log8: the heads split over three workgroups per range
+    (_lib.KV_FP8, 512, 64, 24, _lib.RMS_LOG8, 4, 1, _lib.ERR_WORKSPACE),
+    (_lib.KV_FP8, 512, 64, 24, _lib.RMS_E4M3, 4, 1, _lib.ERR_NOKERNEL),      # other rms formats: 32 rows
     # GLA-g2 with 4 verify tokens: FP8 + log8 only
     (_lib.KV_FP8, 512, 64, 24, _lib.RMS_LOG8, 4, 2, _lib.ERR_WORKSPACE),
     (_lib.KV_BF16, 512, 64, 24, _lib.RMS_BF16, 4, 2, _lib.ERR_NOKERNEL),

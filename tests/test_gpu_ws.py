@@ -66,3 +66,39 @@ def test_ws_climbing_max(gpu):
     # the same through fixed splits
     o2, lse2 = _forward(c, num_splits=5)
     _check("climbing max, 5 splits", c, o2, lse2)
+
+
+@pytest.mark.parametrize("nwg", [1, 2, 3, 4, 5, 7])
+@pytest.mark.parametrize("lens", [[0, 0, 64, 0, 0, 128, 0, 64, 0, 0], [0, 0, 0], [5, 0, 0, 0, 70, 0], [0, 200, 0, 1]])
+def test_ws_empty_requests_at_range_edges(gpu, lens, nwg):
+    """Requests of length 0 before, between and after the others, at the plan positions where the
+    workgroups' ranges start and end, and a batch with no token at all: every row is written (zero
+    output, lse -inf for the empty ones; outputs start as NaN), whichever workgroup owns it."""
+    import qmla
+    c = make_case(batch=len(lens), heads=24, d_c=512, rope_w=64, page_size=64, lens=lens, kv="fp8", rms_mode="log8",
+                  seed=17, device=gpu, rms="spread", amp=2.0)
+    rows = c.q_nope.shape[0]
+    o = torch.full((rows, 24, 512), float("nan"), dtype=torch.bfloat16, device=gpu)
+    lse = torch.full((rows, 24), float("nan"), dtype=torch.float32, device=gpu)
+    _forward(c, num_workgroups=nwg, out=o, lse=lse)
+    assert not torch.isnan(o.float()).any() and not torch.isnan(lse).any(), "unwritten rows"
+    _check(f"empty requests {lens} nwg {nwg}", c, o, lse)
+
+
+@pytest.mark.parametrize("heads,qrows,nwg,splits", [(24, 4, 0, 0), (24, 4, 5, 0), (24, 4, 16, 0), (24, 4, 0, 3),
+                                                    (24, 2, 0, 0), (16, 4, 0, 0), (24, 3, 0, 0)])
+def test_ws_head_split_verify(gpu, heads, qrows, nwg, splits):
+    """More verify rows than one workgroup holds (24 heads x 4 tokens = 96): the request's heads are
+    split over workgroups that read the same token range (8 heads x 4 tokens each), in the balanced
+    mode (default ranges on shared XCDs, a caller's range count, 16 ranges) and with fixed splits;
+    2 tokens x 24 heads and 4 x 16 split in two; 3 tokens x 24 heads in three splits of 24 rows."""
+    import qmla
+    lens = [4, 1500, 3000, 64, 777]
+    c = make_case(batch=len(lens), heads=heads, d_c=512, rope_w=64, page_size=64, lens=lens, kv="fp8",
+                  rms_mode="log8", seed=41 + qrows + heads, device=gpu, qrows=qrows, rms="spread", amp=2.0)
+    rows = c.q_nope.shape[0]
+    o = torch.full((rows, heads, 512), float("nan"), dtype=torch.bfloat16, device=gpu)
+    lse = torch.full((rows, heads), float("nan"), dtype=torch.float32, device=gpu)
+    _forward(c, num_workgroups=nwg, num_splits=splits, out=o, lse=lse)
+    assert not torch.isnan(o.float()).any() and not torch.isnan(lse).any(), "unwritten rows"
+    _check(f"head split {heads}x{qrows} nwg {nwg} S={splits}", c, o, lse)
