@@ -483,10 +483,14 @@ def main():
     k_gbps = k_bytes / (part_ms / 1e3) / 1e9
     traffic = measured_traffic(args.workload)
 
-    # the warp-specialized kernel's fp8 score path serves fp8 + log8 rows, d_c 512, rope 64, one
-    # latent group and at most 32 rows per request, or GLA-g2 with at most 48 rows per group
+    # the warp-specialized kernel's fp8 score path serves fp8 + log8 rows, d_c 512, rope 64: one latent
+    # group with at most 32 rows per workgroup (a request's heads split over up to 4 workgroups), or
+    # GLA-g2 with at most 48 rows per group
+    ws_rows = case.qrows * case.heads // case.groups
     ws_fp8 = (case.kv == "fp8" and case.rms_mode == "log8" and case.d_c // case.groups in (512, 256)
-              and case.rope_w == 64 and case.qrows * case.heads // case.groups <= (32 if case.groups == 1 else 48))
+              and case.rope_w == 64
+              and (ws_rows <= 48 if case.groups == 2 else
+                   any(case.heads % hs == 0 and ws_rows // hs <= 32 for hs in range(1, 5))))
     cpu = None
     if not args.no_cpu:
         cpu = cpu_baseline(case, args.cpu_every or CPU_EVERY.get(args.workload, 2), args.cpu_budget)

@@ -102,3 +102,32 @@ def test_ws_head_split_verify(gpu, heads, qrows, nwg, splits):
     _forward(c, num_workgroups=nwg, num_splits=splits, out=o, lse=lse)
     assert not torch.isnan(o.float()).any() and not torch.isnan(lse).any(), "unwritten rows"
     _check(f"head split {heads}x{qrows} nwg {nwg} S={splits}", c, o, lse)
+
+
+@pytest.mark.parametrize("where", ["latent", "rope", "both"])
+def test_ws_query_outlier_channels(gpu, where):
+    """Query rows whose elements span more than 2^10: a few outlier channels per row (x 1024 over the
+    rest), as the reference's FP8 test draws outlier latent channels (tests/test_fp8_kv.py:23-31). The
+    fp8 score path splits the bf16 query into two e4m3 parts scaled to the row maximum, so the small
+    elements lose low bits to e4m3 subnormals; the output stays within the parity bound."""
+    lens = [700, 3000, 64, 1500]
+    c = make_case(batch=len(lens), heads=24, d_c=512, rope_w=64, page_size=64, lens=lens, kv="fp8",
+                  rms_mode="log8", seed=77, device=gpu, rms="spread", amp=4.0)
+    g = torch.Generator(device="cpu").manual_seed(78)
+    rows = c.q_nope.shape[0]
+    qn = torch.randn(rows, 24, 512, generator=g) * 0.02
+    qp = torch.randn(rows, 24, 64, generator=g) * 0.02
+    for r in range(rows):
+        for h in range(24):
+            # outliers of magnitude 24 against a median |q| of about 0.0135
+            if where in ("latent", "both"):
+                qn[r, h, torch.randperm(512, generator=g)[:4]] = 24.0 * torch.sign(torch.randn(4, generator=g))
+            if where in ("rope", "both"):
+                qp[r, h, torch.randperm(64, generator=g)[:2]] = 24.0 * torch.sign(torch.randn(2, generator=g))
+    c.q_nope = qn.to(torch.bfloat16).to(gpu)
+    c.q_pe = qp.to(torch.bfloat16).to(gpu)
+    amax = torch.cat([qn, qp], -1).abs().amax(-1)
+    amin = torch.cat([qn, qp], -1).abs().clamp_min(1e-30).median(-1).values
+    assert (amax / amin).min() > 2 ** 10
+    o, lse = _forward(c, num_workgroups=9)
+    _check(f"query outliers in {where}", c, o, lse)
