@@ -35,7 +35,7 @@
 extern "C" {
 #endif
 
-#define QMLA_ABI_VERSION 1
+#define QMLA_ABI_VERSION 2
 
 /* error codes */
 #define QMLA_OK 0
@@ -46,6 +46,7 @@ extern "C" {
 #define QMLA_ERR_MODE (-5)        /* unknown dtype / rms mode / split mode */
 #define QMLA_ERR_LAUNCH (-6)      /* the HIP launch itself failed */
 #define QMLA_ERR_NOKERNEL (-7)    /* no compiled kernel instance for this shape */
+#define QMLA_ERR_PAGE (-8)        /* (stored into *status) a block-table entry outside [0, num_pages) */
 
 /* cache element formats */
 #define QMLA_KV_BF16 0
@@ -134,6 +135,14 @@ typedef struct qmla_decode_params {
 
   /* balanced mode only: workgroups to launch, 0 = one per compute unit times occupancy */
   int32_t num_workgroups;
+
+  /* page-id bound. num_pages > 0: every block-table entry a kernel reads is checked against
+   * [0, num_pages); an entry outside it reads page 0 instead (in bounds; the outputs of that request
+   * are then meaningless) and, when status is not NULL, the pass stores QMLA_ERR_PAGE into *status
+   * (device int32) before it ends. The library never clears *status. num_pages == 0: entries are
+   * trusted, as the reference trusts them. */
+  int32_t num_pages;
+  int32_t* status;
 } qmla_decode_params;
 
 /* ABI version (QMLA_ABI_VERSION) and a static build string. */

@@ -47,7 +47,20 @@ struct KParams {
   int q_vec;        // query rows and strides 16-byte aligned: 16-byte query loads (else element loads)
   int hsplit;       // warp-specialized kernel: workgroups sharing a request's token range, each with
                     // heads/hsplit of its heads (balanced mode: nwg ranges x hsplit workgroups)
+  uint32_t page_bound;  // block-table entries must lie in [0, page_bound)
+  int* status;          // QMLA_ERR_PAGE is stored here when one does not (may be null)
 };
+
+// A block-table entry checked against the page bound: an entry outside [0, page_bound) reads page 0
+// (in bounds) and raises `bad`, which the kernel reports once its memory traffic has drained.
+__device__ __forceinline__ int checked_page(const KParams& p, int id, int& bad) {
+  const bool ok = (uint32_t)id < p.page_bound;
+  bad |= ok ? 0 : 1;
+  return ok ? id : 0;
+}
+__device__ __forceinline__ void report_pages(const KParams& p, int bad) {
+  if (bad && p.status) *p.status = QMLA_ERR_PAGE;
+}
 
 // 8 consecutive query elements: one 16-byte load when the caller's query rows are 16-byte aligned,
 // else eight element loads (queries are read once per request or segment, so this costs nothing

@@ -143,7 +143,7 @@ __device__ __forceinline__ void wait_tile(bool steady, bool rms_wave) {
 // One contiguous token range [ta, te) of request `req` (length L), all query rows.
 template <class C>
 __device__ __forceinline__ void segment(const KParams& p, Smem<C>& sm, int req, int ta, int te, int L,
-                                        const SegOut& so, float kscale) {
+                                        const SegOut& so, float kscale, int& bad) {
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -280,7 +280,7 @@ __device__ __forceinline__ void segment(const KParams& p, Smem<C>& sm, int req, 
     const int np = (se - 1) / P - pbase + 1;
     wait_vmcnt<0>();
     lds_barrier();   // every wave is done with the previous sub-range's page ids
-    for (int i = tid; i < np; i += C::NTHR) sm.pid[i] = btrow[pbase + i];
+    for (int i = tid; i < np; i += C::NTHR) sm.pid[i] = checked_page(p, btrow[pbase + i], bad);
     __syncthreads();
     const int nt = (se - sa + C::TT - 1) / C::TT;
 
@@ -794,10 +794,12 @@ __global__ __launch_bounds__(C::NTHR, 1) void cs_kernel(const KParams p) {
   // the reference does (mla_decode_attention.py:451-463)
   const float kscale = (C::EB == 1 && p.k_scale) ? *p.k_scale : 1.0f;
   if (p.num_splits == 0 && blockIdx.x == 0 && blockIdx.z == 0 && threadIdx.x < 64) store_plan(p);   // for the combine
+  int bad = 0;
   for_each_segment<C::DCG>(p, [&](int req, int a, int e, int L, const SegOut& so) {
-    segment<C>(p, sm, req, a, e, L, so, kscale);
+    segment<C>(p, sm, req, a, e, L, so, kscale, bad);
     // the next range starts its sub-range set-up with a full barrier; nothing else to reset
   });
+  report_pages(p, bad);
 }
 
 struct Inst {

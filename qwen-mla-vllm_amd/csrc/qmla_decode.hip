@@ -135,7 +135,7 @@ struct Smem {
 // accumulator (O = P . V) keeps the D layout: lane (col ln16, lg) holds rows mb*16 + 4*lg + i.
 template <class C>
 __device__ __forceinline__ void process_segment(const KParams& p, Smem<C>& sm, int req, int tok_a, int tok_e,
-                                                int L, const SegOut& so, float kscale) {
+                                                int L, const SegOut& so, float kscale, int& bad) {
   constexpr int TILE = C::TILE;
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform -> SGPR
@@ -190,7 +190,7 @@ __device__ __forceinline__ void process_segment(const KParams& p, Smem<C>& sm, i
     if (tok0 / P == (tok0 + TILE - 1) / P && p.token_stride_b == C::RB) {
       // the TILE rows are consecutive in one page: one contiguous block, addressed through a
       // buffer resource so the per-tile cost is scalar (rows past tok_e stay inside the page)
-      const int page = __builtin_amdgcn_readfirstlane(pidt[0]);
+      const int page = checked_page(p, __builtin_amdgcn_readfirstlane(pidt[0]), bad);
       const char* base = p.kv + (int64_t)page * p.page_stride_b + (int64_t)(tok0 % P) * p.token_stride_b;
       const __amdgpu_buffer_rsrc_t rsrc = make_rsrc(base, (uint32_t)(TILE * C::RB));
 #pragma unroll
@@ -202,7 +202,7 @@ __device__ __forceinline__ void process_segment(const KParams& p, Smem<C>& sm, i
     }
     int tok = tok0 + (lane < TILE ? lane : TILE - 1);
     tok = tok < tok_e ? tok : tok_e - 1;
-    const int64_t off = (int64_t)pidt[lane < TILE ? lane : TILE - 1] * p.page_stride_b +
+    const int64_t off = (int64_t)checked_page(p, pidt[lane < TILE ? lane : TILE - 1], bad) * p.page_stride_b +
                         (int64_t)(tok % P) * p.token_stride_b;
     const int off_lo = (int)(uint32_t)off, off_hi = (int)(uint32_t)((uint64_t)off >> 32);
 #pragma unroll
@@ -598,9 +598,11 @@ __global__ __launch_bounds__(C::NTHR, C::WGPC) void partial_kernel(const KParams
   // the reference does (mla_decode_attention.py:451-463)
   const float kscale = (C::EB == 1 && p.k_scale) ? *p.k_scale : 1.0f;
   if (p.num_splits == 0 && blockIdx.x == 0 && threadIdx.x < 64) store_plan(p);   // for the combine
+  int bad = 0;
   for_each_segment<C::DCG>(p, [&](int req, int a, int e, int L, const SegOut& so) {
-    process_segment<C>(p, sm, req, a, e, L, so, kscale);
+    process_segment<C>(p, sm, req, a, e, L, so, kscale, bad);
   });
+  report_pages(p, bad);
 }
 
 // Balanced plan: tiles per request, prefix sums, per-workgroup chunk. One workgroup.
@@ -821,6 +823,12 @@ static const Inst kInst[] = {
     QMLA_INST(2, QMLA_RMS_BF16, 512, 64, 2, 1, 2, 75, false, 64, 1, 4),
     QMLA_INST(2, QMLA_RMS_BF16, 512, 64, 2, 1, 2, 75, true, 64, 1, 4),
     QMLA_INST(2, QMLA_RMS_NONE, 512, 64, 2, 1, 2, 72, false, 64, 1, 4),
+    // GLA-g2 (two latent groups of 256, 12 heads each, up to 4 verify tokens: 48 rows per group) on
+    // the cache formats the warp-specialized kernel does not take: fp8 rows with e4m3 or bf16-byte
+    // rms, bf16 rows with bf16 rms (the reference decodes them as its rank-local TP = 2 shape)
+    QMLA_INST(1, QMLA_RMS_E4M3, 256, 64, 3, 2, 3, 38, false, 64, 1, 4),
+    QMLA_INST(1, QMLA_RMS_BF16_BYTES, 256, 64, 3, 2, 3, 39, false, 64, 1, 4),
+    QMLA_INST(2, QMLA_RMS_BF16, 256, 64, 3, 2, 3, 75, false, 32, 1, 4),
     // the plugin's deployed fp8 layouts (tests/test_fp8_kv.py): partial rope of 4 groups x 58 = 232
     // with 24 heads (one GPU) or 2 x 58 = 116 with 12 heads (rank-local at TP 2), latent ranks 256
     // and 768; rows [latent | rope | rms (1 byte, or 2 for raw bf16) | pad to 16 bytes]
@@ -910,7 +918,7 @@ static int validate(const qmla_decode_params* p) {
   if (p->heads % p->groups || p->d_c % p->groups) return QMLA_ERR_SHAPE;
   if (p->rms_mode != QMLA_RMS_NONE && (p->rms_heads < p->heads / p->groups * p->groups || p->rms_heads <= 0))
     return QMLA_ERR_SHAPE;
-  if (p->num_splits < 0 || p->num_splits > CF_MAXS || p->split_align < 0) return QMLA_ERR_SHAPE;
+  if (p->num_splits < 0 || p->num_splits > CF_MAXS || p->split_align < 0 || p->num_pages < 0) return QMLA_ERR_SHAPE;
   const int eb = elem_bytes(p->kv_dtype);
   if (!aligned16(p->kv_cache) || (p->page_stride * eb) % 16 || (p->token_stride * eb) % 16) return QMLA_ERR_ALIGN;
   if (needed_row_bytes(p) > p->token_stride * eb && p->page_size > 1) return QMLA_ERR_SHAPE;
@@ -1017,6 +1025,9 @@ static KParams make_kparams(const qmla_decode_params* p) {
   k.ws_sr = p->ws_stride_row;
   k.ws_sh = p->ws_stride_head;
   k.ws_ss = p->ws_stride_split;
+  // without a page count only negative entries are caught
+  k.page_bound = p->num_pages > 0 ? (uint32_t)p->num_pages : 0x80000000u;
+  k.status = p->status;
   k.nwg = 0;
   k.plan = nullptr;
   k.part_o = nullptr;

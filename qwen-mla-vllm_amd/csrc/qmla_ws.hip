@@ -331,7 +331,7 @@ __device__ void plan_window(const KParams& p, Smem<C>& sm, bool fixed, int lo, i
 // registers live (score waves the query fragments, value waves the accumulators).
 template <class C, int ROLE>
 __device__ __forceinline__ void role_main(const KParams& p, Smem<C>& sm, float kscale, bool fixed, int lo,
-                                          int hi, int b0, int c0, int wr, int hz) {
+                                          int hi, int b0, int c0, int wr, int hz, int& bad) {
   constexpr int NTHR = C::NTHR;
   constexpr bool F8 = C::EB == 1;
   constexpr int NB = C::DCG / 128;       // latent blocks of the fp8 product
@@ -612,7 +612,8 @@ __device__ __forceinline__ void role_main(const KParams& p, Smem<C>& sm, float k
       }
       const SegD& d = sm.seg[k0];
       // a folded request reads the block-table row of its last verify row, as its length does
-      sm.pid[f] = p.bt[((int64_t)d.req * qrows + qrows - 1) * p.bt_stride + d.ta / P + (f - d.pf)];
+      sm.pid[f] = checked_page(p, p.bt[((int64_t)d.req * qrows + qrows - 1) * p.bt_stride + d.ta / P + (f - d.pf)],
+                               bad);
     }
     __syncthreads();
 
@@ -1098,8 +1099,10 @@ __global__ __launch_bounds__(C::NTHR, 1) void ws_kernel(const KParams p) {
     c0 = r.c0;
     if (lo >= hi) return;
   }
-  if (wv < 4) role_main<C, SCORE>(p, sm, kscale, fixed, lo, hi, b0, c0, wr, hz);
-  else role_main<C, VALUE>(p, sm, kscale, fixed, lo, hi, b0, c0, wr, hz);
+  int bad = 0;
+  if (wv < 4) role_main<C, SCORE>(p, sm, kscale, fixed, lo, hi, b0, c0, wr, hz, bad);
+  else role_main<C, VALUE>(p, sm, kscale, fixed, lo, hi, b0, c0, wr, hz, bad);
+  report_pages(p, bad);
 }
 
 struct Inst {

@@ -14,11 +14,11 @@ import torch  # noqa: F401  (loads the HIP runtime the library binds to)
 LIB_NAME = "libqmla.so"
 LIB_PATH = pathlib.Path(__file__).resolve().parent / LIB_NAME
 
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 # error codes (include/qmla.h)
 OK = 0
-ERR_NULL, ERR_SHAPE, ERR_ALIGN, ERR_WORKSPACE, ERR_MODE, ERR_LAUNCH, ERR_NOKERNEL = -1, -2, -3, -4, -5, -6, -7
+ERR_NULL, ERR_SHAPE, ERR_ALIGN, ERR_WORKSPACE, ERR_MODE, ERR_LAUNCH, ERR_NOKERNEL, ERR_PAGE = -1, -2, -3, -4, -5, -6, -7, -8
 ERR_NAMES = {
     ERR_NULL: "QMLA_ERR_NULL (a required pointer is NULL)",
     ERR_SHAPE: "QMLA_ERR_SHAPE (unsupported or inconsistent dimension)",
@@ -27,6 +27,7 @@ ERR_NAMES = {
     ERR_MODE: "QMLA_ERR_MODE (unknown dtype / rms mode / split mode)",
     ERR_LAUNCH: "QMLA_ERR_LAUNCH (HIP launch failed)",
     ERR_NOKERNEL: "QMLA_ERR_NOKERNEL (no compiled kernel instance for this shape)",
+    ERR_PAGE: "QMLA_ERR_PAGE (a block-table entry outside [0, num_pages))",
 }
 
 KV_BF16, KV_FP8 = 0, 1
@@ -80,6 +81,8 @@ class DecodeParams(ctypes.Structure):
         ("ws_stride_head", ctypes.c_int64),
         ("ws_stride_split", ctypes.c_int64),
         ("num_workgroups", ctypes.c_int32),
+        ("num_pages", ctypes.c_int32),
+        ("status", ctypes.c_void_p),
     ]
 
 

@@ -109,9 +109,13 @@ def _check_layout(*, q_nope, q_pe, kv_cache, block_table, seq_lens, out, lse) ->
 def build_params(*, q_nope, q_pe, kv_cache, block_table, seq_lens, out, lse, d_c, rope_w, rms_offset,
                  rms_mode, kv, page_size, sm_scale, k_scale=None, logit_cap=0.0, qrows=1, groups=1,
                  rms_heads=None, num_splits=0, split_align=0, workspace=None, ws_strides=(0, 0, 0),
-                 num_workgroups=0) -> DecodeParams:
+                 num_workgroups=0, status=None) -> DecodeParams:
     """Fill the C parameter block. Pure host work (no device access), so it is testable anywhere.
-    Raises TypeError / ValueError for metadata or strides the kernels cannot read as given."""
+    Raises TypeError / ValueError for metadata or strides the kernels cannot read as given.
+
+    The cache's page count bounds every block-table entry the kernels read: an entry outside it
+    reads page 0 instead of faulting, and QMLA_ERR_PAGE is stored into `status` (a device int32
+    tensor the caller clears) when one is given."""
     _check_layout(q_nope=q_nope, q_pe=q_pe if (q_pe is not None and rope_w > 0) else None, kv_cache=kv_cache,
                   block_table=block_table, seq_lens=seq_lens, out=out, lse=lse)
     rows, heads = q_nope.shape[0], q_nope.shape[1]
@@ -151,6 +155,11 @@ def build_params(*, q_nope, q_pe, kv_cache, block_table, seq_lens, out, lse, d_c
         p.workspace_bytes = workspace.numel() * workspace.element_size()
     p.ws_stride_row, p.ws_stride_head, p.ws_stride_split = ws_strides
     p.num_workgroups = num_workgroups
+    p.num_pages = kv_cache.shape[0] if kv_cache.dim() == 4 else kv_cache.shape[0] // page_size
+    if status is not None:
+        if status.dtype != torch.int32 or status.numel() < 1:
+            raise TypeError("status must be a device int32 tensor")
+        p.status = _ptr(status)
     return p
 
 
@@ -251,14 +260,15 @@ _default_ws: dict = {}
 def forward(q_nope, q_rope, kv_cache, block_table, seq_lens, *, d_c=None, rope_w=None, rms_offset=None,
             page_size, sm_scale, kv_fp8=None, fp8_rms="log8", k_scale=None, qrows=1, groups=1,
             rms_heads=None, logit_cap=0.0, out=None, lse=None, num_splits=0, workspace=None,
-            num_workgroups=0, return_lse=True):
+            num_workgroups=0, return_lse=True, status=None):
     """Decode every query row against its paged latent rows; returns (o, lse).
 
     q_nope [rows, H, d_c/G] absorbed latent queries, q_rope [rows, H, rope_w]; kv_cache
     [num_pages, page_size, (1,) row] with rows [latent d_c | rope rope_w | rms | pad]; block_table
     [rows, max_pages] int32, seq_lens [rows] int32 (spec-verify requests flattened one row per
     token). groups = 2 computes GLA-g2 (head h reads latent group h // (H/2)) in one launch and
-    returns [rows, H, d_c/2]. num_splits = 0 selects the balanced split mode.
+    returns [rows, H, d_c/2]. num_splits = 0 selects the balanced split mode. Block-table entries
+    outside the cache's pages read page 0 and store QMLA_ERR_PAGE into `status` (device int32).
     """
     _check_device(q_nope, kv_cache, block_table, seq_lens)
     rows, H = q_nope.shape[0], q_nope.shape[1]
@@ -285,7 +295,7 @@ def forward(q_nope, q_rope, kv_cache, block_table, seq_lens, *, d_c=None, rope_w
                 out=out, lse=lse, d_c=d_c, rope_w=rope_w, rms_offset=rms_offset, rms_mode=mode, kv=kv,
                 page_size=page_size, sm_scale=sm_scale, k_scale=k_scale, logit_cap=logit_cap, qrows=qrows,
                 groups=groups, rms_heads=rms_heads, num_splits=num_splits,
-                split_align=16 if page_size % 16 == 0 else 0, num_workgroups=num_workgroups)
+                split_align=16 if page_size % 16 == 0 else 0, num_workgroups=num_workgroups, status=status)
     lib = _lib.lib()
     ws_t = None
     ws_strides = (0, 0, 0)

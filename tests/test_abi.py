@@ -41,6 +41,7 @@ def test_version_and_constants_match_header():
     for name, val in [("QMLA_ERR_NULL", _lib.ERR_NULL), ("QMLA_ERR_SHAPE", _lib.ERR_SHAPE),
                       ("QMLA_ERR_ALIGN", _lib.ERR_ALIGN), ("QMLA_ERR_WORKSPACE", _lib.ERR_WORKSPACE),
                       ("QMLA_ERR_MODE", _lib.ERR_MODE), ("QMLA_ERR_NOKERNEL", _lib.ERR_NOKERNEL),
+                      ("QMLA_ERR_PAGE", _lib.ERR_PAGE),
                       ("QMLA_KV_FP8", _lib.KV_FP8), ("QMLA_RMS_LOG8", _lib.RMS_LOG8),
                       ("QMLA_RMS_E4M3", _lib.RMS_E4M3), ("QMLA_DT_F32", _lib.DT_F32)]:
         assert int(consts[name]) == val, name
@@ -136,13 +137,13 @@ def _layout(kv, d_c, rope, heads, rms, qrows=1, groups=1):
     entry returns ERR_WORKSPACE once it has an instance for the shape and ERR_NOKERNEL otherwise: the
     routing is checked without a launch."""
     eb = 1 if kv == _lib.KV_FP8 else 2
-    rb = 2 if rms in (_lib.RMS_BF16, _lib.RMS_BF16_BYTES) else 1
+    rb = 2 if rms in (_lib.RMS_BF16, _lib.RMS_BF16_BYTES) else 0 if rms == _lib.RMS_NONE else 1
     row_bytes = d_c * eb + rope * eb + heads * rb
     row_bytes += (-row_bytes) % 16
     ts = row_bytes // eb
     dcg = d_c // groups
     return _valid_params(kv_dtype=kv, d_c=d_c, rope_w=rope, heads=heads, rms_heads=heads, rms_mode=rms,
-                         rms_offset=d_c + rope, token_stride=ts, page_stride=64 * ts, qrows=qrows, groups=groups,
+                         rms_offset=-1 if rms == _lib.RMS_NONE else d_c + rope, token_stride=ts, page_stride=64 * ts, qrows=qrows, groups=groups,
                          rows=2 * qrows, q_nope_stride_row=heads * dcg, q_nope_stride_head=dcg,
                          q_pe_stride_row=heads * rope, q_pe_stride_head=rope, out_stride_row=heads * dcg,
                          out_stride_head=dcg, workspace=None, num_splits=4)
@@ -165,9 +166,13 @@ def _layout(kv, d_c, rope, heads, rms, qrows=1, groups=1):
     # 24 heads x 4 verify tokens, FP8 + log8: the heads split over three workgroups per range
     (_lib.KV_FP8, 512, 64, 24, _lib.RMS_LOG8, 4, 1, _lib.ERR_WORKSPACE),
     (_lib.KV_FP8, 512, 64, 24, _lib.RMS_E4M3, 4, 1, _lib.ERR_NOKERNEL),      # other rms formats: 32 rows
-    # GLA-g2 with 4 verify tokens: FP8 + log8 only
+    # GLA-g2 with 4 verify tokens: FP8 + log8 (warp-specialized), FP8 + e4m3 / bf16-byte rms and
+    # bf16 rows (per-group kernel); no instance without an rms tail
     (_lib.KV_FP8, 512, 64, 24, _lib.RMS_LOG8, 4, 2, _lib.ERR_WORKSPACE),
-    (_lib.KV_BF16, 512, 64, 24, _lib.RMS_BF16, 4, 2, _lib.ERR_NOKERNEL),
+    (_lib.KV_FP8, 512, 64, 24, _lib.RMS_E4M3, 4, 2, _lib.ERR_WORKSPACE),
+    (_lib.KV_FP8, 512, 64, 24, _lib.RMS_BF16_BYTES, 4, 2, _lib.ERR_WORKSPACE),
+    (_lib.KV_BF16, 512, 64, 24, _lib.RMS_BF16, 4, 2, _lib.ERR_WORKSPACE),
+    (_lib.KV_BF16, 512, 64, 24, _lib.RMS_NONE, 4, 2, _lib.ERR_NOKERNEL),
 ])
 def test_routing_without_launch(kv, d_c, rope, heads, rms, qrows, groups, code):
     lib = _lib.lib()
@@ -220,6 +225,23 @@ def test_build_params_reads_real_strides():
                       d_c=512, rope_w=64, rms_offset=576, rms_mode=_lib.RMS_LOG8, kv=_lib.KV_FP8, page_size=64,
                       sm_scale=0.1)
     assert (p3.page_stride, p3.token_stride) == (64 * 608, 608) and p3.lse is None
+    # the page bound: pages of the 4-D view, tokens / page_size of the 3-D cache; no status word
+    assert p.num_pages == 7 and p3.num_pages == 10 and not p.status
+    status = torch.zeros(1, dtype=torch.int32)
+    p4 = build_params(q_nope=qn, q_pe=qp, kv_cache=flat, block_table=bt, seq_lens=sl, out=out, lse=None,
+                      d_c=512, rope_w=64, rms_offset=576, rms_mode=_lib.RMS_LOG8, kv=_lib.KV_FP8, page_size=64,
+                      sm_scale=0.1, status=status)
+    assert p4.status == status.data_ptr()
+    with pytest.raises(TypeError):
+        build_params(q_nope=qn, q_pe=qp, kv_cache=flat, block_table=bt, seq_lens=sl, out=out, lse=None,
+                     d_c=512, rope_w=64, rms_offset=576, rms_mode=_lib.RMS_LOG8, kv=_lib.KV_FP8, page_size=64,
+                     sm_scale=0.1, status=torch.zeros(1, dtype=torch.int64))
+
+
+def test_negative_page_count_rejected():
+    lib = _lib.lib()
+    p = _valid_params(num_splits=4, num_pages=-1)
+    assert lib.qmla_decode(ctypes.byref(p), None) == _lib.ERR_SHAPE
 
 
 def _bp_args(**over):

@@ -60,3 +60,24 @@ def test_gla_long_requests(gpu):
     c = _case(gpu, [40000, 31001], seed=57)
     o, lse = _forward(c, num_workgroups=64)
     _check("gla 2 long requests over 64 workgroups", c, o, lse)
+
+
+# GLA-g2 on the cache formats of the per-group kernel (fp8 rows with e4m3 or bf16-byte rms, bf16 rows
+# with bf16 rms): 48 rows per group with 4 verify tokens, 12 with one
+GLA_FORMATS = [("fp8", "e4m3"), ("fp8", "bf16_bytes"), ("bf16", "bf16")]
+
+
+@pytest.mark.parametrize("kv,rms_mode", GLA_FORMATS)
+@pytest.mark.parametrize("qrows,splits", [(4, 0), (4, 5), (1, 0)])
+def test_gla_other_formats(gpu, kv, rms_mode, qrows, splits):
+    import qmla
+    lens = [1, 900, 4097, 2500, 33, 0] if splits == 0 else [1, 900, 4097, 2500, 33]
+    c = make_case(batch=len(lens), heads=24, d_c=512, rope_w=64, page_size=64, lens=lens, kv=kv,
+                  rms_mode=rms_mode, seed=60 + qrows + splits, device=gpu, qrows=qrows, groups=2, rms="spread",
+                  amp=4.0 if kv == "fp8" else 1.0)
+    fp8_rms = {"e4m3": "e4m3", "bf16_bytes": "bf16"}.get(rms_mode, "log8")
+    o, lse = qmla.forward(c.q_nope, c.q_pe, c.cache, c.block_table, c.seq_lens, d_c=c.d_c, page_size=c.page_size,
+                          sm_scale=c.sm_scale, kv_fp8=kv == "fp8", fp8_rms=fp8_rms, k_scale=c.k_scale,
+                          qrows=qrows, groups=2, num_splits=splits, num_workgroups=0 if splits else 6)
+    torch.cuda.synchronize()
+    _check(f"gla {kv}/{rms_mode} q{qrows} splits {splits}", c, o, lse)
