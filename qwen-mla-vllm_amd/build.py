@@ -31,6 +31,7 @@ SOURCES = [
     (CSRC / "qmla_decode.hip", ["-mllvm", "-amdgpu-mfma-vgpr-form"]),
     (CSRC / "qmla_cs.hip", ["-mllvm", "-amdgpu-mfma-vgpr-form"]),
     (CSRC / "qmla_ws.hip", ["-mllvm", "-amdgpu-mfma-vgpr-form"]),
+    (CSRC / "qmla_ro.hip", ["-mllvm", "-amdgpu-mfma-vgpr-form"]),
     (CSRC / "qmla_write.hip", []),
     (CSRC / "qmla_prep.hip", []),
 ]

@@ -264,6 +264,11 @@ int ws_select(const qmla_decode_params* p);
 int ws_head_split(const qmla_decode_params* p);
 int ws_launch(int inst, const qmla_decode_params* p, const KParams& k, int nwg, hipStream_t st);
 
+// ---- host-side interface of the row-owner translation unit (qmla_ro.hip) ----
+// Index of a compiled row-owner instance for these params (GLA-g2 on fp8 + log8 rows), or -1.
+int ro_select(const qmla_decode_params* p);
+int ro_launch(int inst, const qmla_decode_params* p, const KParams& k, int nwg, hipStream_t st);
+
 // ---- host-side interface of the column-split translation unit (qmla_cs.hip) ----
 // Index of a compiled column-split instance for these params, or -1.
 int cs_select(const qmla_decode_params* p);

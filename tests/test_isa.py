@@ -68,6 +68,18 @@ def test_ws_scalar_loads_drained_before_lds(tmp_path):
     assert n >= 1
 
 
+def test_ro_scalar_loads_drained_before_lds(tmp_path):
+    """The row-owner GLA decode counts its LDS waits the same way."""
+    lines = _assembly(tmp_path, "qmla_ro.hip")
+    n = 0
+    for name, body in _kernels(lines, r"^_ZN4qmla2ro9ro_kernel\S*:"):
+        n += 1
+        hz = _hazards(body)
+        assert not hz, f"{name}: scalar load in flight at an LDS operation: {hz[:3]}"
+        assert any("lgkmcnt(" in l and "lgkmcnt(0)" not in l for l in body), "counted waits expected"
+    assert n >= 1
+
+
 def test_hazard_check_sees_a_planted_overlap():
     body = ["s_load_dword s4, s[0:1], 0x10", "ds_read_b128 v[0:3], v4", "s_waitcnt lgkmcnt(0)"]
     assert _hazards(body)
