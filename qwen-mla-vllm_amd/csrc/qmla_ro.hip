@@ -111,7 +111,9 @@ __device__ __forceinline__ void role_main(const KParams& p, Smem<C>& sm, float k
 
   i32x8 qh8[ROLE == COMPUTE ? C::NBQ : 1], ql8[ROLE == COMPUTE ? C::NBQ : 1];
   int qsc = 127;   // E8M0 scale of the row's query parts: 2^-e
-  const float lc2 = 3.0f + fast_log2(c2b);   // rms multiplier c2b / rms = 2^(lc2 - code*6/255)
+  // rms multiplier |c2b| / rms = 2^(lc2 - code*6/255); the sign of c2b goes into the query
+  const float lc2 = 3.0f + fast_log2(c2b != 0.f ? fabsf(c2b) : 1.0f);
+  const float qsign = c2b > 0.f ? 1.0f : c2b < 0.f ? -1.0f : 0.0f;
   float mref = kNegInf, lpart = 0.f;
   f32x4 acc[ROLE == COMPUTE ? C::CB : 1];
 #pragma unroll
@@ -141,7 +143,7 @@ __device__ __forceinline__ void role_main(const KParams& p, Smem<C>& sm, float k
       for (int e = 0; e < 8; ++e) mx = fmaxf(mx, fabsf((float)qn[k][e]));
     mx = max_lg(mx);
     const float ex = mx > 0.f ? fminf(floorf(fast_log2(224.0f / mx)), 126.0f) : 0.0f;
-    const float qs = fast_exp2(ex);
+    const float qs = fast_exp2(ex) * qsign;
     qsc = 127 - (int)ex;
     int hq[2 * C::KQ], lq[2 * C::KQ];
 #pragma unroll
@@ -548,7 +550,7 @@ static const RoFn kRo[] = {&ro_kernel<RO<5>>};
 // at most 48 rows per group, 608-byte staged rows holding every head's code, no logit cap.
 int ro_select(const qmla_decode_params* p) {
   if (p->groups != 2 || p->kv_dtype != QMLA_KV_FP8 || p->rms_mode != QMLA_RMS_LOG8) return -1;
-  if (p->d_c != 512 || p->rope_w != 64 || p->logit_cap > 0.f || !(p->sm_scale > 0.f)) return -1;
+  if (p->d_c != 512 || p->rope_w != 64 || p->logit_cap > 0.f) return -1;
   if (p->qrows * (p->heads / 2) > 48) return -1;
   if (p->token_stride < 608 || (int64_t)p->rms_offset + p->heads > 608) return -1;
   return 0;

@@ -916,8 +916,8 @@ static const Inst kInst[] = {
     QMLA_WS(1, QMLA_RMS_LOG8, 512, 3, 38, false, false, 1, 1),
     // ... up to 16 heads (592-byte rows), rms codes read per row
     QMLA_WS(1, QMLA_RMS_LOG8, 512, 3, 37, false, false, 1, 1),
-    // GLA-g2: two latent groups of 256 columns, up to 48 rows per group (12 heads x 4 verify tokens)
-    QMLA_WS(1, QMLA_RMS_LOG8, 256, 3, 38, false, false, 1, 2),
+    // (GLA-g2 on these rows runs in the row-owner kernel, qmla_ro.hip; the G = 2 form of this
+    // template is kept but not instantiated)
 };
 
 }  // namespace ws

@@ -81,3 +81,13 @@ def test_gla_other_formats(gpu, kv, rms_mode, qrows, splits):
                           qrows=qrows, groups=2, num_splits=splits, num_workgroups=0 if splits else 6)
     torch.cuda.synchronize()
     _check(f"gla {kv}/{rms_mode} q{qrows} splits {splits}", c, o, lse)
+
+
+@pytest.mark.parametrize("sm_scale", [-0.05, 0.0])
+def test_gla_sign_of_the_scale(gpu, sm_scale):
+    """A negative or zero softmax scale (the reference takes any float): the row-owner kernel folds
+    its sign into the query parts."""
+    c = _case(gpu, [700, 33, 2049], seed=70)
+    c.sm_scale = sm_scale
+    o, lse = _forward(c, num_workgroups=4)
+    _check(f"gla sm_scale {sm_scale}", c, o, lse)
