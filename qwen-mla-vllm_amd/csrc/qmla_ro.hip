@@ -16,10 +16,11 @@
 // The workgroup meets once per tile at one barrier (the ring stage of tile g is refilled after it).
 // Rows are ordered head-major within a group (row = head * qrows + verify token).
 //
-// Staged rows are rotated by 16-byte chunks: chunk c of row r sits at position (c + f(r)) mod CPR,
-// f(r) = (r & 15) ^ ((r >> 1) & 8). With 608-byte rows that keeps the K reads (16 consecutive rows)
-// and the transposed V reads (rows 4lg..4lg+3 and 16+4lg..16+4lg+3 of lane group lg) on distinct
-// banks.
+// Staged rows keep each 16-byte chunk inside its region (four latent blocks of 8 chunks, the rope's
+// 4, the rms codes' 2), rotated there by f(r) = ((r >> 3) + (r >> 4)) & 1. With 608-byte rows (152
+// dwords, 24 banks apart) that keeps the K reads (16 consecutive rows) and the transposed V reads
+// (rows 4lg..4lg+3 and 16+4lg..16+4lg+3 of lane group lg) on distinct banks, and a lane's reads of
+// every latent block share one base register: the block and chunk go into the offset fields.
 //
 // Reference semantics: qwen_mla/ops/mla_decode_attention.py:297-586 (stage 1: fp8 dequant :451-463,
 // rms divide :466-507, online softmax :553-560, partial store :562-586), with the GLA-g2 head-to-group
@@ -40,9 +41,11 @@ using namespace ws;
 constexpr float SHIFT = 15.0f;   // P = exp2(s - ref) <= 2^15 (fp16) before a row's reference moves
 enum Role { COMPUTE, DMA };
 
-// A tiles in flight ahead of the compute waves (ring of A + 1 stages).
-template <int A_>
+// A tiles in flight ahead of the compute waves (ring of A + 1 stages); QUAD: 4 verify rows per head,
+// whose lanes 4k..4k+3 share each rms code through a DPP broadcast.
+template <int A_, bool QUAD_>
 struct RO {
+  static constexpr bool QUAD = QUAD_;
   static constexpr int DCG = 256, G = 2, DC = G * DCG;   // latent columns per group, of a row
   static constexpr int NB = DCG / 128;                   // 128-column blocks of the fp8 product
   static constexpr int A = A_, S = A_ + 1;
@@ -52,12 +55,13 @@ struct RO {
   static constexpr int NCH = TILE * CPR;                 // 16-byte chunks per tile
   static constexpr int NI = (NCH + 63) / 64;             // DMA instructions per tile
   static constexpr int DPW = (NI + NDW - 1) / NDW;       // ... per DMA wave (at most)
-  static constexpr int NBQ = NB + 1;                     // ... and the rope as one more, half zero
+  static constexpr int NBQ = NB + 1;                     // ... and the rope as one more
   static constexpr int KPT = 2 * NBQ;                    // 16-byte K reads per lane and token block
   static constexpr int KQ = 4 * NBQ;                     // query loads (8 bf16) per lane
   static constexpr int CB = DCG / 16;                    // 16-column output blocks per wave
   static_assert(CPR * 16 >= DC + 64 + 24, "row slice: latent, rope, 24 log8 codes");
   static_assert(A >= 2 && A * DPW < 64, "lookahead / vmcnt range");
+  static_assert(CPR == 38, "row regions: 4 latent blocks of 8 chunks, rope 4, rms 2");
 };
 
 template <class C>
@@ -68,23 +72,44 @@ struct Smem {
   int win[4];
 };
 
-// rotation of staged row r (see the file comment)
-__device__ __forceinline__ int rrot(int r) { return (r & 15) ^ ((r >> 1) & 8); }
-template <int CPR>
-__device__ __forceinline__ int rpos(int c, int r) {
-  const int q = c + rrot(r);
-  return q >= CPR ? q - CPR : q;
+// the staged row layout (see the file comment): flip of row r, chunk c's region, its position in a
+// row with flip f, and the inverse
+__device__ __forceinline__ int rflip(int r) { return ((r >> 3) + (r >> 4)) & 1; }
+__device__ __forceinline__ int region_base(int c) { return c < 32 ? (c & ~7) : c < 36 ? 32 : 36; }
+__device__ __forceinline__ int region_mask(int c) { return c < 32 ? 7 : c < 36 ? 3 : 1; }
+__device__ __forceinline__ int chunk_pos(int c, int f) {
+  const int b = region_base(c);
+  return b + ((c - b + f) & region_mask(c));
 }
-template <int CPR>
-__device__ __forceinline__ int rbyte(int r, int b) {
-  return r * (16 * CPR) + 16 * rpos<CPR>(b >> 4, r) + (b & 15);
+__device__ __forceinline__ int pos_chunk(int q, int f) {
+  const int b = region_base(q);
+  return b + ((q - b - f) & region_mask(q));
 }
 
-// lane 4k + I's value, to the 4 lanes 4k .. 4k+3
+// LDS reads at a base address plus an immediate offset (the loop keeps one base register per lane
+// and read pattern, not one address per read)
+template <int OFF>
+__device__ __forceinline__ i32x4 ldsr128_at(uint32_t a) {
+  i32x4 r;
+  asm volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(r) : "v"(a), "n"(OFF));
+  return r;
+}
+template <int OFF>
+__device__ __forceinline__ i32x2 ldstr8_at(uint32_t a) {
+  i32x2 r;
+  asm volatile("ds_read_b64_tr_b8 %0, %1 offset:%2" : "=v"(r) : "v"(a), "n"(OFF));
+  return r;
+}
+__device__ __forceinline__ uint32_t ldsr8_at(uint32_t a) {
+  uint32_t r;
+  asm volatile("ds_read_u8 %0, %1" : "=v"(r) : "v"(a));
+  return r;
+}
+
+// lane 4k + I's value, to the 4 lanes 4k .. 4k+3 (every lane is written: no old value)
 template <int I>
 __device__ __forceinline__ float quad_bcast(float x) {
-  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), I | (I << 2) | (I << 4) | (I << 6), 0xF, 0xF,
-                                                    false));
+  return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(x), I | (I << 2) | (I << 4) | (I << 6), 0xF, 0xF, true));
 }
 
 template <class C, int ROLE>
@@ -109,7 +134,7 @@ __device__ __forceinline__ void role_main(const KParams& p, Smem<C>& sm, float k
   const bool live = ROLE == COMPUTE && 16 * rbk < nrows;   // the wave has rows
   const float c2b = p.sm_scale * kscale * kLog2e;
 
-  i32x8 qh8[ROLE == COMPUTE ? C::NBQ : 1], ql8[ROLE == COMPUTE ? C::NBQ : 1];
+  i32x8 qh8[ROLE == COMPUTE ? C::NBQ : 1], ql8[ROLE == COMPUTE ? C::NB : 1];
   int qsc = 127;   // E8M0 scale of the row's query parts: 2^-e
   // rms multiplier |c2b| / rms = 2^(lc2 - code*6/255); the sign of c2b goes into the query
   const float lc2 = 3.0f + fast_log2(c2b != 0.f ? fabsf(c2b) : 1.0f);
@@ -120,9 +145,11 @@ __device__ __forceinline__ void role_main(const KParams& p, Smem<C>& sm, float k
   for (int cb = 0; cb < (ROLE == COMPUTE ? C::CB : 1); ++cb) acc[cb] = f32x4{0.f, 0.f, 0.f, 0.f};
 
   // the query of row rg of request req as fp8 MFMA operands in 128-column blocks (lane group lg
-  // holding columns 128b + 32lg .. +32): the group's latent, then the rope as one more block whose
-  // columns 64 .. 127 are zero (lane groups 2 and 3). Each part is e4m3 hi + lo of q * 2^e
-  // (|q| * 2^e in (112, 448]); the MFMA's B scale 2^-e undoes the shift
+  // holding columns 128b + 32lg .. +32), as e4m3 hi + lo parts of q * 2^e (|q| * 2^e in (112, 448];
+  // the MFMA's B scale 2^-e undoes the shift): the group's latent blocks (a hi and a lo MFMA each),
+  // then the rope as one block whose lane groups 0, 1 hold the hi parts of rope columns 32lg .. +32
+  // and lane groups 2, 3 the lo parts of the same columns (their K reads repeat lane groups 0, 1's),
+  // so one MFMA takes both
   auto load_q = [&](int req) {
     const int row = req * qrows + jq;
     const __bf16* qnp = p.q_nope + (int64_t)row * p.qn_sr + (int64_t)head * p.qn_sh;
@@ -131,9 +158,9 @@ __device__ __forceinline__ void role_main(const KParams& p, Smem<C>& sm, float k
 #pragma unroll
     for (int k = 0; k < C::KQ; ++k) {
       const bool rope = k >= 4 * C::NB;
-      const int col = rope ? 32 * lg + 8 * (k & 3) : 128 * (k >> 2) + 32 * lg + 8 * (k & 3);
+      const int col = rope ? 32 * (lg & 1) + 8 * (k & 3) : 128 * (k >> 2) + 32 * lg + 8 * (k & 3);
       bf16x8 v = bf16x8{};
-      if (rok && (!rope || lg < 2)) v = load_q8(rope ? qpp + col : qnp + col, p.q_vec);
+      if (rok) v = load_q8(rope ? qpp + col : qnp + col, p.q_vec);
       qn[k] = v;
     }
     float mx = 0.f;
@@ -166,12 +193,14 @@ __device__ __forceinline__ void role_main(const KParams& p, Smem<C>& sm, float k
       }
     }
 #pragma unroll
-    for (int b = 0; b < C::NBQ; ++b)
+    for (int b = 0; b < C::NB; ++b)
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
         qh8[b][e] = hq[8 * b + e];
         ql8[b][e] = lq[8 * b + e];
       }
+#pragma unroll
+    for (int e = 0; e < 8; ++e) qh8[C::NB][e] = lg < 2 ? hq[8 * C::NB + e] : lq[8 * C::NB + e];
   };
 
   // normalize and write the rows of request req (accumulator row 16rbk + 4lg + i on this lane)
@@ -210,7 +239,7 @@ __device__ __forceinline__ void role_main(const KParams& p, Smem<C>& sm, float k
   };
 
   // ---- DMA wave: instruction i = dw + 2j covers LDS chunks 64i .. 64i+63 of a stage (staged row
-  //      q / CPR, position q % CPR, i.e. row chunk (position - f(row)) mod CPR) ----
+  //      q / CPR, position q % CPR, i.e. row chunk pos_chunk(position, flip of the row)) ----
   const int dw = w - C::NCW;
   uint32_t doff[ROLE == DMA ? C::DPW : 1];
   int drow[ROLE == DMA ? C::DPW : 1];
@@ -220,9 +249,7 @@ __device__ __forceinline__ void role_main(const KParams& p, Smem<C>& sm, float k
       int q = (dw + C::NDW * j) * 64 + lane;
       q = q < C::NCH ? q : C::NCH - 1;
       const int rr = q / C::CPR, pp = q - rr * C::CPR;
-      int c = pp - rrot(rr);
-      c = c < 0 ? c + C::CPR : c;
-      doff[j] = (uint32_t)(rr * C::RB + 16 * c);
+      doff[j] = (uint32_t)(rr * C::RB + 16 * pos_chunk(pp, rflip(rr)));
       drow[j] = rr;
     }
   }
@@ -349,12 +376,38 @@ __device__ __forceinline__ void role_main(const KParams& p, Smem<C>& sm, float k
     } else {
       lds_barrier();
       int ks = 0, ts = 0, s_ta = 0, s_nt = 0, s_fl = 0, s_req = 0, lim = 0, lim_min = 0;
-      const bool quad = qrows == 4;
+      constexpr bool quad = C::QUAD;
       // transposed V reads: lanes 2r', 2r'+1 of lane group lg supply the tile row that holds the
       // lane group's score token r' (4lg + r' for r' < 4, 16 + 4lg + r' - 4 after), so the value
       // operand's k order is the score registers' token order
       const int vr = (ln16 >> 1) < 4 ? 4 * lg + (ln16 >> 1) : 16 + 4 * lg + (ln16 >> 1) - 4;
-      const int vcol = grp * C::DCG + 8 * (ln16 & 1);
+      // ---- per-lane read offsets within a stage ----
+      // K: token block tb, 16-byte half h of the lane group's 32 columns; latent block b adds 128b
+      // bytes. The rope block: lane groups 2, 3 read lane groups 0, 1's rope chunks again (the
+      // rms bytes past the rope could read as fp8 NaN)
+      uint32_t koff[2][2], kofr[2][2];
+#pragma unroll
+      for (int tb = 0; tb < 2; ++tb)
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+          const int krow = 16 * tb + ln16, fk = rflip(krow);
+          koff[tb][h] = (uint32_t)(krow * C::RB + 16 * (grp * (C::DCG / 16) + ((2 * lg + h + fk) & 7)));
+          kofr[tb][h] = (uint32_t)(krow * C::RB + 16 * (C::DC / 16 + ((2 * lg + h + fk) & 3)));
+        }
+      // V: 16-column block c = 8b + kk of the group sits at chunk position (kk + f) & 7 of latent block b
+      const int fv = rflip(vr);
+      const uint32_t vb0 = (uint32_t)(vr * C::RB + 16 * (grp * (C::DCG / 16) + fv) + 8 * (ln16 & 1));
+      const uint32_t vb7 = (uint32_t)(vr * C::RB + 16 * (grp * (C::DCG / 16) + ((7 + fv) & 7)) + 8 * (ln16 & 1));
+      // rms codes: the lane's head in token row 16tb + 4lg + (the lane's quad slot, or i)
+      constexpr int NCI = quad ? 1 : 4;
+      uint32_t coff[2][NCI];
+#pragma unroll
+      for (int tb = 0; tb < 2; ++tb)
+#pragma unroll
+        for (int i = 0; i < NCI; ++i) {
+          const int row = 16 * tb + 4 * lg + (quad ? (ln16 & 3) : i);
+          coff[tb][i] = (uint32_t)(row * C::RB + 16 * chunk_pos(rms_b >> 4, rflip(row)) + (rms_b & 15));
+        }
 #pragma clang loop unroll(disable)
       for (int g = 0; g < ntot; ++g) {
         if (ts == 0) {
@@ -376,38 +429,32 @@ __device__ __forceinline__ void role_main(const KParams& p, Smem<C>& sm, float k
           lim_min = d.L - (qrows - 1) < d.te ? d.L - (qrows - 1) : d.te;
         }
         if (live) {
-          const char* kvs = sm.kv[g % C::S];
+          const uint32_t sb = lds_addr(sm.kv[g % C::S]);
           const int tok0 = s_ta + ts * TILE;
           // ---- LDS reads: rms codes, then the K rows of both token blocks (2 x 5) ----
           // 4 verify tokens: lanes 4k..4k+3 hold the 4 verify rows of one head, so lane j reads the
           // codes of tokens 4lg+j (block 0) and 16+4lg+j (block 1) and the quad shares them
-          uint32_t code[2][4];
-          if (quad) {
+          uint32_t code[2][NCI];
 #pragma unroll
-            for (int tb = 0; tb < 2; ++tb) code[tb][0] = ldsr8(kvs + rbyte<C::CPR>(16 * tb + 4 * lg + (ln16 & 3), rms_b));
-          } else {
+          for (int tb = 0; tb < 2; ++tb)
 #pragma unroll
-            for (int tb = 0; tb < 2; ++tb)
-#pragma unroll
-              for (int i = 0; i < 4; ++i) code[tb][i] = ldsr8(kvs + rbyte<C::CPR>(16 * tb + 4 * lg + i, rms_b));
-          }
+            for (int i = 0; i < NCI; ++i) code[tb][i] = ldsr8_at(sb + coff[tb][i]);
+          // K: per token block the latent blocks' two halves, then the rope block's
           i32x4 kr[2][C::KPT];
 #pragma unroll
           for (int tb = 0; tb < 2; ++tb) {
-            const int krow = 16 * tb + ln16;
-            const char* rowp = kvs + krow * C::RB;
-#pragma unroll
-            for (int jj = 0; jj < C::KPT; ++jj) {
-              // latent block jj/2 of the group; the rope block (lane groups 2, 3 read the rope again:
-              // their query columns are zero, and the rms bytes past the rope could read as fp8 NaN)
-              const int ch = jj < 2 * C::NB ? grp * (C::DCG / 16) + 8 * (jj >> 1) + 2 * lg + (jj & 1)
-                                            : C::DC / 16 + 2 * (lg & 1) + (jj & 1);
-              kr[tb][jj] = ldsr128(rowp + 16 * rpos<C::CPR>(ch, krow));
-            }
+            const uint32_t a0 = sb + koff[tb][0], a1 = sb + koff[tb][1];
+            static_for<0, C::NB>([&](auto bc) {
+              constexpr int b = decltype(bc)::value;
+              kr[tb][2 * b] = ldsr128_at<128 * b>(a0);
+              kr[tb][2 * b + 1] = ldsr128_at<128 * b>(a1);
+            });
+            kr[tb][2 * C::NB] = ldsr128_at<0>(sb + kofr[tb][0]);
+            kr[tb][2 * C::NB + 1] = ldsr128_at<0>(sb + kofr[tb][1]);
           }
           // ---- score multipliers c2b / rms (log8: 2^(3 + log2 c2b - c*6/255)) as the codes land ----
           float rsc[2][4];
-          if (quad) {
+          if constexpr (quad) {
             float r0[2];
             lds_wait_n<cmin15(2 * C::KPT + 1)>(code[0][0]);
             r0[0] = fast_exp2(fmaf((float)code[0][0], -6.0f / 255.0f, lc2));
@@ -447,15 +494,23 @@ __device__ __forceinline__ void role_main(const KParams& p, Smem<C>& sm, float k
                              kr[tb][2 * b + 1][0], kr[tb][2 * b + 1][1], kr[tb][2 * b + 1][2], kr[tb][2 * b + 1][3]};
               sl[tb] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(ka[tb], qh8[b], sl[tb], 0, 0, 0, 127, 0, qsc);
             });
-            static_for<0, 2>([&](auto tc) {
-              constexpr int tb = decltype(tc)::value;
-              sl[tb] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(ka[tb], ql8[b], sl[tb], 0, 0, 0, 127, 0, qsc);
-            });
+            if constexpr (b < C::NB) {
+              static_for<0, 2>([&](auto tc) {
+                constexpr int tb = decltype(tc)::value;
+                sl[tb] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(ka[tb], ql8[b], sl[tb], 0, 0, 0, 127, 0, qsc);
+              });
+            }
           });
           // ---- V^T reads of the tile (the K reads have all landed) ----
           i32x2 vraw[C::CB];
-#pragma unroll
-          for (int c = 0; c < C::CB; ++c) vraw[c] = lds_read_tr8_async(kvs + rbyte<C::CPR>(vr, vcol + 16 * c));
+          {
+            const uint32_t a0 = sb + vb0, a7 = sb + vb7;
+            static_for<0, C::CB>([&](auto cc) {
+              constexpr int c = decltype(cc)::value, b = c / 8, kk = c % 8;
+              if constexpr (kk < 7) vraw[c] = ldstr8_at<128 * b + 16 * kk>(a0);
+              else vraw[c] = ldstr8_at<128 * b>(a7);
+            });
+          }
           // ---- rms divide and scale; mask only a tile that reaches a row's limit; tile max ----
           float v[2][4];
 #pragma unroll
@@ -542,7 +597,8 @@ __global__ __launch_bounds__(C::NTHR, 1) void ro_kernel(const KParams p) {
 }
 
 typedef void (*RoFn)(const KParams);
-static const RoFn kRo[] = {&ro_kernel<RO<5>>};
+// [0]: 4 verify rows per head, [1]: other verify counts
+static const RoFn kRo[] = {&ro_kernel<RO<5, true>>, &ro_kernel<RO<5, false>>};
 
 }  // namespace ro
 
@@ -553,7 +609,7 @@ int ro_select(const qmla_decode_params* p) {
   if (p->d_c != 512 || p->rope_w != 64 || p->logit_cap > 0.f) return -1;
   if (p->qrows * (p->heads / 2) > 48) return -1;
   if (p->token_stride < 608 || (int64_t)p->rms_offset + p->heads > 608) return -1;
-  return 0;
+  return p->qrows == 4 ? 0 : 1;
 }
 
 int ro_launch(int inst, const qmla_decode_params* p, const KParams& k, int nwg, hipStream_t st) {
