@@ -72,40 +72,6 @@ struct Smem {
   int win[4];
 };
 
-// the staged row layout (see the file comment): flip of row r, chunk c's region, its position in a
-// row with flip f, and the inverse
-__device__ __forceinline__ int rflip(int r) { return ((r >> 3) + (r >> 4)) & 1; }
-__device__ __forceinline__ int region_base(int c) { return c < 32 ? (c & ~7) : c < 36 ? 32 : 36; }
-__device__ __forceinline__ int region_mask(int c) { return c < 32 ? 7 : c < 36 ? 3 : 1; }
-__device__ __forceinline__ int chunk_pos(int c, int f) {
-  const int b = region_base(c);
-  return b + ((c - b + f) & region_mask(c));
-}
-__device__ __forceinline__ int pos_chunk(int q, int f) {
-  const int b = region_base(q);
-  return b + ((q - b - f) & region_mask(q));
-}
-
-// LDS reads at a base address plus an immediate offset (the loop keeps one base register per lane
-// and read pattern, not one address per read)
-template <int OFF>
-__device__ __forceinline__ i32x4 ldsr128_at(uint32_t a) {
-  i32x4 r;
-  asm volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(r) : "v"(a), "n"(OFF));
-  return r;
-}
-template <int OFF>
-__device__ __forceinline__ i32x2 ldstr8_at(uint32_t a) {
-  i32x2 r;
-  asm volatile("ds_read_b64_tr_b8 %0, %1 offset:%2" : "=v"(r) : "v"(a), "n"(OFF));
-  return r;
-}
-__device__ __forceinline__ uint32_t ldsr8_at(uint32_t a) {
-  uint32_t r;
-  asm volatile("ds_read_u8 %0, %1" : "=v"(r) : "v"(a));
-  return r;
-}
-
 // lane 4k + I's value, to the 4 lanes 4k .. 4k+3 (every lane is written: no old value)
 template <int I>
 __device__ __forceinline__ float quad_bcast(float x) {
@@ -249,7 +215,7 @@ __device__ __forceinline__ void role_main(const KParams& p, Smem<C>& sm, float k
       int q = (dw + C::NDW * j) * 64 + lane;
       q = q < C::NCH ? q : C::NCH - 1;
       const int rr = q / C::CPR, pp = q - rr * C::CPR;
-      doff[j] = (uint32_t)(rr * C::RB + 16 * pos_chunk(pp, rflip(rr)));
+      doff[j] = (uint32_t)(rr * C::RB + 16 * pos_chunk<C::CPR>(pp, lflip<C::CPR>(rr)));
       drow[j] = rr;
     }
   }
@@ -390,12 +356,12 @@ __device__ __forceinline__ void role_main(const KParams& p, Smem<C>& sm, float k
       for (int tb = 0; tb < 2; ++tb)
 #pragma unroll
         for (int h = 0; h < 2; ++h) {
-          const int krow = 16 * tb + ln16, fk = rflip(krow);
+          const int krow = 16 * tb + ln16, fk = lflip<C::CPR>(krow);
           koff[tb][h] = (uint32_t)(krow * C::RB + 16 * (grp * (C::DCG / 16) + ((2 * lg + h + fk) & 7)));
           kofr[tb][h] = (uint32_t)(krow * C::RB + 16 * (C::DC / 16 + ((2 * lg + h + fk) & 3)));
         }
       // V: 16-column block c = 8b + kk of the group sits at chunk position (kk + f) & 7 of latent block b
-      const int fv = rflip(vr);
+      const int fv = lflip<C::CPR>(vr);
       const uint32_t vb0 = (uint32_t)(vr * C::RB + 16 * (grp * (C::DCG / 16) + fv) + 8 * (ln16 & 1));
       const uint32_t vb7 = (uint32_t)(vr * C::RB + 16 * (grp * (C::DCG / 16) + ((7 + fv) & 7)) + 8 * (ln16 & 1));
       // rms codes: the lane's head in token row 16tb + 4lg + (the lane's quad slot, or i)
@@ -406,7 +372,7 @@ __device__ __forceinline__ void role_main(const KParams& p, Smem<C>& sm, float k
 #pragma unroll
         for (int i = 0; i < NCI; ++i) {
           const int row = 16 * tb + 4 * lg + (quad ? (ln16 & 3) : i);
-          coff[tb][i] = (uint32_t)(row * C::RB + 16 * chunk_pos(rms_b >> 4, rflip(row)) + (rms_b & 15));
+          coff[tb][i] = (uint32_t)(row * C::RB + 16 * chunk_pos<C::CPR>(rms_b >> 4, lflip<C::CPR>(row)) + (rms_b & 15));
         }
 #pragma clang loop unroll(disable)
       for (int g = 0; g < ntot; ++g) {

@@ -100,15 +100,60 @@ struct SegD {
   int nt, pf, fl, pad;
 };
 
-// rotated row layout: chunk c of staged row r at position (c + (r & 15)) mod CPR
+// Staged row layout of fp8 MLA rows (4 latent blocks of 8 16-byte chunks, the rope's 4 chunks, then
+// the rms codes' CPR - 36): each chunk stays in its region, rotated there by the row's flip f(r).
+// 608-byte rows (CPR 38, 152 dwords: rows 24 banks apart, 8 rows per bank period) flip by
+// ((r >> 3) + (r >> 4)) & 1, so 16 consecutive rows (K reads) and rows r, r + 16 (transposed V reads
+// of one lane group) land on distinct banks; 592-byte rows (CPR 37, 20 banks apart) need no flip for
+// those patterns. Reads of one latent block then share a base register per lane and pattern, the
+// block and chunk going into the instructions' offset fields.
 template <int CPR>
-__device__ __forceinline__ int rot(int c, int r) {
-  const int p = c + (r & 15);
-  return p >= CPR ? p - CPR : p;
+__device__ __forceinline__ int lflip(int r) {
+  return CPR == 38 ? ((r >> 3) + (r >> 4)) & 1 : 0;
 }
 template <int CPR>
+__device__ __forceinline__ int region_base(int c) {
+  return c < 32 ? (c & ~7) : c < 36 ? 32 : 36;
+}
+template <int CPR>
+__device__ __forceinline__ int region_mask(int c) {
+  return c < 32 ? 7 : c < 36 ? 3 : (CPR - 36 >= 2 ? 1 : 0);
+}
+// position of chunk c in a row with flip f, and the inverse
+template <int CPR>
+__device__ __forceinline__ int chunk_pos(int c, int f) {
+  const int b = region_base<CPR>(c);
+  return b + ((c - b + f) & region_mask<CPR>(c));
+}
+template <int CPR>
+__device__ __forceinline__ int pos_chunk(int q, int f) {
+  const int b = region_base<CPR>(q);
+  return b + ((q - b - f) & region_mask<CPR>(q));
+}
+// byte b of staged row r
+template <int CPR>
 __device__ __forceinline__ int lbyte(int r, int b) {
-  return r * (16 * CPR) + 16 * rot<CPR>(b >> 4, r) + (b & 15);
+  return r * (16 * CPR) + 16 * chunk_pos<CPR>(b >> 4, lflip<CPR>(r)) + (b & 15);
+}
+
+// LDS reads at a base address plus an immediate offset (the loop keeps one base register per lane
+// and read pattern, not one address per read)
+template <int OFF>
+__device__ __forceinline__ i32x4 ldsr128_at(uint32_t a) {
+  i32x4 r;
+  asm volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(r) : "v"(a), "n"(OFF));
+  return r;
+}
+template <int OFF>
+__device__ __forceinline__ i32x2 ldstr8_at(uint32_t a) {
+  i32x2 r;
+  asm volatile("ds_read_b64_tr_b8 %0, %1 offset:%2" : "=v"(r) : "v"(a), "n"(OFF));
+  return r;
+}
+__device__ __forceinline__ uint32_t ldsr8_at(uint32_t a) {
+  uint32_t r;
+  asm volatile("ds_read_u8 %0, %1" : "=v"(r) : "v"(a));
+  return r;
 }
 
 

@@ -101,6 +101,7 @@ struct WS {
   static_assert(G == 1 || (G == 2 && EB == 1 && !RTR), "latent groups: fp8 rows, rms codes read per row");
   static_assert(A >= 2 && A * DPW < 64, "lookahead / vmcnt range");
   static_assert(EB == 2 || DCG % 128 == 0, "fp8 latent in 128-column MFMA blocks");
+  static_assert(CPR == 37 || CPR == 38, "staged row layout of fp8 rows (lbyte)");
 };
 
 template <class C>
@@ -162,6 +163,24 @@ __device__ __forceinline__ void role_main(const KParams& p, Smem<C>& sm, float k
     rms_b[m] = p.rms_off_b + hd[m] * C::RMS_EB;
   }
   const bool contig = p.token_stride_b == C::RB;
+  // per-lane read offsets within a stage (staged row layout: lbyte). Score wave: K row 16tb + ln16,
+  // 16-byte half h of the lane group's 32 columns of each latent block (block b adds 128b bytes), and
+  // its rope chunk; value wave: transposed V row 8lg + ln16/2, its 128 columns' latent block, chunks
+  // 0..6 and 7 (the flip may wrap the last)
+  uint32_t koff[2] = {0u, 0u}, kofr = 0u, vb0 = 0u, vb7 = 0u;
+  if constexpr (ROLE == SCORE && C::EB == 1) {
+    const int krow = 16 * tb + ln16, fk = lflip<C::CPR>(krow);
+#pragma unroll
+    for (int h = 0; h < 2; ++h)
+      koff[h] = (uint32_t)(krow * C::RB + 16 * (sg * (C::DCG / 16) + ((2 * lg + h + fk) & 7)));
+    kofr = (uint32_t)(krow * C::RB + 16 * (C::DC / 16 + ((lg + fk) & 3)));
+  }
+  if constexpr (ROLE == VALUE && C::EB == 1) {
+    const int vr = 8 * lg + (ln16 >> 1), fv = lflip<C::CPR>(vr);
+    const int c0 = (vg * C::DCG + C::VC * vh) / 16;
+    vb0 = (uint32_t)(vr * C::RB + 16 * (c0 + fv) + 8 * (ln16 & 1));
+    vb7 = (uint32_t)(vr * C::RB + 16 * (c0 + ((7 + fv) & 7)) + 8 * (ln16 & 1));
+  }
 
   // ---- score wave: query fragments (fp8 cache: e4m3 hi/lo parts scaled per row by a power of two
   //      folded into c2; the latent in 128-column blocks, lane group lg holding columns
@@ -263,7 +282,7 @@ __device__ __forceinline__ void role_main(const KParams& p, Smem<C>& sm, float k
   zero_acc();
 
   // ---- value wave DMA: instruction i = vw + 4j covers LDS chunks 64i .. 64i+63 of a stage: staged
-  //      row q / CPR, position q % CPR, i.e. row chunk (position - (row & 15)) mod CPR ----
+  //      row q / CPR, position q % CPR, i.e. row chunk pos_chunk(position, flip of the row) ----
   uint32_t doff[ND];
   int drow[ND];
   if constexpr (ISSUER) {
@@ -272,9 +291,7 @@ __device__ __forceinline__ void role_main(const KParams& p, Smem<C>& sm, float k
       int q = (dw + C::NIW * j) * 64 + lane;
       q = q < C::NCH ? q : C::NCH - 1;
       const int rr = q / C::CPR, pp = q - rr * C::CPR;
-      int c = pp - (rr & 15);
-      c = c < 0 ? c + C::CPR : c;
-      doff[j] = (uint32_t)(rr * C::RB + 16 * c);
+      doff[j] = (uint32_t)(rr * C::RB + 16 * pos_chunk<C::CPR>(pp, lflip<C::CPR>(rr)));
       drow[j] = rr;
     }
   }
@@ -530,8 +547,6 @@ __device__ __forceinline__ void role_main(const KParams& p, Smem<C>& sm, float k
           float tpart[C::MBG];   // unused at g == 0
 #pragma unroll
           for (int m = 0; m < C::MBG; ++m) tpart[m] = ldsr32f(&sm.tmax[(g + 1) & 1][tb ^ 1][r[m]]);
-          const int krow = 16 * tb + ln16;
-          const char* rowp = kvs + krow * C::RB;
           uint32_t code[C::MBG][4];
 #pragma unroll
           for (int m = 0; m < C::MBG; ++m)
@@ -554,14 +569,24 @@ __device__ __forceinline__ void role_main(const KParams& p, Smem<C>& sm, float k
             }
           }
           i32x4 kr0[C::KP], kr1[C::EB == 2 ? C::KP : 1];
+          if constexpr (F8) {
+            // latent block b of the wave's group (halves h = 0, 1 at one base each), then the rope
+            // after the whole latent
+            const uint32_t sb = lds_addr(kvs);
+            const uint32_t a0 = sb + koff[0], a1 = sb + koff[1];
+            static_for<0, NB>([&](auto bc) {
+              constexpr int b = decltype(bc)::value;
+              kr0[2 * b] = ldsr128_at<128 * b>(a0);
+              kr0[2 * b + 1] = ldsr128_at<128 * b>(a1);
+            });
+            kr0[2 * NB] = ldsr128_at<0>(sb + kofr);
+          } else {
 #pragma unroll
-          for (int jj = 0; jj < C::KP; ++jj) {
-            const int cbyte = (64 * jj + 16 * lg) * C::EB;
-            // fp8: latent block jj/2 of the wave's group, then the rope after the whole latent
-            const int ch = !F8 ? cbyte >> 4
-                               : jj < 2 * NB ? sg * (C::DCG / 16) + 8 * (jj >> 1) + 2 * lg + (jj & 1) : C::DC / 16 + lg;
-            kr0[jj] = ldsr128(rowp + 16 * rot<C::CPR>(ch, krow));
-            if constexpr (C::EB == 2) kr1[jj] = ldsr128(rowp + 16 * rot<C::CPR>((cbyte >> 4) + 1, krow));
+            for (int jj = 0; jj < C::KP; ++jj) {
+              const int cbyte = (64 * jj + 16 * lg) * C::EB;
+              kr0[jj] = ldsr128(kvs + lbyte<C::CPR>(16 * tb + ln16, cbyte));
+              kr1[jj] = ldsr128(kvs + lbyte<C::CPR>(16 * tb + ln16, cbyte + 16));
+            }
           }
           // ---- reference check of tile g-1 (its writes follow the score product); at the first
           //      tile of a request: publish the previous request's sums, switch the query ----
@@ -768,13 +793,18 @@ __device__ __forceinline__ void role_main(const KParams& p, Smem<C>& sm, float k
           else fl4 = ldsr128(&sm.flag[pj][vg][0]);
 #pragma unroll
           for (int mb = 0; mb < C::MBV; ++mb) pr[mb] = ldsr128(&sm.p[pj][vr0 + 16 * mb + ln16][(8 * lg) * 2]);
+          if constexpr (C::EB == 1) {
+            // 16-column block cb of the wave's 128 columns: chunk position (cb + f) & 7 of their latent block
+            const uint32_t a0 = lds_addr(kvs) + vb0, a7 = lds_addr(kvs) + vb7;
+            static_for<0, C::CB>([&](auto cc) {
+              constexpr int c = decltype(cc)::value;
+              if constexpr (c < 7) vraw[c][0] = ldstr8_at<16 * c>(a0);
+              else vraw[c][0] = ldstr8_at<0>(a7);
+            });
+          } else {
 #pragma unroll
-          for (int cb = 0; cb < C::CB; ++cb) {
-            const int col0 = C::VC * vh + 16 * cb;
-            if constexpr (C::EB == 1) {
-              const int vr = 8 * lg + (ln16 >> 1);
-              vraw[cb][0] = lds_read_tr8_async(kvs + lbyte<C::CPR>(vr, vg * C::DCG + col0 + 8 * (ln16 & 1)));
-            } else {
+            for (int cb = 0; cb < C::CB; ++cb) {
+              const int col0 = C::VC * vh + 16 * cb;
               const int vr = 8 * lg + (ln16 >> 2);
               const int vb = (col0 + 4 * (ln16 & 3)) * 2;
               vraw[cb][0] = lds_read_tr16_async(kvs + lbyte<C::CPR>(vr, vb));
