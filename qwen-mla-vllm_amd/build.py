@@ -30,8 +30,10 @@ COMMON_FLAGS = [
 SOURCES = [
     (CSRC / "qmla_decode.hip", ["-mllvm", "-amdgpu-mfma-vgpr-form"]),
     (CSRC / "qmla_cs.hip", ["-mllvm", "-amdgpu-mfma-vgpr-form"]),
-    (CSRC / "qmla_ws.hip", ["-mllvm", "-amdgpu-mfma-vgpr-form"]),
-    (CSRC / "qmla_ro.hip", ["-mllvm", "-amdgpu-mfma-vgpr-form"]),
+    # the softmax never sees a NaN (masked scores are -inf, infinities stay honoured): no canonicalizing
+    # v_max before every fmaxf of the tile maxima
+    (CSRC / "qmla_ws.hip", ["-mllvm", "-amdgpu-mfma-vgpr-form", "-fno-honor-nans"]),
+    (CSRC / "qmla_ro.hip", ["-mllvm", "-amdgpu-mfma-vgpr-form", "-fno-honor-nans"]),
     (CSRC / "qmla_write.hip", []),
     (CSRC / "qmla_prep.hip", []),
 ]
