@@ -186,6 +186,14 @@ int qmla_plan(const qmla_decode_params* p, void* stream);
 int qmla_decode_partial(const qmla_decode_params* p, void* stream);
 int qmla_combine(const qmla_decode_params* p, void* stream);
 
+/* The balanced plan's per-request tile count is ceil(L / 64) plus this many tiles for a non-empty
+ * request (0 for an empty one): the fixed work of a request piece (query load, output write),
+ * charged as tokens so that workgroups holding more pieces get fewer tokens. It depends on the
+ * kernel the params select; 0 in fixed-split mode. Negative QMLA_ERR_* for invalid params. No
+ * counterpart in the reference (FlashInfer's work split, qwen_mla/fi_decode.py:210-233, counts
+ * tokens only). */
+int qmla_plan_switch_tiles(const qmla_decode_params* p);
+
 /* ---- cache-row writer ---------------------------------------------------------------------
  * Replaces QwenMLATritonImpl.do_kv_cache_update (qwen_mla/mla_impl.py:309-342) and, for the rows it
  * hands to vLLM (bf16 caches; FP8 caches whose rms is stored as e4m3), vLLM's concat_and_cache_mla:

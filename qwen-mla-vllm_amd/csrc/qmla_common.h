@@ -11,6 +11,10 @@
 namespace qmla {
 
 constexpr int PLAN_TILE = 64;  // balancing granularity of the balanced plan (tokens)
+// plan tiles the balanced plan charges per request switch (see plan_tiles), per kernel family: the
+// warp-specialized and row-owner decode (measured: a piece's query load and output write cost about
+// two plan tiles of work), the per-group and column-split kernels (none)
+constexpr int kPlanSwitchWs = 2, kPlanSwitchRo = 2, kPlanSwitchOther = 0;
 
 struct KParams {
   const __bf16* q_nope;
@@ -49,6 +53,9 @@ struct KParams {
                     // heads/hsplit of its heads (balanced mode: nwg ranges x hsplit workgroups)
   uint32_t page_bound;  // block-table entries must lie in [0, page_bound)
   int* status;          // QMLA_ERR_PAGE is stored here when one does not (may be null)
+  int plan_sw;          // plan tiles charged for a request switch (see plan_tiles): read by the
+                        // combine and the plan kernel; the decode kernels have their family's as a
+                        // constant
 };
 
 // A block-table entry checked against the page bound: an entry outside [0, page_bound) reads page 0
@@ -95,9 +102,13 @@ __device__ __forceinline__ int req_len(const KParams& p, int req) {
 }
 
 // ---- the balanced plan, computed by the decode kernels themselves ---------------------------------
-// Request b owns PLAN_TILE-token plan tiles [C_b, C_b + T_b) of the concatenated requests, with
-// T_b = ceil(L_b / PLAN_TILE) and C_b the exclusive prefix of the T's; workgroup w of nwg owns plan
-// tiles [w*chunk, min((w+1)*chunk, total)) with chunk = ceil(total / nwg). Every workgroup derives
+// Request b owns plan tiles [C_b, C_b + T_b) of the concatenated requests, with T_b = ceil(L_b /
+// PLAN_TILE) + plan_sw for a non-empty request (0 for an empty one) and C_b the exclusive prefix of
+// the T's; workgroup w of nwg owns plan tiles [w*chunk, min((w+1)*chunk, total)) with chunk =
+// ceil(total / nwg). A request's first plan_sw tiles hold no tokens: they charge the fixed work of
+// a piece (the query load, the output write) to the workgroup that starts the request, so a
+// workgroup holding two pieces gets fewer tokens than one holding one; the following tiles hold
+// PLAN_TILE tokens each. Every workgroup derives
 // its own range from seq_lens at its start (no planning launch: a launch of its own costs more
 // than the scan, and inside a HIP graph far more), and workgroup 0 also stores the plan for the
 // balanced combine.
@@ -112,9 +123,27 @@ __device__ __forceinline__ int wave_incl_sum(int x) {
   return x;
 }
 
+template <int SW>
 __device__ __forceinline__ int plan_tiles(const KParams& p, int b) {
   const int L = req_len(p, b);
-  return (L + PLAN_TILE - 1) / PLAN_TILE;
+  return L > 0 ? (L + PLAN_TILE - 1) / PLAN_TILE + SW : 0;
+}
+
+// The tokens [a, e) of a request of length L with plan tiles [c0, c1) that plan tiles [lo, hi) hold
+// (e <= a: none), and whether they are all of its tokens.
+struct PieceTok {
+  int a, e;
+  bool whole;
+};
+template <int SW>
+__device__ __forceinline__ PieceTok piece_tokens(int L, int c0, int c1, int lo, int hi) {
+  const int v_lo = (lo > c0 ? lo : c0) - c0 - SW, v_hi = (hi < c1 ? hi : c1) - c0 - SW;
+  const int t_lo = v_lo > 0 ? v_lo : 0, t_hi = v_hi > 0 ? v_hi : 0;
+  PieceTok r;
+  r.a = t_lo * PLAN_TILE;
+  r.e = t_hi * PLAN_TILE < L ? t_hi * PLAN_TILE : L;
+  r.whole = t_lo == 0 && t_hi == c1 - c0 - SW;
+  return r;
 }
 
 struct BalRange {
@@ -124,13 +153,14 @@ struct BalRange {
 };
 
 // One wave computes workgroup w's range (wave-uniform results; any wave may call it).
+template <int SW>
 __device__ inline BalRange balanced_range(const KParams& p, int w) {
   const int lane = threadIdx.x & 63;
   BalRange r;
   int total = 0;
   for (int base = 0; base < p.n_req; base += 64) {
     const int b = base + lane;
-    total += __shfl(wave_incl_sum(b < p.n_req ? plan_tiles(p, b) : 0), 63, 64);
+    total += __shfl(wave_incl_sum(b < p.n_req ? plan_tiles<SW>(p, b) : 0), 63, 64);
   }
   // wave-uniform values: scalar registers (shuffle results are vector registers to the compiler)
   total = __builtin_amdgcn_readfirstlane(total);
@@ -144,7 +174,7 @@ __device__ inline BalRange balanced_range(const KParams& p, int w) {
   int run = 0;
   for (int base = 0; base < p.n_req && run <= r.lo; base += 64) {
     const int b = base + lane;
-    const int t = b < p.n_req ? plan_tiles(p, b) : 0;
+    const int t = b < p.n_req ? plan_tiles<SW>(p, b) : 0;
     const int incl = wave_incl_sum(t);
     const int c = run + incl - t;
     const uint64_t m = __builtin_amdgcn_ballot_w64(b < p.n_req && c <= r.lo);
@@ -162,12 +192,13 @@ __device__ inline BalRange balanced_range(const KParams& p, int w) {
 
 // One wave of one workgroup stores the plan the balanced combine reads: [0] chunk, [1] total,
 // [2 + b] = C_b for b <= n_req.
+template <int SW>
 __device__ inline void store_plan(const KParams& p) {
   const int lane = threadIdx.x & 63;
   int run = 0;
   for (int base = 0; base <= p.n_req; base += 64) {
     const int b = base + lane;
-    const int t = b < p.n_req ? plan_tiles(p, b) : 0;
+    const int t = b < p.n_req ? plan_tiles<SW>(p, b) : 0;
     const int incl = wave_incl_sum(t);
     if (b <= p.n_req) p.plan[2 + b] = run + incl - t;
     run += __shfl(incl, 63, 64);
@@ -218,7 +249,7 @@ __device__ __forceinline__ SegOut seg_out(const KParams& p, int b, bool final_ou
 //   balanced (num_splits == 0): workgroup w owns global PLAN_TILE-token tiles [w*chunk, (w+1)*chunk)
 //     of the concatenated requests; a request it covers alone is finished in place, others leave a
 //     partial in slot w + b.
-template <int DV, class F>
+template <int DV, int SW, class F>
 __device__ __forceinline__ void for_each_segment(const KParams& p, F&& f) {
   // one call site of f, so the (large, inlined) segment body exists once per kernel
   const bool fixed = p.num_splits > 0;
@@ -227,7 +258,7 @@ __device__ __forceinline__ void for_each_segment(const KParams& p, F&& f) {
     b_lo = blockIdx.y;
     b_hi = b_lo + 1;
   } else {
-    const BalRange r = balanced_range(p, blockIdx.x);
+    const BalRange r = balanced_range<SW>(p, blockIdx.x);
     lo = r.lo;
     hi = r.hi;
     if (lo >= hi) return;
@@ -245,14 +276,14 @@ __device__ __forceinline__ void for_each_segment(const KParams& p, F&& f) {
       e = a + per < L ? a + per : L;
       so = seg_out<DV>(p, b, p.num_splits == 1);
     } else {
-      const int c0 = c, c1 = c + (L + PLAN_TILE - 1) / PLAN_TILE;
+      const int c0 = c, c1 = c + (L > 0 ? (L + PLAN_TILE - 1) / PLAN_TILE + SW : 0);
       c = c1;
       if (c0 >= hi) break;
       if (c1 <= lo) continue;
-      const int t_lo = (lo > c0 ? lo : c0) - c0, t_hi = (hi < c1 ? hi : c1) - c0;
-      a = t_lo * PLAN_TILE;
-      e = t_hi * PLAN_TILE < L ? t_hi * PLAN_TILE : L;
-      so = seg_out<DV>(p, b, t_lo == 0 && t_hi == c1 - c0);
+      const PieceTok pt = piece_tokens<SW>(L, c0, c1, lo, hi);
+      a = pt.a;
+      e = pt.e;
+      so = seg_out<DV>(p, b, pt.whole);
     }
     if (e <= a) continue;
     f(b, a, e, L, so);

@@ -793,9 +793,9 @@ __global__ __launch_bounds__(C::NTHR, 1) void cs_kernel(const KParams p) {
   // the per-layer scale dequantizes fp8 rows (and e4m3 rms codes); a bf16 cache ignores it, as
   // the reference does (mla_decode_attention.py:451-463)
   const float kscale = (C::EB == 1 && p.k_scale) ? *p.k_scale : 1.0f;
-  if (p.num_splits == 0 && blockIdx.x == 0 && blockIdx.z == 0 && threadIdx.x < 64) store_plan(p);   // for the combine
+  if (p.num_splits == 0 && blockIdx.x == 0 && blockIdx.z == 0 && threadIdx.x < 64) store_plan<kPlanSwitchOther>(p);   // for the combine
   int bad = 0;
-  for_each_segment<C::DCG>(p, [&](int req, int a, int e, int L, const SegOut& so) {
+  for_each_segment<C::DCG, kPlanSwitchOther>(p, [&](int req, int a, int e, int L, const SegOut& so) {
     segment<C>(p, sm, req, a, e, L, so, kscale, bad);
     // the next range starts its sub-range set-up with a full barrier; nothing else to reset
   });

@@ -597,9 +597,9 @@ __global__ __launch_bounds__(C::NTHR, C::WGPC) void partial_kernel(const KParams
   // the per-layer scale dequantizes fp8 rows (and e4m3 rms codes); a bf16 cache ignores it, as
   // the reference does (mla_decode_attention.py:451-463)
   const float kscale = (C::EB == 1 && p.k_scale) ? *p.k_scale : 1.0f;
-  if (p.num_splits == 0 && blockIdx.x == 0 && threadIdx.x < 64) store_plan(p);   // for the combine
+  if (p.num_splits == 0 && blockIdx.x == 0 && threadIdx.x < 64) store_plan<kPlanSwitchOther>(p);   // for the combine
   int bad = 0;
-  for_each_segment<C::DCG>(p, [&](int req, int a, int e, int L, const SegOut& so) {
+  for_each_segment<C::DCG, kPlanSwitchOther>(p, [&](int req, int a, int e, int L, const SegOut& so) {
     process_segment<C>(p, sm, req, a, e, L, so, kscale, bad);
   });
   report_pages(p, bad);
@@ -607,7 +607,7 @@ __global__ __launch_bounds__(C::NTHR, C::WGPC) void partial_kernel(const KParams
 
 // Balanced plan: tiles per request, prefix sums, per-workgroup chunk. One workgroup.
 __global__ __launch_bounds__(1024) void plan_kernel(const int* seq_lens, int n_req, int qrows, int nwg,
-                                                    int* plan) {
+                                                    int plan_sw, int* plan) {
   __shared__ int wsum[16];
   __shared__ int carry;
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
@@ -618,7 +618,7 @@ __global__ __launch_bounds__(1024) void plan_kernel(const int* seq_lens, int n_r
     int n = 0;
     if (b < n_req) {
       int L = seq_lens[(int64_t)b * qrows + qrows - 1];
-      n = L > 0 ? (L + PLAN_TILE - 1) / PLAN_TILE : 0;
+      n = L > 0 ? (L + PLAN_TILE - 1) / PLAN_TILE + plan_sw : 0;
     }
     // inclusive wave scan
     int x = n;
@@ -734,7 +734,8 @@ __global__ __launch_bounds__(256) void combine_bal_kernel(const KParams p, int d
     if (tid < nh && p.lse) store_out(p.lse, p.lse_dt, (int64_t)row * p.lse_sr + h0 + tid, kNegInf);
     return;
   }
-  const int w0 = c0 / chunk, w1 = (c1 - 1) / chunk;
+  // the first workgroup with tokens of the request holds its first token's tile (c0 + plan_sw)
+  const int w0 = (c0 + p.plan_sw) / chunk, w1 = (c1 - 1) / chunk;
   if (w0 == w1) return;
   const int nseg = w1 - w0 + 1;
   const int64_t nrow = (int64_t)p.qrows * p.heads;
@@ -984,6 +985,16 @@ static BalancedLayout balanced_layout(const qmla_decode_params* p) {
   return b;
 }
 
+// Plan tiles (of PLAN_TILE tokens) the balanced plan charges per request switch, per kernel family:
+// what a workgroup spends on a piece besides its tokens (the query load and conversion at its first
+// tile, the output write at its last), measured as the time of that many tiles. Fixed splits: 0.
+static int plan_switch(const qmla_decode_params* p) {
+  if (p->num_splits != 0) return 0;
+  if (ro_select(p) >= 0) return kPlanSwitchRo;
+  if (ws_select(p) >= 0) return kPlanSwitchWs;
+  return kPlanSwitchOther;
+}
+
 static KParams make_kparams(const qmla_decode_params* p) {
   KParams k;
   const int eb = elem_bytes(p->kv_dtype);
@@ -1029,6 +1040,7 @@ static KParams make_kparams(const qmla_decode_params* p) {
   k.page_bound = p->num_pages > 0 ? (uint32_t)p->num_pages : 0x80000000u;
   k.status = p->status;
   k.nwg = 0;
+  k.plan_sw = plan_switch(p);
   k.plan = nullptr;
   k.part_o = nullptr;
   k.part_lse = nullptr;
@@ -1085,9 +1097,9 @@ static int run_combine(const qmla_decode_params* p, KParams& k, hipStream_t st) 
 
 static int run_plan(const qmla_decode_params* p, KParams& k, hipStream_t st) {
   const int* sl = p->seq_lens;
-  int n_req = k.n_req, qrows = k.qrows, nwg = k.nwg;
+  int n_req = k.n_req, qrows = k.qrows, nwg = k.nwg, sw = k.plan_sw;
   int* plan = k.plan;
-  void* args[] = {&sl, &n_req, &qrows, &nwg, &plan};
+  void* args[] = {&sl, &n_req, &qrows, &nwg, &sw, &plan};
   return launch((const void*)&plan_kernel, dim3(1, 1, 1), dim3(1024, 1, 1), args, st);
 }
 
@@ -1136,6 +1148,11 @@ static int check_fixed_ws(const qmla_decode_params* p) {
                        (int64_t)(p->num_splits - 1) * p->ws_stride_split + dv;
   if (p->rows > 0 && (last + 1) * 4 > (int64_t)p->workspace_bytes) return QMLA_ERR_WORKSPACE;
   return QMLA_OK;
+}
+
+int qmla_plan_switch_tiles(const qmla_decode_params* p) {
+  const int rc = validate(p);
+  return rc ? rc : qmla::plan_switch(p);
 }
 
 int qmla_plan(const qmla_decode_params* p, void* stream) {

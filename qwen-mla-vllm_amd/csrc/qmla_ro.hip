@@ -245,7 +245,7 @@ __device__ __forceinline__ void role_main(const KParams& p, Smem<C>& sm, float k
   int cb = fixed ? (int)blockIdx.y : b0, ctok = 0, cp = c0;
 
   for (;;) {
-    if (w == 0) plan_window(p, sm, fixed, lo, hi, cb, ctok, cp);
+    if (w == 0) plan_window<kPlanSwitchRo>(p, sm, fixed, lo, hi, cb, ctok, cp);
     __syncthreads();
     const int nseg = sm.win[0], ntot = sm.win[1], npg = sm.win[2], more = sm.win[3];
     if (nseg == 0) break;
@@ -548,8 +548,8 @@ __global__ __launch_bounds__(C::NTHR, 1) void ro_kernel(const KParams p) {
   const int wr = blockIdx.x;
   int lo = 0, hi = 0, b0 = 0, c0 = 0;
   if (!fixed) {
-    if (wr == 0 && wv == 1) store_plan(p);   // for the balanced combine
-    const BalRange r = balanced_range(p, wr);
+    if (wr == 0 && wv == 1) store_plan<kPlanSwitchRo>(p);   // for the balanced combine
+    const BalRange r = balanced_range<kPlanSwitchRo>(p, wr);
     lo = r.lo;
     hi = r.hi;
     b0 = r.b0;

@@ -172,7 +172,7 @@ __device__ __forceinline__ void wait_tiles(int ahead) {
 // Lane l looks at request cb + l; pieces are taken in request order while their pages fit PIDN (the
 // first piece that does not fit is cut at a page boundary). Balanced mode: cp is the plan prefix
 // C_cb of the cursor's request, and the lanes' C_b follow from a scan of their tile counts.
-template <class SM>
+template <int SW, class SM>
 __device__ void plan_window(const KParams& p, SM& sm, bool fixed, int lo, int hi, int& cb, int& ctok,
                             int& cp) {
   const int lane = threadIdx.x & 63;
@@ -183,7 +183,7 @@ __device__ void plan_window(const KParams& p, SM& sm, bool fixed, int lo, int hi
     const int b = cb + lane;
     int a = 0, e = 0, L = 0, fl = 0;
     // plan tiles [c0, c1) of request b (balanced mode)
-    const int tb = (!fixed && b < p.n_req) ? plan_tiles(p, b) : 0;
+    const int tb = (!fixed && b < p.n_req) ? plan_tiles<SW>(p, b) : 0;
     const int tincl = wave_incl_sum(tb);
     const int c0 = cp + tincl - tb, c1 = cp + tincl;
     bool beyond;
@@ -203,11 +203,11 @@ __device__ void plan_window(const KParams& p, SM& sm, bool fixed, int lo, int hi
         beyond = c0 >= hi;
         if (!beyond && c1 > lo) {
           L = req_len(p, b);
-          const int t_lo = (lo > c0 ? lo : c0) - c0, t_hi = (hi < c1 ? hi : c1) - c0;
-          const int a0 = t_lo * PLAN_TILE;
-          e = t_hi * PLAN_TILE < L ? t_hi * PLAN_TILE : L;
+          const PieceTok pt = piece_tokens<SW>(L, c0, c1, lo, hi);
+          const int a0 = pt.a;
+          e = pt.e;
           a = lane == 0 && ctok > a0 ? ctok : a0;
-          fl = (a == a0 ? SEG_FIRST : 0) | SEG_LAST | (t_lo == 0 && t_hi == c1 - c0 ? SEG_FINAL : 0);
+          fl = (a == a0 ? SEG_FIRST : 0) | SEG_LAST | (pt.whole ? SEG_FINAL : 0);
         }
       }
     }

@@ -180,6 +180,21 @@ def test_routing_without_launch(kv, d_c, rope, heads, rms, qrows, groups, code):
     assert lib.qmla_decode(ctypes.byref(p), None) == code
 
 
+@pytest.mark.parametrize("kv,rms,qrows,groups,splits,tiles", [
+    (_lib.KV_FP8, _lib.RMS_LOG8, 1, 1, 0, 2),     # warp-specialized decode, balanced
+    (_lib.KV_FP8, _lib.RMS_LOG8, 4, 2, 0, 2),     # row-owner GLA-g2 decode, balanced
+    (_lib.KV_BF16, _lib.RMS_BF16, 1, 1, 0, 0),    # per-group kernel
+    (_lib.KV_FP8, _lib.RMS_LOG8, 1, 1, 4, 0),     # fixed splits: no plan
+])
+def test_plan_switch_tiles(kv, rms, qrows, groups, splits, tiles):
+    """The balanced plan's per-request switch charge follows the kernel the params select."""
+    p = _layout(kv, 512, 64, 24, rms, qrows, groups)
+    p.num_splits = splits
+    assert _lib.lib().qmla_plan_switch_tiles(ctypes.byref(p)) == tiles
+    p.d_c = 0
+    assert _lib.lib().qmla_plan_switch_tiles(ctypes.byref(p)) < 0
+
+
 def test_null_params_and_balanced_workspace_errors():
     lib = _lib.lib()
     assert lib.qmla_decode(None, None) == _lib.ERR_NULL

@@ -1,5 +1,6 @@
 """The balanced plan (qmla_plan) on its own, bit for bit: per-request exclusive prefix sums of
-64-token tile counts, the total and the per-workgroup chunk, against numpy. Batch sizes straddle the
+64-token tile counts (plus the switch cost qmla_plan_switch_tiles reports for a non-empty request),
+the total and the per-workgroup chunk, against numpy. Batch sizes straddle the
 kernel's 1024-request batches; with verify rows the last row of a request carries its length. The
 plan stands in for FlashInfer's work-split plan (qwen_mla/fi_decode.py:210-233).
 """
@@ -33,10 +34,12 @@ def test_plan_prefix_sums(gpu, n_req, qrows, nwg):
     _lib.check("qmla_plan", _lib.lib().qmla_plan(p, _stream()))
     torch.cuda.synchronize()
     got = ws[:n_req + 3].cpu().numpy()
-    tiles = (L + 63) // 64
+    sw = _lib.lib().qmla_plan_switch_tiles(p)
+    assert sw >= 0
+    tiles = (L + 63) // 64 + sw * (L > 0)
     total = int(tiles.sum())
     exp = np.concatenate([[max(-(-total // nwg), 1), total], np.cumsum(tiles) - tiles, [total]])
-    print(f"[plan n_req {n_req} qrows {qrows} nwg {nwg}] total {total} tiles", flush=True)
+    print(f"[plan n_req {n_req} qrows {qrows} nwg {nwg}] total {total} tiles (switch {sw})", flush=True)
     assert np.array_equal(got, exp), np.argwhere(got != exp)[:5].ravel().tolist()
 
 
@@ -63,7 +66,9 @@ def test_decode_kernels_store_the_plan(gpu, kv, rms, d_c, n_req, nwg):
     _lib.check("qmla_decode_partial", _lib.lib().qmla_decode_partial(p, _stream()))
     torch.cuda.synchronize()
     got = ws[:n_req + 3].cpu().numpy()
-    tiles = (L + 63) // 64
+    sw = _lib.lib().qmla_plan_switch_tiles(p)
+    assert sw >= 0
+    tiles = (L + 63) // 64 + sw * (L > 0)
     total = int(tiles.sum())
     exp = np.concatenate([[max(-(-total // nwg), 1), total], np.cumsum(tiles) - tiles, [total]])
     assert np.array_equal(got, exp), np.argwhere(got != exp)[:5].ravel().tolist()
