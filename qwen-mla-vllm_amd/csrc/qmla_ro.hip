@@ -225,10 +225,9 @@ __device__ __forceinline__ void role_main(const KParams& p, Smem<C>& sm, float k
 
   // one piece descriptor (wave-uniform fields: scalar registers)
   auto read_seg = [&](int k) {
-    i32x4 a = ldsr128(&sm.seg[k].req);
-    i32x4 b = ldsr128(&sm.seg[k].nt);
-    lds_wait_n<1>(a);
-    lds_wait_n<0>(b);
+    // drained (a kernel argument the compiler reloads nearby may still be in flight)
+    i32x4 a, b;
+    ldsr128x2_drained(&sm.seg[k].req, &sm.seg[k].nt, a, b);
     SegD d;
     d.req = __builtin_amdgcn_readfirstlane(a[0]);
     d.ta = __builtin_amdgcn_readfirstlane(a[1]);
@@ -564,7 +563,7 @@ __global__ __launch_bounds__(C::NTHR, 1) void ro_kernel(const KParams p) {
 
 typedef void (*RoFn)(const KParams);
 // [0]: 4 verify rows per head, [1]: other verify counts
-static const RoFn kRo[] = {&ro_kernel<RO<5, true>>, &ro_kernel<RO<5, false>>};
+static const RoFn kRo[] = {&ro_kernel<RO<3, true>>, &ro_kernel<RO<3, false>>};
 
 }  // namespace ro
 
