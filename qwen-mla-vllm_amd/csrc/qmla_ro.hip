@@ -9,18 +9,24 @@
 //                        as e4m3 hi + lo parts resident in VGPRs, the K bytes as stored), divides by
 //                        the rms, keeps the rows' online softmax in its own registers and accumulates
 //                        P . V over the group's 256 latent columns (fp16 MFMA; P stays in the score
-//                        registers, whose token order the transposed V reads follow). No other wave
-//                        takes part in a row, so a tile needs no exchange of maxima or P through LDS;
-//   DMA waves (6-7):     stream tiles global -> LDS with LDS-DMA, A tiles ahead, into a ring of A+1
-//                        stages, each waiting only for its own loads.
+//                        registers and V comes from LDS already as fp16 operands in the score
+//                        registers' token order). No other wave takes part in a row, so a tile needs
+//                        no exchange of maxima or P through LDS;
+//   DMA waves (6-7):     wave h streams rows 16h..16h+15 of every tile global -> LDS with LDS-DMA,
+//                        A tiles ahead, into a ring of A+1 stages, waiting only for its own loads;
+//                        once its half of the next tile is in, it converts that half's V (both
+//                        groups) to fp16 MFMA operands in a second, double-buffered area. The three
+//                        compute waves of a group would each convert the same V; this way it is done
+//                        once, on the SIMDs that hold one compute wave instead of two.
 // The workgroup meets once per tile at one barrier (the ring stage of tile g is refilled after it).
 // Rows are ordered head-major within a group (row = head * qrows + verify token).
 //
 // Staged rows keep each 16-byte chunk inside its region (four latent blocks of 8 chunks, the rope's
 // 4, the rms codes' 2), rotated there by f(r) = ((r >> 3) + (r >> 4)) & 1. With 608-byte rows (152
 // dwords, 24 banks apart) that keeps the K reads (16 consecutive rows) and the transposed V reads
-// (rows 4lg..4lg+3 and 16+4lg..16+4lg+3 of lane group lg) on distinct banks, and a lane's reads of
-// every latent block share one base register: the block and chunk go into the offset fields.
+// (8 consecutive rows) on distinct banks, and a lane's reads of every latent block share one base
+// register: the block and chunk go into the offset fields. A stage is two halves of 16 rows, each
+// padded to whole DMA instructions, so each DMA wave's loads hold exactly its half.
 //
 // Reference semantics: qwen_mla/ops/mla_decode_attention.py:297-586 (stage 1: fp8 dequant :451-463,
 // rms divide :466-507, online softmax :553-560, partial store :562-586), with the GLA-g2 head-to-group
@@ -49,12 +55,13 @@ struct RO {
   static constexpr int DCG = 256, G = 2, DC = G * DCG;   // latent columns per group, of a row
   static constexpr int NB = DCG / 128;                   // 128-column blocks of the fp8 product
   static constexpr int A = A_, S = A_ + 1;
-  static constexpr int CPR = 38, RB = 16 * CPR, STAGE = TILE * RB;   // 608-byte rows
+  static constexpr int CPR = 38, RB = 16 * CPR;   // 608-byte rows
+  // a stage holds two halves of 16 rows, each padded to whole DMA instructions (640 chunks)
+  static constexpr int HCH = 640, HALF = 16 * HCH, STAGE = 2 * HALF;
   static constexpr int NW = 8, NTHR = 64 * NW, NCW = 6, NDW = 2;
   static constexpr int NRB = 3;                          // row blocks per group (48 rows)
-  static constexpr int NCH = TILE * CPR;                 // 16-byte chunks per tile
-  static constexpr int NI = (NCH + 63) / 64;             // DMA instructions per tile
-  static constexpr int DPW = (NI + NDW - 1) / NDW;       // ... per DMA wave (at most)
+  static constexpr int NI = 2 * HCH / 64;                // DMA instructions per tile
+  static constexpr int DPW = NI / NDW;                   // ... per DMA wave: its half's 16 rows
   static constexpr int NBQ = NB + 1;                     // ... and the rope as one more
   static constexpr int KPT = 2 * NBQ;                    // 16-byte K reads per lane and token block
   static constexpr int KQ = 4 * NBQ;                     // query loads (8 bf16) per lane
@@ -67,12 +74,25 @@ struct RO {
 template <class C>
 struct Smem {
   char kv[C::S][C::STAGE];
+  // V of a tile as fp16 MFMA B operands: [tile parity][group][16-column block][lane], 8 values each
+  // (bytes 0-7 from the tile's first 16 rows, 8-15 from the second)
+  alignas(16) char vh[2][C::G][C::CB][64][16];
   alignas(16) SegD seg[NSEG];
   alignas(16) int pid[PIDN];
   int win[4];
 };
 
 // lane 4k + I's value, to the 4 lanes 4k .. 4k+3 (every lane is written: no old value)
+template <class C>
+__device__ __forceinline__ int rowoff(int r) {
+  return (r >> 4) * C::HALF + (r & 15) * C::RB;
+}
+
+template <int OFF>
+__device__ __forceinline__ void ldsw64_at(uint32_t a, const i32x2& v) {
+  asm volatile("ds_write_b64 %0, %1 offset:%2" : : "v"(a), "v"(v), "n"(OFF));
+}
+
 template <int I>
 __device__ __forceinline__ float quad_bcast(float x) {
   return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(x), I | (I << 2) | (I << 4) | (I << 6), 0xF, 0xF, true));
@@ -212,15 +232,26 @@ __device__ __forceinline__ void role_main(const KParams& p, Smem<C>& sm, float k
   if constexpr (ROLE == DMA) {
 #pragma unroll
     for (int j = 0; j < C::DPW; ++j) {
-      int q = (dw + C::NDW * j) * 64 + lane;
-      q = q < C::NCH ? q : C::NCH - 1;
-      const int rr = q / C::CPR, pp = q - rr * C::CPR;
-      doff[j] = (uint32_t)(rr * C::RB + 16 * pos_chunk<C::CPR>(pp, lflip<C::CPR>(rr)));
-      drow[j] = rr;
+      // chunk qq of half dw: row 16dw + qq / CPR, position qq % CPR; chunks past the 16 rows are
+      // padding (an offset past every buffer: they read zeros, or are not issued)
+      const int qq = 64 * j + lane;
+      const bool pad = qq >= 16 * C::CPR;
+      const int q = pad ? 0 : qq;
+      const int rr = 16 * dw + q / C::CPR, pp = q % C::CPR;
+      doff[j] = pad ? 0x80000000u : (uint32_t)(rr * C::RB + 16 * pos_chunk<C::CPR>(pp, lflip<C::CPR>(rr)));
+      drow[j] = pad ? -1 : rr;
     }
   }
-  const int nmine = ROLE == DMA ? (C::NI - dw + C::NDW - 1) / C::NDW : 0;   // DMA instructions per tile
-  const bool big = nmine == C::DPW;
+  // the DMA wave's transposed reads of its half for the fp16 V: lane group L takes 16-column block
+  // 2cp + (L & 1) of rows 16dw + 8(L >> 1) .. +7 (lane pair 2r', 2r'+1: row r'), whose bytes 0-3 are
+  // column n's tokens for lane group 2(L >> 1) and bytes 4-7 for lane group 2(L >> 1) + 1
+  uint32_t cva = 0, cvb = 0, cvw = 0;
+  if constexpr (ROLE == DMA) {
+    const int R = 16 * dw + 8 * (lg >> 1) + (ln16 >> 1), fr = lflip<C::CPR>(R), k0 = lg & 1;
+    cva = (uint32_t)(rowoff<C>(R) + 16 * (k0 + fr) + 8 * (ln16 & 1));
+    cvb = (uint32_t)(rowoff<C>(R) + 16 * ((6 + k0 + fr) & 7) + 8 * (ln16 & 1));
+    cvw = (uint32_t)(k0 * 1024 + (32 * (lg >> 1) + ln16) * 16 + 8 * dw);
+  }
   const bool contig = p.token_stride_b == C::RB;
 
   // one piece descriptor (wave-uniform fields: scalar registers)
@@ -287,16 +318,13 @@ __device__ __forceinline__ void role_main(const KParams& p, Smem<C>& sm, float k
           const char* base = p.kv + (int64_t)pg * p.page_stride_b + (int64_t)ioff * p.token_stride_b;
           const __amdgpu_buffer_rsrc_t rs = make_rsrc(base, (uint32_t)(nvalid * C::RB));
 #pragma unroll
-          for (int j = 0; j < C::DPW; ++j) {
-            const int i = dw + C::NDW * j;
-            if (i < C::NI) dma16_buf(rs, doff[j], dst + i * 1024);
-          }
+          for (int j = 0; j < C::DPW; ++j) dma16_buf(rs, doff[j], dst + (C::DPW * dw + j) * 1024);
         } else {
           // per-lane page lookup; rows past the piece end repeat its last row
 #pragma unroll
           for (int j = 0; j < C::DPW; ++j) {
-            const int i = dw + C::NDW * j;
-            if (i < C::NI) {
+            const int i = C::DPW * dw + j;
+            if (drow[j] >= 0) {
               const int rr = drow[j] < nvalid ? drow[j] : nvalid - 1;
               const int tok = tok0 + rr;
               const int q = tok / P;
@@ -322,19 +350,42 @@ __device__ __forceinline__ void role_main(const KParams& p, Smem<C>& sm, float k
       // wait until tile t landed, with tiles t+1 .. last issued after it
       auto wait_tile = [&](int t, int last) {
         const int ahead = last - t;
-        if (big) wait_tiles<C::DPW, C::A - 1>(ahead);
-        else wait_tiles<(C::NI % C::NDW == 0 ? C::DPW : C::DPW - 1), C::A - 1>(ahead);
+        wait_tiles<C::DPW, C::A - 1>(ahead);
+      };
+      // this wave's half of tile t (landed) as fp16 V operands of both groups into vh[t & 1]
+      auto convert = [&](int t) {
+        const uint32_t sb = lds_addr(sm.kv[t % C::S]);
+        const uint32_t vo = lds_addr(&sm.vh[t & 1][0][0][0][0]) + cvw;
+        i32x2 raw[2 * 8];
+        static_for<0, 16>([&](auto kc) {
+          constexpr int k = decltype(kc)::value, gg = k / 8, cp = k % 8, b = 2 * gg + cp / 4;
+          if constexpr (cp % 4 < 3) raw[k] = ldstr8_at<128 * b + 32 * (cp % 4)>(sb + cva);
+          else raw[k] = ldstr8_at<128 * b>(sb + cvb);
+        });
+        // read k has 15 - k reads and 2k writes issued after it when it is awaited (LDS operations
+        // complete in order)
+        static_for<0, 16>([&](auto kc) {
+          constexpr int k = decltype(kc)::value, gg = k / 8, cp = k % 8;
+          lds_wait_n<15>(raw[k]);
+          const i32x4 v = __builtin_bit_cast(i32x4, fp8x8_to_f16(raw[k]));
+          ldsw64_at<1024 * (C::CB * gg + 2 * cp)>(vo, i32x2{v[0], v[1]});
+          ldsw64_at<1024 * (C::CB * gg + 2 * cp) + 256>(vo, i32x2{v[2], v[3]});
+        });
       };
       enter_i();
       pidv = ldsr32(&sm.pid[ipg]);
       for (int t = 0; t < C::A && t < ntot; ++t) issue(t);
       wait_tile(0, (C::A < ntot ? C::A : ntot) - 1);
+      convert(0);
       lds_barrier();
 #pragma clang loop unroll(disable)
       for (int g = 0; g < ntot; ++g) {
         // stage (g + A) % S held tile g - 1, which every compute wave finished before the last barrier
         if (g + C::A < ntot) issue(g + C::A);
-        if (g + 1 < ntot) wait_tile(g + 1, g + C::A < ntot - 1 ? g + C::A : ntot - 1);
+        if (g + 1 < ntot) {
+          wait_tile(g + 1, g + C::A < ntot - 1 ? g + C::A : ntot - 1);
+          convert(g + 1);
+        }
         lds_barrier();
       }
       wait_vmcnt<0>();
@@ -342,10 +393,6 @@ __device__ __forceinline__ void role_main(const KParams& p, Smem<C>& sm, float k
       lds_barrier();
       int ks = 0, ts = 0, s_ta = 0, s_nt = 0, s_fl = 0, s_req = 0, lim = 0, lim_min = 0;
       constexpr bool quad = C::QUAD;
-      // transposed V reads: lanes 2r', 2r'+1 of lane group lg supply the tile row that holds the
-      // lane group's score token r' (4lg + r' for r' < 4, 16 + 4lg + r' - 4 after), so the value
-      // operand's k order is the score registers' token order
-      const int vr = (ln16 >> 1) < 4 ? 4 * lg + (ln16 >> 1) : 16 + 4 * lg + (ln16 >> 1) - 4;
       // ---- per-lane read offsets within a stage ----
       // K: token block tb, 16-byte half h of the lane group's 32 columns; latent block b adds 128b
       // bytes. The rope block: lane groups 2, 3 read lane groups 0, 1's rope chunks again (the
@@ -356,13 +403,9 @@ __device__ __forceinline__ void role_main(const KParams& p, Smem<C>& sm, float k
 #pragma unroll
         for (int h = 0; h < 2; ++h) {
           const int krow = 16 * tb + ln16, fk = lflip<C::CPR>(krow);
-          koff[tb][h] = (uint32_t)(krow * C::RB + 16 * (grp * (C::DCG / 16) + ((2 * lg + h + fk) & 7)));
-          kofr[tb][h] = (uint32_t)(krow * C::RB + 16 * (C::DC / 16 + ((2 * lg + h + fk) & 3)));
+          koff[tb][h] = (uint32_t)(rowoff<C>(krow) + 16 * (grp * (C::DCG / 16) + ((2 * lg + h + fk) & 7)));
+          kofr[tb][h] = (uint32_t)(rowoff<C>(krow) + 16 * (C::DC / 16 + ((2 * lg + h + fk) & 3)));
         }
-      // V: 16-column block c = 8b + kk of the group sits at chunk position (kk + f) & 7 of latent block b
-      const int fv = lflip<C::CPR>(vr);
-      const uint32_t vb0 = (uint32_t)(vr * C::RB + 16 * (grp * (C::DCG / 16) + fv) + 8 * (ln16 & 1));
-      const uint32_t vb7 = (uint32_t)(vr * C::RB + 16 * (grp * (C::DCG / 16) + ((7 + fv) & 7)) + 8 * (ln16 & 1));
       // rms codes: the lane's head in token row 16tb + 4lg + (the lane's quad slot, or i)
       constexpr int NCI = quad ? 1 : 4;
       uint32_t coff[2][NCI];
@@ -371,7 +414,7 @@ __device__ __forceinline__ void role_main(const KParams& p, Smem<C>& sm, float k
 #pragma unroll
         for (int i = 0; i < NCI; ++i) {
           const int row = 16 * tb + 4 * lg + (quad ? (ln16 & 3) : i);
-          coff[tb][i] = (uint32_t)(row * C::RB + 16 * chunk_pos<C::CPR>(rms_b >> 4, lflip<C::CPR>(row)) + (rms_b & 15));
+          coff[tb][i] = (uint32_t)(rowoff<C>(row) + 16 * chunk_pos<C::CPR>(rms_b >> 4, lflip<C::CPR>(row)) + (rms_b & 15));
         }
 #pragma clang loop unroll(disable)
       for (int g = 0; g < ntot; ++g) {
@@ -466,14 +509,13 @@ __device__ __forceinline__ void role_main(const KParams& p, Smem<C>& sm, float k
               });
             }
           });
-          // ---- V^T reads of the tile (the K reads have all landed) ----
-          i32x2 vraw[C::CB];
+          // ---- V of the tile as fp16, converted by the DMA waves (the K reads have all landed) ----
+          i32x4 vraw[C::CB];
           {
-            const uint32_t a0 = sb + vb0, a7 = sb + vb7;
+            const uint32_t a0 = lds_addr(&sm.vh[g & 1][grp][0][0][0]) + 16 * lane;
             static_for<0, C::CB>([&](auto cc) {
-              constexpr int c = decltype(cc)::value, b = c / 8, kk = c % 8;
-              if constexpr (kk < 7) vraw[c] = ldstr8_at<128 * b + 16 * kk>(a0);
-              else vraw[c] = ldstr8_at<128 * b>(a7);
+              constexpr int c = decltype(cc)::value;
+              vraw[c] = ldsr128_at<1024 * c>(a0);
             });
           }
           // ---- rms divide and scale; mask only a tile that reaches a row's limit; tile max ----
@@ -521,8 +563,7 @@ __device__ __forceinline__ void role_main(const KParams& p, Smem<C>& sm, float k
           static_for<0, C::CB>([&](auto cc) {
             constexpr int c = decltype(cc)::value;
             lds_wait_n<cmin15(C::CB - 1 - c)>(vraw[c]);
-            const f16x8 vf = fp8x8_to_f16(vraw[c]);
-            acc[c] = mfma16(pf, vf, acc[c]);
+            acc[c] = mfma16(pf, __builtin_bit_cast(f16x8, vraw[c]), acc[c]);
           });
         }
         if (++ts == s_nt) {
