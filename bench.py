@@ -517,9 +517,10 @@ def main():
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "fp8+bf16" if ws_fp8 else "bf16",
+        "dtype": "fp8+fp16" if ws_fp8 else "bf16",
         "storage": (("e4m3 latent/rope + u8 log8 rms; scores on the fp8 MFMAs (cache bytes as stored, query as "
-                     "e4m3 hi+lo, 8 significant bits), bf16 P.V, fp32 accumulate and softmax")
+                     "e4m3 hi+lo, 8 significant bits), P.V on the fp16 MFMAs (V exact, P with 11 significant "
+                     "bits), fp32 accumulate and softmax")
                     if ws_fp8 else
                     "e4m3 latent/rope + u8 log8 rms; bf16 MFMA operands, fp32 accumulate and softmax"
                     if case.kv == "fp8" else "bf16 cache; bf16 MFMA operands, fp32 accumulate and softmax"),
