@@ -511,7 +511,7 @@ __device__ __forceinline__ void role_main(const KParams& p, Smem<C>& sm, float k
     }
     lds_barrier();
 
-    // iteration g: value waves issue tile g+A, take tile g-2 and wait for tile g+1; score waves fix
+    // iteration g: value waves issue tile g+A, wait for tile g+1 and take tile g-2; score waves fix
     // tile g-1 and score tile g
 #pragma clang loop unroll(disable)
     for (int g = 0; g <= ntot + 1; ++g) {
@@ -780,6 +780,11 @@ __device__ __forceinline__ void role_main(const KParams& p, Smem<C>& sm, float k
         if constexpr (C::ISS == 1 || C::ISS == 2) {
           if (g + C::A < ntot) issue(g + C::A, false);
         }
+        // issuing value waves wait for the next tile before their P . V rather than after it (the
+        // fp8 B 128 workload measured 0.6% faster so)
+        if constexpr (C::ISS == 1) {
+          if (g + 1 < ntot) wait_tile(g + 1, g + C::A < ntot - 1 ? g + C::A : ntot - 1);
+        }
         // ---- P . V for tile j = g-2 over columns VC*vw .. +VC: reads first ----
         const int j = g - 2, pj = (g + 1) % 3;
         const int vr0 = 16 * C::MBV * vg;   // the group's first row in the workgroup's arrays
@@ -884,7 +889,9 @@ __device__ __forceinline__ void role_main(const KParams& p, Smem<C>& sm, float k
         if constexpr (C::ISS == 0) {
           if (g + C::A < ntot) issue(g + C::A, false);
         }
-        if (g + 1 < ntot) wait_tile(g + 1, g + C::A < ntot - 1 ? g + C::A : ntot - 1);
+        if constexpr (C::ISS != 1) {
+          if (g + 1 < ntot) wait_tile(g + 1, g + C::A < ntot - 1 ? g + C::A : ntot - 1);
+        }
       }
       lds_barrier();
     }
