@@ -82,7 +82,7 @@ struct Smem {
   int win[4];
 };
 
-// lane 4k + I's value, to the 4 lanes 4k .. 4k+3 (every lane is written: no old value)
+// byte offset of staged row r in a stage (two halves of 16 rows)
 template <class C>
 __device__ __forceinline__ int rowoff(int r) {
   return (r >> 4) * C::HALF + (r & 15) * C::RB;
@@ -93,6 +93,7 @@ __device__ __forceinline__ void ldsw64_at(uint32_t a, const i32x2& v) {
   asm volatile("ds_write_b64 %0, %1 offset:%2" : : "v"(a), "v"(v), "n"(OFF));
 }
 
+// lane 4k + I's value, to the 4 lanes 4k .. 4k+3 (every lane is written: no old value)
 template <int I>
 __device__ __forceinline__ float quad_bcast(float x) {
   return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(x), I | (I << 2) | (I << 4) | (I << 6), 0xF, 0xF, true));
