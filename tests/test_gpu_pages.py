@@ -1,8 +1,13 @@
-"""Block-table entries outside the cache's pages, on the GPU: each kernel family (warp-specialized FP8
-+ log8, per-group bf16, column-split d_c 1792) checks every entry it reads against the page count
-the wrapper passes, reads page 0 instead of the bad page, and stores QMLA_ERR_PAGE into the status
-word; the requests whose entries are all valid still match the oracle, in the balanced and the
-fixed-split modes. The reference trusts the table (a bad entry is an out-of-bounds read there)."""
+"""Page-table and cache-layout cases on the GPU.
+
+Block-table entries outside the cache's pages: each kernel family (warp-specialized FP8 + log8,
+per-group bf16, column-split d_c 1792) checks every entry it reads against the page count the
+wrapper passes, reads page 0 instead of the bad page, and stores QMLA_ERR_PAGE into the status word;
+the requests whose entries are all valid still match the oracle, in the balanced and the fixed-split
+modes. The reference trusts the table (a bad entry is an out-of-bounds read there).
+
+A cache whose token stride is wider than its rows (bytes past every row set to NaN) matches the
+oracle in the warp-specialized, row-owner and per-group kernels."""
 import pytest
 import torch
 
@@ -50,3 +55,39 @@ def test_out_of_range_page_ids(gpu, family, splits):
     # the intact table leaves the status word untouched
     _, _, st = run(c.block_table)
     assert st == 0
+
+
+# A cache whose token stride is wider than the row (a view of a wider tensor): the kernels take the
+# per-lane page-lookup path instead of one buffer range per tile.
+PADDED = {
+    "ws_fp8_log8": dict(d_c=512, kv="fp8", rms_mode="log8", qrows=1, groups=1),
+    "ro_gla_fp8_log8": dict(d_c=512, kv="fp8", rms_mode="log8", qrows=4, groups=2),
+    "partial_bf16": dict(d_c=512, kv="bf16", rms_mode="bf16", qrows=1, groups=1),
+}
+
+
+@pytest.mark.parametrize("splits", [0, 4])
+@pytest.mark.parametrize("family", sorted(PADDED))
+def test_padded_token_stride(gpu, family, splits):
+    import qmla
+    f = PADDED[family]
+    c = make_case(batch=3, heads=24, d_c=f["d_c"], rope_w=64, page_size=64, lens=[700, 1500, 33], kv=f["kv"],
+                  rms_mode=f["rms_mode"], seed=73, device=gpu, qrows=f["qrows"], groups=f["groups"],
+                  rms="spread")
+    pages, P, one, row = c.cache.shape
+    pad = 32 if f["kv"] == "fp8" else 16   # elements: 32 bytes past every row
+    wide = torch.full((pages, P, one, row + pad), 0x7F if f["kv"] == "fp8" else float("nan"),
+                      dtype=c.cache.dtype, device=gpu)
+    wide[..., :row] = c.cache
+    view = wide[..., :row]
+    assert view.stride(1) == row + pad
+    print(f"[padded stride {family} splits {splits}] row {row}, token stride {row + pad}", flush=True)
+    o, lse = qmla.forward(c.q_nope, c.q_pe, view, c.block_table, c.seq_lens, d_c=c.d_c, page_size=c.page_size,
+                          sm_scale=c.sm_scale, kv_fp8=c.kv == "fp8", fp8_rms="log8", k_scale=c.k_scale,
+                          qrows=c.qrows, groups=c.groups, num_splits=splits, num_workgroups=0 if splits else 5)
+    torch.cuda.synchronize()
+    ro, rl = run_oracle(c)
+    err = (o.float().cpu() - ro).abs().max().item()
+    lerr = (lse.cpu() - rl).abs().max().item()
+    print(f"  max-abs {err:.3e} lse {lerr:.3e}", flush=True)
+    assert err < TOL[c.kv] and lerr < 1e-2
