@@ -56,6 +56,8 @@ struct KParams {
   int plan_sw;          // plan tiles charged for a request switch (see plan_tiles): read by the
                         // combine and the plan kernel; the decode kernels have their family's as a
                         // constant
+  int part_h;           // balanced partial outputs in fp16 and without the fp8 scale (fp8 caches:
+                        // |value| <= 448), which the combine applies; else fp32
 };
 
 // A block-table entry checked against the page bound: an entry outside [0, page_bound) reads page 0

@@ -737,9 +737,11 @@ __device__ __forceinline__ void segment(const KParams& p, Smem<C>& sm, int req, 
     const float l = lrow[mb];
     const float lse_v = l > 0.f ? (mref[mb] + fast_log2(l)) * kLn2 : kNegInf;
     const float inv = l > 0.f ? kscale / l : 0.f;   // fp8 values were accumulated unscaled
+    const float invh = l > 0.f ? 1.0f / l : 0.f;    // ... and are stored so as fp16 partials
+    const bool ph = !so.final_out && so.plse && p.part_h;
     float iv[4];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) iv[i] = __shfl(inv, 4 * lg + i);
+    for (int i = 0; i < 4; ++i) iv[i] = __shfl(ph ? invh : inv, 4 * lg + i);
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int r = rbase + 16 * mb + 4 * lg + i;
@@ -762,6 +764,10 @@ __device__ __forceinline__ void segment(const KParams& p, Smem<C>& sm, int req, 
 #pragma unroll
           for (int cb = 0; cb < C::CB; ++cb) o[16 * cb] = acc[mb][cb][i] * iv[i];
         }
+      } else if (ph) {
+        _Float16* ob = reinterpret_cast<_Float16*>(so.po) + (int64_t)jq * so.po_sr + (int64_t)head * so.po_sh + col;
+#pragma unroll
+        for (int cb = 0; cb < C::CB; ++cb) ob[16 * cb] = (_Float16)(acc[mb][cb][i] * iv[i]);
       } else {
         float* ob = so.po + (int64_t)jq * so.po_sr + (int64_t)head * so.po_sh + col;
 #pragma unroll

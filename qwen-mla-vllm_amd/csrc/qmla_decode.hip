@@ -571,6 +571,7 @@ __device__ __forceinline__ void process_segment(const KParams& p, Smem<C>& sm, i
       const int jq = r / hpg, h = r - jq * hpg;
       const int head = g * hpg + h;
       const float inv = l > 0.f ? kscale / l : 0.f;   // fp8 values were accumulated unscaled
+      const float invh = l > 0.f ? 1.0f / l : 0.f;    // ... and are stored so as fp16 partials
       const float lse_v = l > 0.f ? (m + fast_log2(l)) * kLn2 : kNegInf;
       if (so.final_out) {
         const int64_t ob = (int64_t)(row0 + jq) * p.o_sr + (int64_t)head * p.o_sh + wl * C::NCOL + ln16;
@@ -578,6 +579,11 @@ __device__ __forceinline__ void process_segment(const KParams& p, Smem<C>& sm, i
         for (int cb = 0; cb < C::CB; ++cb) store_out(p.out, p.out_dt, ob + cb * 16, acc[mb][cb][i] * inv);
         if (wl == 0 && ln16 == 0 && p.lse)
           store_out(p.lse, p.lse_dt, (int64_t)(row0 + jq) * p.lse_sr + head, lse_v);
+      } else if (so.plse && p.part_h) {
+        _Float16* ob = reinterpret_cast<_Float16*>(so.po) + (int64_t)jq * so.po_sr + (int64_t)head * so.po_sh + wl * C::NCOL + ln16;
+#pragma unroll
+        for (int cb = 0; cb < C::CB; ++cb) ob[cb * 16] = (_Float16)(acc[mb][cb][i] * invh);
+        if (wl == 0 && ln16 == 0) so.plse[(int64_t)jq * so.plse_sr + head] = lse_v;
       } else {
         float* ob = so.po + (int64_t)jq * so.po_sr + (int64_t)head * so.po_sh + wl * C::NCOL + ln16;
 #pragma unroll
@@ -719,27 +725,14 @@ __global__ __launch_bounds__(256) void combine_kernel(const KParams p, int dv) {
 // per workgroup: at 128 x 24 rows the merge took 11.0 us against 11.9 (4 heads) and 15.1 (8 heads).
 constexpr int CH_HB = 2;
 constexpr int CH_NS = 4;   // segments per batch of loads
-__global__ __launch_bounds__(256) void combine_bal_kernel(const KParams p, int dv) {
-  const int hblk = blockIdx.x, row = blockIdx.y;
+// the columns of one (row, head block): H = fp16 partials without the fp8 scale, osc applies it
+template <bool H>
+__device__ __forceinline__ void combine_cols(const KParams& p, int dv, int row, int jq, int req, int h0, int nh,
+                                             int w0, int nseg) {
   const int tid = threadIdx.x;
-  const int req = row / p.qrows, jq = row - req * p.qrows;
-  const int h0 = hblk * CH_HB;
-  const int nh = p.heads - h0 < CH_HB ? p.heads - h0 : CH_HB;
-  const int chunk = p.plan[0];
-  const int c0 = p.plan[2 + req], c1 = p.plan[3 + req];
-  if (c1 <= c0) {  // empty request: zero output, -inf lse
-    for (int h = 0; h < nh; ++h)
-      for (int c = tid; c < dv; c += 256)
-        store_out(p.out, p.out_dt, (int64_t)row * p.o_sr + (int64_t)(h0 + h) * p.o_sh + c, 0.f);
-    if (tid < nh && p.lse) store_out(p.lse, p.lse_dt, (int64_t)row * p.lse_sr + h0 + tid, kNegInf);
-    return;
-  }
-  // the first workgroup with tokens of the request holds its first token's tile (c0 + plan_sw)
-  const int w0 = (c0 + p.plan_sw) / chunk, w1 = (c1 - 1) / chunk;
-  if (w0 == w1) return;
-  const int nseg = w1 - w0 + 1;
   const int64_t nrow = (int64_t)p.qrows * p.heads;
   const int rl0 = jq * p.heads + h0;
+  const float osc = H && p.k_scale ? *p.k_scale : 1.0f;
   for (int cb = 2 * tid; cb < dv; cb += 512) {
     float m[CH_HB], l[CH_HB], a0[CH_HB], a1[CH_HB];
 #pragma unroll
@@ -752,12 +745,19 @@ __global__ __launch_bounds__(256) void combine_bal_kernel(const KParams p, int d
         const int sg = s0 + k < nseg ? s0 + k : nseg - 1;   // past the end: a valid slot, weight 0
         const int64_t slot = (int64_t)w0 + sg + req;
         const float* pl = p.part_lse + slot * nrow + rl0;
-        const float* po = p.part_o + (slot * nrow + rl0) * (int64_t)dv + cb;
 #pragma unroll
         for (int h = 0; h < CH_HB; ++h) {
           const int hh = h < nh ? h : 0;
           ls[k][h] = s0 + k < nseg ? pl[hh] : kNegInf;
-          v[k][h] = *reinterpret_cast<const float2*>(po + (int64_t)hh * dv);
+          const int64_t e = (slot * nrow + rl0 + hh) * (int64_t)dv + cb;   // the slot's element
+          if constexpr (H) {
+            // fp16 partials: the slot's rows at the start of its (fp32-sized) area
+            const f16x2 t = *reinterpret_cast<const f16x2*>(reinterpret_cast<const _Float16*>(
+                                p.part_o + slot * nrow * (int64_t)dv) + (e - slot * nrow * (int64_t)dv));
+            v[k][h] = make_float2((float)t[0], (float)t[1]);
+          } else {
+            v[k][h] = *reinterpret_cast<const float2*>(p.part_o + e);
+          }
         }
       }
 #pragma unroll
@@ -783,13 +783,36 @@ __global__ __launch_bounds__(256) void combine_bal_kernel(const KParams p, int d
 #pragma unroll
     for (int h = 0; h < CH_HB; ++h) {
       if (h >= nh) continue;
-      const float inv = l[h] > 0.f ? 1.0f / l[h] : 0.f;
+      const float inv = l[h] > 0.f ? osc / l[h] : 0.f;
       const int64_t ob = (int64_t)row * p.o_sr + (int64_t)(h0 + h) * p.o_sh + cb;
       store_out(p.out, p.out_dt, ob, a0[h] * inv);
       if (cb + 1 < dv) store_out(p.out, p.out_dt, ob + 1, a1[h] * inv);
       if (cb == 0 && p.lse) store_out(p.lse, p.lse_dt, (int64_t)row * p.lse_sr + h0 + h, l[h] > 0.f ? m[h] + __logf(l[h]) : kNegInf);
     }
   }
+}
+
+__global__ __launch_bounds__(256) void combine_bal_kernel(const KParams p, int dv) {
+  const int hblk = blockIdx.x, row = blockIdx.y;
+  const int tid = threadIdx.x;
+  const int req = row / p.qrows, jq = row - req * p.qrows;
+  const int h0 = hblk * CH_HB;
+  const int nh = p.heads - h0 < CH_HB ? p.heads - h0 : CH_HB;
+  const int chunk = p.plan[0];
+  const int c0 = p.plan[2 + req], c1 = p.plan[3 + req];
+  if (c1 <= c0) {  // empty request: zero output, -inf lse
+    for (int h = 0; h < nh; ++h)
+      for (int c = tid; c < dv; c += 256)
+        store_out(p.out, p.out_dt, (int64_t)row * p.o_sr + (int64_t)(h0 + h) * p.o_sh + c, 0.f);
+    if (tid < nh && p.lse) store_out(p.lse, p.lse_dt, (int64_t)row * p.lse_sr + h0 + tid, kNegInf);
+    return;
+  }
+  // the first workgroup with tokens of the request holds its first token's tile (c0 + plan_sw)
+  const int w0 = (c0 + p.plan_sw) / chunk, w1 = (c1 - 1) / chunk;
+  if (w0 == w1) return;
+  const int nseg = w1 - w0 + 1;
+  if (p.part_h) combine_cols<true>(p, dv, row, jq, req, h0, nh, w0, nseg);
+  else combine_cols<false>(p, dv, row, jq, req, h0, nh, w0, nseg);
 }
 
 }  // namespace qmla
@@ -1041,6 +1064,7 @@ static KParams make_kparams(const qmla_decode_params* p) {
   k.status = p->status;
   k.nwg = 0;
   k.plan_sw = plan_switch(p);
+  k.part_h = p->kv_dtype == QMLA_KV_FP8 ? 1 : 0;
   k.plan = nullptr;
   k.part_o = nullptr;
   k.part_lse = nullptr;

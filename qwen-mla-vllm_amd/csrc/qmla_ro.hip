@@ -195,6 +195,7 @@ __device__ __forceinline__ void role_main(const KParams& p, Smem<C>& sm, float k
     const SegOut so = seg_out<C::DCG>(p, req, (fl & SEG_FINAL) != 0, wr);
     const float l = sum_lg(lpart);
     const float inv = l > 0.f ? kscale / l : 0.f;   // fp8 values were accumulated unscaled
+    const float invh = l > 0.f ? 1.0f / l : 0.f;    // ... and are stored so as fp16 partials
     const float lse_v = l > 0.f ? (mref + fast_log2(l)) * kLn2 : kNegInf;
     const int row0 = req * qrows;
 #pragma unroll
@@ -208,6 +209,11 @@ __device__ __forceinline__ void role_main(const KParams& p, Smem<C>& sm, float k
         const int64_t ob = (int64_t)(row0 + jr) * p.o_sr + (int64_t)h * p.o_sh + col;
 #pragma unroll
         for (int cb = 0; cb < C::CB; ++cb) store_out(p.out, p.out_dt, ob + 16 * cb, acc[cb][i] * inv_i);
+      } else if (so.plse && p.part_h) {
+        _Float16* ob = reinterpret_cast<_Float16*>(so.po) + (int64_t)jr * so.po_sr + (int64_t)h * so.po_sh + col;
+        const float invh_i = __shfl(invh, 4 * lg + i, 64);
+#pragma unroll
+        for (int cb = 0; cb < C::CB; ++cb) ob[16 * cb] = (_Float16)(acc[cb][i] * invh_i);
       } else {
         float* ob = so.po + (int64_t)jr * so.po_sr + (int64_t)h * so.po_sh + col;
 #pragma unroll

@@ -392,6 +392,12 @@ __device__ __forceinline__ void role_main(const KParams& p, Smem<C>& sm, float k
 #pragma unroll
           for (int cb = 0; cb < C::CB; ++cb) store_out(p.out, p.out_dt, ob + 16 * cb, acc[mb][cb][i] * inv);
           if (vh == 0 && ln16 == 0 && p.lse) store_out(p.lse, p.lse_dt, (int64_t)(row0 + jr) * p.lse_sr + h, lse_v);
+        } else if (so.plse && p.part_h) {
+          _Float16* ob = reinterpret_cast<_Float16*>(so.po) + (int64_t)jr * so.po_sr + (int64_t)h * so.po_sh + col;
+          const float invh = l > 0.f ? 1.0f / l : 0.f;
+#pragma unroll
+          for (int cb = 0; cb < C::CB; ++cb) ob[16 * cb] = (_Float16)(acc[mb][cb][i] * invh);
+          if (vh == 0 && ln16 == 0) so.plse[(int64_t)jr * so.plse_sr + h] = lse_v;
         } else {
           float* ob = so.po + (int64_t)jr * so.po_sr + (int64_t)h * so.po_sh + col;
 #pragma unroll
