@@ -155,21 +155,57 @@ def cpu_baseline(case, sample_every: int, budget_s: float):
                        rms_offset=case.rms_offset, kv=case.kv, rms_mode=rms_map[case.rms_mode], k_scale=ks,
                        sm_scale=case.sm_scale, rms_heads=case.heads, groups=case.groups)
 
-    times = []
-    t_all = time.perf_counter()
-    while True:
-        t0 = time.perf_counter()
-        run()
-        times.append(time.perf_counter() - t0)
-        if time.perf_counter() - t_all > budget_s or len(times) >= 3:
-            break
-    t = statistics.median(times)
+    t, k = _cpu_runs(run, budget_s)
     toks = int(sll.to(torch.int64).sum())
     return {"value": round(len(rows) / t, 3), "unit": "tokens/s", "cores": cores, "kind": "port",
             "cpu": cpu_model(),
             "sample": f"{len(picks)} of {n_req} requests (every {sample_every}th, {len(rows)} rows, "
-                      f"{toks} cached tokens), fp32 torch oracle, median of {len(times)} runs "
-                      f"({t:.2f} s each), scaled per request"}
+                      f"{toks} cached tokens), fp32 torch oracle, {CPU_WARMUP} warm-up runs then the median "
+                      f"of {k} ({t:.2f} s each), scaled per request"}
+
+
+CPU_WARMUP, CPU_RUNS = 2, 5
+
+
+def _cpu_runs(fn, budget_s):
+    """CPU_WARMUP untimed runs, then the median of CPU_RUNS timed ones (fewer, but at least one,
+    when a run takes longer than the budget allows)."""
+    for _ in range(CPU_WARMUP):
+        fn()
+    times, t_all = [], time.perf_counter()
+    while True:
+        t0 = time.perf_counter()
+        fn()
+        times.append(time.perf_counter() - t0)
+        if len(times) >= CPU_RUNS or time.perf_counter() - t_all > budget_s:
+            return statistics.median(times), len(times)
+
+
+def cpu_reference_small():
+    """The CPU-runnable reference configuration timed in full on this host's cores: B=4 rows, 24
+    heads sharing one latent row, d_c 512, d_r 64, 2048 tokens each, bf16 cache in 16-token pages
+    behind a random-permutation block table, N(0,1) inputs with seed 0, row-RMS divisor, fp32
+    softmax, bf16 output; the fp32 torch oracle (decode rows per second)."""
+    import torch
+    from oracle import mla_oracle as ora
+    from qmla.synth import make_case
+    cores = len(os.sched_getaffinity(0))
+    torch.set_num_threads(cores)
+    from qmla.synth import compact_requests
+    c = make_case(batch=4, heads=24, d_c=512, rope_w=64, page_size=16, lens=[2048] * 4, kv="bf16",
+                  rms_mode="bf16", seed=0, device="cpu", rms="row", amp=1.0)
+    cache, bt, sl, qn, qp, _ = compact_requests(c, list(range(4)))
+
+    def run():
+        o, _ = ora.mla_decode(qn, qp, cache, bt, sl, page_size=16, d_c=512, rope_w=64, rms_offset=c.rms_offset,
+                              kv="bf16", rms_mode=ora.RMS_BF16, k_scale=1.0, sm_scale=c.sm_scale, rms_heads=24,
+                              groups=1)
+        o.to(torch.bfloat16)
+
+    t, k = _cpu_runs(run, 20.0)
+    return {"value": round(4 / t, 2), "unit": "tokens/s", "cores": cores, "kind": "port", "cpu": cpu_model(),
+            "sample": f"all of it: B 4 x 2048 tokens, bf16 cache, P 16, fp32 torch oracle, {CPU_WARMUP} warm-up runs "
+                      f"then the median of {k} ({t * 1e3:.1f} ms each)"}
 
 
 # ------------------------------------------------------------------------------------------------
@@ -200,16 +236,6 @@ def _time_launches(fn, steps, warmup):
     e1.record(st)
     torch.cuda.synchronize()
     return e0.elapsed_time(e1) / steps, time.perf_counter() - t
-
-
-def _cpu_time(fn, budget_s):
-    times, t_all = [], time.perf_counter()
-    while True:
-        t0 = time.perf_counter()
-        fn()
-        times.append(time.perf_counter() - t0)
-        if time.perf_counter() - t_all > budget_s or len(times) >= 5:
-            return statistics.median(times), len(times)
 
 
 def adjacent(args):
@@ -285,7 +311,7 @@ def adjacent(args):
         kr = torch.randn(n, kvh * rd, generator=g).to(torch.bfloat16)
         ku = (torch.randn(H * nope, d_c, generator=g) * d_c ** -0.5).to(torch.bfloat16)
         wn = (torch.randn(hd, generator=g) * 0.1).to(torch.bfloat16)
-        tab = torch.from_numpy(ora.partial_rope_table(list(range(rd // 2)), rd, 1e7, w["max_pos"])).to(torch.bfloat16)
+        tab = qmla.partial_rope_table(list(range(rd // 2)), rd, 1e7, w["max_pos"]).to(torch.bfloat16)
         pos = torch.randint(0, w["max_pos"], (n,), generator=g)
         a = [t.to(dev) for t in (pos, q, lat, kr, ku)]
         gain = qmla.k_gain(wn.to(dev), rd)
@@ -332,9 +358,9 @@ def adjacent(args):
     if not args.no_cpu:
         from threadpoolctl import threadpool_limits
         with threadpool_limits(1):                      # numpy / BLAS on one thread: cores = 1
-            t, k = _cpu_time(cpu_fn, min(args.cpu_budget, 10.0))
+            t, k = _cpu_runs(cpu_fn, min(args.cpu_budget, 10.0))
         cpu = {"value": round(cpu_rows / t, 1), "unit": "tokens/s", "cores": 1, "kind": "port",
-               "cpu": cpu_model(), "sample": f"{sample}, median of {k} runs ({t:.3f} s each)"}
+               "cpu": cpu_model(), "sample": f"{sample}, {CPU_WARMUP} warm-up runs then the median of {k} ({t:.3f} s each)"}
     print(json.dumps({
         "metric": metric, "value": round(n_rows / (ms / 1e3), 1), "unit": "tokens/s", "n_gpus": 1,
         "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms, 5), "higher_is_better": True,
@@ -496,9 +522,11 @@ def main():
               and case.rope_w == 64
               and (ws_rows <= 48 if case.groups == 2 else
                    any(case.heads % hs == 0 and ws_rows // hs <= 32 for hs in range(1, 5))))
-    cpu = None
+    cpu = cpu_small = None
     if not args.no_cpu:
         cpu = cpu_baseline(case, args.cpu_every or CPU_EVERY.get(args.workload, 2), args.cpu_budget)
+        if args.workload == "fp8_b128":
+            cpu_small = cpu_reference_small()
 
     if spec[0] == "lognormal":
         ctx = f"lognormal median {spec[1]} sigma {spec[2]} clipped [{spec[3]}, {spec[4]}]"
@@ -544,6 +572,8 @@ def main():
                      "frac": round(k_gbps / HBM_PEAK_GBPS, 4), "traffic": traffic,
                      "algorithmic_bytes_per_launch": k_bytes},
         "cpu_baseline": cpu,
+        # the CPU-runnable reference configuration (B 4 x 2048, bf16, 16-token pages), timed in full
+        "cpu_reference_b4_ctx2048": cpu_small,
     }
     print(json.dumps(res), flush=True)
 

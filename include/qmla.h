@@ -139,8 +139,9 @@ typedef struct qmla_decode_params {
   /* page-id bound. num_pages > 0: every block-table entry a kernel reads is checked against
    * [0, num_pages); an entry outside it reads page 0 instead (in bounds; the outputs of that request
    * are then meaningless) and, when status is not NULL, the pass stores QMLA_ERR_PAGE into *status
-   * (device int32) before it ends. The library never clears *status. num_pages == 0: entries are
-   * trusted, as the reference trusts them. */
+   * (device int32) before it ends. The library never clears *status. num_pages == 0: there is no
+   * upper bound, so non-negative entries are trusted as the reference trusts them; a negative entry
+   * still reads page 0 and stores QMLA_ERR_PAGE into *status. */
   int32_t num_pages;
   int32_t* status;
 } qmla_decode_params;

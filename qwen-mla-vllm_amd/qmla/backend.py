@@ -53,17 +53,13 @@ class QwenMLAHipImpl:
         self._workspace = Workspace()
 
     def reserve_decode_workspace(self, max_rows: int, device, qrows: int = 1) -> int:
-        """Allocate the balanced-mode workspace for up to `max_rows` decode rows (call once before
-        graph capture: the captured decode then allocates nothing). Returns its size in bytes."""
+        """Allocate the balanced-mode workspace for up to `max_rows` decode rows whose requests carry
+        up to `qrows` query tokens each (1 + the speculative tokens of a verify step). Call it once
+        before graph capture: every captured decode of at most that many rows and tokens per request
+        then allocates nothing. Returns the size in bytes."""
         if max_rows % qrows:
             raise ValueError(f"max_rows {max_rows} is not a multiple of qrows {qrows}")
-        p = _lib.DecodeParams()
-        p.rows, p.heads, p.rms_heads, p.qrows, p.groups = max_rows, max(self.mla_local_heads, 1), \
-            max(self.mla_local_heads, 1), qrows, 1
-        p.d_c, p.rope_w, p.rms_offset = self.kv_lora_rank, max(self.rms_offset - self.kv_lora_rank, 0), self.rms_offset
-        p.kv_dtype = _lib.KV_FP8 if self.mla_kv_fp8 else _lib.KV_BF16
-        p.num_splits, p.num_workgroups = 0, 0
-        n = int(_lib.lib().qmla_workspace_bytes(p))
+        n = max(reserve_bytes(self, max_rows, q) for q in range(1, qrows + 1) if max_rows % q == 0)
         self._workspace.reserve(n, device)
         return n
 
@@ -76,6 +72,40 @@ def _verify_rows(attn_metadata) -> int:
     (qwen_mla/mla_impl.py:455-459; QWEN_MLA_GROUPED_VERIFY=0 keeps one kernel row per token)."""
     grouped = bool(attn_metadata.causal) and os.environ.get("QWEN_MLA_GROUPED_VERIFY", "1") != "0"
     return int(getattr(attn_metadata.decode, "_mla_q", 1) or 1) if grouped else 1
+
+
+def _impl_rms_mode(impl) -> tuple[int, int]:
+    """(kv dtype code, rms mode code) of the impl's cache rows, as decode_params sets them."""
+    if impl.mla_kv_fp8:
+        return _lib.KV_FP8, {"log8": _lib.RMS_LOG8, "bf16": _lib.RMS_BF16_BYTES,
+                             "e4m3": _lib.RMS_E4M3}[mla_fp8_rms_mode()]
+    return _lib.KV_BF16, _lib.RMS_BF16
+
+
+def reserve_bytes(impl, rows: int, qtok: int) -> int:
+    """Workspace bytes of a decode of `rows` flattened rows in requests of `qtok` query tokens, with
+    the parameters decode_params builds (rms format, verify folding). The kernel family, and with
+    it the balanced layout, can depend on the cache's row stride, which is not known before the
+    cache exists: the size is the larger of the tightest row of this layout and a wide padded row."""
+    heads = max(impl.mla_local_heads, 1)
+    rank, rope_w = impl.kv_lora_rank, max(impl.rms_offset - impl.kv_lora_rank, 0)
+    kv, mode = _impl_rms_mode(impl)
+    fold = qtok
+    if qtok > 1:
+        fold = _fold_rows(qtok, heads, 1, _ws_family(kv, mode, rank, rope_w, 1, 0.0))
+    eb = 1 if kv == _lib.KV_FP8 else 2
+    rb = 2 if mode in (_lib.RMS_BF16, _lib.RMS_BF16_BYTES) else 1
+    tight = -(-((rank + rope_w) * eb + heads * rb) // 16) * 16 // eb
+    need = 0
+    for row in (tight, 1 << 14):
+        p = _lib.DecodeParams()
+        p.rows, p.heads, p.rms_heads, p.qrows, p.groups = rows, heads, heads, fold, 1
+        p.d_c, p.rope_w, p.rms_offset = rank, rope_w, impl.rms_offset
+        p.kv_dtype, p.rms_mode = kv, mode
+        p.token_stride, p.page_stride, p.page_size = row, row * 64, 64
+        p.num_splits, p.num_workgroups = 0, 0
+        need = max(need, int(_lib.lib().qmla_workspace_bytes(p)))
+    return need
 
 
 def decode_params(impl, q, kv_c_and_k_pe_cache, attn_metadata, layer, out, lse):
@@ -97,11 +127,7 @@ def decode_params(impl, q, kv_c_and_k_pe_cache, attn_metadata, layer, out, lse):
     # vLLM's MLA cache is [num_blocks, block_size, head_size]; the paged-row view adds the kv-head
     # dim, as the reference does for its Triton call
     cache = kv_c_and_k_pe_cache.unsqueeze(2) if kv_c_and_k_pe_cache.dim() == 3 else kv_c_and_k_pe_cache
-    kv = _lib.KV_FP8 if impl.mla_kv_fp8 else _lib.KV_BF16
-    if kv == _lib.KV_FP8:
-        rms_mode = {"log8": _lib.RMS_LOG8, "bf16": _lib.RMS_BF16_BYTES, "e4m3": _lib.RMS_E4M3}[mla_fp8_rms_mode()]
-    else:
-        rms_mode = _lib.RMS_BF16
+    kv, rms_mode = _impl_rms_mode(impl)
     k_scale = getattr(layer, "_k_scale", None) if kv == _lib.KV_FP8 else None
     if k_scale is not None and k_scale.dtype != torch.float32:
         raise TypeError("layer._k_scale must be a float32 device scalar")

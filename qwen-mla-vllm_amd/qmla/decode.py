@@ -157,8 +157,9 @@ def build_params(*, q_nope, q_pe, kv_cache, block_table, seq_lens, out, lse, d_c
     p.num_workgroups = num_workgroups
     p.num_pages = kv_cache.shape[0] if kv_cache.dim() == 4 else kv_cache.shape[0] // page_size
     if status is not None:
-        if status.dtype != torch.int32 or status.numel() < 1:
-            raise TypeError("status must be a device int32 tensor")
+        # the kernels store into it from the device: it must live where the cache lives
+        if status.dtype != torch.int32 or status.numel() < 1 or status.device != kv_cache.device:
+            raise TypeError("status must be an int32 tensor on the cache's device")
         p.status = _ptr(status)
     return p
 
@@ -208,6 +209,11 @@ def decode_attention_fwd(q, k_buffer, v_buffer, o, lse, req_to_token, b_seq_len,
     accepted for signature parity; the latent serves as both key and value, so k_scale applies to
     both, as in the reference (mla_decode_attention.py:451-463).
     """
+    if k_scale is not None and (not torch.is_tensor(k_scale) or k_scale.dtype != torch.float32
+                                or k_scale.device != q.device):
+        # the kernels read the scale through a device pointer; converting here would allocate,
+        # which a caller inside HIP-graph capture cannot do
+        raise TypeError("k_scale must be a float32 tensor on the query's device (the layer's _k_scale)")
     _check_device(q, k_buffer, o, req_to_token, b_seq_len, attn_logits)
     if k_buffer.shape[-2] != 1:
         raise NotImplementedError("only MLA (one latent KV head) is implemented")
@@ -221,10 +227,6 @@ def decode_attention_fwd(q, k_buffer, v_buffer, o, lse, req_to_token, b_seq_len,
         qrows = _fold_rows(qrows, H, 1, _ws_family(kv, mode, Lv, Lk - Lv, 1, logit_cap))
     else:
         qrows = 1
-    if k_scale is not None and not torch.is_tensor(k_scale):
-        k_scale = torch.tensor(float(k_scale), dtype=torch.float32, device=q.device)
-    if k_scale is not None and k_scale.dtype != torch.float32:
-        k_scale = k_scale.float()
     cache = k_buffer if k_buffer.dim() == 4 else k_buffer
     split_align = 16 if page_size % 16 == 0 else 0
     p = build_params(q_nope=q, q_pe=q[..., Lv:] if Lk > Lv else None, kv_cache=cache,
@@ -270,7 +272,7 @@ def forward(q_nope, q_rope, kv_cache, block_table, seq_lens, *, d_c=None, rope_w
     returns [rows, H, d_c/2]. num_splits = 0 selects the balanced split mode. Block-table entries
     outside the cache's pages read page 0 and store QMLA_ERR_PAGE into `status` (device int32).
     """
-    _check_device(q_nope, kv_cache, block_table, seq_lens)
+    _check_device(q_nope, kv_cache, block_table, seq_lens, status)
     rows, H = q_nope.shape[0], q_nope.shape[1]
     if d_c is None:
         d_c = q_nope.shape[-1] * groups

@@ -251,6 +251,12 @@ def test_build_params_reads_real_strides():
         build_params(q_nope=qn, q_pe=qp, kv_cache=flat, block_table=bt, seq_lens=sl, out=out, lse=None,
                      d_c=512, rope_w=64, rms_offset=576, rms_mode=_lib.RMS_LOG8, kv=_lib.KV_FP8, page_size=64,
                      sm_scale=0.1, status=torch.zeros(1, dtype=torch.int64))
+    # the kernels store into *status from the device: a status word off the cache's device (a host
+    # tensor beside a device cache, here a meta tensor beside a host one) is refused
+    with pytest.raises(TypeError):
+        build_params(q_nope=qn, q_pe=qp, kv_cache=flat, block_table=bt, seq_lens=sl, out=out, lse=None,
+                     d_c=512, rope_w=64, rms_offset=576, rms_mode=_lib.RMS_LOG8, kv=_lib.KV_FP8, page_size=64,
+                     sm_scale=0.1, status=torch.zeros(1, dtype=torch.int32, device="meta"))
 
 
 def test_negative_page_count_rejected():

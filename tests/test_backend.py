@@ -101,3 +101,42 @@ def test_backend_triple():
     assert QwenMLAHipBackend.get_impl_cls() is QwenMLAHipImpl
     assert QwenMLAHipBackend.get_builder_cls() is DecodeMetadataBuilder
     assert hasattr(QwenMLAHipImpl, "forward_mqa") and hasattr(DecodeMetadataBuilder, "build_decode")
+
+
+@pytest.mark.parametrize("fp8,mode,heads,row", [(True, "log8", 24, 608), (True, "log8", 8, 592), (True, "e4m3", 24, 608),
+                                                 (False, "log8", 24, 600), (True, "log8", 24, 1024)])
+@pytest.mark.parametrize("qtok", [1, 2, 4])
+def test_reserved_workspace_covers_the_decode(monkeypatch, fp8, mode, heads, row, qtok):
+    """reserve_decode_workspace sizes the buffer with the parameters forward_mqa builds (rms format,
+    verify folding, the head split of a folded 24-head x 4-token step), whatever the reserve's own
+    qrows: a spec-verify decode inside graph capture must find it large enough."""
+    monkeypatch.setenv("QWEN_MLA_FP8_RMS", mode)
+    impl = _impl(fp8)
+    impl.mla_local_heads = heads
+    B = 16 * qtok
+    q = torch.zeros(B, heads, 512 + 96, dtype=torch.bfloat16)
+    cache = torch.zeros(10, 64, row, dtype=torch.uint8 if fp8 else torch.bfloat16)
+    out = torch.empty(B, heads, 512, dtype=torch.bfloat16)
+    lse = torch.empty(B, heads)
+    layer = SimpleNamespace(_k_scale=torch.tensor(0.5))
+    need = _lib.lib().qmla_workspace_bytes(decode_params(impl, q, cache, _metadata(B, q=qtok), layer, out, lse))
+    got = impl.reserve_decode_workspace(B, "cpu", qrows=4)      # up to 4 query tokens per request
+    assert got >= need, (got, need)
+    assert impl._workspace.buf.numel() >= need
+
+
+def test_decode_attention_fwd_refuses_a_host_scale():
+    """The kernels read k_scale through a device pointer: a Python float or a tensor of another dtype
+    or device is refused rather than converted (a conversion allocates, which graph capture forbids)."""
+    from qmla.decode import decode_attention_fwd
+    B, H = 2, 24
+    q = torch.zeros(B, H, 576, dtype=torch.bfloat16)
+    cache = torch.zeros(4, 64, 1, 608, dtype=torch.uint8)
+    o = torch.empty(B, H, 512, dtype=torch.bfloat16)
+    lse = torch.empty(B, H)
+    logits = torch.empty(B, H, 4, 513)
+    args = (q, cache, cache[..., :512], o, lse, torch.zeros(B, 4, dtype=torch.int32), torch.ones(B, dtype=torch.int32),
+            logits, 4, 0.1, 64)
+    for ks in (0.5, torch.tensor(0.5, dtype=torch.float64)):
+        with pytest.raises(TypeError, match="k_scale"):
+            decode_attention_fwd(*args, k_scale=ks, is_mla=True, rms_offset=576, rms_log8=True)

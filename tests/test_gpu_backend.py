@@ -39,7 +39,7 @@ def test_forward_mqa(gpu, monkeypatch, kv, heads, qtok, tuple_q):
     assert torch.equal(md.seq_lens, c.seq_lens) and torch.equal(md.block_table, c.block_table)
     attn_metadata = SimpleNamespace(causal=True, num_decode_tokens=rows, decode=md)
     cache3 = c.cache[:, :, 0, :]                                   # vLLM's [num_blocks, block_size, head_size]
-    impl.reserve_decode_workspace(rows, gpu, qrows=1)
+    impl.reserve_decode_workspace(rows, gpu, qrows=qtok)
     qa = (q[..., :512], q[..., 512:]) if tuple_q else q
     o, lse = impl.forward_mqa(qa, cache3, attn_metadata, layer)
     torch.cuda.synchronize()
