@@ -302,7 +302,7 @@ __device__ __forceinline__ void segment(const KParams& p, Smem<C>& sm, int req, 
           int row;
           const int off = src_off(k, ln, row);
           if (64 * k + 64 <= C::NCH || 64 * k + ln < C::NCH)
-            dma16_buf(rs, (uint32_t)((tb0 + row) * (int)TS + off), dst + k * 1024);
+            dma16_buf<kCpolDefault>(rs, (uint32_t)((tb0 + row) * (int)TS + off), dst + k * 1024);
         }
         if (rms_wave) {
 #pragma unroll
@@ -310,7 +310,7 @@ __device__ __forceinline__ void segment(const KParams& p, Smem<C>& sm, int req, 
             const int j = 64 * k + ln;
             const int row = j / (C::CRM > 0 ? C::CRM : 1);
             if (64 * k + 64 <= C::T * C::CRM || j < C::T * C::CRM)
-              dma16_buf(rs, (uint32_t)((tb0 + row) * (int)TS + roff_al + 16 * (j - row * C::CRM)), rdst + k * 1024);
+              dma16_buf<kCpolDefault>(rs, (uint32_t)((tb0 + row) * (int)TS + roff_al + 16 * (j - row * C::CRM)), rdst + k * 1024);
           }
         }
       } else {
@@ -326,7 +326,7 @@ __device__ __forceinline__ void segment(const KParams& p, Smem<C>& sm, int req, 
             const int tok = nv > 0 ? tb0 + rr : se - 1;
             const int q = tok / P;
             const int pg = sm.pid[q - pbase];
-            dma16(p.kv + (int64_t)pg * PS + (int64_t)(tok - q * P) * TS + off, dst + k * 1024);
+            dma16<kCpolDefault>(p.kv + (int64_t)pg * PS + (int64_t)(tok - q * P) * TS + off, dst + k * 1024);
           }
         }
         if (rms_wave) {
@@ -339,7 +339,7 @@ __device__ __forceinline__ void segment(const KParams& p, Smem<C>& sm, int req, 
               const int tok = nv > 0 ? tb0 + rr : se - 1;
               const int q = tok / P;
               const int pg = sm.pid[q - pbase];
-              dma16(p.kv + (int64_t)pg * PS + (int64_t)(tok - q * P) * TS + roff_al + 16 * (j - row * C::CRM),
+              dma16<kCpolDefault>(p.kv + (int64_t)pg * PS + (int64_t)(tok - q * P) * TS + roff_al + 16 * (j - row * C::CRM),
                     rdst + k * 1024);
             }
           }

@@ -118,14 +118,22 @@ __device__ __forceinline__ void lds_wait(T& v, U& w) {
   asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(v), "+v"(w));
 }
 
+// Cache policy of the loads that stream cached rows into LDS. Non-temporal (nt) by default: a row is
+// read once per call, and keeping it cached only displaces other lines (measured, alternating runs
+// on one box: the FP8 B 128 decode kernel 237-239 us with nt against 245-248 us without, the bf16
+// B 64 one 269 against 274 us, the GLA-g2 and 24-head verify ones 1-2% faster). The column-split
+// wide kernel keeps the default policy (with nt it measured 1720 us against 1600 us).
+constexpr int kCpolStream = 2, kCpolDefault = 0;
 // 16 bytes per lane, global -> LDS (wave-uniform LDS base; lane l writes base + 16*l)
+template <int CPOL = kCpolStream>
 __device__ __forceinline__ void dma16(const void* gsrc, char* lds_base) {
-  __builtin_amdgcn_global_load_lds(gsrc, QMLA_LDS(void, lds_base), 16, 0, 0);
+  __builtin_amdgcn_global_load_lds(gsrc, QMLA_LDS(void, lds_base), 16, 0, CPOL);
 }
 // 16 bytes per lane from a buffer resource (base in SGPRs, per-lane byte offset voff); lanes
 // whose offset falls outside the resource read zeros
+template <int CPOL = kCpolStream>
 __device__ __forceinline__ void dma16_buf(__amdgpu_buffer_rsrc_t rsrc, uint32_t voff, char* lds_base) {
-  __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, QMLA_LDS(void, lds_base), 16, voff, 0, 0, 0);
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, QMLA_LDS(void, lds_base), 16, voff, 0, 0, CPOL);
 }
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t bytes) {
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, 0x00020000);

@@ -43,6 +43,9 @@ def _kernels(lines, pattern):
 
 
 def _hazards(body):
+    """(load line, LDS line, text) for every scalar load followed, along the straight-line code after
+    it, by an LDS operation or a counted wait before an lgkmcnt(0). The scan follows fall-through
+    only: it ends at an unconditional branch (the next line is not on that path)."""
     found = []
     for i, line in enumerate(body):
         if not re.search(r"\bs_(buffer_)?load_", line):
@@ -53,6 +56,8 @@ def _hazards(body):
                 break
             if re.search(r"\bds_(read|write)", t) or re.search(r"lgkmcnt\([1-9]", t):
                 found.append((i, j, t.strip()))
+                break
+            if re.match(r"\s*s_(branch|setpc_b64|endpgm)\b", t):
                 break
     return found
 
