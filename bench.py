@@ -46,6 +46,10 @@ WORKLOADS = {
     # so each cached row is read once from HBM: the heads split over 3 workgroups on one XCD)
     "verify_b64x4": dict(batch=64, heads=24, d_c=512, rope_w=64, page_size=64, kv="fp8", rms_mode="log8", seed=5,
                          amp=4.0, lens=("lognormal", 16384, 0.5, 1024, 65536), qrows=4),
+    # the same verify step on a bf16 cache: the per-group kernel splits the 96 rows over 3 workgroups
+    # that read each token range together
+    "verify_bf16_b64x4": dict(batch=64, heads=24, d_c=512, rope_w=64, page_size=64, kv="bf16", rms_mode="bf16",
+                              seed=5, amp=1.0, lens=("lognormal", 16384, 0.5, 1024, 65536), qrows=4),
     # wide latent: 16 fixed splits in the reference's attn_logits layout, then the combine
     "wide_b32": dict(batch=32, heads=24, d_c=1792, rope_w=64, page_size=1600, kv="bf16", rms_mode="bf16", seed=3,
                      amp=1.0, lens=("fixed", 65536), splits=16),
@@ -379,6 +383,9 @@ def main():
     ap.add_argument("--workload", default="fp8_b128", choices=sorted(WORKLOADS))
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-graph", action="store_true", help="skip the HIP-graph replay timing")
+    ap.add_argument("--unfold", action="store_true",
+                    help="verify workloads: decode every query token as a request of its own (no folding), "
+                         "the way a caller without folding reads the cache once per token")
     ap.add_argument("--settle-ms", type=float, default=250.0,
                     help="run the call back to back this long before the warm-up steps (clock ramp)")
     ap.add_argument("--cpu-every", type=int, default=0, help="oracle on every k-th request (0: per workload)")
@@ -405,6 +412,8 @@ def main():
     case, spec = make_workload(args.workload, dev)
     rows, H = case.q_nope.shape[0], case.heads
     splits = WORKLOADS[args.workload].get("splits", 0)
+    if args.unfold:
+        case.qrows = 1                      # the flattened rows are requests of their own
     p, out, lse, keep = decode_call(case, splits, dev)
     lib = qmla.lib()
     st = torch.cuda.current_stream().cuda_stream

@@ -195,6 +195,14 @@ int qmla_combine(const qmla_decode_params* p, void* stream);
  * tokens only). */
 int qmla_plan_switch_tiles(const qmla_decode_params* p);
 
+/* QMLA_OK when a compiled kernel serves these params (cache format, rms tail, latent and rope
+ * widths, heads, verify tokens per request, groups), else QMLA_ERR_NOKERNEL or the first check that
+ * fails. Checks shapes and modes only: the pointers may be NULL. Pure host work. The host side uses
+ * it to fold spec-verify rows: the reference folds up to QWEN_MLA_VERIFY_MAX_ROWS rows per request
+ * group (qwen_mla/ops/mla_decode_attention.py:1291-1310); here a request's rows may split over up to
+ * four workgroups that read its token range together. */
+int qmla_decode_supported(const qmla_decode_params* p);
+
 /* ---- cache-row writer ---------------------------------------------------------------------
  * Replaces QwenMLATritonImpl.do_kv_cache_update (qwen_mla/mla_impl.py:309-342) and, for the rows it
  * hands to vLLM (bf16 caches; FP8 caches whose rms is stored as e4m3), vLLM's concat_and_cache_mla:

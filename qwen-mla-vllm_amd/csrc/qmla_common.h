@@ -305,6 +305,8 @@ int ro_launch(int inst, const qmla_decode_params* p, const KParams& k, int nwg, 
 // ---- host-side interface of the column-split translation unit (qmla_cs.hip) ----
 // Index of a compiled column-split instance for these params, or -1.
 int cs_select(const qmla_decode_params* p);
+// Workgroups per token range (row splits along gridDim.z) of the selected instance, or 0.
+int cs_row_splits(const qmla_decode_params* p);
 // Launch the partial pass of column-split instance `inst` (grid per split mode).
 int cs_launch(int inst, const qmla_decode_params* p, const KParams& k, int nwg, hipStream_t st);
 

@@ -822,6 +822,9 @@ struct Inst {
 static const Inst kInst[] = {
     // bf16 cache, d_c 1792 (the reference's two-pass widths): 8 column slices, 16-token tiles
     QMLA_CS(2, QMLA_RMS_BF16, 1792, 1, 8, 1, 1, 2, 2, 4, false, true, 64),
+    // ... the same rows with verify tokens (rows are tokens x heads, so the rms codes are read per row;
+    // 16 rows per workgroup: 32 spill 66 registers), e.g. 2 tokens x 24 heads over 3 workgroups
+    QMLA_CS(2, QMLA_RMS_BF16, 1792, 1, 8, 1, 1, 1, 2, 3, false, false, 64),
     QMLA_CS(2, QMLA_RMS_NONE, 1792, 1, 8, 1, 1, 2, 2, 0, false, false, 64),
     // bf16 cache, rank 768 with a rope window of 256 (the plugin's 24-head rope 232 layout,
     // tests/test_fi_partial_rope.py:105-110, and full rope 256): 8 slices of 96 columns; the
@@ -891,6 +894,11 @@ int cs_select(const qmla_decode_params* p) {
     }
   }
   return best;
+}
+
+int cs_row_splits(const qmla_decode_params* p) {
+  const int i = cs_select(p);
+  return i >= 0 ? cs::row_splits(cs::kInst[i], p) : 0;
 }
 
 int cs_launch(int inst, const qmla_decode_params* p, const KParams& k, int nwg, hipStream_t st) {

@@ -143,7 +143,10 @@ __device__ __forceinline__ void process_segment(const KParams& p, Smem<C>& sm, i
   const int mgrp = wl / C::WPM, wt = wl % C::WPM;   // row-block set and token-block phase (scores)
   const int ln16 = lane & 15, lg = lane >> 4;
   const int qrows = p.qrows, hpg = p.hpg;
-  const int nrows = qrows * hpg;  // valid rows per group
+  const int nrows = qrows * hpg;  // valid rows per group (verify token x head, token-major)
+  // rows [rbase, rbase + ROWS) of the group are this workgroup's: a request with more rows than one
+  // workgroup holds splits them over gridDim.z workgroups that read the same token range
+  const int rbase = (int)blockIdx.z * C::ROWS;
   const int row0 = req * qrows;   // first flattened query row of this request
   const int* bt = p.bt + (int64_t)(row0 + qrows - 1) * p.bt_stride;
   const int ntiles = (tok_e - tok_a + TILE - 1) / TILE;
@@ -155,7 +158,7 @@ __device__ __forceinline__ void process_segment(const KParams& p, Smem<C>& sm, i
   int lim_off[C::MBW];  // qrows-1-jq: verify token jq sees the first L-(qrows-1-jq) tokens
 #pragma unroll
   for (int mbl = 0; mbl < C::MBW; ++mbl) {
-    const int r = (mgrp * C::MBW + mbl) * 16 + ln16;
+    const int r = rbase + (mgrp * C::MBW + mbl) * 16 + ln16;
     const int rr = r < nrows ? r : nrows - 1;
     const int jq = rr / hpg, h = rr - jq * hpg;
     rms_b[mbl] = p.rms_off_b + (g * hpg + h) * RMS_EB;
@@ -222,7 +225,7 @@ __device__ __forceinline__ void process_segment(const KParams& p, Smem<C>& sm, i
   bf16x8 qf[C::MBW][C::KQ];
 #pragma unroll
   for (int mbl = 0; mbl < C::MBW; ++mbl) {
-    const int r = (mgrp * C::MBW + mbl) * 16 + ln16;
+    const int r = rbase + (mgrp * C::MBW + mbl) * 16 + ln16;
     const bool rv = r < nrows;
     const int rr = rv ? r : 0;
     const int jq = rr / hpg, h = rr - jq * hpg;
@@ -564,11 +567,11 @@ __device__ __forceinline__ void process_segment(const KParams& p, Smem<C>& sm, i
   for (int mb = 0; mb < C::MB; ++mb)
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      const int r = mb * 16 + 4 * lg + i;
-      if (r >= nrows) continue;
+      const int r = mb * 16 + 4 * lg + i;   // row of the workgroup; rbase + r of the group
+      if (rbase + r >= nrows) continue;
       const float m = sm.fin[0][g][r];
       const float l = sm.fin[1][g][r];
-      const int jq = r / hpg, h = r - jq * hpg;
+      const int jq = (rbase + r) / hpg, h = rbase + r - jq * hpg;
       const int head = g * hpg + h;
       const float inv = l > 0.f ? kscale / l : 0.f;   // fp8 values were accumulated unscaled
       const float invh = l > 0.f ? 1.0f / l : 0.f;    // ... and are stored so as fp16 partials
@@ -603,7 +606,7 @@ __global__ __launch_bounds__(C::NTHR, C::WGPC) void partial_kernel(const KParams
   // the per-layer scale dequantizes fp8 rows (and e4m3 rms codes); a bf16 cache ignores it, as
   // the reference does (mla_decode_attention.py:451-463)
   const float kscale = (C::EB == 1 && p.k_scale) ? *p.k_scale : 1.0f;
-  if (p.num_splits == 0 && blockIdx.x == 0 && threadIdx.x < 64) store_plan<kPlanSwitchOther>(p);   // for the combine
+  if (p.num_splits == 0 && blockIdx.x == 0 && blockIdx.z == 0 && threadIdx.x < 64) store_plan<kPlanSwitchOther>(p);   // for the combine
   int bad = 0;
   for_each_segment<C::DCG, kPlanSwitchOther>(p, [&](int req, int a, int e, int L, const SegOut& so) {
     process_segment<C>(p, sm, req, a, e, L, so, kscale, bad);
@@ -920,10 +923,12 @@ static int64_t needed_row_bytes(const qmla_decode_params* p) {
 
 static bool aligned16(const void* ptr) { return ((uintptr_t)ptr & 15) == 0; }
 
-static int validate(const qmla_decode_params* p) {
+// Checks of a parameter block; `ptrs` = false checks the shapes and modes only (no pointers, no
+// address alignment), for questions asked before the tensors exist.
+static int validate(const qmla_decode_params* p, bool ptrs = true) {
   if (!p) return QMLA_ERR_NULL;
-  if (!p->q_nope || !p->kv_cache || !p->block_table || !p->seq_lens || !p->out) return QMLA_ERR_NULL;
-  if (p->rope_w > 0 && !p->q_pe) return QMLA_ERR_NULL;
+  if (ptrs && (!p->q_nope || !p->kv_cache || !p->block_table || !p->seq_lens || !p->out)) return QMLA_ERR_NULL;
+  if (ptrs && p->rope_w > 0 && !p->q_pe) return QMLA_ERR_NULL;
   if (p->kv_dtype != QMLA_KV_BF16 && p->kv_dtype != QMLA_KV_FP8) return QMLA_ERR_MODE;
   if (p->out_dtype < 0 || p->out_dtype > 2 || (p->lse && (p->lse_dtype < 0 || p->lse_dtype > 2)))
     return QMLA_ERR_MODE;
@@ -944,49 +949,68 @@ static int validate(const qmla_decode_params* p) {
     return QMLA_ERR_SHAPE;
   if (p->num_splits < 0 || p->num_splits > CF_MAXS || p->split_align < 0 || p->num_pages < 0) return QMLA_ERR_SHAPE;
   const int eb = elem_bytes(p->kv_dtype);
-  if (!aligned16(p->kv_cache) || (p->page_stride * eb) % 16 || (p->token_stride * eb) % 16) return QMLA_ERR_ALIGN;
+  if ((ptrs && !aligned16(p->kv_cache)) || (p->page_stride * eb) % 16 || (p->token_stride * eb) % 16)
+    return QMLA_ERR_ALIGN;
   if (needed_row_bytes(p) > p->token_stride * eb && p->page_size > 1) return QMLA_ERR_SHAPE;
   // queries: element alignment (16-byte aligned rows take the vector loads)
-  if ((uintptr_t)p->q_nope % 2 || (p->rope_w > 0 && (uintptr_t)p->q_pe % 2)) return QMLA_ERR_ALIGN;
+  if (ptrs && ((uintptr_t)p->q_nope % 2 || (p->rope_w > 0 && (uintptr_t)p->q_pe % 2))) return QMLA_ERR_ALIGN;
   return QMLA_OK;
 }
 
+// Workgroups per token range of a per-group instance: a request's rows per group (verify tokens x
+// heads) in blocks of 16*MB, at most kMaxRowSplit of them (each reads the range's cached rows; the
+// balanced mode places them on one XCD, whose L2 then serves all but the first read).
+constexpr int kMaxRowSplit = 4;
+static int row_splits(const Inst& in, const qmla_decode_params* p) {
+  const int rows_pg = p->qrows * (p->heads / p->groups);
+  return (rows_pg + 16 * in.mb - 1) / (16 * in.mb);
+}
+
+// The instance with the fewest workgroups per token range, then the fewest row blocks (no idle
+// rows), then the fewest staged bytes.
 static const Inst* find_inst(const qmla_decode_params* p) {
   const int eb = elem_bytes(p->kv_dtype);
   const int dcg = p->d_c / p->groups;
-  const int hpg = p->heads / p->groups;
-  const int rows_pg = p->qrows * hpg;
   const int64_t need = needed_row_bytes(p);
   const bool cap = p->logit_cap > 0.f;
   const Inst* best = nullptr;
+  int best_hs = 0;
   for (const Inst& in : kInst) {
     if (in.eb != eb || in.rms != p->rms_mode || in.dcg != dcg || in.g != p->groups || in.cap != cap) continue;
     if (in.wp != wp_of(p->rope_w)) continue;
-    if (rows_pg > 16 * in.mb) continue;
+    const int hs = row_splits(in, p);
+    if (hs > kMaxRowSplit) continue;
     if ((int64_t)in.cpr * 16 < need) continue;
     if ((int64_t)in.cpr * 16 > p->token_stride * eb) continue;   // never read past the row
-    if (!best || in.mb < best->mb || (in.mb == best->mb && in.cpr < best->cpr)) best = &in;
+    if (!best || hs < best_hs || (hs == best_hs && (in.mb < best->mb || (in.mb == best->mb && in.cpr < best->cpr)))) {
+      best = &in;
+      best_hs = hs;
+    }
   }
   return best;
 }
-
-static const Inst* find_inst(const qmla_decode_params* p);
 
 // Token ranges of the balanced mode (workgroups, except that the warp-specialized kernel's head split
 // runs hsplit workgroups per range): one workgroup per compute unit; with a head split a multiple of
 // 8 ranges, so each range's workgroups share an XCD.
 static int balanced_nwg(const qmla_decode_params* p) {
   if (p->num_workgroups > 0) return p->num_workgroups;
+  // workgroups sharing each token range: the warp-specialized kernel's head split, the column-split
+  // and per-group kernels' row splits
+  int hs = 1, wgpc = 1;
   if (ws_select(p) >= 0) {
-    const int hs = ws_head_split(p);
-    if (hs > 1) {
-      const int r = cu_count() / (8 * hs) * 8;
-      return r > 8 ? r : 8;
-    }
-    return cu_count();
+    hs = ws_head_split(p);
+  } else if (cs_select(p) >= 0) {
+    hs = cs_row_splits(p);
+  } else if (const Inst* in = find_inst(p)) {
+    hs = row_splits(*in, p);
+    wgpc = in->wgpc;
   }
-  const Inst* in = find_inst(p);
-  return cu_count() * (in ? in->wgpc : 1);
+  if (hs > 1) {   // every workgroup resident at once, a range's workgroups on one XCD
+    const int r = cu_count() * wgpc / (8 * hs) * 8;
+    return r > 8 ? r : 8;
+  }
+  return cu_count() * wgpc;
 }
 
 struct BalancedLayout {
@@ -1087,9 +1111,12 @@ static int launch(const void* fn, dim3 grid, dim3 block, void** args, hipStream_
 
 static int run_partial(const qmla_decode_params* p, const Inst* in, KParams& k, hipStream_t st) {
   void* args[] = {&k};
+  // a range's row splits are consecutive in z: workgroup (x, 0, z) is dispatched as x + z * nwg, so
+  // with nwg a multiple of 8 the splits of range x share XCD x % 8
+  const int hs = row_splits(*in, p);
   if (p->num_splits > 0)
-    return launch((const void*)in->fn, dim3(p->num_splits, k.n_req, 1), dim3(in->nthr, 1, 1), args, st);
-  return launch((const void*)in->fn, dim3(k.nwg, 1, 1), dim3(in->nthr, 1, 1), args, st);
+    return launch((const void*)in->fn, dim3(p->num_splits, k.n_req, hs), dim3(in->nthr, 1, 1), args, st);
+  return launch((const void*)in->fn, dim3(k.nwg, 1, hs), dim3(in->nthr, 1, 1), args, st);
 }
 
 // One split: the decode kernels write final rows for the token ranges they own, and a request of
@@ -1172,6 +1199,13 @@ static int check_fixed_ws(const qmla_decode_params* p) {
                        (int64_t)(p->num_splits - 1) * p->ws_stride_split + dv;
   if (p->rows > 0 && (last + 1) * 4 > (int64_t)p->workspace_bytes) return QMLA_ERR_WORKSPACE;
   return QMLA_OK;
+}
+
+int qmla_decode_supported(const qmla_decode_params* p) {
+  const int rc = validate(p, false);
+  if (rc) return rc;
+  if (p->d_c / p->groups > 2048) return QMLA_ERR_SHAPE;
+  return (ws_select(p) >= 0 || cs_select(p) >= 0 || find_inst(p)) ? QMLA_OK : QMLA_ERR_NOKERNEL;
 }
 
 int qmla_plan_switch_tiles(const qmla_decode_params* p) {

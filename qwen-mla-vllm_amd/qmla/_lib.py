@@ -194,6 +194,7 @@ SIGNATURES = {
     "qmla_decode_partial": (ctypes.c_int, [_P, ctypes.c_void_p]),
     "qmla_combine": (ctypes.c_int, [_P, ctypes.c_void_p]),
     "qmla_plan_switch_tiles": (ctypes.c_int, [_P]),
+    "qmla_decode_supported": (ctypes.c_int, [_P]),
     "qmla_cache_write": (ctypes.c_int, [_W, ctypes.c_void_p]),
     "qmla_gather": (ctypes.c_int, [_G, ctypes.c_void_p]),
     "qmla_prep": (ctypes.c_int, [_R, ctypes.c_void_p]),

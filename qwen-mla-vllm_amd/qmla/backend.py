@@ -29,7 +29,7 @@ from types import SimpleNamespace
 import torch
 
 from . import _lib
-from .decode import Workspace, _fold_rows, _ws_family, build_params, workspace_bytes
+from .decode import Workspace, build_params, fold_rows, workspace_bytes
 from .layout import mla_fp8_rms_mode
 
 
@@ -90,20 +90,18 @@ def reserve_bytes(impl, rows: int, qtok: int) -> int:
     heads = max(impl.mla_local_heads, 1)
     rank, rope_w = impl.kv_lora_rank, max(impl.rms_offset - impl.kv_lora_rank, 0)
     kv, mode = _impl_rms_mode(impl)
-    fold = qtok
-    if qtok > 1:
-        fold = _fold_rows(qtok, heads, 1, _ws_family(kv, mode, rank, rope_w, 1, 0.0))
     eb = 1 if kv == _lib.KV_FP8 else 2
     rb = 2 if mode in (_lib.RMS_BF16, _lib.RMS_BF16_BYTES) else 1
     tight = -(-((rank + rope_w) * eb + heads * rb) // 16) * 16 // eb
     need = 0
     for row in (tight, 1 << 14):
         p = _lib.DecodeParams()
-        p.rows, p.heads, p.rms_heads, p.qrows, p.groups = rows, heads, heads, fold, 1
+        p.rows, p.heads, p.rms_heads, p.qrows, p.groups = rows, heads, heads, 1, 1
         p.d_c, p.rope_w, p.rms_offset = rank, rope_w, impl.rms_offset
         p.kv_dtype, p.rms_mode = kv, mode
         p.token_stride, p.page_stride, p.page_size = row, row * 64, 64
         p.num_splits, p.num_workgroups = 0, 0
+        p.qrows = fold_rows(p, qtok) if qtok > 1 else 1
         need = max(need, int(_lib.lib().qmla_workspace_bytes(p)))
     return need
 
@@ -134,14 +132,15 @@ def decode_params(impl, q, kv_c_and_k_pe_cache, attn_metadata, layer, out, lse):
     md = attn_metadata.decode
     page_size = cache.shape[1]
     qrows = _verify_rows(attn_metadata)
+    if qrows > 1 and q_nope.shape[0] % qrows:
+        raise ValueError(f"{q_nope.shape[0]} decode rows are not whole requests of {qrows} query tokens")
+    p = build_params(q_nope=q_nope, q_pe=q_pe, kv_cache=cache, block_table=md.block_table, seq_lens=md.seq_lens,
+                     out=out, lse=lse, d_c=rank, rope_w=rope_w, rms_offset=impl.rms_offset, rms_mode=rms_mode,
+                     kv=kv, page_size=page_size, sm_scale=impl.scale, k_scale=k_scale,
+                     qrows=1, groups=1, rms_heads=q_nope.shape[1], num_splits=0)
     if qrows > 1:
-        if q_nope.shape[0] % qrows:
-            raise ValueError(f"{q_nope.shape[0]} decode rows are not whole requests of {qrows} query tokens")
-        qrows = _fold_rows(qrows, q_nope.shape[1], 1, _ws_family(kv, rms_mode, rank, rope_w, 1, 0.0))
-    return build_params(q_nope=q_nope, q_pe=q_pe, kv_cache=cache, block_table=md.block_table, seq_lens=md.seq_lens,
-                        out=out, lse=lse, d_c=rank, rope_w=rope_w, rms_offset=impl.rms_offset, rms_mode=rms_mode,
-                        kv=kv, page_size=page_size, sm_scale=impl.scale, k_scale=k_scale,
-                        qrows=qrows, groups=1, rms_heads=q_nope.shape[1], num_splits=0)
+        p.qrows = fold_rows(p, qrows)
+    return p
 
 
 def forward_mqa(impl, q, kv_c_and_k_pe_cache, attn_metadata, layer):

@@ -76,17 +76,6 @@ def _ptr(t: torch.Tensor | None) -> int | None:
     return None if t is None else t.data_ptr()
 
 
-def _fold_group(qrows: int, hpg: int, max_rows: int) -> int:
-    """Verify tokens folded per kernel request: the largest divisor d of qrows with d*hpg rows per
-    latent group within the kernel's row tiles (as the reference caps its groups at
-    QWEN_MLA_VERIFY_MAX_ROWS, mla_decode_attention.py:1291-1300)."""
-    best = 1
-    for d in range(1, qrows + 1):
-        if qrows % d == 0 and d * hpg <= max_rows:
-            best = d
-    return best
-
-
 def _check_layout(*, q_nope, q_pe, kv_cache, block_table, seq_lens, out, lse) -> None:
     """The kernels read int32 metadata with unit strides along a row (block_table) and along the
     batch (seq_lens), and every tensor row with a unit element stride. Anything else raises here:
@@ -174,27 +163,26 @@ def _check_device(*ts: torch.Tensor) -> None:
             raise RuntimeError("qmla runs on the GPU only; got a tensor on " + str(t.device))
 
 
-# kernel row-tile capacity per latent group, per the compiled instances (MB * 16)
-MAX_ROWS_PER_GROUP = {1: 32, 2: 48}
-# the warp-specialized kernel (FP8 + log8 rows, d_c 512, rope 64, one latent group) also splits a
-# request's heads over up to 4 workgroups that share its token range: up to 128 rows
-MAX_ROWS_HEAD_SPLIT = 128
-
-
-def _ws_family(kv: int, rms_mode: int, d_c: int, rope_w: int, groups: int, logit_cap: float) -> bool:
-    return (kv == _lib.KV_FP8 and rms_mode == _lib.RMS_LOG8 and groups == 1 and d_c == 512 and rope_w == 64
-            and logit_cap <= 0)
-
-
-def _fold_rows(qrows: int, heads: int, groups: int, ws: bool) -> int:
-    """Verify tokens folded per kernel request (see _fold_group); with the warp-specialized kernel's
-    head split a fold must also leave whole heads per workgroup (heads % split == 0)."""
-    if not ws:
-        return _fold_group(qrows, heads // groups, MAX_ROWS_PER_GROUP.get(groups, 32))
+def fold_rows(params: DecodeParams, qrows: int) -> int:
+    """Spec-verify tokens folded into one kernel request: the largest divisor d of qrows for which a
+    compiled kernel serves d tokens x the heads as one request (qmla_decode_supported), so the cache
+    is read once per group of d tokens instead of once per token. The reference folds groups of up
+    to QWEN_MLA_VERIFY_MAX_ROWS = 64 rows (mla_decode_attention.py:1291-1310); the kernels here take
+    up to 32 rows per workgroup and split a request's rows over up to four workgroups that read its
+    token range together (48 rows per latent group for GLA-g2). `params` is left as it was."""
+    lib = _lib.lib()
+    saved = params.qrows
     best = 1
-    for d in range(1, qrows + 1):
-        if qrows % d == 0 and any(heads % hs == 0 and d * heads // hs <= 32 for hs in range(1, 5)):
-            best = d
+    try:
+        for d in range(qrows, 1, -1):
+            if qrows % d or params.rows % d:
+                continue
+            params.qrows = d
+            if lib.qmla_decode_supported(params) == 0:
+                best = d
+                break
+    finally:
+        params.qrows = saved
     return best
 
 
@@ -223,18 +211,16 @@ def decode_attention_fwd(q, k_buffer, v_buffer, o, lse, req_to_token, b_seq_len,
     B, H = q.shape[0], q.shape[1]
     kv = _kv_code(k_buffer, None)
     mode = _rms_mode(kv, rms_offset, rms_bf16, rms_log8)
-    if qrows > 1 and B % qrows == 0:
-        qrows = _fold_rows(qrows, H, 1, _ws_family(kv, mode, Lv, Lk - Lv, 1, logit_cap))
-    else:
-        qrows = 1
     cache = k_buffer if k_buffer.dim() == 4 else k_buffer
     split_align = 16 if page_size % 16 == 0 else 0
     p = build_params(q_nope=q, q_pe=q[..., Lv:] if Lk > Lv else None, kv_cache=cache,
                      block_table=req_to_token, seq_lens=b_seq_len, out=o, lse=lse, d_c=Lv, rope_w=Lk - Lv,
                      rms_offset=rms_offset, rms_mode=mode, kv=kv, page_size=page_size, sm_scale=sm_scale,
-                     k_scale=k_scale, logit_cap=logit_cap, qrows=qrows, groups=1, rms_heads=H,
+                     k_scale=k_scale, logit_cap=logit_cap, qrows=1, groups=1, rms_heads=H,
                      num_splits=num_kv_splits, split_align=split_align, workspace=attn_logits,
                      ws_strides=(attn_logits.stride(0), attn_logits.stride(1), attn_logits.stride(2)))
+    if qrows > 1 and B % qrows == 0:
+        p.qrows = fold_rows(p, qrows)
     lib = _lib.lib()
     st = _stream()
     _lib.check("qmla_decode_partial", lib.qmla_decode_partial(p, st))
@@ -289,10 +275,14 @@ def forward(q_nope, q_rope, kv_cache, block_table, seq_lens, *, d_c=None, rope_w
         lse = torch.empty(rows, H, dtype=torch.float32, device=q_nope.device)
     if k_scale is not None and not torch.is_tensor(k_scale):
         k_scale = torch.tensor(float(k_scale), dtype=torch.float32, device=q_nope.device)
+    if qrows > 1 and rows % qrows:
+        raise ValueError(f"rows {rows} not a multiple of qrows {qrows}")
     if qrows > 1:
-        if rows % qrows:
-            raise ValueError(f"rows {rows} not a multiple of qrows {qrows}")
-        qrows = _fold_rows(qrows, H, groups, _ws_family(kv, mode, d_c, rope_w, groups, logit_cap))
+        probe = build_params(q_nope=q_nope, q_pe=q_rope, kv_cache=kv_cache, block_table=block_table,
+                             seq_lens=seq_lens, out=out, lse=lse, d_c=d_c, rope_w=rope_w, rms_offset=rms_offset,
+                             rms_mode=mode, kv=kv, page_size=page_size, sm_scale=sm_scale, logit_cap=logit_cap,
+                             groups=groups, rms_heads=rms_heads, num_splits=num_splits)
+        qrows = fold_rows(probe, qrows)
     args = dict(q_nope=q_nope, q_pe=q_rope, kv_cache=kv_cache, block_table=block_table, seq_lens=seq_lens,
                 out=out, lse=lse, d_c=d_c, rope_w=rope_w, rms_offset=rms_offset, rms_mode=mode, kv=kv,
                 page_size=page_size, sm_scale=sm_scale, k_scale=k_scale, logit_cap=logit_cap, qrows=qrows,

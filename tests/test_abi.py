@@ -165,7 +165,8 @@ def _layout(kv, d_c, rope, heads, rms, qrows=1, groups=1):
     (_lib.KV_BF16, 1792, 300, 24, _lib.RMS_BF16, 1, 1, _lib.ERR_NOKERNEL),      # wider than any window
     # 24 heads x 4 verify tokens, FP8 + log8: the heads split over three workgroups per range
     (_lib.KV_FP8, 512, 64, 24, _lib.RMS_LOG8, 4, 1, _lib.ERR_WORKSPACE),
-    (_lib.KV_FP8, 512, 64, 24, _lib.RMS_E4M3, 4, 1, _lib.ERR_NOKERNEL),      # other rms formats: 32 rows
+    # other rms formats: the per-group kernel splits the 96 rows over three workgroups per range
+    (_lib.KV_FP8, 512, 64, 24, _lib.RMS_E4M3, 4, 1, _lib.ERR_WORKSPACE),
     # GLA-g2 with 4 verify tokens: FP8 + log8 (warp-specialized), FP8 + e4m3 / bf16-byte rms and
     # bf16 rows (per-group kernel); no instance without an rms tail
     (_lib.KV_FP8, 512, 64, 24, _lib.RMS_LOG8, 4, 2, _lib.ERR_WORKSPACE),
@@ -193,6 +194,37 @@ def test_plan_switch_tiles(kv, rms, qrows, groups, splits, tiles):
     assert _lib.lib().qmla_plan_switch_tiles(ctypes.byref(p)) == tiles
     p.d_c = 0
     assert _lib.lib().qmla_plan_switch_tiles(ctypes.byref(p)) < 0
+
+
+@pytest.mark.parametrize("kv,d_c,rope,heads,rms,fold", [
+    (_lib.KV_FP8, 512, 64, 24, _lib.RMS_LOG8, 4),          # warp-specialized: heads over 3 workgroups
+    (_lib.KV_FP8, 512, 64, 24, _lib.RMS_E4M3, 4),          # per-group kernel: 96 rows over 3 workgroups
+    (_lib.KV_FP8, 512, 64, 24, _lib.RMS_BF16_BYTES, 4),
+    (_lib.KV_BF16, 512, 64, 24, _lib.RMS_BF16, 4),
+    (_lib.KV_FP8, 768, 232, 24, _lib.RMS_LOG8, 4),         # the plugin's deployed rows (rope 232, TP 1)
+    (_lib.KV_FP8, 768, 232, 24, _lib.RMS_E4M3, 4),
+    (_lib.KV_FP8, 256, 232, 24, _lib.RMS_BF16_BYTES, 4),
+    (_lib.KV_FP8, 768, 116, 12, _lib.RMS_LOG8, 4),         # ... rope 116, 12 heads (TP 2)
+    (_lib.KV_BF16, 768, 232, 24, _lib.RMS_BF16, 4),        # column-split, 32 rows per workgroup
+    (_lib.KV_FP8, 1792, 232, 24, _lib.RMS_LOG8, 2),        # column-split, 16 rows per workgroup:
+    (_lib.KV_BF16, 1792, 232, 24, _lib.RMS_BF16, 2),       # two tokens x 24 heads over 3 workgroups
+    (_lib.KV_BF16, 1792, 64, 24, _lib.RMS_BF16, 2),
+    (_lib.KV_BF16, 1792, 300, 24, _lib.RMS_BF16, 1),       # no instance at all: no fold
+])
+def test_verify_fold_every_format(kv, d_c, rope, heads, rms, fold):
+    """Spec-verify folding asks the library which fold a compiled kernel serves: 4 query tokens x 24
+    heads fold into one request for every cache format and deployed layout up to rank 768 (2 on the
+    rank-1792 column-split instances with 16 rows per workgroup), so the cache is read once per
+    request, or once per pair of tokens, instead of once per token (no launch, no pointers). The
+    reference folds 2 tokens at 24 heads (64-row groups, mla_decode_attention.py:1291-1300)."""
+    from qmla.decode import fold_rows
+    p = _layout(kv, d_c, rope, heads, rms, 1, 1)
+    p.rows = 8 * 4
+    p.q_nope = p.q_pe = p.kv_cache = p.block_table = p.seq_lens = p.out = None   # shape questions only
+    assert fold_rows(p, 4) == fold
+    assert p.qrows == 1                                                       # left as it was
+    p.qrows = fold
+    assert _lib.lib().qmla_decode_supported(ctypes.byref(p)) == (_lib.OK if fold > 1 else _lib.ERR_NOKERNEL)
 
 
 def test_null_params_and_balanced_workspace_errors():

@@ -57,7 +57,9 @@ def test_decode_params_from_metadata(monkeypatch, fp8, mode, code):
     monkeypatch.setenv("QWEN_MLA_FP8_RMS", mode)
     B, H = 8, 24
     q = torch.zeros(B, H, 512 + 96, dtype=torch.bfloat16)          # declared rope 96: slots, rms, pad
-    cache = torch.zeros(10, 64, 608, dtype=torch.uint8 if fp8 else torch.bfloat16)   # vLLM's 3-D MLA cache
+    # vLLM's 3-D MLA cache; FP8 rows with two-byte rms codes are 16 bytes wider (the kernel stages 624)
+    width = 624 if fp8 and mode == "bf16" else 608
+    cache = torch.zeros(10, 64, width, dtype=torch.uint8 if fp8 else torch.bfloat16)
     layer = SimpleNamespace(_k_scale=torch.tensor(0.5))
     out = torch.empty(B, H, 512, dtype=torch.bfloat16)
     lse = torch.empty(B, H)
@@ -70,7 +72,7 @@ def test_decode_params_from_metadata(monkeypatch, fp8, mode, code):
     assert (p.d_c, p.rope_w, p.rms_offset, p.rms_mode) == (512, 64, 576, code)
     assert p.kv_dtype == (_lib.KV_FP8 if fp8 else _lib.KV_BF16)
     assert p.qrows == 4 and p.rows == B and p.heads == H and p.page_size == 64
-    assert (p.page_stride, p.token_stride) == (64 * 608, 608)
+    assert (p.page_stride, p.token_stride) == (64 * width, width)
     assert (p.k_scale is not None) == fp8
     assert p.seq_lens == md.decode.seq_lens.data_ptr() and p.block_table == md.decode.block_table.data_ptr()
     # the tuple form reads the same memory without a copy
