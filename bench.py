@@ -50,11 +50,25 @@ WORKLOADS = {
     # that read each token range together
     "verify_bf16_b64x4": dict(batch=64, heads=24, d_c=512, rope_w=64, page_size=64, kv="bf16", rms_mode="bf16",
                               seed=5, amp=1.0, lens=("lognormal", 16384, 0.5, 1024, 65536), qrows=4),
+    # the shapes of the reference's own kernel timings (qwen_mla/kernels/qwen_mla.cuh:1450-1454,
+    # ops/mla_decode_attention.py:925-927): B 64 x ctx 32k, 12 heads (TP 2 rank-local), bf16 rows of
+    # [latent | packed rope 116 | 12 bf16 rms] (the 128-column window after the latent), ranks 256,
+    # 768 and 1792; balanced split mode
+    "pub_r256_h12": dict(batch=64, heads=12, d_c=256, rope_w=116, page_size=64, kv="bf16", rms_mode="bf16",
+                         seed=11, amp=1.0, lens=("fixed", 32768)),
+    "pub_r768_h12": dict(batch=64, heads=12, d_c=768, rope_w=116, page_size=64, kv="bf16", rms_mode="bf16",
+                         seed=12, amp=1.0, lens=("fixed", 32768)),
+    "pub_r1792_h12": dict(batch=64, heads=12, d_c=1792, rope_w=116, page_size=64, kv="bf16", rms_mode="bf16",
+                          seed=13, amp=1.0, lens=("fixed", 32768)),
+    # the plugin's deployed FP8 row at TP 1: rank 768, packed rope 232, 24 log8 rms codes (1024 bytes),
+    # with the headline's batch and lengths
+    "fp8_r768_b128": dict(batch=128, heads=24, d_c=768, rope_w=232, page_size=64, kv="fp8", rms_mode="log8",
+                          seed=14, amp=4.0, lens=("lognormal", 16384, 0.5, 1024, 65536)),
     # wide latent: 16 fixed splits in the reference's attn_logits layout, then the combine
     "wide_b32": dict(batch=32, heads=24, d_c=1792, rope_w=64, page_size=1600, kv="bf16", rms_mode="bf16", seed=3,
                      amp=1.0, lens=("fixed", 65536), splits=16),
 }
-CPU_EVERY = {"wide_b32": 8}
+CPU_EVERY = {"wide_b32": 8, "pub_r256_h12": 4, "pub_r768_h12": 8, "pub_r1792_h12": 16}
 GRAPH_CALLS = 16   # decode calls recorded into one HIP graph (one per layer of a 16-layer forward)
 
 

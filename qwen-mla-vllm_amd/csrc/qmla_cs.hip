@@ -735,9 +735,9 @@ __device__ __forceinline__ void segment(const KParams& p, Smem<C>& sm, int req, 
 #pragma unroll
   for (int mb = 0; mb < C::MB; ++mb) {
     const float l = lrow[mb];
-    const float lse_v = l > 0.f ? (mref[mb] + fast_log2(l)) * kLn2 : kNegInf;
-    const float inv = l > 0.f ? kscale / l : 0.f;   // fp8 values were accumulated unscaled
-    const float invh = l > 0.f ? 1.0f / l : 0.f;    // ... and are stored so as fp16 partials
+    const float lse_v = row_lse(mref[mb], l);
+    const float inv = inv_sum(kscale, l);   // fp8 values were accumulated unscaled
+    const float invh = inv_sum(1.0f, l);    // ... and are stored so as fp16 partials
     const bool ph = !so.final_out && so.plse && p.part_h;
     float iv[4];
 #pragma unroll

@@ -573,9 +573,9 @@ __device__ __forceinline__ void process_segment(const KParams& p, Smem<C>& sm, i
       const float l = sm.fin[1][g][r];
       const int jq = (rbase + r) / hpg, h = rbase + r - jq * hpg;
       const int head = g * hpg + h;
-      const float inv = l > 0.f ? kscale / l : 0.f;   // fp8 values were accumulated unscaled
-      const float invh = l > 0.f ? 1.0f / l : 0.f;    // ... and are stored so as fp16 partials
-      const float lse_v = l > 0.f ? (m + fast_log2(l)) * kLn2 : kNegInf;
+      const float inv = inv_sum(kscale, l);   // fp8 values were accumulated unscaled
+      const float invh = inv_sum(1.0f, l);    // ... and are stored so as fp16 partials
+      const float lse_v = row_lse(m, l);
       if (so.final_out) {
         const int64_t ob = (int64_t)(row0 + jq) * p.o_sr + (int64_t)head * p.o_sh + wl * C::NCOL + ln16;
 #pragma unroll
@@ -694,7 +694,8 @@ __global__ __launch_bounds__(256) void combine_kernel(const KParams p, int dv) {
   const float m = fmaxf(fmaxf(s_red[0][0], s_red[0][1]), fmaxf(s_red[0][2], s_red[0][3]));
   float sloc = 0.f;
   for (int s = tid; s < nl; s += 256) {
-    const float e = m == kNegInf ? 0.f : __expf(s_w[s] - m);
+    // a split without tokens (lse -inf) weighs 0; a NaN lse stays NaN (fmaxf above skipped it)
+    const float e = is_neg_inf(s_w[s]) ? 0.f : __expf(s_w[s] - m);
     s_w[s] = e;
     sloc += e;
   }
@@ -702,8 +703,8 @@ __global__ __launch_bounds__(256) void combine_kernel(const KParams p, int dv) {
   if ((tid & 63) == 0) s_red[1][tid >> 6] = sloc;
   __syncthreads();
   const float l = (s_red[1][0] + s_red[1][1]) + (s_red[1][2] + s_red[1][3]);
-  const float inv = l > 0.f ? 1.0f / l : 0.f;
-  if (tid == 0 && p.lse) store_out(p.lse, p.lse_dt, (int64_t)row * p.lse_sr + head, l > 0.f ? m + __logf(l) : kNegInf);
+  const float inv = inv_sum(1.0f, l);
+  if (tid == 0 && p.lse) store_out(p.lse, p.lse_dt, (int64_t)row * p.lse_sr + head, empty_sum(l) ? kNegInf : m + __logf(l));
   for (int c = tid; c < dv; c += 256) {
     float acc = 0.f;
     int s = 0;
@@ -765,17 +766,23 @@ __device__ __forceinline__ void combine_cols(const KParams& p, int dv, int row, 
       }
 #pragma unroll
       for (int h = 0; h < CH_HB; ++h) {
+        // segments without tokens (lse -inf) weigh 0 and a batch of them only is skipped; a NaN lse
+        // (fmaxf skips it) weighs NaN, so a row whose inputs hold a NaN merges to NaN
         float mm = m[h];
+        bool live = false;
 #pragma unroll
-        for (int k = 0; k < CH_NS; ++k) mm = fmaxf(mm, ls[k][h]);
-        if (mm == kNegInf) continue;
+        for (int k = 0; k < CH_NS; ++k) {
+          mm = fmaxf(mm, ls[k][h]);
+          live |= !is_neg_inf(ls[k][h]);
+        }
+        if (!live) continue;
         const float sc = m[h] == kNegInf ? 0.f : __expf(m[h] - mm);
         l[h] *= sc;
         a0[h] *= sc;
         a1[h] *= sc;
 #pragma unroll
         for (int k = 0; k < CH_NS; ++k) {
-          const float wgt = ls[k][h] == kNegInf ? 0.f : __expf(ls[k][h] - mm);
+          const float wgt = is_neg_inf(ls[k][h]) ? 0.f : __expf(ls[k][h] - mm);
           l[h] += wgt;
           a0[h] += wgt * v[k][h].x;
           a1[h] += wgt * v[k][h].y;
@@ -786,11 +793,11 @@ __device__ __forceinline__ void combine_cols(const KParams& p, int dv, int row, 
 #pragma unroll
     for (int h = 0; h < CH_HB; ++h) {
       if (h >= nh) continue;
-      const float inv = l[h] > 0.f ? osc / l[h] : 0.f;
+      const float inv = inv_sum(osc, l[h]);
       const int64_t ob = (int64_t)row * p.o_sr + (int64_t)(h0 + h) * p.o_sh + cb;
       store_out(p.out, p.out_dt, ob, a0[h] * inv);
       if (cb + 1 < dv) store_out(p.out, p.out_dt, ob + 1, a1[h] * inv);
-      if (cb == 0 && p.lse) store_out(p.lse, p.lse_dt, (int64_t)row * p.lse_sr + h0 + h, l[h] > 0.f ? m[h] + __logf(l[h]) : kNegInf);
+      if (cb == 0 && p.lse) store_out(p.lse, p.lse_dt, (int64_t)row * p.lse_sr + h0 + h, empty_sum(l[h]) ? kNegInf : m[h] + __logf(l[h]));
     }
   }
 }

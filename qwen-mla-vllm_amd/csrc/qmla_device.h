@@ -192,8 +192,21 @@ __device__ __forceinline__ void lds_barrier() {
   asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
 }
 
+// A row's softmax sum is exactly +0 when the row saw no token (it is a sum of exponentials, each
+// >= +0) and NaN when one of its scores was. The empty-row results (zero output, lse -inf) are keyed
+// on the bits, so a NaN sum reaches the output and the lse as NaN, as in the reference's decode,
+// whatever a translation unit built without NaN semantics assumes about comparisons.
+__device__ __forceinline__ bool empty_sum(float l) { return __float_as_uint(l) == 0u; }
+__device__ __forceinline__ bool is_neg_inf(float x) { return __float_as_uint(x) == 0xff800000u; }
+// num / l, or 0 for an empty row
+__device__ __forceinline__ float inv_sum(float num, float l) { return empty_sum(l) ? 0.f : num / l; }
+
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 __device__ __forceinline__ float fast_log2(float x) { return __builtin_amdgcn_logf(x); }
+// natural-log lse of a row from its log2-domain reference max and its sum (-inf for an empty row)
+__device__ __forceinline__ float row_lse(float m_log2, float l) {
+  return empty_sum(l) ? kNegInf : (m_log2 + fast_log2(l)) * kLn2;
+}
 
 // How far a row's tile maximum may exceed its softmax reference before the reference moves, given
 // the row's running sum l (relative to the reference). A token that does not move it has

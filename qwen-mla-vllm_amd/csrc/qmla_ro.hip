@@ -194,9 +194,9 @@ __device__ __forceinline__ void role_main(const KParams& p, Smem<C>& sm, float k
   auto finalize = [&](int req, int fl) {
     const SegOut so = seg_out<C::DCG>(p, req, (fl & SEG_FINAL) != 0, wr);
     const float l = sum_lg(lpart);
-    const float inv = l > 0.f ? kscale / l : 0.f;   // fp8 values were accumulated unscaled
-    const float invh = l > 0.f ? 1.0f / l : 0.f;    // ... and are stored so as fp16 partials
-    const float lse_v = l > 0.f ? (mref + fast_log2(l)) * kLn2 : kNegInf;
+    const float inv = inv_sum(kscale, l);   // fp8 values were accumulated unscaled
+    const float invh = inv_sum(1.0f, l);    // ... and are stored so as fp16 partials
+    const float lse_v = row_lse(mref, l);
     const int row0 = req * qrows;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {

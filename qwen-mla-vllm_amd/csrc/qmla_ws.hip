@@ -384,8 +384,8 @@ __device__ __forceinline__ void role_main(const KParams& p, Smem<C>& sm, float k
         if (rr >= nrows) continue;
         const float l = l0 + l1;
         const int jr = rr / hpw, h = vg * hpg + h0 + rr - jr * hpw;
-        const float inv = l > 0.f ? kscale / l : 0.f;   // fp8 values were accumulated unscaled
-        const float lse_v = l > 0.f ? (m + fast_log2(l)) * kLn2 : kNegInf;
+        const float inv = inv_sum(kscale, l);   // fp8 values were accumulated unscaled
+        const float lse_v = row_lse(m, l);
         const int col = C::VC * vh + ln16;
         if (so.final_out) {
           const int64_t ob = (int64_t)(row0 + jr) * p.o_sr + (int64_t)h * p.o_sh + col;
@@ -394,7 +394,7 @@ __device__ __forceinline__ void role_main(const KParams& p, Smem<C>& sm, float k
           if (vh == 0 && ln16 == 0 && p.lse) store_out(p.lse, p.lse_dt, (int64_t)(row0 + jr) * p.lse_sr + h, lse_v);
         } else if (so.plse && p.part_h) {
           _Float16* ob = reinterpret_cast<_Float16*>(so.po) + (int64_t)jr * so.po_sr + (int64_t)h * so.po_sh + col;
-          const float invh = l > 0.f ? 1.0f / l : 0.f;
+          const float invh = inv_sum(1.0f, l);
 #pragma unroll
           for (int cb = 0; cb < C::CB; ++cb) ob[16 * cb] = (_Float16)(acc[mb][cb][i] * invh);
           if (vh == 0 && ln16 == 0) so.plse[(int64_t)jr * so.plse_sr + h] = lse_v;

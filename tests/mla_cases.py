@@ -92,8 +92,11 @@ def check_decode(name: str, case: Case, o, lse, *, logit_cap: float = 0.0, num_s
             lerr = (lg[~empty] - rl[~empty]).abs().max().item()
             ref_lerr = (el[~empty] - rl[~empty]).abs().max().item()
     lbound = max(LSE_TOL, C_REF * ref_lerr)
-    print(f"[{name}] max-abs {err:.3e} (tol {tol}, reference roundings {ref_err:.3e}, bound {bound:.3e}) "
-          f"lse {lerr:.3e} (reference {ref_lerr:.3e}, bound {lbound:.3e})", flush=True)
+    # which clause decides: the plain tolerance, or C_REF x the reference roundings' own error
+    clause = "plain" if err < tol else f"reference x{C_REF}"
+    lclause = "plain" if lerr < LSE_TOL else f"reference x{C_REF}"
+    print(f"[{name}] max-abs {err:.3e} (tol {tol}, reference roundings {ref_err:.3e}, bound {bound:.3e}: {clause}) "
+          f"lse {lerr:.3e} (reference {ref_lerr:.3e}, bound {lbound:.3e}: {lclause})", flush=True)
     assert err < bound, f"[{name}] max-abs {err:.3e} >= bound {bound:.3e}"
     assert lerr < lbound, f"[{name}] lse error {lerr:.3e} >= bound {lbound:.3e}"
     return err, ref_err, lerr

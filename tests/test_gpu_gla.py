@@ -91,3 +91,33 @@ def test_gla_sign_of_the_scale(gpu, sm_scale):
     c.sm_scale = sm_scale
     o, lse = _forward(c, num_workgroups=4)
     _check(f"gla sm_scale {sm_scale}", c, o, lse)
+
+
+@pytest.mark.parametrize("qrows", [4, 1])
+@pytest.mark.parametrize("where", ["latent", "rope", "both"])
+def test_gla_query_outlier_channels(gpu, where, qrows):
+    """The row-owner kernel's query split (e4m3 hi + lo parts of q * 2^e per row, the row's 2^-e as
+    the MFMA's B scale, the rope's hi and lo parts sharing one MFMA) on query rows whose elements span
+    more than 2^10: a few outlier channels per row (x 1024 over the rest), as the reference's FP8 test
+    draws outlier latent channels (tests/test_fp8_kv.py:23-31). 4 verify tokens take the quad-shared
+    rms instance, 1 token the other one."""
+    lens = [700, 3000, 64, 1500, 5]
+    c = _case(gpu, lens, qrows=qrows, seed=81 + qrows)
+    g = torch.Generator(device="cpu").manual_seed(82)
+    rows = c.q_nope.shape[0]
+    qn = torch.randn(rows, 24, 256, generator=g) * 0.02
+    qp = torch.randn(rows, 24, 64, generator=g) * 0.02
+    for r in range(rows):
+        for h in range(24):
+            # outliers of magnitude 24 against a median |q| of about 0.0135
+            if where in ("latent", "both"):
+                qn[r, h, torch.randperm(256, generator=g)[:3]] = 24.0 * torch.sign(torch.randn(3, generator=g))
+            if where in ("rope", "both"):
+                qp[r, h, torch.randperm(64, generator=g)[:2]] = 24.0 * torch.sign(torch.randn(2, generator=g))
+    c.q_nope = qn.to(torch.bfloat16).to(gpu)
+    c.q_pe = qp.to(torch.bfloat16).to(gpu)
+    amax = torch.cat([qn, qp], -1).abs().amax(-1)
+    amin = torch.cat([qn, qp], -1).abs().clamp_min(1e-30).median(-1).values
+    assert (amax / amin).min() > 2 ** 10
+    o, lse = _forward(c, num_workgroups=7)
+    _check(f"gla q{qrows} query outliers in {where}", c, o, lse)
