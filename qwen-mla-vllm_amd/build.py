@@ -34,6 +34,7 @@ SOURCES = [
     (CSRC / "qmla_cs.hip", ["-mllvm", "-amdgpu-mfma-vgpr-form", "-fno-honor-nans"]),
     (CSRC / "qmla_ws.hip", ["-mllvm", "-amdgpu-mfma-vgpr-form", "-fno-honor-nans"]),
     (CSRC / "qmla_ro.hip", ["-mllvm", "-amdgpu-mfma-vgpr-form", "-fno-honor-nans"]),
+    (CSRC / "qmla_wsb.hip", ["-mllvm", "-amdgpu-mfma-vgpr-form", "-fno-honor-nans"]),
     (CSRC / "qmla_write.hip", []),
     (CSRC / "qmla_prep.hip", []),
 ]

@@ -302,6 +302,11 @@ int ws_launch(int inst, const qmla_decode_params* p, const KParams& k, int nwg, 
 int ro_select(const qmla_decode_params* p);
 int ro_launch(int inst, const qmla_decode_params* p, const KParams& k, int nwg, hipStream_t st);
 
+// ---- host-side interface of the bf16 warp-specialized translation unit (qmla_wsb.hip) ----
+// Index of a compiled instance for these params (bf16 rows, d_c 512, rope 64), or -1.
+int wsb_select(const qmla_decode_params* p);
+int wsb_launch(int inst, const qmla_decode_params* p, const KParams& k, int nwg, hipStream_t st);
+
 // ---- host-side interface of the column-split translation unit (qmla_cs.hip) ----
 // Index of a compiled column-split instance for these params, or -1.
 int cs_select(const qmla_decode_params* p);

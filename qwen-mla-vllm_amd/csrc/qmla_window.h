@@ -150,6 +150,18 @@ __device__ __forceinline__ i32x2 ldstr8_at(uint32_t a) {
   asm volatile("ds_read_b64_tr_b8 %0, %1 offset:%2" : "=v"(r) : "v"(a), "n"(OFF));
   return r;
 }
+template <int OFF>
+__device__ __forceinline__ i32x2 ldstr16_at(uint32_t a) {
+  i32x2 r;
+  asm volatile("ds_read_b64_tr_b16 %0, %1 offset:%2" : "=v"(r) : "v"(a), "n"(OFF));
+  return r;
+}
+template <int OFF>
+__device__ __forceinline__ uint32_t ldsr16_at(uint32_t a) {
+  uint32_t r;
+  asm volatile("ds_read_u16 %0, %1 offset:%2" : "=v"(r) : "v"(a), "n"(OFF));
+  return r;
+}
 __device__ __forceinline__ uint32_t ldsr8_at(uint32_t a) {
   uint32_t r;
   asm volatile("ds_read_u8 %0, %1" : "=v"(r) : "v"(a));
@@ -169,10 +181,10 @@ __device__ __forceinline__ void wait_tiles(int ahead) {
 }
 
 // Wave 0: the next window of pieces, from request cb at token ctok on, into sm.seg / sm.win.
-// Lane l looks at request cb + l; pieces are taken in request order while their pages fit PIDN (the
+// Lane l looks at request cb + l; pieces are taken in request order while their pages fit PN (the
 // first piece that does not fit is cut at a page boundary). Balanced mode: cp is the plan prefix
 // C_cb of the cursor's request, and the lanes' C_b follow from a scan of their tile counts.
-template <int SW, class SM>
+template <int SW, int PN = PIDN, class SM>
 __device__ void plan_window(const KParams& p, SM& sm, bool fixed, int lo, int hi, int& cb, int& ctok,
                             int& cp) {
   const int lane = threadIdx.x & 63;
@@ -215,10 +227,10 @@ __device__ void plan_window(const KParams& p, SM& sm, bool fixed, int lo, int hi
     const int pages = live ? (e - 1) / P - a / P + 1 : 0;
     const int cum = wave_incl_sum(pages);
     const int excl = cum - pages;
-    const bool take = live && excl < PIDN;
+    const bool take = live && excl < PN;
     int et = e;
-    if (take && cum > PIDN) {
-      const int cut = (a / P + (PIDN - excl)) * P;   // page-aligned, > a
+    if (take && cum > PN) {
+      const int cut = (a / P + (PN - excl)) * P;   // page-aligned, > a
       et = cut < e ? cut : e;
     }
     if (et < e) fl &= ~SEG_LAST;

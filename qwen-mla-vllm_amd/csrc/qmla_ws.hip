@@ -978,8 +978,8 @@ int ws_head_split(const qmla_decode_params* p) {
 }
 
 // Instances past the warp-specialized table are the row-owner kernel's (qmla_ro.hip), which takes
-// the GLA-g2 shapes it serves.
-constexpr int kRoBase = 1000;
+// the GLA-g2 shapes it serves, and the bf16 warp-specialized kernel's (qmla_wsb.hip).
+constexpr int kRoBase = 1000, kWsbBase = 2000;
 
 int ws_select(const qmla_decode_params* p) {
   const int ri = ro_select(p);
@@ -1005,10 +1005,12 @@ int ws_select(const qmla_decode_params* p) {
     }
     return i;
   }
-  return -1;
+  const int bi = wsb_select(p);
+  return bi >= 0 ? kWsbBase + bi : -1;
 }
 
 int ws_launch(int inst, const qmla_decode_params* p, const KParams& k, int nwg, hipStream_t st) {
+  if (inst >= kWsbBase) return wsb_launch(inst - kWsbBase, p, k, nwg, st);
   if (inst >= kRoBase) return ro_launch(inst - kRoBase, p, k, nwg, st);
   KParams kk = k;
   kk.hsplit = ws_head_split(p);

@@ -1,0 +1,609 @@
+// qmla_wsb.hip -- gfx950 warp-specialized MLA decode of bf16 rows: d_c 512, rope 64, one bf16 rms
+// per head (or none), <= 32 query rows per workgroup (24 heads, one token each; 24 heads x 4 verify
+// tokens split over 3 workgroups of 8 heads).
+//
+// A workgroup owns a contiguous range of the concatenated requests' tokens (balanced mode) or one
+// split of one request (fixed splits), with all of its query rows, and walks it as one sequence of
+// 32-token tiles across request boundaries (the window walk of qmla_window.h). A bf16 row is 1200
+// staged bytes, twice an fp8 one, so a 32-token tile is 37.5 KB and the LDS holds a ring of four.
+// That decides the split of the work: the softmax of a tile has to be final within the step that
+// scores it, so the value waves can take the tile one step later and the ring needs only the tiles
+// in flight, the one being scored and the one being accumulated (A + 2 stages).
+//
+// Its 6 waves take two roles:
+//   score waves (4, 5): wave 4 + u owns 16 query rows (row block u) for all 32 tokens of a tile. It
+//                       computes S^T = K . Q^T on the 16x16x32 bf16 MFMA (query fragments resident
+//                       in VGPRs, K fragments read from the staged rows), divides by the rms, applies
+//                       the mask, and runs the rows' online softmax entirely in its own registers (a
+//                       row's tile max is a reduction over its 4 lane groups). The reference max moves
+//                       only when a row's tile max exceeds it by more than ref_shift(the row's sum),
+//                       so a dominant token gets P = 1 exactly and the bf16 rounding of P costs no
+//                       more than in the reference; the wave then publishes the factor by which the
+//                       value waves rescale their accumulators. P (bf16) goes to LDS. At a request's
+//                       last tile it publishes the rows' max and sum;
+//   value waves (0-3):  wave v accumulates P . V over latent columns [128v, 128v+128) for all 32 rows
+//                       one tile behind the score waves, with V^T fragments read transposed from the
+//                       staged rows (ds_read_b64_tr_b16), writes a request's output when its last
+//                       tile is in, and streams the tiles global -> LDS by LDS-DMA, A tiles ahead of
+//                       the score waves (each value wave waits only for its own loads).
+// The two score waves sit on SIMDs 0 and 1 beside value waves 0 and 1 (waves are placed on SIMDs in
+// order); SIMDs 2 and 3 hold one value wave each. The workgroup meets once per tile at one barrier.
+// Inside a step a wave issues its LDS reads and waits for them in order with counted lgkmcnt waits.
+//
+// Reference semantics: qwen_mla/ops/mla_decode_attention.py:297-586 (stage 1: tile loop, rms divide
+// :466-507, softmax :553-560, partial store :562-586).
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "qmla.h"
+#include "qmla_common.h"
+#include "qmla_device.h"
+#include "qmla_window.h"
+
+namespace qmla {
+namespace wsb {
+using namespace ws;   // TILE, NSEG, SegD, the counted LDS reads, plan_window, wait_tiles
+
+constexpr float SHIFT_CAP = 8.0f;   // P = exp2(s - ref) <= 2^8 before a row's reference moves
+constexpr int PIDB = 256;        // page ids per window (the ring leaves no room for more)
+enum Role { SCORE, VALUE };
+
+// Compile-time shape: RMS tail format (bf16 per head, or none), CPR 16-byte chunks staged per row
+// (rows are staged unrotated: 1200-byte rows put the 16 rows of a K read on distinct banks), A tiles
+// in flight ahead of the score waves, CAP tanh logit cap.
+template <int RMS_, int CPR_, int A_, bool CAP_>
+struct WB {
+  static constexpr int RMS = RMS_, CPR = CPR_, A = A_, S = A_ + 2;
+  static constexpr bool CAP = CAP_;
+  static constexpr int DC = 512, ROPE = 64;
+  static constexpr int RB = 16 * CPR, STAGE = TILE * RB;
+  static constexpr int NW = 6, NTHR = 64 * NW;   // value waves 0-3, score waves 4-5
+  static constexpr int ROWS = 32;
+  static constexpr int NCH = TILE * CPR;          // 16-byte chunks per tile
+  static constexpr int NI = (NCH + 63) / 64;      // DMA instructions per tile
+  static constexpr int NIW = 4;                   // issuing waves
+  static constexpr int DPW = (NI + NIW - 1) / NIW;
+  static constexpr int KQ = (DC + ROPE) / 32;     // k-steps of the score product
+  static constexpr int KP = KQ / 2;               // 64-column pairs: two 16-byte K reads per lane
+  static constexpr int VC = DC / 4, CB = VC / 16; // columns per value wave, 16-column blocks
+  static constexpr int PST = TILE * 2 + 16;       // P row stride in LDS (bytes)
+  static constexpr int NCODE = RMS == QMLA_RMS_NONE ? 0 : 8;   // rms reads per lane and tile
+  static_assert(RMS == QMLA_RMS_NONE || RMS == QMLA_RMS_BF16, "bf16 rows: one bf16 rms per head, or none");
+  static_assert(CPR * 16 >= (DC + ROPE) * 2, "row slice");
+  static_assert(A >= 2 && A * DPW < 64, "lookahead / vmcnt range");
+};
+
+template <class C>
+struct Smem {
+  char kv[C::S][C::STAGE];
+  alignas(16) char p[2][C::ROWS][C::PST];   // P (bf16) of tile g, at g & 1
+  alignas(16) float alpha[2][C::ROWS];      // [g & 1][row] accumulator rescale at tile g
+  alignas(16) float fin[2][2][C::ROWS];     // [piece & 1][max, sum][row] of a finished request
+  alignas(16) int flag[2][4];               // [g & 1][row block]: its reference moved at tile g
+  alignas(16) SegD seg[NSEG];
+  alignas(16) int pid[PIDB];
+  int win[4];
+};
+
+template <class C>
+__device__ __forceinline__ constexpr int dpw(int d) { return (C::NI - d + C::NIW - 1) / C::NIW; }
+
+// The whole range of this workgroup, seen from one role. All roles run the same window / tile /
+// barrier sequence; each keeps only its own registers live.
+template <class C, int ROLE>
+__device__ __forceinline__ void role_main(const KParams& p, Smem<C>& sm, bool fixed, int lo, int hi, int b0,
+                                          int c0, int wr, int hz, int& bad) {
+  constexpr int NTHR = C::NTHR;
+  constexpr bool QS = ROLE == SCORE;
+  constexpr int ND = QS ? 1 : C::DPW;
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int su = w & 1;    // score wave: its row block
+  const int vw = w & 3;    // value wave: its columns, its first DMA instruction of a tile
+  const int ln16 = lane & 15, lg = lane >> 4;
+  const int qrows = p.qrows;
+  // the workgroup's heads: hpw of them from h0 (head split hz of p.hsplit)
+  const int hpw = p.hpg / p.hsplit, h0 = hz * hpw;
+  const int nrows = qrows * hpw;
+  const int P = p.page_size;
+  const int64_t tsb = p.token_stride_b;
+  const float c2 = p.sm_scale * kLog2e;
+  // score wave: its row (verify token jq, head hd)
+  const int rg = 16 * su + ln16;
+  const bool rok = rg < nrows;
+  const int jq = rok ? rg / hpw : 0;
+  const int hd = h0 + (rok ? rg - jq * hpw : 0);
+
+  // ---- score wave: query fragments, pair jj and lane group lg holding columns 64jj + 16lg .. +16
+  //      (k-step 2jj the first 8, 2jj + 1 the next 8) ----
+  bf16x8 qf[QS ? C::KQ : 1];
+  auto load_q = [&](int req) {
+    const int row = req * qrows + jq;
+    const __bf16* qnp = p.q_nope + (int64_t)row * p.qn_sr + (int64_t)hd * p.qn_sh;
+    const __bf16* qpp = p.q_pe + (int64_t)row * p.qp_sr + (int64_t)hd * p.qp_sh;
+#pragma unroll
+    for (int k = 0; k < C::KQ; ++k) {
+      const int col = 64 * (k >> 1) + 16 * lg + 8 * (k & 1);
+      bf16x8 v = load_q8(col < C::DC ? qnp + col : qpp + (col - C::DC), p.q_vec);
+      if (!rok) v = bf16x8{};
+      qf[k] = v;
+    }
+  };
+  float mref = kNegInf, lpart = 0.f;   // the row's reference max (log2 domain) and partial sum
+  int lim = 0;                          // the row's token limit in the current piece
+
+  // ---- value wave: accumulator of rows 16mb + 4lg + i x columns VC*vw + 16cb + ln16 ----
+  f32x4 acc[2][QS ? 1 : C::CB];
+  auto zero_acc = [&]() {
+#pragma unroll
+    for (int mb = 0; mb < 2; ++mb)
+#pragma unroll
+      for (int cb = 0; cb < (QS ? 1 : C::CB); ++cb) acc[mb][cb] = f32x4{0.f, 0.f, 0.f, 0.f};
+  };
+  zero_acc();
+
+  // ---- value wave DMA: instruction i = vw + 4j covers chunks 64i .. 64i+63 of a tile, staged in
+  //      order (chunk q at LDS byte 16q: row q / CPR, 16-byte chunk q % CPR of the row) ----
+  uint32_t goff[ND];
+  int drow[ND];
+  if constexpr (!QS) {
+#pragma unroll
+    for (int j = 0; j < ND; ++j) {
+      int q = (vw + C::NIW * j) * 64 + lane;
+      q = q < C::NCH ? q : C::NCH - 1;
+      const int rr = q / C::CPR, pp = q - rr * C::CPR;
+      goff[j] = (uint32_t)(rr * tsb + 16 * pp);
+      drow[j] = rr;
+    }
+  }
+  const bool big = dpw<C>(vw) == C::DPW;
+
+  // one piece descriptor (drained reads: its fields are wave-uniform and live in scalar registers)
+  auto read_seg = [&](int k) {
+    i32x4 a, b;
+    ldsr128x2_drained(&sm.seg[k].req, &sm.seg[k].nt, a, b);
+    SegD d;
+    d.req = __builtin_amdgcn_readfirstlane(a[0]);
+    d.ta = __builtin_amdgcn_readfirstlane(a[1]);
+    d.te = __builtin_amdgcn_readfirstlane(a[2]);
+    d.L = __builtin_amdgcn_readfirstlane(a[3]);
+    d.nt = __builtin_amdgcn_readfirstlane(b[0]);
+    d.pf = __builtin_amdgcn_readfirstlane(b[1]);
+    d.fl = __builtin_amdgcn_readfirstlane(b[2]);
+    d.pad = 0;
+    return d;
+  };
+
+  // value wave: normalize and write the output of request req, whose sums are in fin[k & 1]
+  auto finalize = [&](int k, int req, int fl) {
+    const SegOut so = seg_out<C::DC>(p, req, (fl & SEG_FINAL) != 0, wr);
+    const int row0 = req * qrows;
+#pragma unroll
+    for (int mb = 0; mb < 2; ++mb) {
+      i32x4 mr, lr;
+      ldsr128x2_drained(&sm.fin[k & 1][0][16 * mb + 4 * lg], &sm.fin[k & 1][1][16 * mb + 4 * lg], mr, lr);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int rr = 16 * mb + 4 * lg + i;
+        if (rr >= nrows) continue;
+        const float m = __int_as_float(mr[i]), l = __int_as_float(lr[i]);
+        const int jr = rr / hpw, h = h0 + rr - jr * hpw;
+        const float inv = inv_sum(1.0f, l);
+        const float lse_v = row_lse(m, l);
+        const int col = C::VC * vw + ln16;
+        if (so.final_out) {
+          const int64_t ob = (int64_t)(row0 + jr) * p.o_sr + (int64_t)h * p.o_sh + col;
+#pragma unroll
+          for (int cb = 0; cb < C::CB; ++cb) store_out(p.out, p.out_dt, ob + 16 * cb, acc[mb][cb][i] * inv);
+          if (vw == 0 && ln16 == 0 && p.lse) store_out(p.lse, p.lse_dt, (int64_t)(row0 + jr) * p.lse_sr + h, lse_v);
+        } else {
+          float* ob = so.po + (int64_t)jr * so.po_sr + (int64_t)h * so.po_sh + col;
+#pragma unroll
+          for (int cb = 0; cb < C::CB; ++cb) ob[16 * cb] = acc[mb][cb][i] * inv;
+          if (vw == 0 && ln16 == 0) {
+            if (so.plse) so.plse[(int64_t)jr * so.plse_sr + h] = lse_v;
+            else so.po[(int64_t)jr * so.po_sr + (int64_t)h * so.po_sh + C::DC] = lse_v;
+          }
+        }
+      }
+    }
+    zero_acc();
+  };
+
+  // window planning cursor (wave 0 only): request, token, plan prefix of the request
+  int cb = fixed ? (int)blockIdx.y : b0, ctok = 0, cp = c0;
+
+  for (;;) {
+    if (w == 0) plan_window<kPlanSwitchWs, PIDB>(p, sm, fixed, lo, hi, cb, ctok, cp);
+    __syncthreads();
+    const int nseg = sm.win[0], ntot = sm.win[1], npg = sm.win[2], more = sm.win[3];
+    if (nseg == 0) break;
+    // page ids of the window: page f belongs to the last piece with pf <= f
+    for (int f = tid; f < npg; f += NTHR) {
+      int k0 = 0, k1 = nseg - 1;
+      while (k0 < k1) {
+        const int mid = (k0 + k1 + 1) >> 1;
+        if (sm.seg[mid].pf <= f) k0 = mid;
+        else k1 = mid - 1;
+      }
+      const SegD& d = sm.seg[k0];
+      // a folded request reads the block-table row of its last verify row, as its length does
+      sm.pid[f] = checked_page(p, p.bt[((int64_t)d.req * qrows + qrows - 1) * p.bt_stride + d.ta / P + (f - d.pf)],
+                               bad);
+    }
+    __syncthreads();
+
+    // ---- DMA cursor (value waves): piece ki, tile ti, window page index ipg, token offset ioff ----
+    int ki = 0, ti = 0, i_ta = 0, i_te = 0, i_nt = 0, i_pf = 0, ipg = 0, ioff = 0, pidv = 0;
+    auto enter_i = [&]() {
+      const SegD d = read_seg(ki);
+      i_ta = d.ta;
+      i_te = d.te;
+      i_nt = d.nt;
+      i_pf = d.pf;
+      ipg = d.pf;
+      ioff = d.ta % P;
+    };
+    // issues tile g (the cursor's) into ring stage g % S and advances the cursor; pidv holds the
+    // page id of the cursor's page, read at the previous issue (a barrier has drained it since)
+    auto issue = [&](int g) {
+      const int tok0 = i_ta + ti * TILE;
+      const int nvalid = i_te - tok0 < TILE ? i_te - tok0 : TILE;
+      char* dst = sm.kv[g % C::S];
+      if (ioff + TILE <= P) {
+        // the tile's rows are in one page; rows past the piece end read as zeros
+        lds_wait_n<0>(pidv);
+        const int pg = __builtin_amdgcn_readfirstlane(pidv);
+        const char* base = p.kv + (int64_t)pg * p.page_stride_b + (int64_t)ioff * tsb;
+        const __amdgpu_buffer_rsrc_t rs = make_rsrc(base, (uint32_t)(nvalid * tsb));
+#pragma unroll
+        for (int j = 0; j < ND; ++j) {
+          const int i = vw + C::NIW * j;
+          if (i < C::NI && (i * 64 + 64 <= C::NCH || i * 64 + lane < C::NCH)) dma16_buf(rs, goff[j], dst + i * 1024);
+        }
+      } else {
+        // per-lane page lookup; rows past the piece end repeat its last row
+#pragma unroll
+        for (int j = 0; j < ND; ++j) {
+          const int i = vw + C::NIW * j;
+          if (i < C::NI && (i * 64 + 64 <= C::NCH || i * 64 + lane < C::NCH)) {
+            const int rr = drow[j] < nvalid ? drow[j] : nvalid - 1;
+            const int tok = tok0 + rr;
+            const int q = tok / P;
+            int pg = ldsr32(&sm.pid[i_pf + q - i_ta / P]);
+            lds_wait_n<0>(pg);
+            const uint32_t cbo = goff[j] - (uint32_t)(drow[j] * tsb);
+            dma16(p.kv + (int64_t)pg * p.page_stride_b + (int64_t)(tok - q * P) * tsb + cbo, dst + i * 1024);
+          }
+        }
+      }
+      ioff += TILE;
+      while (ioff >= P) {
+        ioff -= P;
+        ++ipg;
+      }
+      if (++ti == i_nt) {
+        ti = 0;
+        if (++ki < nseg) enter_i();
+      }
+      pidv = ldsr32(&sm.pid[ipg < npg ? ipg : npg - 1]);
+    };
+    // wait until tile t landed, with tiles t+1 .. last issued after it
+    auto wait_tile = [&](int t, int last) {
+      const int ahead = last - t;
+      if (big) wait_tiles<C::DPW, C::A - 1>(ahead);
+      else wait_tiles<(C::NI % C::NIW == 0 ? C::DPW : C::DPW - 1), C::A - 1>(ahead);
+    };
+    // score: piece ks, tile ts; value: piece kv, tile tv
+    int ks = 0, ts = 0, s_ta = 0, s_nt = 0, s_fl = 0;
+    int kv = 0, tv = 0, v_req = 0, v_nt = 0, v_fl = 0;
+    if constexpr (ROLE == VALUE) {
+      const SegD d = read_seg(0);
+      v_req = d.req;
+      v_nt = d.nt;
+      v_fl = d.fl;
+      enter_i();
+      pidv = ldsr32(&sm.pid[ipg]);
+      lds_wait_n<0>(pidv);
+      // prologue: tiles 0 .. A-1 in flight, tile 0 landed
+      for (int t = 0; t < C::A && t < ntot; ++t) issue(t);
+      wait_tile(0, (C::A < ntot ? C::A : ntot) - 1);
+    }
+    lds_barrier();
+
+    // iteration g: value waves issue tile g+A, wait for tile g+1 and accumulate tile g-1; score
+    // waves score tile g
+#pragma clang loop unroll(disable)
+    for (int g = 0; g <= ntot; ++g) {
+      if constexpr (ROLE == SCORE) {
+        if (g < ntot) {
+          if (ts == 0) {
+            const SegD d = read_seg(ks);
+            s_ta = d.ta;
+            s_nt = d.nt;
+            s_fl = d.fl;
+            if (d.fl & SEG_FIRST) {
+              load_q(d.req);
+              mref = kNegInf;
+              lpart = 0.f;
+            }
+            const int lr = d.L - (qrows - 1 - jq);
+            lim = rok ? (lr < d.te ? lr : d.te) : 0;
+          }
+          const uint32_t sb = lds_addr(sm.kv[g % C::S]);
+          const int tok0 = s_ta + ts * TILE;
+          // ---- LDS reads: rms of tokens 16tb + 4lg + i (head hd), then the K rows of token block 0 ----
+          uint32_t code[2][4];
+          if constexpr (C::RMS != QMLA_RMS_NONE) {
+            const uint32_t ca = sb + (uint32_t)(4 * lg * C::RB + p.rms_off_b + 2 * hd);
+            static_for<0, 2>([&](auto tc) {
+              constexpr int tb = decltype(tc)::value;
+              static_for<0, 4>([&](auto ic) {
+                constexpr int i = decltype(ic)::value;
+                code[tb][i] = ldsr16_at<(16 * tb + i) * C::RB>(ca);
+              });
+            });
+          }
+          // K row 16tb + ln16, columns 64jj + 16lg .. +8 and +8 .. +16
+          const uint32_t ka = sb + (uint32_t)(ln16 * C::RB + 32 * lg);
+          i32x4 kr[C::KQ];
+          static_for<0, C::KP>([&](auto jc) {
+            constexpr int jj = decltype(jc)::value;
+            kr[2 * jj] = ldsr128_at<128 * jj>(ka);
+            kr[2 * jj + 1] = ldsr128_at<128 * jj + 16>(ka);
+          });
+          // ---- S^T = K . Q^T: token block 0 as its rows land, each of its reads followed by the
+          //      same read of token block 1, whose products run after ----
+          f32x4 sc[2];
+          {
+            f32x4 sa = f32x4{0.f, 0.f, 0.f, 0.f}, sbb = sa;
+            i32x4 kq[C::KQ];
+            static_for<0, C::KQ>([&](auto kc) {
+              constexpr int kk = decltype(kc)::value;
+              // issued after kr[kk]: reads kk+1 .. KQ-1 of block 0 and 0 .. kk-1 of block 1
+              lds_wait_n<cmin15(C::KQ - 1)>(kr[kk]);
+              if constexpr (kk & 1) sbb = mfma16(__builtin_bit_cast(bf16x8, kr[kk]), qf[kk], sbb);
+              else sa = mfma16(__builtin_bit_cast(bf16x8, kr[kk]), qf[kk], sa);
+              constexpr int jj = kk >> 1;
+              kq[kk] = ldsr128_at<16 * C::RB + 128 * jj + 16 * (kk & 1)>(ka);
+            });
+            sc[0] = sa + sbb;
+            sa = f32x4{0.f, 0.f, 0.f, 0.f};
+            sbb = sa;
+            static_for<0, C::KQ>([&](auto kc) {
+              constexpr int kk = decltype(kc)::value;
+              lds_wait_n<cmin15(C::KQ - 1 - kk)>(kq[kk]);
+              if constexpr (kk & 1) sbb = mfma16(__builtin_bit_cast(bf16x8, kq[kk]), qf[kk], sbb);
+              else sa = mfma16(__builtin_bit_cast(bf16x8, kq[kk]), qf[kk], sa);
+            });
+            sc[1] = sa + sbb;
+          }
+          if constexpr (C::RMS != QMLA_RMS_NONE) {
+#pragma unroll
+            for (int tb = 0; tb < 2; ++tb)
+#pragma unroll
+              for (int i = 0; i < 4; ++i) lds_wait_n<0>(code[tb][i]);
+          }
+          // ---- rms divide, scale, cap, mask; the rows' tile max ----
+          float tm = kNegInf;
+#pragma unroll
+          for (int tb = 0; tb < 2; ++tb)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+              float rinv = 1.0f;
+              if constexpr (C::RMS == QMLA_RMS_BF16) {
+                const float rv = bf16_bits_to_f32(code[tb][i]);
+                rinv = rv > 0.f ? __builtin_amdgcn_rcpf(rv) : 1.0f;
+              }
+              float v;
+              if constexpr (C::CAP) {
+                const float sn = sc[tb][i] * (c2 * kLn2) * rinv;
+                const float th = 1.0f - 2.0f / (fast_exp2(2.0f * kLog2e * (sn / p.logit_cap)) + 1.0f);
+                v = p.logit_cap * th * kLog2e;
+              } else {
+                v = sc[tb][i] * c2 * rinv;
+              }
+              v = tok0 + 16 * tb + 4 * lg + i < lim ? v : kNegInf;
+              sc[tb][i] = v;
+              tm = fmaxf(tm, v);
+            }
+          tm = max_lg(tm);
+          // ---- the reference moves when a row's tile max exceeds it by more than the shift its
+          //      running sum allows ----
+          const bool ch = tm > mref + ref_shift(sum_lg(lpart), SHIFT_CAP);
+          const bool rare = __builtin_amdgcn_ballot_w64(ch) != 0;
+          if (rare) {
+            const float mn = ch ? tm : mref;
+            const float alpha_f = ch ? (mref == kNegInf ? 0.f : fast_exp2(mref - mn)) : 1.0f;
+            mref = mn;
+            lpart *= alpha_f;
+            if (lg == 0) sm.alpha[g & 1][rg] = alpha_f;
+          }
+          if (lane == 0) sm.flag[g & 1][su] = rare ? 1 : 0;
+          // ---- P against the reference ----
+          const float mu = mref == kNegInf ? 0.f : mref;
+          float ps = 0.f;
+#pragma unroll
+          for (int tb = 0; tb < 2; ++tb) {
+            bf16x4 pk;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+              const float e = fast_exp2(sc[tb][i] - mu);
+              ps += e;
+              pk[i] = (__bf16)e;
+            }
+            *reinterpret_cast<bf16x4*>(&sm.p[g & 1][rg][(16 * tb + 4 * lg) * 2]) = pk;
+          }
+          lpart += ps;
+          if (++ts == s_nt) {
+            // the piece's last tile: publish its rows' max and sum for the value waves
+            if (s_fl & SEG_LAST) {
+              const float l = sum_lg(lpart);
+              if (lg == 0) {
+                sm.fin[ks & 1][0][rg] = mref;
+                sm.fin[ks & 1][1][rg] = l;
+              }
+            }
+            ts = 0;
+            ++ks;
+          }
+        }
+      } else {
+        if (g + C::A < ntot) issue(g + C::A);
+        if (g + 1 < ntot) wait_tile(g + 1, g + C::A < ntot - 1 ? g + C::A : ntot - 1);
+        if (g >= 1) {
+          // ---- P . V of tile j = g - 1 over columns VC*vw .. +VC: reads first ----
+          const int j = g - 1, pj = j & 1;
+          const i32x2 fl = ldsr64(&sm.flag[pj][0]);
+          i32x4 pr[2];
+#pragma unroll
+          for (int mb = 0; mb < 2; ++mb) pr[mb] = ldsr128(&sm.p[pj][16 * mb + ln16][16 * lg]);
+          // V^T: lane (ln16, lg) gets column VC*vw + 16cb + ln16 of rows 8lg .. 8lg+3 and 8lg+4 .. +7
+          const uint32_t va = lds_addr(sm.kv[j % C::S]) +
+                              (uint32_t)((8 * lg + (ln16 >> 2)) * C::RB + (C::VC * vw + 4 * (ln16 & 3)) * 2);
+          i32x2 vraw[C::CB][2];
+          static_for<0, C::CB>([&](auto cc) {
+            constexpr int c = decltype(cc)::value;
+            vraw[c][0] = ldstr16_at<32 * c>(va);
+            vraw[c][1] = ldstr16_at<32 * c + 4 * C::RB>(va);
+          });
+          i32x2 flw = fl;
+          lds_wait_n<cmin15(2 + 2 * C::CB)>(flw);
+          const int f0 = __builtin_amdgcn_readfirstlane(flw[0]), f1 = __builtin_amdgcn_readfirstlane(flw[1]);
+          if (f0 | f1) {
+            // some row's reference moved at tile j: rescale before adding it
+            i32x4 ar[2];
+#pragma unroll
+            for (int mb = 0; mb < 2; ++mb) ar[mb] = ldsr128(&sm.alpha[pj][16 * mb + 4 * lg]);
+#pragma unroll
+            for (int mb = 0; mb < 2; ++mb) lds_wait_n<0>(ar[mb]);
+#pragma unroll
+            for (int mb = 0; mb < 2; ++mb) {
+              if ((mb == 0 ? f0 : f1) == 0) continue;
+              const f32x4 al = __builtin_bit_cast(f32x4, ar[mb]);
+#pragma unroll
+              for (int i = 0; i < 4; ++i)
+#pragma unroll
+                for (int cb = 0; cb < C::CB; ++cb) acc[mb][cb][i] *= al[i];
+            }
+          }
+          bf16x8 pf[2];
+          lds_wait_n<cmin15(1 + 2 * C::CB)>(pr[0]);
+          lds_wait_n<cmin15(2 * C::CB)>(pr[1]);
+          pf[0] = __builtin_bit_cast(bf16x8, pr[0]);
+          pf[1] = __builtin_bit_cast(bf16x8, pr[1]);
+          static_for<0, C::CB>([&](auto cc) {
+            constexpr int c = decltype(cc)::value;
+            lds_wait_n<cmin15(2 * (C::CB - 1 - c) + 1)>(vraw[c][0]);
+            lds_wait_n<cmin15(2 * (C::CB - 1 - c))>(vraw[c][1]);
+            const i32x4 w4 = {vraw[c][0][0], vraw[c][0][1], vraw[c][1][0], vraw[c][1][1]};
+            const bf16x8 vf = __builtin_bit_cast(bf16x8, w4);
+#pragma unroll
+            for (int mb = 0; mb < 2; ++mb) acc[mb][c] = mfma16(pf[mb], vf, acc[mb][c]);
+          });
+          if (++tv == v_nt) {
+            // the request's last tile: its sums were published with it
+            if (v_fl & SEG_LAST) finalize(kv, v_req, v_fl);
+            tv = 0;
+            if (++kv < nseg) {
+              const SegD d = read_seg(kv);
+              v_req = d.req;
+              v_nt = d.nt;
+              v_fl = d.fl;
+            }
+          }
+        }
+      }
+      lds_barrier();
+    }
+    wait_vmcnt<0>();
+    if (!more) break;
+  }
+}
+
+template <class C>
+__global__ __launch_bounds__(C::NTHR, 1) void wsb_kernel(const KParams p) {
+  static_assert(sizeof(Smem<C>) <= 163840, "LDS budget of a workgroup");
+  __shared__ __attribute__((aligned(16))) Smem<C> sm;
+  const bool fixed = p.num_splits > 0;
+  const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  // head split: the p.hsplit workgroups of one token range are consecutive on one XCD (workgroup i
+  // runs on XCD i % 8), so their shared reads of the range's rows are served by that XCD's L2
+  int hz = fixed ? (int)blockIdx.z : 0, wr = blockIdx.x;
+  if (!fixed && p.hsplit > 1) {
+    if ((p.nwg & 7) == 0) {
+      const int slot = (int)blockIdx.x >> 3;
+      hz = slot % p.hsplit;
+      wr = (slot / p.hsplit) * 8 + ((int)blockIdx.x & 7);
+    } else {   // a caller's range count: the split's workgroups are at least adjacent in launch order
+      hz = (int)blockIdx.x % p.hsplit;
+      wr = (int)blockIdx.x / p.hsplit;
+    }
+  }
+  int lo = 0, hi = 0, b0 = 0, c0 = 0;
+  if (!fixed) {
+    if (wr == 0 && hz == 0 && wv == 1) store_plan<kPlanSwitchWs>(p);   // for the balanced combine
+    const BalRange r = balanced_range<kPlanSwitchWs>(p, wr);
+    lo = r.lo;
+    hi = r.hi;
+    b0 = r.b0;
+    c0 = r.c0;
+    if (lo >= hi) return;
+  }
+  int bad = 0;
+  if (wv >= 4) role_main<C, SCORE>(p, sm, fixed, lo, hi, b0, c0, wr, hz, bad);
+  else role_main<C, VALUE>(p, sm, fixed, lo, hi, b0, c0, wr, hz, bad);
+  report_pages(p, bad);
+}
+
+struct Inst {
+  int rms, cpr;
+  bool cap;
+  int nthr;
+  void (*fn)(const KParams);
+};
+
+#define QMLA_WSB(RMS, CPR, A, CAP) \
+  {RMS, CPR, CAP, WB<RMS, CPR, A, CAP>::NTHR, &wsb_kernel<WB<RMS, CPR, A, CAP>>}
+
+static const Inst kInst[] = {
+    // bf16 rows [latent 512 | rope 64 | 24 bf16 rms]: 1200 bytes staged, 2 tiles ahead (4 stages)
+    QMLA_WSB(QMLA_RMS_BF16, 75, 2, false),
+    QMLA_WSB(QMLA_RMS_BF16, 75, 2, true),
+    // ... without an rms tail: 1152 bytes
+    QMLA_WSB(QMLA_RMS_NONE, 72, 2, false),
+};
+
+}  // namespace wsb
+
+// A compiled instance for bf16 rows of one latent group (d_c 512, rope 64) whose rows fit a
+// workgroup (the warp-specialized head split), or -1.
+int wsb_select(const qmla_decode_params* p) {
+  if (p->kv_dtype != QMLA_KV_BF16 || p->groups != 1 || p->d_c != 512 || p->rope_w != 64) return -1;
+  if (ws_head_split(p) == 0) return -1;
+  const bool cap = p->logit_cap > 0.f;
+  const int64_t ts = p->token_stride * 2;
+  for (int i = 0; i < (int)(sizeof(wsb::kInst) / sizeof(wsb::kInst[0])); ++i) {
+    const wsb::Inst& in = wsb::kInst[i];
+    if (in.rms != p->rms_mode || in.cap != cap) continue;
+    if ((int64_t)in.cpr * 16 > ts) continue;   // never read past a row
+    if (p->rms_mode != QMLA_RMS_NONE && (int64_t)p->rms_offset * 2 + (int64_t)p->heads * 2 > in.cpr * 16) continue;
+    return i;
+  }
+  return -1;
+}
+
+int wsb_launch(int inst, const qmla_decode_params* p, const KParams& k, int nwg, hipStream_t st) {
+  KParams kk = k;
+  kk.hsplit = ws_head_split(p);
+  void* args[] = {&kk};
+  dim3 grid = p->num_splits > 0 ? dim3(p->num_splits, k.n_req, kk.hsplit) : dim3(nwg * kk.hsplit, 1, 1);
+  if (grid.x == 0 || grid.y == 0) return QMLA_OK;
+  hipError_t e =
+      hipLaunchKernel((const void*)wsb::kInst[inst].fn, grid, dim3(wsb::kInst[inst].nthr, 1, 1), args, 0, st);
+  return e == hipSuccess ? QMLA_OK : QMLA_ERR_LAUNCH;
+}
+
+}  // namespace qmla

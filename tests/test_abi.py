@@ -184,7 +184,8 @@ def test_routing_without_launch(kv, d_c, rope, heads, rms, qrows, groups, code):
 @pytest.mark.parametrize("kv,rms,qrows,groups,splits,tiles", [
     (_lib.KV_FP8, _lib.RMS_LOG8, 1, 1, 0, 2),     # warp-specialized decode, balanced
     (_lib.KV_FP8, _lib.RMS_LOG8, 4, 2, 0, 2),     # row-owner GLA-g2 decode, balanced
-    (_lib.KV_BF16, _lib.RMS_BF16, 1, 1, 0, 0),    # per-group kernel
+    (_lib.KV_BF16, _lib.RMS_BF16, 1, 1, 0, 2),    # bf16 warp-specialized decode, balanced
+    (_lib.KV_FP8, _lib.RMS_E4M3, 1, 1, 0, 0),     # per-group kernel
     (_lib.KV_FP8, _lib.RMS_LOG8, 1, 1, 4, 0),     # fixed splits: no plan
 ])
 def test_plan_switch_tiles(kv, rms, qrows, groups, splits, tiles):
