@@ -162,6 +162,12 @@ __device__ __forceinline__ uint32_t ldsr16_at(uint32_t a) {
   asm volatile("ds_read_u16 %0, %1 offset:%2" : "=v"(r) : "v"(a), "n"(OFF));
   return r;
 }
+template <int OFF>
+__device__ __forceinline__ uint32_t ldsr8_off(uint32_t a) {
+  uint32_t r;
+  asm volatile("ds_read_u8 %0, %1 offset:%2" : "=v"(r) : "v"(a), "n"(OFF));
+  return r;
+}
 __device__ __forceinline__ uint32_t ldsr8_at(uint32_t a) {
   uint32_t r;
   asm volatile("ds_read_u8 %0, %1" : "=v"(r) : "v"(a));

@@ -978,12 +978,12 @@ int ws_head_split(const qmla_decode_params* p) {
 }
 
 // Instances past the warp-specialized table are the row-owner kernel's (qmla_ro.hip), which takes
-// the GLA-g2 shapes it serves, and the bf16 warp-specialized kernel's (qmla_wsb.hip).
+// the GLA-g2 shapes it serves, and the wide-row warp-specialized kernel's (qmla_wsb.hip: bf16 rows,
+// the deployed fp8 layouts).
 constexpr int kRoBase = 1000, kWsbBase = 2000;
 
-int ws_select(const qmla_decode_params* p) {
-  const int ri = ro_select(p);
-  if (ri >= 0) return kRoBase + ri;
+// the fp8 warp-specialized table's instance, or -1
+static int ws_table_select(const qmla_decode_params* p) {
   if (p->rope_w != 64 || (p->groups != 1 && p->groups != 2)) return -1;
   const int hs = ws_head_split(p);
   if (hs == 0) return -1;
@@ -1005,6 +1005,14 @@ int ws_select(const qmla_decode_params* p) {
     }
     return i;
   }
+  return -1;
+}
+
+int ws_select(const qmla_decode_params* p) {
+  const int ri = ro_select(p);
+  if (ri >= 0) return kRoBase + ri;
+  const int wi = ws_table_select(p);
+  if (wi >= 0) return wi;
   const int bi = wsb_select(p);
   return bi >= 0 ? kWsbBase + bi : -1;
 }

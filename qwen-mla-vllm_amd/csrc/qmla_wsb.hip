@@ -1,40 +1,54 @@
-// qmla_wsb.hip -- gfx950 warp-specialized MLA decode of bf16 rows: d_c 512, rope 64, one bf16 rms
-// per head (or none), <= 32 query rows per workgroup (24 heads, one token each; 24 heads x 4 verify
-// tokens split over 3 workgroups of 8 heads).
+// qmla_wsb.hip -- gfx950 warp-specialized MLA decode of wide rows, <= 32 query rows per workgroup
+// (24 heads, one token each; 24 heads x 4 verify tokens split over 3 workgroups of 8 heads):
+//   bf16 rows: d_c 512, rope 64, one bf16 rms per head (or none): 1200 staged bytes;
+//   fp8 rows (the plugin's deployed layouts): latent d_c 768 or 256, a partial rope of 232 columns
+//   read as a 256-column window, one rms code per head: 1024 or 512 bytes.
 //
 // A workgroup owns a contiguous range of the concatenated requests' tokens (balanced mode) or one
 // split of one request (fixed splits), with all of its query rows, and walks it as one sequence of
-// 32-token tiles across request boundaries (the window walk of qmla_window.h). A bf16 row is 1200
-// staged bytes, twice an fp8 one, so a 32-token tile is 37.5 KB and the LDS holds a ring of four.
-// That decides the split of the work: the softmax of a tile has to be final within the step that
-// scores it, so the value waves can take the tile one step later and the ring needs only the tiles
-// in flight, the one being scored and the one being accumulated (A + 2 stages).
+// 32-token tiles across request boundaries (the window walk of qmla_window.h). A 32-token tile of
+// these rows is 32-37.5 KB, so the LDS holds a ring of four. That decides the split of the work: the
+// softmax of a tile has to be final within the step that scores it, so the value waves can take the
+// tile one step later and the ring needs only the tiles in flight, the one being scored and the one
+// being accumulated (A + 2 stages).
 //
 // Its 6 waves take two roles:
 //   score waves (4, 5): wave 4 + u owns 16 query rows (row block u) for all 32 tokens of a tile. It
-//                       computes S^T = K . Q^T on the 16x16x32 bf16 MFMA (query fragments resident
-//                       in VGPRs, K fragments read from the staged rows), divides by the rms, applies
-//                       the mask, and runs the rows' online softmax entirely in its own registers (a
+//                       computes S^T = K . Q^T on MFMA with the query fragments resident in VGPRs and
+//                       the K fragments read from the staged rows: bf16 rows on the 16x16x32 bf16
+//                       MFMA; fp8 rows with their bytes as stored on the 16x16x128 fp8 MFMA, the
+//                       query split per row into two e4m3 parts (hi + lo, 8 significant bits like
+//                       bf16), the rope window's columns past the rope zeroed in K (they hold the rms
+//                       codes). It divides by the rms, applies the mask, and runs the rows' online
+//                       softmax entirely in its own registers (a
 //                       row's tile max is a reduction over its 4 lane groups). The reference max moves
 //                       only when a row's tile max exceeds it by more than ref_shift(the row's sum),
 //                       so a dominant token gets P = 1 exactly and the bf16 rounding of P costs no
 //                       more than in the reference; the wave then publishes the factor by which the
 //                       value waves rescale their accumulators. P (bf16) goes to LDS. At a request's
 //                       last tile it publishes the rows' max and sum;
-//   value waves (0-3):  wave v accumulates P . V over latent columns [128v, 128v+128) for all 32 rows
-//                       one tile behind the score waves, with V^T fragments read transposed from the
-//                       staged rows (ds_read_b64_tr_b16), writes a request's output when its last
-//                       tile is in, and streams the tiles global -> LDS by LDS-DMA, A tiles ahead of
-//                       the score waves (each value wave waits only for its own loads).
+//   value waves (0-3):  wave v accumulates P . V over latent columns [v d_c/4, (v+1) d_c/4) for all 32
+//                       rows one tile behind the score waves, with V^T fragments read transposed from
+//                       the staged rows (ds_read_b64_tr_b16; fp8 rows ds_read_b64_tr_b8, converted
+//                       exactly to fp16, P in fp16), writes a request's output when its last tile is
+//                       in, and streams the tiles global -> LDS by LDS-DMA, A tiles ahead of the
+//                       score waves (each value wave waits only for its own loads).
 // The two score waves sit on SIMDs 0 and 1 beside value waves 0 and 1 (waves are placed on SIMDs in
 // order); SIMDs 2 and 3 hold one value wave each. The workgroup meets once per tile at one barrier.
 // Inside a step a wave issues its LDS reads and waits for them in order with counted lgkmcnt waits.
+// fp8 rows are 256 dwords (or 128) long, which puts every staged row on the same LDS banks: they are
+// staged with each 16-byte chunk rotated inside its 256-byte region by the row index (chunk c of a
+// region of row r at position (c + r) & 15), so the K reads of 16 consecutive rows and the
+// transposed V reads of 8 consecutive rows land on distinct banks; 1200-byte bf16 rows need none.
 //
-// Reference semantics: qwen_mla/ops/mla_decode_attention.py:297-586 (stage 1: tile loop, rms divide
-// :466-507, softmax :553-560, partial store :562-586).
+// Reference semantics: qwen_mla/ops/mla_decode_attention.py:297-586 (stage 1: tile loop, fp8 dequant
+// :451-463, rms divide :466-507, softmax :553-560, partial store :562-586); the deployed fp8 layouts
+// (partial rope, rms codes after it) of qwen_mla/mla_impl.py:125-145, 261-271.
 
 #include <hip/hip_runtime.h>
 #include <stdint.h>
+
+#include <type_traits>
 
 #include "qmla.h"
 #include "qmla_common.h"
@@ -49,14 +63,14 @@ constexpr float SHIFT_CAP = 8.0f;   // P = exp2(s - ref) <= 2^8 before a row's r
 constexpr int PIDB = 256;        // page ids per window (the ring leaves no room for more)
 enum Role { SCORE, VALUE };
 
-// Compile-time shape: RMS tail format (bf16 per head, or none), CPR 16-byte chunks staged per row
-// (rows are staged unrotated: 1200-byte rows put the 16 rows of a K read on distinct banks), A tiles
-// in flight ahead of the score waves, CAP tanh logit cap.
-template <int RMS_, int CPR_, int A_, bool CAP_>
+// Compile-time shape: EB cache element bytes (2 bf16, 1 fp8 e4m3), RMS tail format, DC latent
+// columns, RW rope columns read as a window of WIN (the columns past RW are masked), CPR 16-byte
+// chunks staged per row, A tiles in flight ahead of the score waves, CAP tanh logit cap.
+template <int EB_, int RMS_, int DC_, int RW_, int WIN_, int CPR_, int A_, bool CAP_>
 struct WB {
-  static constexpr int RMS = RMS_, CPR = CPR_, A = A_, S = A_ + 2;
+  static constexpr int EB = EB_, RMS = RMS_, DC = DC_, RW = RW_, WIN = WIN_, CPR = CPR_, A = A_, S = A_ + 2;
   static constexpr bool CAP = CAP_;
-  static constexpr int DC = 512, ROPE = 64;
+  static constexpr bool ROT = EB == 1;            // rows rotated inside 256-byte regions
   static constexpr int RB = 16 * CPR, STAGE = TILE * RB;
   static constexpr int NW = 6, NTHR = 64 * NW;   // value waves 0-3, score waves 4-5
   static constexpr int ROWS = 32;
@@ -64,15 +78,39 @@ struct WB {
   static constexpr int NI = (NCH + 63) / 64;      // DMA instructions per tile
   static constexpr int NIW = 4;                   // issuing waves
   static constexpr int DPW = (NI + NIW - 1) / NIW;
-  static constexpr int KQ = (DC + ROPE) / 32;     // k-steps of the score product
-  static constexpr int KP = KQ / 2;               // 64-column pairs: two 16-byte K reads per lane
+  // bf16 rows: 32-column k-steps of the score product (pairs: two 16-byte K reads per lane)
+  static constexpr int KQ = EB == 2 ? (DC + WIN) / 32 : 1;
+  static constexpr int KP = KQ / 2;
+  // fp8 rows: 128-column blocks (latent, then the rope window); KW blocks of K reads in flight
+  static constexpr int NBT = EB == 1 ? (DC + WIN) / 128 : 1;
+  static constexpr int KW = 2;
   static constexpr int VC = DC / 4, CB = VC / 16; // columns per value wave, 16-column blocks
   static constexpr int PST = TILE * 2 + 16;       // P row stride in LDS (bytes)
-  static constexpr int NCODE = RMS == QMLA_RMS_NONE ? 0 : 8;   // rms reads per lane and tile
-  static_assert(RMS == QMLA_RMS_NONE || RMS == QMLA_RMS_BF16, "bf16 rows: one bf16 rms per head, or none");
-  static_assert(CPR * 16 >= (DC + ROPE) * 2, "row slice");
+  static constexpr int RMS_EB = (RMS == QMLA_RMS_BF16 || RMS == QMLA_RMS_BF16_BYTES) ? 2 : 1;
+  // P and the P . V operands: fp16 for fp8 rows (every e4m3 value is exact in fp16, P keeps 11
+  // significant bits), bf16 for bf16 rows
+  using PT = std::conditional_t<EB == 1, _Float16, __bf16>;
+  using PX4 = std::conditional_t<EB == 1, f16x4, bf16x4>;
+  using PX8 = std::conditional_t<EB == 1, f16x8, bf16x8>;
+  static_assert(EB == 1 || (RW == WIN && WIN % 64 == 0 && DC % 64 == 0 &&
+                            (RMS == QMLA_RMS_NONE || RMS == QMLA_RMS_BF16) && CPR * 16 >= (DC + WIN) * 2),
+                "bf16 rows: whole 64-column pairs, one bf16 rms per head or none");
+  static_assert(EB == 2 || (DC % 128 == 0 && WIN % 128 == 0 && RW <= WIN && RW > WIN - 128 && CPR % 16 == 0 &&
+                            DC + WIN <= CPR * 16 && RMS != QMLA_RMS_NONE && RMS != QMLA_RMS_BF16),
+                "fp8 rows: 128-column blocks, whole 256-byte regions, rms codes after the rope");
+  static_assert(DC % 64 == 0 && CB >= 1, "column split of the value waves");
   static_assert(A >= 2 && A * DPW < 64, "lookahead / vmcnt range");
 };
+
+// staged position (16-byte chunk) of chunk c of row r, and the inverse
+template <class C>
+__device__ __forceinline__ int stage_pos(int c, int r) {
+  return C::ROT ? (c & ~15) + ((c + r) & 15) : c;
+}
+template <class C>
+__device__ __forceinline__ int stage_chunk(int q, int r) {
+  return C::ROT ? (q & ~15) + ((q - r) & 15) : q;
+}
 
 template <class C>
 struct Smem {
@@ -92,10 +130,11 @@ __device__ __forceinline__ constexpr int dpw(int d) { return (C::NI - d + C::NIW
 // The whole range of this workgroup, seen from one role. All roles run the same window / tile /
 // barrier sequence; each keeps only its own registers live.
 template <class C, int ROLE>
-__device__ __forceinline__ void role_main(const KParams& p, Smem<C>& sm, bool fixed, int lo, int hi, int b0,
-                                          int c0, int wr, int hz, int& bad) {
+__device__ __forceinline__ void role_main(const KParams& p, Smem<C>& sm, float kscale, bool fixed, int lo, int hi,
+                                          int b0, int c0, int wr, int hz, int& bad) {
   constexpr int NTHR = C::NTHR;
   constexpr bool QS = ROLE == SCORE;
+  constexpr bool F8 = C::EB == 1;
   constexpr int ND = QS ? 1 : C::DPW;
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -109,28 +148,90 @@ __device__ __forceinline__ void role_main(const KParams& p, Smem<C>& sm, bool fi
   const int nrows = qrows * hpw;
   const int P = p.page_size;
   const int64_t tsb = p.token_stride_b;
-  const float c2 = p.sm_scale * kLog2e;
+  const float c2b = p.sm_scale * kscale * kLog2e;   // fp8 rows: the values are scaled by kscale
   // score wave: its row (verify token jq, head hd)
   const int rg = 16 * su + ln16;
   const bool rok = rg < nrows;
   const int jq = rok ? rg / hpw : 0;
   const int hd = h0 + (rok ? rg - jq * hpw : 0);
 
-  // ---- score wave: query fragments, pair jj and lane group lg holding columns 64jj + 16lg .. +16
-  //      (k-step 2jj the first 8, 2jj + 1 the next 8) ----
-  bf16x8 qf[QS ? C::KQ : 1];
+  // ---- score wave: query fragments. bf16 rows: pair jj and lane group lg hold columns
+  //      64jj + 16lg .. +16 (k-step 2jj the first 8, 2jj + 1 the next 8). fp8 rows: block b and lane
+  //      group lg hold columns 128b + 32lg .. +32 as e4m3 hi and lo parts of the query scaled by a
+  //      power of two per row (undone in c2); rope columns past RW are zero ----
+  bf16x8 qf[QS && !F8 ? C::KQ : 1];
+  i32x8 qh8[QS && F8 ? C::NBT : 1], ql8[QS && F8 ? C::NBT : 1];
+  float c2 = c2b;
+  // 8 query columns from col (latent, then rope; rope columns past RW read as zero)
+  auto q8 = [&](const __bf16* qnp, const __bf16* qpp, int col) {
+    if (col < C::DC) return load_q8(qnp + col, p.q_vec);
+    const int rc = col - C::DC;
+    if (rc + 8 <= C::RW) return load_q8(qpp + rc, p.q_vec);
+    bf16x8 v{};
+#pragma unroll
+    for (int e = 0; e < 8; ++e)
+      if (rc + e < C::RW) v[e] = qpp[rc + e];
+    return v;
+  };
   auto load_q = [&](int req) {
     const int row = req * qrows + jq;
     const __bf16* qnp = p.q_nope + (int64_t)row * p.qn_sr + (int64_t)hd * p.qn_sh;
     const __bf16* qpp = p.q_pe + (int64_t)row * p.qp_sr + (int64_t)hd * p.qp_sh;
+    if constexpr (!F8) {
 #pragma unroll
-    for (int k = 0; k < C::KQ; ++k) {
-      const int col = 64 * (k >> 1) + 16 * lg + 8 * (k & 1);
-      bf16x8 v = load_q8(col < C::DC ? qnp + col : qpp + (col - C::DC), p.q_vec);
-      if (!rok) v = bf16x8{};
-      qf[k] = v;
+      for (int k = 0; k < C::KQ; ++k) {
+        bf16x8 v = q8(qnp, qpp, 64 * (k >> 1) + 16 * lg + 8 * (k & 1));
+        if (!rok) v = bf16x8{};
+        qf[k] = v;
+      }
+    } else {
+      bf16x8 qn[4 * C::NBT];
+#pragma unroll
+      for (int k = 0; k < 4 * C::NBT; ++k) {
+        qn[k] = q8(qnp, qpp, 128 * (k >> 2) + 32 * lg + 8 * (k & 3));
+        if (!rok) qn[k] = bf16x8{};
+      }
+      float mx = 0.f;
+#pragma unroll
+      for (int k = 0; k < 4 * C::NBT; ++k)
+#pragma unroll
+        for (int e = 0; e < 8; ++e) mx = fmaxf(mx, fabsf((float)qn[k][e]));
+      mx = max_lg(mx);
+      // |q| * qs in (112, 448]: e4m3 keeps 4 significant bits in hi and 4 more in lo
+      const float ex = mx > 0.f ? fminf(floorf(fast_log2(224.0f / mx)), 126.0f) : 0.0f;
+      const float qs = fast_exp2(ex);
+      c2 = c2b * fast_exp2(-ex);
+      // each block's parts are built whole, so the previous request's parts die here
+#pragma unroll
+      for (int b = 0; b < C::NBT; ++b) {
+        int hq[8], lq[8];
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+#pragma unroll
+          for (int hw = 0; hw < 2; ++hw) {
+            float v[4], rsd[4];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) v[e] = (float)qn[4 * b + k][4 * hw + e] * qs;
+            int hb = __builtin_amdgcn_cvt_pk_fp8_f32(v[0], v[1], 0, false);
+            hb = __builtin_amdgcn_cvt_pk_fp8_f32(v[2], v[3], hb, true);
+            rsd[0] = v[0] - __builtin_amdgcn_cvt_f32_fp8(hb, 0);
+            rsd[1] = v[1] - __builtin_amdgcn_cvt_f32_fp8(hb, 1);
+            rsd[2] = v[2] - __builtin_amdgcn_cvt_f32_fp8(hb, 2);
+            rsd[3] = v[3] - __builtin_amdgcn_cvt_f32_fp8(hb, 3);
+            int lb = __builtin_amdgcn_cvt_pk_fp8_f32(rsd[0], rsd[1], 0, false);
+            lb = __builtin_amdgcn_cvt_pk_fp8_f32(rsd[2], rsd[3], lb, true);
+            hq[2 * k + hw] = hb;
+            lq[2 * k + hw] = lb;
+          }
+        }
+        qh8[b] = i32x8{hq[0], hq[1], hq[2], hq[3], hq[4], hq[5], hq[6], hq[7]};
+        ql8[b] = i32x8{lq[0], lq[1], lq[2], lq[3], lq[4], lq[5], lq[6], lq[7]};
+      }
     }
   };
+  // fp8 rows: the K bytes of the last window block's columns past RW (the rms codes) are zeroed:
+  // lane group lg keeps the first kvalid of its 32 bytes
+  const int kvalid = F8 ? min(32, max(0, C::RW - (C::WIN - 128) - 32 * lg)) : 32;
   float mref = kNegInf, lpart = 0.f;   // the row's reference max (log2 domain) and partial sum
   int lim = 0;                          // the row's token limit in the current piece
 
@@ -154,11 +255,37 @@ __device__ __forceinline__ void role_main(const KParams& p, Smem<C>& sm, bool fi
       int q = (vw + C::NIW * j) * 64 + lane;
       q = q < C::NCH ? q : C::NCH - 1;
       const int rr = q / C::CPR, pp = q - rr * C::CPR;
-      goff[j] = (uint32_t)(rr * tsb + 16 * pp);
+      goff[j] = (uint32_t)(rr * tsb + 16 * stage_chunk<C>(pp, rr));
       drow[j] = rr;
     }
   }
   const bool big = dpw<C>(vw) == C::DPW;
+  // per-lane LDS offsets within a stage. Score wave: the rms of rows 4lg + i (+16tb); K row ln16
+  // (+16tb): bf16 rows at byte 32lg of each 64-column pair, fp8 rows chunk 2lg + h of each block of
+  // parity e. Value wave: transposed V reads of its 16-column blocks
+  uint32_t coff[4] = {0u, 0u, 0u, 0u}, koff[2][2] = {{0u, 0u}, {0u, 0u}}, voff[QS ? 1 : C::CB];
+  if constexpr (QS) {
+    const int rb = p.rms_off_b + C::RMS_EB * hd;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int rr = 4 * lg + i;
+      coff[i] = (uint32_t)(rr * C::RB + 16 * stage_pos<C>(rb >> 4, rr) + (rb & 15));
+    }
+#pragma unroll
+    for (int e = 0; e < 2; ++e)
+#pragma unroll
+      for (int h = 0; h < 2; ++h)
+        koff[e][h] = F8 ? (uint32_t)(ln16 * C::RB + 16 * stage_pos<C>(8 * e + 2 * lg + h, ln16))
+                        : (uint32_t)(ln16 * C::RB + 32 * lg + 16 * h);
+  } else {
+    const int vr = F8 ? 8 * lg + (ln16 >> 1) : 8 * lg + (ln16 >> 2);
+#pragma unroll
+    for (int c = 0; c < C::CB; ++c) {
+      const int col = C::VC * vw + 16 * c;
+      voff[c] = F8 ? (uint32_t)(vr * C::RB + 16 * stage_pos<C>(col >> 4, vr) + 8 * (ln16 & 1))
+                   : (uint32_t)(vr * C::RB + (col + 4 * (ln16 & 3)) * 2);
+    }
+  }
 
   // one piece descriptor (drained reads: its fields are wave-uniform and live in scalar registers)
   auto read_seg = [&](int k) {
@@ -190,7 +317,7 @@ __device__ __forceinline__ void role_main(const KParams& p, Smem<C>& sm, bool fi
         if (rr >= nrows) continue;
         const float m = __int_as_float(mr[i]), l = __int_as_float(lr[i]);
         const int jr = rr / hpw, h = h0 + rr - jr * hpw;
-        const float inv = inv_sum(1.0f, l);
+        const float inv = inv_sum(kscale, l);   // fp8 values were accumulated unscaled
         const float lse_v = row_lse(m, l);
         const int col = C::VC * vw + ln16;
         if (so.final_out) {
@@ -198,6 +325,13 @@ __device__ __forceinline__ void role_main(const KParams& p, Smem<C>& sm, bool fi
 #pragma unroll
           for (int cb = 0; cb < C::CB; ++cb) store_out(p.out, p.out_dt, ob + 16 * cb, acc[mb][cb][i] * inv);
           if (vw == 0 && ln16 == 0 && p.lse) store_out(p.lse, p.lse_dt, (int64_t)(row0 + jr) * p.lse_sr + h, lse_v);
+        } else if (so.plse && p.part_h) {
+          // fp16 partials without the fp8 scale, which the combine applies
+          _Float16* ob = reinterpret_cast<_Float16*>(so.po) + (int64_t)jr * so.po_sr + (int64_t)h * so.po_sh + col;
+          const float invh = inv_sum(1.0f, l);
+#pragma unroll
+          for (int cb = 0; cb < C::CB; ++cb) ob[16 * cb] = (_Float16)(acc[mb][cb][i] * invh);
+          if (vw == 0 && ln16 == 0) so.plse[(int64_t)jr * so.plse_sr + h] = lse_v;
         } else {
           float* ob = so.po + (int64_t)jr * so.po_sr + (int64_t)h * so.po_sh + col;
 #pragma unroll
@@ -334,30 +468,30 @@ __device__ __forceinline__ void role_main(const KParams& p, Smem<C>& sm, bool fi
           }
           const uint32_t sb = lds_addr(sm.kv[g % C::S]);
           const int tok0 = s_ta + ts * TILE;
-          // ---- LDS reads: rms of tokens 16tb + 4lg + i (head hd), then the K rows of token block 0 ----
+          // ---- LDS reads: rms of tokens 16tb + 4lg + i (head hd), then the K rows ----
           uint32_t code[2][4];
           if constexpr (C::RMS != QMLA_RMS_NONE) {
-            const uint32_t ca = sb + (uint32_t)(4 * lg * C::RB + p.rms_off_b + 2 * hd);
             static_for<0, 2>([&](auto tc) {
               constexpr int tb = decltype(tc)::value;
               static_for<0, 4>([&](auto ic) {
                 constexpr int i = decltype(ic)::value;
-                code[tb][i] = ldsr16_at<(16 * tb + i) * C::RB>(ca);
+                if constexpr (C::RMS_EB == 2) code[tb][i] = ldsr16_at<16 * tb * C::RB>(sb + coff[i]);
+                else code[tb][i] = ldsr8_off<16 * tb * C::RB>(sb + coff[i]);
               });
             });
           }
-          // K row 16tb + ln16, columns 64jj + 16lg .. +8 and +8 .. +16
-          const uint32_t ka = sb + (uint32_t)(ln16 * C::RB + 32 * lg);
-          i32x4 kr[C::KQ];
-          static_for<0, C::KP>([&](auto jc) {
-            constexpr int jj = decltype(jc)::value;
-            kr[2 * jj] = ldsr128_at<128 * jj>(ka);
-            kr[2 * jj + 1] = ldsr128_at<128 * jj + 16>(ka);
-          });
-          // ---- S^T = K . Q^T: token block 0 as its rows land, each of its reads followed by the
-          //      same read of token block 1, whose products run after ----
           f32x4 sc[2];
-          {
+          if constexpr (!F8) {
+            // K row 16tb + ln16, columns 64jj + 16lg .. +8 and +8 .. +16
+            const uint32_t ka = sb + koff[0][0];
+            i32x4 kr[C::KQ];
+            static_for<0, C::KP>([&](auto jc) {
+              constexpr int jj = decltype(jc)::value;
+              kr[2 * jj] = ldsr128_at<128 * jj>(ka);
+              kr[2 * jj + 1] = ldsr128_at<128 * jj + 16>(ka);
+            });
+            // S^T = K . Q^T: token block 0 as its rows land, each of its reads followed by the same
+            // read of token block 1, whose products run after
             f32x4 sa = f32x4{0.f, 0.f, 0.f, 0.f}, sbb = sa;
             i32x4 kq[C::KQ];
             static_for<0, C::KQ>([&](auto kc) {
@@ -379,6 +513,51 @@ __device__ __forceinline__ void role_main(const KParams& p, Smem<C>& sm, bool fi
               else sa = mfma16(__builtin_bit_cast(bf16x8, kq[kk]), qf[kk], sa);
             });
             sc[1] = sa + sbb;
+          } else {
+            // block b of K row 16tb + ln16: chunks 2lg, 2lg + 1 of its 256-byte region's half b & 1,
+            // read KW blocks ahead of the products (both token blocks, hi and lo chains each)
+            const uint32_t ka[2][2] = {{sb + koff[0][0], sb + koff[0][1]}, {sb + koff[1][0], sb + koff[1][1]}};
+            i32x4 kr[C::NBT][2][2];
+            auto rd = [&](auto bc) {
+              constexpr int b = decltype(bc)::value;
+              kr[b][0][0] = ldsr128_at<256 * (b >> 1)>(ka[b & 1][0]);
+              kr[b][0][1] = ldsr128_at<256 * (b >> 1)>(ka[b & 1][1]);
+              kr[b][1][0] = ldsr128_at<16 * C::RB + 256 * (b >> 1)>(ka[b & 1][0]);
+              kr[b][1][1] = ldsr128_at<16 * C::RB + 256 * (b >> 1)>(ka[b & 1][1]);
+            };
+            static_for<0, (C::KW < C::NBT ? C::KW : C::NBT)>(rd);
+            f32x4 s0h = f32x4{0.f, 0.f, 0.f, 0.f}, s0l = s0h, s1h = s0h, s1l = s0h;
+            static_for<0, C::NBT>([&](auto bc) {
+              constexpr int b = decltype(bc)::value;
+              constexpr int na = (C::KW - 1 < C::NBT - 1 - b ? C::KW - 1 : C::NBT - 1 - b);   // blocks issued after b
+              lds_wait_n<cmin15(3 + 4 * na)>(kr[b][0][0]);
+              lds_wait_n<cmin15(2 + 4 * na)>(kr[b][0][1]);
+              lds_wait_n<cmin15(1 + 4 * na)>(kr[b][1][0]);
+              lds_wait_n<cmin15(4 * na)>(kr[b][1][1]);
+              i32x8 k0 = {kr[b][0][0][0], kr[b][0][0][1], kr[b][0][0][2], kr[b][0][0][3],
+                          kr[b][0][1][0], kr[b][0][1][1], kr[b][0][1][2], kr[b][0][1][3]};
+              i32x8 k1 = {kr[b][1][0][0], kr[b][1][0][1], kr[b][1][0][2], kr[b][1][0][3],
+                          kr[b][1][1][0], kr[b][1][1][1], kr[b][1][1][2], kr[b][1][1][3]};
+              if constexpr (b == C::NBT - 1 && C::RW < C::WIN) {
+#pragma unroll
+                for (int d = 0; d < 8; ++d) {
+                  const int nb = kvalid - 4 * d;   // valid bytes of dword d
+                  const uint32_t m = nb >= 4 ? 0xffffffffu : nb <= 0 ? 0u : (1u << (8 * nb)) - 1u;
+                  k0[d] &= (int)m;
+                  k1[d] &= (int)m;
+                }
+              }
+              s0h = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(k0, qh8[b], s0h, 0, 0, 0, 127, 0, 127);
+              s1h = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(k1, qh8[b], s1h, 0, 0, 0, 127, 0, 127);
+              s0l = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(k0, ql8[b], s0l, 0, 0, 0, 127, 0, 127);
+              s1l = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(k1, ql8[b], s1l, 0, 0, 0, 127, 0, 127);
+              if constexpr (b + C::KW < C::NBT) rd(std::integral_constant<int, b + C::KW>{});
+              // the block's products stay here: sunk past later reads they would keep every K
+              // fragment of the tile live at once
+              __builtin_amdgcn_sched_barrier(0);
+            });
+            sc[0] = s0h + s0l;
+            sc[1] = s1h + s1l;
           }
           if constexpr (C::RMS != QMLA_RMS_NONE) {
 #pragma unroll
@@ -393,7 +572,12 @@ __device__ __forceinline__ void role_main(const KParams& p, Smem<C>& sm, bool fi
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
               float rinv = 1.0f;
-              if constexpr (C::RMS == QMLA_RMS_BF16) {
+              if constexpr (C::RMS == QMLA_RMS_LOG8) {
+                rinv = fast_exp2(fmaf((float)code[tb][i], -6.0f / 255.0f, 3.0f));   // 1 / 2^(-3 + c*6/255)
+              } else if constexpr (C::RMS == QMLA_RMS_E4M3) {
+                const float rv = fp8_to_f32(code[tb][i]) * kscale;
+                rinv = rv > 0.f ? __builtin_amdgcn_rcpf(rv) : 1.0f;
+              } else if constexpr (C::RMS == QMLA_RMS_BF16 || C::RMS == QMLA_RMS_BF16_BYTES) {
                 const float rv = bf16_bits_to_f32(code[tb][i]);
                 rinv = rv > 0.f ? __builtin_amdgcn_rcpf(rv) : 1.0f;
               }
@@ -427,14 +611,14 @@ __device__ __forceinline__ void role_main(const KParams& p, Smem<C>& sm, bool fi
           float ps = 0.f;
 #pragma unroll
           for (int tb = 0; tb < 2; ++tb) {
-            bf16x4 pk;
+            typename C::PX4 pk;
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
               const float e = fast_exp2(sc[tb][i] - mu);
               ps += e;
-              pk[i] = (__bf16)e;
+              pk[i] = (typename C::PT)e;
             }
-            *reinterpret_cast<bf16x4*>(&sm.p[g & 1][rg][(16 * tb + 4 * lg) * 2]) = pk;
+            *reinterpret_cast<typename C::PX4*>(&sm.p[g & 1][rg][(16 * tb + 4 * lg) * 2]) = pk;
           }
           lpart += ps;
           if (++ts == s_nt) {
@@ -460,17 +644,22 @@ __device__ __forceinline__ void role_main(const KParams& p, Smem<C>& sm, bool fi
           i32x4 pr[2];
 #pragma unroll
           for (int mb = 0; mb < 2; ++mb) pr[mb] = ldsr128(&sm.p[pj][16 * mb + ln16][16 * lg]);
-          // V^T: lane (ln16, lg) gets column VC*vw + 16cb + ln16 of rows 8lg .. 8lg+3 and 8lg+4 .. +7
-          const uint32_t va = lds_addr(sm.kv[j % C::S]) +
-                              (uint32_t)((8 * lg + (ln16 >> 2)) * C::RB + (C::VC * vw + 4 * (ln16 & 3)) * 2);
-          i32x2 vraw[C::CB][2];
+          // V^T: lane (ln16, lg) gets column VC*vw + 16cb + ln16 of rows 8lg .. 8lg+7 (bf16 rows: two
+          // reads of 4 rows each)
+          constexpr int NVR = F8 ? 1 : 2;   // V reads per 16-column block
+          const uint32_t sj = lds_addr(sm.kv[j % C::S]);
+          i32x2 vraw[C::CB][NVR];
           static_for<0, C::CB>([&](auto cc) {
             constexpr int c = decltype(cc)::value;
-            vraw[c][0] = ldstr16_at<32 * c>(va);
-            vraw[c][1] = ldstr16_at<32 * c + 4 * C::RB>(va);
+            if constexpr (F8) {
+              vraw[c][0] = ldstr8_at<0>(sj + voff[c]);
+            } else {
+              vraw[c][0] = ldstr16_at<0>(sj + voff[c]);
+              vraw[c][NVR - 1] = ldstr16_at<4 * C::RB>(sj + voff[c]);
+            }
           });
           i32x2 flw = fl;
-          lds_wait_n<cmin15(2 + 2 * C::CB)>(flw);
+          lds_wait_n<cmin15(2 + NVR * C::CB)>(flw);
           const int f0 = __builtin_amdgcn_readfirstlane(flw[0]), f1 = __builtin_amdgcn_readfirstlane(flw[1]);
           if (f0 | f1) {
             // some row's reference moved at tile j: rescale before adding it
@@ -489,17 +678,24 @@ __device__ __forceinline__ void role_main(const KParams& p, Smem<C>& sm, bool fi
                 for (int cb = 0; cb < C::CB; ++cb) acc[mb][cb][i] *= al[i];
             }
           }
-          bf16x8 pf[2];
-          lds_wait_n<cmin15(1 + 2 * C::CB)>(pr[0]);
-          lds_wait_n<cmin15(2 * C::CB)>(pr[1]);
-          pf[0] = __builtin_bit_cast(bf16x8, pr[0]);
-          pf[1] = __builtin_bit_cast(bf16x8, pr[1]);
+          using PX8 = typename C::PX8;
+          PX8 pf[2];
+          lds_wait_n<cmin15(1 + NVR * C::CB)>(pr[0]);
+          lds_wait_n<cmin15(NVR * C::CB)>(pr[1]);
+          pf[0] = __builtin_bit_cast(PX8, pr[0]);
+          pf[1] = __builtin_bit_cast(PX8, pr[1]);
           static_for<0, C::CB>([&](auto cc) {
             constexpr int c = decltype(cc)::value;
-            lds_wait_n<cmin15(2 * (C::CB - 1 - c) + 1)>(vraw[c][0]);
-            lds_wait_n<cmin15(2 * (C::CB - 1 - c))>(vraw[c][1]);
-            const i32x4 w4 = {vraw[c][0][0], vraw[c][0][1], vraw[c][1][0], vraw[c][1][1]};
-            const bf16x8 vf = __builtin_bit_cast(bf16x8, w4);
+            PX8 vf;
+            if constexpr (F8) {
+              lds_wait_n<cmin15(C::CB - 1 - c)>(vraw[c][0]);
+              vf = fp8x8_to_f16(vraw[c][0]);
+            } else {
+              lds_wait_n<cmin15(2 * (C::CB - 1 - c) + 1)>(vraw[c][0]);
+              lds_wait_n<cmin15(2 * (C::CB - 1 - c))>(vraw[c][NVR - 1]);
+              const i32x4 w4 = {vraw[c][0][0], vraw[c][0][1], vraw[c][NVR - 1][0], vraw[c][NVR - 1][1]};
+              vf = __builtin_bit_cast(PX8, w4);
+            }
 #pragma unroll
             for (int mb = 0; mb < 2; ++mb) acc[mb][c] = mfma16(pf[mb], vf, acc[mb][c]);
           });
@@ -527,6 +723,7 @@ template <class C>
 __global__ __launch_bounds__(C::NTHR, 1) void wsb_kernel(const KParams p) {
   static_assert(sizeof(Smem<C>) <= 163840, "LDS budget of a workgroup");
   __shared__ __attribute__((aligned(16))) Smem<C> sm;
+  const float kscale = (C::EB == 1 && p.k_scale) ? *p.k_scale : 1.0f;
   const bool fixed = p.num_splits > 0;
   const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   // head split: the p.hsplit workgroups of one token range are consecutive on one XCD (workgroup i
@@ -553,43 +750,55 @@ __global__ __launch_bounds__(C::NTHR, 1) void wsb_kernel(const KParams p) {
     if (lo >= hi) return;
   }
   int bad = 0;
-  if (wv >= 4) role_main<C, SCORE>(p, sm, fixed, lo, hi, b0, c0, wr, hz, bad);
-  else role_main<C, VALUE>(p, sm, fixed, lo, hi, b0, c0, wr, hz, bad);
+  if (wv >= 4) role_main<C, SCORE>(p, sm, kscale, fixed, lo, hi, b0, c0, wr, hz, bad);
+  else role_main<C, VALUE>(p, sm, kscale, fixed, lo, hi, b0, c0, wr, hz, bad);
   report_pages(p, bad);
 }
 
 struct Inst {
-  int rms, cpr;
+  int eb, rms, dc, rw, cpr;
   bool cap;
   int nthr;
   void (*fn)(const KParams);
 };
 
-#define QMLA_WSB(RMS, CPR, A, CAP) \
-  {RMS, CPR, CAP, WB<RMS, CPR, A, CAP>::NTHR, &wsb_kernel<WB<RMS, CPR, A, CAP>>}
+#define QMLA_WSB(EB, RMS, DC, RW, WIN, CPR, A, CAP)                                                        \
+  {EB, RMS, DC, RW, CPR, CAP, WB<EB, RMS, DC, RW, WIN, CPR, A, CAP>::NTHR,                              \
+   &wsb_kernel<WB<EB, RMS, DC, RW, WIN, CPR, A, CAP>>}
 
 static const Inst kInst[] = {
     // bf16 rows [latent 512 | rope 64 | 24 bf16 rms]: 1200 bytes staged, 2 tiles ahead (4 stages)
-    QMLA_WSB(QMLA_RMS_BF16, 75, 2, false),
-    QMLA_WSB(QMLA_RMS_BF16, 75, 2, true),
+    QMLA_WSB(2, QMLA_RMS_BF16, 512, 64, 64, 75, 2, false),
+    QMLA_WSB(2, QMLA_RMS_BF16, 512, 64, 64, 75, 2, true),
     // ... without an rms tail: 1152 bytes
-    QMLA_WSB(QMLA_RMS_NONE, 72, 2, false),
+    QMLA_WSB(2, QMLA_RMS_NONE, 512, 64, 64, 72, 2, false),
+    // the plugin's fp8 rows at TP 1 (24 heads): rank 768 [latent | rope 232 | 24 codes] = 1024 bytes,
+    // 2 tiles ahead (4 stages, 128 KB); rank 256: 512 bytes, 4 ahead
+    QMLA_WSB(1, QMLA_RMS_LOG8, 768, 232, 256, 64, 2, false),
+    QMLA_WSB(1, QMLA_RMS_E4M3, 768, 232, 256, 64, 2, false),
+    QMLA_WSB(1, QMLA_RMS_LOG8, 256, 232, 256, 32, 4, false),
+    QMLA_WSB(1, QMLA_RMS_E4M3, 256, 232, 256, 32, 4, false),
 };
 
 }  // namespace wsb
 
-// A compiled instance for bf16 rows of one latent group (d_c 512, rope 64) whose rows fit a
-// workgroup (the warp-specialized head split), or -1.
+// A compiled instance for these rows (one latent group) whose query rows fit a workgroup (the
+// warp-specialized head split), or -1.
 int wsb_select(const qmla_decode_params* p) {
-  if (p->kv_dtype != QMLA_KV_BF16 || p->groups != 1 || p->d_c != 512 || p->rope_w != 64) return -1;
-  if (ws_head_split(p) == 0) return -1;
+  if (p->groups != 1 || ws_head_split(p) == 0) return -1;
+  const int eb = p->kv_dtype == QMLA_KV_FP8 ? 1 : 2;
   const bool cap = p->logit_cap > 0.f;
-  const int64_t ts = p->token_stride * 2;
+  const int64_t ts = p->token_stride * eb;
   for (int i = 0; i < (int)(sizeof(wsb::kInst) / sizeof(wsb::kInst[0])); ++i) {
     const wsb::Inst& in = wsb::kInst[i];
-    if (in.rms != p->rms_mode || in.cap != cap) continue;
+    if (in.eb != eb || in.rms != p->rms_mode || in.dc != p->d_c || in.rw != p->rope_w || in.cap != cap) continue;
     if ((int64_t)in.cpr * 16 > ts) continue;   // never read past a row
-    if (p->rms_mode != QMLA_RMS_NONE && (int64_t)p->rms_offset * 2 + (int64_t)p->heads * 2 > in.cpr * 16) continue;
+    if (p->rms_mode != QMLA_RMS_NONE) {
+      const int rb = (p->rms_mode == QMLA_RMS_BF16 || p->rms_mode == QMLA_RMS_BF16_BYTES) ? 2 : 1;
+      const int64_t roff = (int64_t)p->rms_offset * eb;
+      if (roff + (int64_t)p->heads * rb > in.cpr * 16) continue;   // every head's rms is staged
+      if (roff < (int64_t)(in.dc + in.rw) * eb) continue;          // the rms follows the rope
+    }
     return i;
   }
   return -1;
