@@ -7,6 +7,9 @@ combine for the wide latent):
   wide_b32   bf16, d_c 1792, B 32 x 65536 tokens, 1600-token pages, 16 fixed splits, seed 3
   gla_b48    GLA-g2 FP8 + log8, B 48 x 4 causal verify rows, ctx U[8k, 32k], seed 4
   verify_b64x4  FP8 + log8, B 64 x 4 causal verify rows x 24 heads, ctx lognormal(16k, 0.5), seed 5
+  verify_bf16_b64x4  the same on bf16 rows
+  fp8_r768_b128  the plugin's FP8 row at TP 1 (rank 768, rope 232, 24 log8 codes: 1024 bytes), the
+                 headline's batch and lengths
 
 The oracle runs on every 8th request plus the longest and the shortest (whole 4-row requests for
 GLA-g2). The bound is the plain one: max-abs 1e-2 on the output for a bf16 cache and 3e-2 for an
@@ -31,7 +34,8 @@ def _picks(case):
     return sorted(picks)
 
 
-@pytest.mark.parametrize("workload", ["bf16_b64", "fp8_b128", "wide_b32", "gla_b48", "verify_b64x4"])
+@pytest.mark.parametrize("workload", ["bf16_b64", "fp8_b128", "wide_b32", "gla_b48", "verify_b64x4",
+                                      "verify_bf16_b64x4", "fp8_r768_b128"])
 def test_config_workload(gpu, workload):
     import qmla
     from qmla import _lib
