@@ -1170,9 +1170,11 @@ extern "C" {
 int qmla_version(void) { return QMLA_ABI_VERSION; }
 
 const char* qmla_build_info(void) {
-  return "qmla gfx950: warp-specialized FP8 decode (fp8 MFMA scores, query as e4m3 hi+lo), segment decode "
-         "(bf16 MFMA QK/PV) for bf16 / verify / GLA, column-split single-pass wide latent (d_c 1792); "
-         "LDS-DMA paged rows, tr8/tr16 value reads, fixed and balanced split-K + LSE combine; cache-row writer";
+  return "qmla gfx950: warp-specialized FP8 decode (fp8 MFMA scores, query as e4m3 hi+lo), wide-row "
+         "warp-specialized decode (bf16 rows, the deployed fp8 rank-768/256 rows), row-owner GLA-g2 decode, "
+         "segment decode (bf16 MFMA QK/PV) for the other layouts, column-split single-pass wide latent "
+         "(d_c 1792); LDS-DMA paged rows, tr8/tr16 value reads, fixed and balanced split-K + LSE combine; "
+         "cache-row writer";
 }
 
 size_t qmla_workspace_bytes(const qmla_decode_params* p) {
