@@ -46,7 +46,7 @@ WORKLOADS = {
     # so each cached row is read once from HBM: the heads split over 3 workgroups on one XCD)
     "verify_b64x4": dict(batch=64, heads=24, d_c=512, rope_w=64, page_size=64, kv="fp8", rms_mode="log8", seed=5,
                          amp=4.0, lens=("lognormal", 16384, 0.5, 1024, 65536), qrows=4),
-    # the same verify step on a bf16 cache: the per-group kernel splits the 96 rows over 3 workgroups
+    # the same verify step on a bf16 cache: the wide-row kernel splits the heads over 3 workgroups
     # that read each token range together
     "verify_bf16_b64x4": dict(batch=64, heads=24, d_c=512, rope_w=64, page_size=64, kv="bf16", rms_mode="bf16",
                               seed=5, amp=1.0, lens=("lognormal", 16384, 0.5, 1024, 65536), qrows=4),

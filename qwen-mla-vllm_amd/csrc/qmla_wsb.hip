@@ -65,12 +65,19 @@ enum Role { SCORE, VALUE };
 
 // Compile-time shape: EB cache element bytes (2 bf16, 1 fp8 e4m3), RMS tail format, DC latent
 // columns, RW rope columns read as a window of WIN (the columns past RW are masked), CPR 16-byte
-// chunks staged per row, A tiles in flight ahead of the score waves, CAP tanh logit cap.
-template <int EB_, int RMS_, int DC_, int RW_, int WIN_, int CPR_, int A_, bool CAP_>
+// chunks staged per row, A tiles in flight ahead of the score waves, CAP tanh logit cap, CP cache
+// policy of the row loads (non-temporal, or the default for launches whose workgroups share a
+// token range and read its rows from L2).
+template <int EB_, int RMS_, int DC_, int RW_, int WIN_, int CPR_, int A_, bool CAP_, int CP_ = kCpolStream>
 struct WB {
   static constexpr int EB = EB_, RMS = RMS_, DC = DC_, RW = RW_, WIN = WIN_, CPR = CPR_, A = A_, S = A_ + 2;
   static constexpr bool CAP = CAP_;
-  static constexpr bool ROT = EB == 1;            // rows rotated inside 256-byte regions
+  static constexpr int CP = CP_;
+  // fp8 rows are rotated inside whole 256-byte regions, and inside the 128-byte block that follows
+  // them when the row has one (the rope window's last block of 896-byte rows); the rest is unrotated
+  static constexpr bool ROT = EB == 1;
+  static constexpr int FULL = CPR & ~15;                          // chunks in whole regions
+  static constexpr int TAIL8 = (ROT && CPR - FULL >= 8) ? 8 : 0;  // rotated chunks past them
   static constexpr int RB = 16 * CPR, STAGE = TILE * RB;
   static constexpr int NW = 6, NTHR = 64 * NW;   // value waves 0-3, score waves 4-5
   static constexpr int ROWS = 32;
@@ -95,9 +102,9 @@ struct WB {
   static_assert(EB == 1 || (RW == WIN && WIN % 64 == 0 && DC % 64 == 0 &&
                             (RMS == QMLA_RMS_NONE || RMS == QMLA_RMS_BF16) && CPR * 16 >= (DC + WIN) * 2),
                 "bf16 rows: whole 64-column pairs, one bf16 rms per head or none");
-  static_assert(EB == 2 || (DC % 128 == 0 && WIN % 128 == 0 && RW <= WIN && RW > WIN - 128 && CPR % 16 == 0 &&
-                            DC + WIN <= CPR * 16 && RMS != QMLA_RMS_NONE && RMS != QMLA_RMS_BF16),
-                "fp8 rows: 128-column blocks, whole 256-byte regions, rms codes after the rope");
+  static_assert(EB == 2 || (DC % 128 == 0 && WIN % 128 == 0 && RW <= WIN && RW > WIN - 128 &&
+                            (DC + WIN) / 16 <= FULL + TAIL8 && RMS != QMLA_RMS_NONE && RMS != QMLA_RMS_BF16),
+                "fp8 rows: 128-column blocks inside the rotated chunks, rms codes after the rope");
   static_assert(DC % 64 == 0 && CB >= 1, "column split of the value waves");
   static_assert(A >= 2 && A * DPW < 64, "lookahead / vmcnt range");
 };
@@ -105,11 +112,17 @@ struct WB {
 // staged position (16-byte chunk) of chunk c of row r, and the inverse
 template <class C>
 __device__ __forceinline__ int stage_pos(int c, int r) {
-  return C::ROT ? (c & ~15) + ((c + r) & 15) : c;
+  if (!C::ROT) return c;
+  if (c < C::FULL) return (c & ~15) + ((c + r) & 15);
+  if (c < C::FULL + C::TAIL8) return C::FULL + ((c - C::FULL + r) & 7);
+  return c;
 }
 template <class C>
 __device__ __forceinline__ int stage_chunk(int q, int r) {
-  return C::ROT ? (q & ~15) + ((q - r) & 15) : q;
+  if (!C::ROT) return q;
+  if (q < C::FULL) return (q & ~15) + ((q - r) & 15);
+  if (q < C::FULL + C::TAIL8) return C::FULL + ((q - C::FULL - r) & 7);
+  return q;
 }
 
 template <class C>
@@ -263,7 +276,8 @@ __device__ __forceinline__ void role_main(const KParams& p, Smem<C>& sm, float k
   // per-lane LDS offsets within a stage. Score wave: the rms of rows 4lg + i (+16tb); K row ln16
   // (+16tb): bf16 rows at byte 32lg of each 64-column pair, fp8 rows chunk 2lg + h of each block of
   // parity e. Value wave: transposed V reads of its 16-column blocks
-  uint32_t coff[4] = {0u, 0u, 0u, 0u}, koff[2][2] = {{0u, 0u}, {0u, 0u}}, voff[QS ? 1 : C::CB];
+  uint32_t coff[4] = {0u, 0u, 0u, 0u}, koff[2][2] = {{0u, 0u}, {0u, 0u}}, kofft[2] = {0u, 0u};
+  uint32_t voff[QS ? 1 : C::CB];
   if constexpr (QS) {
     const int rb = p.rms_off_b + C::RMS_EB * hd;
 #pragma unroll
@@ -277,6 +291,9 @@ __device__ __forceinline__ void role_main(const KParams& p, Smem<C>& sm, float k
       for (int h = 0; h < 2; ++h)
         koff[e][h] = F8 ? (uint32_t)(ln16 * C::RB + 16 * stage_pos<C>(8 * e + 2 * lg + h, ln16))
                         : (uint32_t)(ln16 * C::RB + 32 * lg + 16 * h);
+#pragma unroll
+    for (int h = 0; h < 2; ++h)   // the block in the rotated 128-byte tail
+      kofft[h] = (uint32_t)(ln16 * C::RB + 16 * stage_pos<C>(C::FULL + 2 * lg + h, ln16));
   } else {
     const int vr = F8 ? 8 * lg + (ln16 >> 1) : 8 * lg + (ln16 >> 2);
 #pragma unroll
@@ -395,7 +412,7 @@ __device__ __forceinline__ void role_main(const KParams& p, Smem<C>& sm, float k
 #pragma unroll
         for (int j = 0; j < ND; ++j) {
           const int i = vw + C::NIW * j;
-          if (i < C::NI && (i * 64 + 64 <= C::NCH || i * 64 + lane < C::NCH)) dma16_buf(rs, goff[j], dst + i * 1024);
+          if (i < C::NI && (i * 64 + 64 <= C::NCH || i * 64 + lane < C::NCH)) dma16_buf<C::CP>(rs, goff[j], dst + i * 1024);
         }
       } else {
         // per-lane page lookup; rows past the piece end repeat its last row
@@ -409,7 +426,8 @@ __device__ __forceinline__ void role_main(const KParams& p, Smem<C>& sm, float k
             int pg = ldsr32(&sm.pid[i_pf + q - i_ta / P]);
             lds_wait_n<0>(pg);
             const uint32_t cbo = goff[j] - (uint32_t)(drow[j] * tsb);
-            dma16(p.kv + (int64_t)pg * p.page_stride_b + (int64_t)(tok - q * P) * tsb + cbo, dst + i * 1024);
+            dma16<C::CP>(p.kv + (int64_t)pg * p.page_stride_b + (int64_t)(tok - q * P) * tsb + cbo,
+                         dst + i * 1024);
           }
         }
       }
@@ -516,14 +534,22 @@ __device__ __forceinline__ void role_main(const KParams& p, Smem<C>& sm, float k
           } else {
             // block b of K row 16tb + ln16: chunks 2lg, 2lg + 1 of its 256-byte region's half b & 1,
             // read KW blocks ahead of the products (both token blocks, hi and lo chains each)
-            const uint32_t ka[2][2] = {{sb + koff[0][0], sb + koff[0][1]}, {sb + koff[1][0], sb + koff[1][1]}};
             i32x4 kr[C::NBT][2][2];
             auto rd = [&](auto bc) {
               constexpr int b = decltype(bc)::value;
-              kr[b][0][0] = ldsr128_at<256 * (b >> 1)>(ka[b & 1][0]);
-              kr[b][0][1] = ldsr128_at<256 * (b >> 1)>(ka[b & 1][1]);
-              kr[b][1][0] = ldsr128_at<16 * C::RB + 256 * (b >> 1)>(ka[b & 1][0]);
-              kr[b][1][1] = ldsr128_at<16 * C::RB + 256 * (b >> 1)>(ka[b & 1][1]);
+              if constexpr (8 * b < C::FULL) {
+                const uint32_t a0 = sb + koff[b & 1][0], a1 = sb + koff[b & 1][1];
+                kr[b][0][0] = ldsr128_at<256 * (b >> 1)>(a0);
+                kr[b][0][1] = ldsr128_at<256 * (b >> 1)>(a1);
+                kr[b][1][0] = ldsr128_at<16 * C::RB + 256 * (b >> 1)>(a0);
+                kr[b][1][1] = ldsr128_at<16 * C::RB + 256 * (b >> 1)>(a1);
+              } else {
+                const uint32_t a0 = sb + kofft[0], a1 = sb + kofft[1];
+                kr[b][0][0] = ldsr128_at<0>(a0);
+                kr[b][0][1] = ldsr128_at<0>(a1);
+                kr[b][1][0] = ldsr128_at<16 * C::RB>(a0);
+                kr[b][1][1] = ldsr128_at<16 * C::RB>(a1);
+              }
             };
             static_for<0, (C::KW < C::NBT ? C::KW : C::NBT)>(rd);
             f32x4 s0h = f32x4{0.f, 0.f, 0.f, 0.f}, s0l = s0h, s1h = s0h, s1l = s0h;
@@ -757,14 +783,17 @@ __global__ __launch_bounds__(C::NTHR, 1) void wsb_kernel(const KParams p) {
 
 struct Inst {
   int eb, rms, dc, rw, cpr;
-  bool cap;
+  bool cap, shared;   // shared: default cache policy, for launches whose ranges have several workgroups
   int nthr;
   void (*fn)(const KParams);
 };
 
 #define QMLA_WSB(EB, RMS, DC, RW, WIN, CPR, A, CAP)                                                        \
-  {EB, RMS, DC, RW, CPR, CAP, WB<EB, RMS, DC, RW, WIN, CPR, A, CAP>::NTHR,                              \
+  {EB, RMS, DC, RW, CPR, CAP, false, WB<EB, RMS, DC, RW, WIN, CPR, A, CAP>::NTHR,                       \
    &wsb_kernel<WB<EB, RMS, DC, RW, WIN, CPR, A, CAP>>}
+#define QMLA_WSB_SHARED(EB, RMS, DC, RW, WIN, CPR, A, CAP)                                                 \
+  {EB, RMS, DC, RW, CPR, CAP, true, WB<EB, RMS, DC, RW, WIN, CPR, A, CAP, kCpolDefault>::NTHR,          \
+   &wsb_kernel<WB<EB, RMS, DC, RW, WIN, CPR, A, CAP, kCpolDefault>>}
 
 static const Inst kInst[] = {
     // bf16 rows [latent 512 | rope 64 | 24 bf16 rms]: 1200 bytes staged, 2 tiles ahead (4 stages)
@@ -776,8 +805,22 @@ static const Inst kInst[] = {
     // 2 tiles ahead (4 stages, 128 KB); rank 256: 512 bytes, 4 ahead
     QMLA_WSB(1, QMLA_RMS_LOG8, 768, 232, 256, 64, 2, false),
     QMLA_WSB(1, QMLA_RMS_E4M3, 768, 232, 256, 64, 2, false),
+    QMLA_WSB(1, QMLA_RMS_BF16_BYTES, 768, 232, 256, 66, 2, false),
     QMLA_WSB(1, QMLA_RMS_LOG8, 256, 232, 256, 32, 4, false),
     QMLA_WSB(1, QMLA_RMS_E4M3, 256, 232, 256, 32, 4, false),
+    QMLA_WSB(1, QMLA_RMS_BF16_BYTES, 256, 232, 256, 34, 4, false),
+    // ... at TP 2 (12 heads): rope 116 in a 128-column window; rank 768 [latent | rope | 12 codes] =
+    // 896 bytes, rank 256 384 bytes
+    QMLA_WSB(1, QMLA_RMS_LOG8, 768, 116, 128, 56, 2, false),
+    QMLA_WSB(1, QMLA_RMS_E4M3, 768, 116, 128, 56, 2, false),
+    QMLA_WSB(1, QMLA_RMS_BF16_BYTES, 768, 116, 128, 57, 2, false),
+    QMLA_WSB(1, QMLA_RMS_LOG8, 256, 116, 128, 24, 4, false),
+    QMLA_WSB(1, QMLA_RMS_E4M3, 256, 116, 128, 24, 4, false),
+    QMLA_WSB(1, QMLA_RMS_BF16_BYTES, 256, 116, 128, 25, 4, false),
+    // verify rows (a request's heads over several workgroups reading the same token range): the
+    // default cache policy keeps the rows in L2 for the range's other workgroups
+    QMLA_WSB_SHARED(2, QMLA_RMS_BF16, 512, 64, 64, 75, 2, false),
+    QMLA_WSB_SHARED(1, QMLA_RMS_LOG8, 768, 232, 256, 64, 2, false),
 };
 
 }  // namespace wsb
@@ -789,6 +832,8 @@ int wsb_select(const qmla_decode_params* p) {
   const int eb = p->kv_dtype == QMLA_KV_FP8 ? 1 : 2;
   const bool cap = p->logit_cap > 0.f;
   const int64_t ts = p->token_stride * eb;
+  const bool shared = ws_head_split(p) > 1;
+  int pick = -1;
   for (int i = 0; i < (int)(sizeof(wsb::kInst) / sizeof(wsb::kInst[0])); ++i) {
     const wsb::Inst& in = wsb::kInst[i];
     if (in.eb != eb || in.rms != p->rms_mode || in.dc != p->d_c || in.rw != p->rope_w || in.cap != cap) continue;
@@ -799,9 +844,10 @@ int wsb_select(const qmla_decode_params* p) {
       if (roff + (int64_t)p->heads * rb > in.cpr * 16) continue;   // every head's rms is staged
       if (roff < (int64_t)(in.dc + in.rw) * eb) continue;          // the rms follows the rope
     }
-    return i;
+    if (in.shared == shared) return i;   // the policy that fits the launch, else any
+    if (pick < 0) pick = i;
   }
-  return -1;
+  return pick;
 }
 
 int wsb_launch(int inst, const qmla_decode_params* p, const KParams& k, int nwg, hipStream_t st) {
