@@ -302,8 +302,8 @@ int ws_launch(int inst, const qmla_decode_params* p, const KParams& k, int nwg, 
 int ro_select(const qmla_decode_params* p);
 int ro_launch(int inst, const qmla_decode_params* p, const KParams& k, int nwg, hipStream_t st);
 
-// ---- host-side interface of the bf16 warp-specialized translation unit (qmla_wsb.hip) ----
-// Index of a compiled instance for these params (bf16 rows, d_c 512, rope 64), or -1.
+// ---- host-side interface of the wide-row warp-specialized translation unit (qmla_wsb.hip) ----
+// Index of a compiled instance for these params (bf16 rows, the deployed fp8 rows), or -1.
 int wsb_select(const qmla_decode_params* p);
 int wsb_launch(int inst, const qmla_decode_params* p, const KParams& k, int nwg, hipStream_t st);
 
