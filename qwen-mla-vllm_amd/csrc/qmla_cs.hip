@@ -30,6 +30,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <type_traits>
+
 #include "qmla.h"
 #include "qmla_common.h"
 #include "qmla_device.h"
@@ -110,6 +112,11 @@ struct CS {
   static constexpr int NRI = CRM > 0 ? (T * CRM + 63) / 64 : 0;   // rms DMA instructions per tile
   static constexpr int ROWS = 16 * MB;
   static constexpr int XBW = NTB * MB;                   // partial-score f32x4 per lane
+  // reduce-scatter of the partial scores (bf16 rows, 16-token tiles, 32 rows over 8 slices): wave c
+  // sums and softmaxes rows 4c .. 4c+3 only, one score per lane, and P reaches the other waves
+  // through LDS; otherwise every wave sums all partials and repeats the whole softmax
+  static constexpr bool RSC = EB == 2 && G == 1 && NCG == 8 && NTG == 1 && NTB == 1 && MB == 2;
+  static constexpr int RPS = 40;                         // P row stride (bytes) of the reduce-scatter
   static_assert(DCG % (32 * NCG) == 0, "whole 32-column k-steps per wave");
   static_assert(NTB == 1 || NTB == 2, "score tiles per token group");
   static_assert(EB == 2 || NTB == 2, "fp8 values are read 8 tokens at a time");
@@ -119,12 +126,24 @@ struct CS {
   static_assert(!RTR || CRM * 16 >= RB * ROWS, "transposed rms reads cover all row heads");
 };
 
+// reduce-scatter: P of the tile's 32 rows (bf16), the rows' rescale factors, per reducer wave
+// whether its rows' reference moved, the rows' final max and sum
+template <int RPS>
+struct RsShared {
+  alignas(16) char rp[32 * RPS];
+  alignas(16) float ra[32];
+  alignas(16) int rf[8];
+  alignas(16) float rfin[2][32];
+};
+struct RsNone {};
+
 template <class C>
 struct Smem {
   char ring[C::S][C::NW][C::SB];
   char rms[C::S + 1][C::NTG][C::T * C::RRS];   // S+1 deep: read after the exchange
   f32x4 xb[C::NW][C::XBW][64];                 // partial scores
   int pid[PIDN];
+  [[no_unique_address]] std::conditional_t<C::RSC, RsShared<C::RPS>, RsNone> rs;
 };
 
 
@@ -241,6 +260,20 @@ __device__ __forceinline__ void segment(const KParams& p, Smem<C>& sm, int req, 
   }
   // smallest row limit: tiles below it need no masking
   const int limmin = L - (p.qrows - 1) < te ? L - (p.qrows - 1) : te;
+  // reduce-scatter: this wave's reducer row rrow = 4c + lane/16 (token lane % 16 of each tile), its
+  // limit and rms byte offset, and the row's softmax state (the same in its 16 lanes; the sum is per
+  // lane)
+  const int rl = lane >> 4, tt = lane & 15, rrow = 4 * c + rl;
+  int rlim = 0, rhb = 0;
+  float rmref = kNegInf, rmthr = kNegInf, rlp = 0.f;
+  if constexpr (C::RSC) {
+    const int r = rbase + rrow;
+    const bool ok = r < rows_pg;
+    const int jq = ok ? r / hpg : 0, hh = ok ? r - jq * hpg : 0;
+    const int lr = L - (p.qrows - 1 - jq);
+    rlim = ok ? (lr < te ? lr : te) : 0;
+    rhb = (ok ? (g * hpg + hh) * C::RB : 0) + rdelta;
+  }
 
   // ---- DMA source of chunk i of the wave's tile slice: row i / CPW, chunk i % CPW of
   //      [latent slice | rope slice | pad]; recomputed at every issue rather than held ----
@@ -420,197 +453,290 @@ __device__ __forceinline__ void segment(const KParams& p, Smem<C>& sm, int req, 
         }
       }
 
-      // ---- sum the NCG partials of (g, tg) in slice order ----
-#pragma unroll
-      for (int tb = 0; tb < C::NTB; ++tb)
-#pragma unroll
-        for (int mb = 0; mb < C::MB; ++mb) sm.xb[w][tb * C::MB + mb][lane] = sp[tb][mb];
-      lds_barrier();
-      f32x4 s[C::NTB][C::MB];
-      {
-        const int w0 = w - c;   // slice 0 of this (g, tg)
-#pragma unroll
-        for (int x = 0; x < C::XBW; ++x) {
-          f32x4 a;
-#pragma unroll
-          for (int v0 = 0; v0 < C::NCG; v0 += 4) {
-            i32x4 xr[4];
-#pragma unroll
-            for (int j = 0; j < 4; ++j)
-              if (v0 + j < C::NCG) xr[j] = ldsr128(reinterpret_cast<const char*>(&sm.xb[w0 + v0 + j][x][lane]));
-#pragma unroll
-            for (int j = 0; j < 4; ++j)
-              if (v0 + j < C::NCG) {
-                lds_wait(xr[j]);
-                const f32x4 y = __builtin_bit_cast(f32x4, xr[j]);
-                a = (v0 + j == 0) ? y : a + y;
-              }
-          }
-          s[x / C::MB][x % C::MB] = a;
-        }
-      }
-      lds_barrier();   // the partial-score buffer is free again
-
-      // ---- this tile's rms divisors. The rms ring is S+1 deep: the loader refills a stage for
-      //      tile t+S only after the first barrier of tile t, by which time every wave has read the
-      //      stages of tiles before t; tile t's own stage is not touched ----
-      float rinv[C::NTB][C::MB][4];
-      if constexpr (C::RMS == QMLA_RMS_NONE) {
-#pragma unroll
-        for (int tb = 0; tb < C::NTB; ++tb)
-#pragma unroll
-          for (int mb = 0; mb < C::MB; ++mb)
-#pragma unroll
-            for (int e = 0; e < 4; ++e) rinv[tb][mb][e] = 1.0f;
-      } else {
-        const char* rs = sm.rms[t % (C::S + 1)][tg];
-        uint32_t code[C::NTB][C::MB][4];
-        if constexpr (C::RTR && C::RB == 1) {
-          // one tr_b8 read per 16 rows: lane (n, q) gets head rbase+16mb+n of the 8 tokens vtok(q, 0..7)
-          i32x2 raw[C::MB];
-          const int rr = vtok(lg, ln16 >> 1);
-#pragma unroll
-          for (int mb = 0; mb < C::MB; ++mb) raw[mb] = lds_read_tr8_async(rs + rr * C::RRS + rbase + 16 * mb + 8 * (ln16 & 1));
-#pragma unroll
-          for (int mb = 0; mb < C::MB; ++mb) {
-            lds_wait(raw[mb]);
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-              code[0][mb][e] = ((uint32_t)raw[mb][0] >> (8 * e)) & 0xFF;
-              if constexpr (C::NTB == 2) code[1][mb][e] = ((uint32_t)raw[mb][1] >> (8 * e)) & 0xFF;
-            }
-          }
-        } else if constexpr (C::RTR && C::RB == 2) {
-          // tr_b16: lanes 4r..4r+3 of a 16-lane block supply token row r; lane n gets head rbase+16mb+n
-#pragma unroll
-          for (int tb = 0; tb < C::NTB; ++tb) {
-            i32x2 raw[C::MB];
-            const int rr = tok_of(tb, 4 * lg + (ln16 >> 2));
-#pragma unroll
-            for (int mb = 0; mb < C::MB; ++mb)
-              raw[mb] = lds_read_tr16_async(rs + rr * C::RRS + 2 * rbase + 32 * mb + 8 * (ln16 & 3));
-#pragma unroll
-            for (int mb = 0; mb < C::MB; ++mb) {
-              lds_wait(raw[mb]);
-              code[tb][mb][0] = (uint32_t)raw[mb][0] & 0xFFFF;
-              code[tb][mb][1] = (uint32_t)raw[mb][0] >> 16;
-              code[tb][mb][2] = (uint32_t)raw[mb][1] & 0xFFFF;
-              code[tb][mb][3] = (uint32_t)raw[mb][1] >> 16;
-            }
-          }
-        } else {
-          // general rows (verify tokens, latent groups): one read per score
-#pragma unroll
-          for (int tb = 0; tb < C::NTB; ++tb)
-#pragma unroll
-            for (int mb = 0; mb < C::MB; ++mb)
-#pragma unroll
-              for (int e = 0; e < 4; ++e) {
-                const char* a = rs + tok_of(tb, 4 * lg + e) * C::RRS + hb[mb];
-                code[tb][mb][e] = C::RB == 1 ? ldsr8(a) : ldsr16(a);
-              }
-#pragma unroll
-          for (int tb = 0; tb < C::NTB; ++tb)
-#pragma unroll
-            for (int mb = 0; mb < C::MB; ++mb)
-#pragma unroll
-              for (int e = 0; e < 4; ++e) lds_wait(code[tb][mb][e]);
-        }
-#pragma unroll
-        for (int tb = 0; tb < C::NTB; ++tb)
-#pragma unroll
-          for (int mb = 0; mb < C::MB; ++mb)
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-              const uint32_t cd = code[tb][mb][e];
-              float ri;
-              if constexpr (C::RMS == QMLA_RMS_LOG8) {
-                // 1 / 2^(-3 + c*6/255) = 2^(3 - c*6/255)  (ops/mla_decode_attention.py:470-479)
-                ri = fast_exp2(fmaf((float)cd, -6.0f / 255.0f, 3.0f));
-              } else if constexpr (C::RMS == QMLA_RMS_E4M3) {
-                const float rv = fp8_to_f32(cd) * kscale;
-                ri = rv > 0.f ? __builtin_amdgcn_rcpf(rv) : 1.0f;
-              } else {
-                const float rv = bf16_bits_to_f32(cd);
-                ri = rv > 0.f ? __builtin_amdgcn_rcpf(rv) : 1.0f;
-              }
-              rinv[tb][mb][e] = ri;
-            }
-      }
-
-      // ---- scale to log2 units, cap, mask; tile max per row ----
-      const bool full = tok0 + C::T <= limmin;
-      float tmax[C::MB];
-#pragma unroll
-      for (int mb = 0; mb < C::MB; ++mb) {
-        float m = kNegInf;
-#pragma unroll
-        for (int tb = 0; tb < C::NTB; ++tb)
-#pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            float v = s[tb][mb][e] * rinv[tb][mb][e] * csc;
-            if constexpr (C::CAP) {
-              // cap * tanh(x / cap) in log2 units: tanh(y) = 1 - 2 / (exp(2y) + 1)
-              const float y = v / cap2;
-              const float e2 = fast_exp2(2.0f * kLog2e * y);
-              v = cap2 * (1.0f - 2.0f / (e2 + 1.0f));
-            }
-            if (!full && tok0 + tok_of(tb, 4 * lg + e) >= lim[mb]) v = kNegInf;
-            s[tb][mb][e] = v;
-            m = fmaxf(m, v);
-          }
-        tmax[mb] = max_lg(m);
-      }
-      // reference max: it moves when a tile max exceeds it by more than ref_shift(the row's running
-      // sum), so a dominant token gets P = 1 exactly as under the reference's running max
-      // (ops/mla_decode_attention.py:553-560) and rounding P to bf16 before P.V costs no more
-      // than it does there; P <= 2^8
-      bool cand = false;
-#pragma unroll
-      for (int mb = 0; mb < C::MB; ++mb) cand |= tmax[mb] > mthr[mb];
-      if (__builtin_amdgcn_ballot_w64(cand)) {
-        bool need = false;
-#pragma unroll
-        for (int mb = 0; mb < C::MB; ++mb) {
-          mthr[mb] = mref[mb] + ref_shift(sum_lg(lpart[mb]), 8.0f);
-          need |= tmax[mb] > mthr[mb];
-        }
-        if (__builtin_amdgcn_ballot_w64(need)) {
-#pragma unroll
-          for (int mb = 0; mb < C::MB; ++mb) {
-            const bool mv = tmax[mb] > mthr[mb];
-            const float mn = mv ? tmax[mb] : mref[mb];
-            const float alpha = mref[mb] == kNegInf ? 0.f : fast_exp2(mref[mb] - mn);
-            lpart[mb] *= alpha;
-            mref[mb] = mn;
-            if (mv) mthr[mb] = mn;   // re-evaluated at the next tile max above the new reference
-            // accumulator rows 4*lg + i live in lanes 4*lg + i of the score layout
-            float al[4];
-#pragma unroll
-            for (int i = 0; i < 4; ++i) al[i] = __shfl(alpha, 4 * lg + i);
-#pragma unroll
-            for (int cb = 0; cb < C::CB; ++cb)
-#pragma unroll
-              for (int i = 0; i < 4; ++i) acc[mb][cb][i] *= al[i];
-          }
-        }
-      }
-
-      // ---- P (bf16) in the A layout of P.V, row sums ----
       bf16x8 pa8[C::MB];
       s16x4 pa4[C::MB];
+      if constexpr (C::RSC) {
+        // ---- reduce-scatter: each wave writes its partial scores as a [32 rows][16 tokens] fp32
+        //      tile; wave c sums the 8 slices' partials of rows 4c .. 4c+3 (one score per lane) ----
+        float* xs = reinterpret_cast<float*>(&sm.xb[0][0][0]);
 #pragma unroll
-      for (int mb = 0; mb < C::MB; ++mb) {
-        const float mu = mref[mb] == kNegInf ? 0.f : mref[mb];
+        for (int mb = 0; mb < C::MB; ++mb)
+          *reinterpret_cast<f32x4*>(xs + (w * 32 + 16 * mb + ln16) * 16 + 4 * lg) = sp[0][mb];
+        lds_barrier();
+        int xr[C::NCG];
 #pragma unroll
-        for (int tb = 0; tb < C::NTB; ++tb)
+        for (int v = 0; v < C::NCG; ++v)
+          xr[v] = ldsr32(reinterpret_cast<const char*>(xs + (v * 32 + rrow) * 16 + tt));
 #pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            const float pv = fast_exp2(s[tb][mb][e] - mu);
-            lpart[mb] += pv;
-            if constexpr (C::NTB == 2) pa8[mb][4 * tb + e] = (__bf16)pv;
-            else pa4[mb][e] = __builtin_bit_cast(short, (__bf16)pv);
+        for (int v = 0; v < C::NCG; ++v) lds_wait(xr[v]);
+        float sv = __int_as_float(xr[0]);
+#pragma unroll
+        for (int v = 1; v < C::NCG; ++v) sv += __int_as_float(xr[v]);
+        // rms divisor of (token tt, the row's head)
+        float ri = 1.0f;
+        if constexpr (C::RMS != QMLA_RMS_NONE) {
+          const char* rsb = sm.rms[t % (C::S + 1)][tg] + tt * C::RRS + rhb;
+          uint32_t cd = C::RB == 1 ? ldsr8(rsb) : ldsr16(rsb);
+          lds_wait(cd);
+          if constexpr (C::RMS == QMLA_RMS_LOG8) {
+            ri = fast_exp2(fmaf((float)cd, -6.0f / 255.0f, 3.0f));
+          } else if constexpr (C::RMS == QMLA_RMS_E4M3) {
+            const float rv = fp8_to_f32(cd) * kscale;
+            ri = rv > 0.f ? __builtin_amdgcn_rcpf(rv) : 1.0f;
+          } else {
+            const float rv = bf16_bits_to_f32(cd);
+            ri = rv > 0.f ? __builtin_amdgcn_rcpf(rv) : 1.0f;
           }
+        }
+        float v = sv * ri * csc;
+        if constexpr (C::CAP) {
+          const float y = v / cap2;
+          const float e2 = fast_exp2(2.0f * kLog2e * y);
+          v = cap2 * (1.0f - 2.0f / (e2 + 1.0f));
+        }
+        if (tok0 + C::T > limmin && tok0 + tt >= rlim) v = kNegInf;
+        const float tm = max16(v);
+        // the row's reference moves as in the other layout (ref_shift of the row's sum, P <= 2^8)
+        bool moved = false;
+        float alpha = 1.0f;
+        if (__builtin_amdgcn_ballot_w64(tm > rmthr)) {
+          rmthr = rmref + ref_shift(sum16(rlp), 8.0f);
+          const bool mv = tm > rmthr;
+          if (__builtin_amdgcn_ballot_w64(mv)) {
+            const float mn = mv ? tm : rmref;
+            alpha = rmref == kNegInf ? 0.f : fast_exp2(rmref - mn);
+            rlp *= alpha;
+            rmref = mn;
+            if (mv) rmthr = mn;
+            moved = true;
+          }
+        }
+        if (moved && tt == 0) sm.rs.ra[rrow] = alpha;
+        if (lane == 0) sm.rs.rf[c] = moved ? 1 : 0;
+        const float pv = fast_exp2(v - (rmref == kNegInf ? 0.f : rmref));
+        rlp += pv;
+        *reinterpret_cast<__bf16*>(sm.rs.rp + rrow * C::RPS + 2 * tt) = (__bf16)pv;
+        lds_barrier();
+        // ---- P of rows 16mb + ln16, tokens 4lg .. 4lg+3 (the A operand); the rows of this lane's
+        //      accumulators (16mb + 4lg + i) belong to reducer wave 4mb + lg: rescale them first if
+        //      its reference moved ----
+        i32x2 pr[C::MB];
+#pragma unroll
+        for (int mb = 0; mb < C::MB; ++mb) pr[mb] = ldsr64(sm.rs.rp + (16 * mb + ln16) * C::RPS + 8 * lg);
+        i32x4 f0 = ldsr128(reinterpret_cast<const char*>(&sm.rs.rf[0])), f1 = ldsr128(reinterpret_cast<const char*>(&sm.rs.rf[4]));
+        lds_wait(f0, f1);
+#pragma unroll
+        for (int mb = 0; mb < C::MB; ++mb) lds_wait(pr[mb]);
+        const int fa = f0[0] | f0[1] | f0[2] | f0[3] | f1[0] | f1[1] | f1[2] | f1[3];
+        if (__builtin_amdgcn_readfirstlane(fa)) {
+#pragma unroll
+          for (int mb = 0; mb < C::MB; ++mb) {
+            const int fl = (mb == 0 ? f0 : f1)[lg];
+            i32x4 ar = ldsr128(reinterpret_cast<const char*>(&sm.rs.ra[16 * mb + 4 * lg]));
+            lds_wait(ar);
+            const f32x4 al = __builtin_bit_cast(f32x4, ar);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+              const float a_i = fl ? al[i] : 1.0f;
+#pragma unroll
+              for (int cb = 0; cb < C::CB; ++cb) acc[mb][cb][i] *= a_i;
+            }
+          }
+        }
+#pragma unroll
+        for (int mb = 0; mb < C::MB; ++mb) pa4[mb] = __builtin_bit_cast(s16x4, pr[mb]);
+      } else {
+        // ---- sum the NCG partials of (g, tg) in slice order ----
+  #pragma unroll
+        for (int tb = 0; tb < C::NTB; ++tb)
+  #pragma unroll
+          for (int mb = 0; mb < C::MB; ++mb) sm.xb[w][tb * C::MB + mb][lane] = sp[tb][mb];
+        lds_barrier();
+        f32x4 s[C::NTB][C::MB];
+        {
+          const int w0 = w - c;   // slice 0 of this (g, tg)
+  #pragma unroll
+          for (int x = 0; x < C::XBW; ++x) {
+            f32x4 a;
+  #pragma unroll
+            for (int v0 = 0; v0 < C::NCG; v0 += 4) {
+              i32x4 xr[4];
+  #pragma unroll
+              for (int j = 0; j < 4; ++j)
+                if (v0 + j < C::NCG) xr[j] = ldsr128(reinterpret_cast<const char*>(&sm.xb[w0 + v0 + j][x][lane]));
+  #pragma unroll
+              for (int j = 0; j < 4; ++j)
+                if (v0 + j < C::NCG) {
+                  lds_wait(xr[j]);
+                  const f32x4 y = __builtin_bit_cast(f32x4, xr[j]);
+                  a = (v0 + j == 0) ? y : a + y;
+                }
+            }
+            s[x / C::MB][x % C::MB] = a;
+          }
+        }
+        lds_barrier();   // the partial-score buffer is free again
+
+        // ---- this tile's rms divisors. The rms ring is S+1 deep: the loader refills a stage for
+        //      tile t+S only after the first barrier of tile t, by which time every wave has read the
+        //      stages of tiles before t; tile t's own stage is not touched ----
+        float rinv[C::NTB][C::MB][4];
+        if constexpr (C::RMS == QMLA_RMS_NONE) {
+  #pragma unroll
+          for (int tb = 0; tb < C::NTB; ++tb)
+  #pragma unroll
+            for (int mb = 0; mb < C::MB; ++mb)
+  #pragma unroll
+              for (int e = 0; e < 4; ++e) rinv[tb][mb][e] = 1.0f;
+        } else {
+          const char* rs = sm.rms[t % (C::S + 1)][tg];
+          uint32_t code[C::NTB][C::MB][4];
+          if constexpr (C::RTR && C::RB == 1) {
+            // one tr_b8 read per 16 rows: lane (n, q) gets head rbase+16mb+n of the 8 tokens vtok(q, 0..7)
+            i32x2 raw[C::MB];
+            const int rr = vtok(lg, ln16 >> 1);
+  #pragma unroll
+            for (int mb = 0; mb < C::MB; ++mb) raw[mb] = lds_read_tr8_async(rs + rr * C::RRS + rbase + 16 * mb + 8 * (ln16 & 1));
+  #pragma unroll
+            for (int mb = 0; mb < C::MB; ++mb) {
+              lds_wait(raw[mb]);
+  #pragma unroll
+              for (int e = 0; e < 4; ++e) {
+                code[0][mb][e] = ((uint32_t)raw[mb][0] >> (8 * e)) & 0xFF;
+                if constexpr (C::NTB == 2) code[1][mb][e] = ((uint32_t)raw[mb][1] >> (8 * e)) & 0xFF;
+              }
+            }
+          } else if constexpr (C::RTR && C::RB == 2) {
+            // tr_b16: lanes 4r..4r+3 of a 16-lane block supply token row r; lane n gets head rbase+16mb+n
+  #pragma unroll
+            for (int tb = 0; tb < C::NTB; ++tb) {
+              i32x2 raw[C::MB];
+              const int rr = tok_of(tb, 4 * lg + (ln16 >> 2));
+  #pragma unroll
+              for (int mb = 0; mb < C::MB; ++mb)
+                raw[mb] = lds_read_tr16_async(rs + rr * C::RRS + 2 * rbase + 32 * mb + 8 * (ln16 & 3));
+  #pragma unroll
+              for (int mb = 0; mb < C::MB; ++mb) {
+                lds_wait(raw[mb]);
+                code[tb][mb][0] = (uint32_t)raw[mb][0] & 0xFFFF;
+                code[tb][mb][1] = (uint32_t)raw[mb][0] >> 16;
+                code[tb][mb][2] = (uint32_t)raw[mb][1] & 0xFFFF;
+                code[tb][mb][3] = (uint32_t)raw[mb][1] >> 16;
+              }
+            }
+          } else {
+            // general rows (verify tokens, latent groups): one read per score
+  #pragma unroll
+            for (int tb = 0; tb < C::NTB; ++tb)
+  #pragma unroll
+              for (int mb = 0; mb < C::MB; ++mb)
+  #pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                  const char* a = rs + tok_of(tb, 4 * lg + e) * C::RRS + hb[mb];
+                  code[tb][mb][e] = C::RB == 1 ? ldsr8(a) : ldsr16(a);
+                }
+  #pragma unroll
+            for (int tb = 0; tb < C::NTB; ++tb)
+  #pragma unroll
+              for (int mb = 0; mb < C::MB; ++mb)
+  #pragma unroll
+                for (int e = 0; e < 4; ++e) lds_wait(code[tb][mb][e]);
+          }
+  #pragma unroll
+          for (int tb = 0; tb < C::NTB; ++tb)
+  #pragma unroll
+            for (int mb = 0; mb < C::MB; ++mb)
+  #pragma unroll
+              for (int e = 0; e < 4; ++e) {
+                const uint32_t cd = code[tb][mb][e];
+                float ri;
+                if constexpr (C::RMS == QMLA_RMS_LOG8) {
+                  // 1 / 2^(-3 + c*6/255) = 2^(3 - c*6/255)  (ops/mla_decode_attention.py:470-479)
+                  ri = fast_exp2(fmaf((float)cd, -6.0f / 255.0f, 3.0f));
+                } else if constexpr (C::RMS == QMLA_RMS_E4M3) {
+                  const float rv = fp8_to_f32(cd) * kscale;
+                  ri = rv > 0.f ? __builtin_amdgcn_rcpf(rv) : 1.0f;
+                } else {
+                  const float rv = bf16_bits_to_f32(cd);
+                  ri = rv > 0.f ? __builtin_amdgcn_rcpf(rv) : 1.0f;
+                }
+                rinv[tb][mb][e] = ri;
+              }
+        }
+
+        // ---- scale to log2 units, cap, mask; tile max per row ----
+        const bool full = tok0 + C::T <= limmin;
+        float tmax[C::MB];
+  #pragma unroll
+        for (int mb = 0; mb < C::MB; ++mb) {
+          float m = kNegInf;
+  #pragma unroll
+          for (int tb = 0; tb < C::NTB; ++tb)
+  #pragma unroll
+            for (int e = 0; e < 4; ++e) {
+              float v = s[tb][mb][e] * rinv[tb][mb][e] * csc;
+              if constexpr (C::CAP) {
+                // cap * tanh(x / cap) in log2 units: tanh(y) = 1 - 2 / (exp(2y) + 1)
+                const float y = v / cap2;
+                const float e2 = fast_exp2(2.0f * kLog2e * y);
+                v = cap2 * (1.0f - 2.0f / (e2 + 1.0f));
+              }
+              if (!full && tok0 + tok_of(tb, 4 * lg + e) >= lim[mb]) v = kNegInf;
+              s[tb][mb][e] = v;
+              m = fmaxf(m, v);
+            }
+          tmax[mb] = max_lg(m);
+        }
+        // reference max: it moves when a tile max exceeds it by more than ref_shift(the row's running
+        // sum), so a dominant token gets P = 1 exactly as under the reference's running max
+        // (ops/mla_decode_attention.py:553-560) and rounding P to bf16 before P.V costs no more
+        // than it does there; P <= 2^8
+        bool cand = false;
+  #pragma unroll
+        for (int mb = 0; mb < C::MB; ++mb) cand |= tmax[mb] > mthr[mb];
+        if (__builtin_amdgcn_ballot_w64(cand)) {
+          bool need = false;
+  #pragma unroll
+          for (int mb = 0; mb < C::MB; ++mb) {
+            mthr[mb] = mref[mb] + ref_shift(sum_lg(lpart[mb]), 8.0f);
+            need |= tmax[mb] > mthr[mb];
+          }
+          if (__builtin_amdgcn_ballot_w64(need)) {
+  #pragma unroll
+            for (int mb = 0; mb < C::MB; ++mb) {
+              const bool mv = tmax[mb] > mthr[mb];
+              const float mn = mv ? tmax[mb] : mref[mb];
+              const float alpha = mref[mb] == kNegInf ? 0.f : fast_exp2(mref[mb] - mn);
+              lpart[mb] *= alpha;
+              mref[mb] = mn;
+              if (mv) mthr[mb] = mn;   // re-evaluated at the next tile max above the new reference
+              // accumulator rows 4*lg + i live in lanes 4*lg + i of the score layout
+              float al[4];
+  #pragma unroll
+              for (int i = 0; i < 4; ++i) al[i] = __shfl(alpha, 4 * lg + i);
+  #pragma unroll
+              for (int cb = 0; cb < C::CB; ++cb)
+  #pragma unroll
+                for (int i = 0; i < 4; ++i) acc[mb][cb][i] *= al[i];
+            }
+          }
+        }
+
+        // ---- P (bf16) in the A layout of P.V, row sums ----
+  #pragma unroll
+        for (int mb = 0; mb < C::MB; ++mb) {
+          const float mu = mref[mb] == kNegInf ? 0.f : mref[mb];
+  #pragma unroll
+          for (int tb = 0; tb < C::NTB; ++tb)
+  #pragma unroll
+            for (int e = 0; e < 4; ++e) {
+              const float pv = fast_exp2(s[tb][mb][e] - mu);
+              lpart[mb] += pv;
+              if constexpr (C::NTB == 2) pa8[mb][4 * tb + e] = (__bf16)pv;
+              else pa4[mb][e] = __builtin_bit_cast(short, (__bf16)pv);
+            }
+        }
+
       }
 
       // ---- P.V over this wave's columns ----
@@ -691,6 +817,16 @@ __device__ __forceinline__ void segment(const KParams& p, Smem<C>& sm, int req, 
   float lrow[C::MB];
 #pragma unroll
   for (int mb = 0; mb < C::MB; ++mb) lrow[mb] = sum_lg(lpart[mb]);
+  // reduce-scatter: the reducer waves hand every row's max and sum to the waves holding its columns
+  float rls = 0.f;
+  if constexpr (C::RSC) {
+    rls = sum16(rlp);
+    if (tt == 0) {
+      sm.rs.rfin[0][rrow] = rmref;
+      sm.rs.rfin[1][rrow] = rls;
+    }
+    lds_barrier();
+  }
   if constexpr (C::NTG == 2) {
     // token group 1 hands (max, sum, acc) to token group 0 through the (now idle) ring
     lds_barrier();
@@ -740,8 +876,16 @@ __device__ __forceinline__ void segment(const KParams& p, Smem<C>& sm, int req, 
     const float invh = inv_sum(1.0f, l);    // ... and are stored so as fp16 partials
     const bool ph = !so.final_out && so.plse && p.part_h;
     float iv[4];
+    if constexpr (C::RSC) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i) iv[i] = __shfl(ph ? invh : inv, 4 * lg + i);
+      for (int i = 0; i < 4; ++i) {
+        const float l_i = sm.rs.rfin[1][16 * mb + 4 * lg + i];
+        iv[i] = ph ? inv_sum(1.0f, l_i) : inv_sum(kscale, l_i);
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) iv[i] = __shfl(ph ? invh : inv, 4 * lg + i);
+    }
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int r = rbase + 16 * mb + 4 * lg + i;
@@ -774,11 +918,27 @@ __device__ __forceinline__ void segment(const KParams& p, Smem<C>& sm, int req, 
         for (int cb = 0; cb < C::CB; ++cb) ob[16 * cb] = acc[mb][cb][i] * iv[i];
       }
     }
-    // lse from the score layout (row ln16 + 16mb), one lane per row
+    // lse from the score layout (row ln16 + 16mb), one lane per row (reduce-scatter: below)
     const int r = rbase + ln16 + 16 * mb;
-    if (c == 0 && lg == 0 && r < rows_pg) {
+    if (!C::RSC && c == 0 && lg == 0 && r < rows_pg) {
       const int jq = r / hpg, hh = r - jq * hpg;
       const int head = g * hpg + hh;
+      if (so.final_out) {
+        if (p.lse) store_out(p.lse, p.lse_dt, (int64_t)(row0 + jq) * p.lse_sr + head, lse_v);
+      } else if (so.plse) {
+        so.plse[(int64_t)jq * so.plse_sr + head] = lse_v;
+      } else {
+        so.po[(int64_t)jq * so.po_sr + (int64_t)head * so.po_sh + C::DCG] = lse_v;
+      }
+    }
+  }
+  if constexpr (C::RSC) {
+    // the reducer lane of each row writes its lse
+    const int r = rbase + rrow;
+    if (tt == 0 && r < rows_pg) {
+      const int jq = r / hpg, hh = r - jq * hpg;
+      const int head = g * hpg + hh;
+      const float lse_v = row_lse(rmref, rls);
       if (so.final_out) {
         if (p.lse) store_out(p.lse, p.lse_dt, (int64_t)(row0 + jq) * p.lse_sr + head, lse_v);
       } else if (so.plse) {
