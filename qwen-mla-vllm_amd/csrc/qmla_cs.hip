@@ -457,16 +457,19 @@ __device__ __forceinline__ void segment(const KParams& p, Smem<C>& sm, int req, 
       s16x4 pa4[C::MB];
       if constexpr (C::RSC) {
         // ---- reduce-scatter: each wave writes its partial scores as a [32 rows][16 tokens] fp32
-        //      tile; wave c sums the 8 slices' partials of rows 4c .. 4c+3 (one score per lane) ----
+        //      tile (row r's 4-token groups rotated by (r & 15) / 4, so the 16 rows of a write and
+        //      the 64 scores of a read fall on distinct banks); wave c sums the 8 slices' partials
+        //      of rows 4c .. 4c+3 (one score per lane) ----
         float* xs = reinterpret_cast<float*>(&sm.xb[0][0][0]);
 #pragma unroll
         for (int mb = 0; mb < C::MB; ++mb)
-          *reinterpret_cast<f32x4*>(xs + (w * 32 + 16 * mb + ln16) * 16 + 4 * lg) = sp[0][mb];
+          *reinterpret_cast<f32x4*>(xs + (w * 32 + 16 * mb + ln16) * 16 + 4 * ((lg + (ln16 >> 2)) & 3)) = sp[0][mb];
         lds_barrier();
+        const int xpos = 4 * (((tt >> 2) + ((rrow & 15) >> 2)) & 3) + (tt & 3);
         int xr[C::NCG];
 #pragma unroll
         for (int v = 0; v < C::NCG; ++v)
-          xr[v] = ldsr32(reinterpret_cast<const char*>(xs + (v * 32 + rrow) * 16 + tt));
+          xr[v] = ldsr32(reinterpret_cast<const char*>(xs + (v * 32 + rrow) * 16 + xpos));
 #pragma unroll
         for (int v = 0; v < C::NCG; ++v) lds_wait(xr[v]);
         float sv = __int_as_float(xr[0]);
