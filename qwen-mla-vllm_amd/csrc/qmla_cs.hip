@@ -996,9 +996,10 @@ static const Inst kInst[] = {
     QMLA_CS(2, QMLA_RMS_BF16, 768, 1, 8, 1, 1, 1, 4, 2, false, false, 256),   // 12 heads, rope 256
     // bf16 cache, rank 1792 with the plugin's partial-rope and full-rope-256 layouts
     // (tests/test_two_pass_1792.py:12-19 on the rows of tests/test_fi_partial_rope.py:27-31): rope 232
-    // or 256 (window 256) and rope 116 (window 128, rms tail at 8 mod 16 bytes); 16 query rows per
-    // workgroup (32 rows with the 256-column window spill 72 registers), so 24 heads take two
-    // workgroups per token range; two stages of 16 tokens
+    // or 256 (window 256) and rope 116 (window 128, rms tail at 8 mod 16 bytes); two stages of 16
+    // tokens. 24 heads in one workgroup per token range (32 rows: the reduce-scatter leaves the tile
+    // loop free of spills), 12 heads in 16 rows
+    QMLA_CS(2, QMLA_RMS_BF16, 1792, 1, 8, 1, 1, 2, 2, 3, false, false, 256),
     QMLA_CS(2, QMLA_RMS_BF16, 1792, 1, 8, 1, 1, 1, 2, 3, false, false, 256),
     QMLA_CS(2, QMLA_RMS_BF16, 1792, 1, 8, 1, 1, 1, 2, 2, false, false, 256),   // 12 heads: 32-byte tail
     QMLA_CS(2, QMLA_RMS_BF16, 1792, 1, 8, 1, 1, 1, 2, 2, false, false, 128),

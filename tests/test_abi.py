@@ -208,7 +208,8 @@ def test_plan_switch_tiles(kv, rms, qrows, groups, splits, tiles):
     (_lib.KV_FP8, 768, 116, 12, _lib.RMS_LOG8, 4),         # ... rope 116, 12 heads (TP 2)
     (_lib.KV_BF16, 768, 232, 24, _lib.RMS_BF16, 4),        # column-split, 32 rows per workgroup
     (_lib.KV_FP8, 1792, 232, 24, _lib.RMS_LOG8, 2),        # column-split, 16 rows per workgroup:
-    (_lib.KV_BF16, 1792, 232, 24, _lib.RMS_BF16, 2),       # two tokens x 24 heads over 3 workgroups
+                                                           # two tokens x 24 heads over 3 workgroups
+    (_lib.KV_BF16, 1792, 232, 24, _lib.RMS_BF16, 4),       # column-split, 32 rows per workgroup
     (_lib.KV_BF16, 1792, 64, 24, _lib.RMS_BF16, 2),
     (_lib.KV_BF16, 1792, 300, 24, _lib.RMS_BF16, 1),       # no instance at all: no fold
 ])

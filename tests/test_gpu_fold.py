@@ -23,7 +23,7 @@ FAMILIES = [
     ("bf16", "bf16", 768, 24, 232, 4),         # column-split kernel, 32 rows per workgroup
     ("bf16", "bf16", 1792, 24, 64, 2),         # column-split kernel, 16 rows per workgroup
     ("fp8", "log8", 1792, 24, 232, 2),
-    ("bf16", "bf16", 1792, 24, 232, 2),
+    ("bf16", "bf16", 1792, 24, 232, 4),        # column-split kernel, 32 rows per workgroup
 ]
 QTOK = 4
 LENS = [3, 1, 900, 2500, 64, 1700]
