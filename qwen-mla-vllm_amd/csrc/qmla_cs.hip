@@ -112,11 +112,19 @@ struct CS {
   static constexpr int NRI = CRM > 0 ? (T * CRM + 63) / 64 : 0;   // rms DMA instructions per tile
   static constexpr int ROWS = 16 * MB;
   static constexpr int XBW = NTB * MB;                   // partial-score f32x4 per lane
-  // reduce-scatter of the partial scores (bf16 rows, 16-token tiles, 32 rows over 8 slices): wave c
-  // sums and softmaxes rows 4c .. 4c+3 only, one score per lane, and P reaches the other waves
-  // through LDS; otherwise every wave sums all partials and repeats the whole softmax
-  static constexpr bool RSC = EB == 2 && G == 1 && NCG == 8 && NTG == 1 && NTB == 1 && MB == 2;
-  static constexpr int RPS = 40;                         // P row stride (bytes) of the reduce-scatter
+  // reduce-scatter of the partial scores over the 8 slices (one latent group and token group: bf16
+  // rows with 16-token tiles and 32 rows, fp8 rows with 32-token tiles and 16 or 32 rows): wave c
+  // sums and softmaxes its RPW rows only, RE scores per lane, and P reaches the other waves through
+  // LDS; otherwise every wave sums all partials and repeats the whole softmax
+  static constexpr int RPW = ROWS / 8;                   // rows per reducer wave
+  static constexpr int RLR = 64 / T;                     // rows per wave instruction (T tokens each)
+  static constexpr int RPS = 2 * T + (T == 16 ? 8 : 16); // P row stride (bytes) of the reduce-scatter
+  // LDS of the ring, rms stages, partial scores and page ids, and what the reduce-scatter adds
+  static constexpr int LDS0 = S * NW * SB + (S + 1) * NTG * T * RRS + NW * XBW * 64 * 16 + 4 * PIDN;
+  static constexpr int LDSR = ROWS * RPS + 12 * ROWS + 32 + 48;
+  static constexpr bool RSC = G == 1 && NCG == 8 && NTG == 1 && LDS0 + LDSR <= 163840 &&
+                              ((EB == 2 && NTB == 1 && MB == 2) || (EB == 1 && NTB == 2));
+  static constexpr int RE = RSC ? RPW / RLR : 1;         // scores per lane
   static_assert(DCG % (32 * NCG) == 0, "whole 32-column k-steps per wave");
   static_assert(NTB == 1 || NTB == 2, "score tiles per token group");
   static_assert(EB == 2 || NTB == 2, "fp8 values are read 8 tokens at a time");
@@ -128,12 +136,12 @@ struct CS {
 
 // reduce-scatter: P of the tile's 32 rows (bf16), the rows' rescale factors, per reducer wave
 // whether its rows' reference moved, the rows' final max and sum
-template <int RPS>
+template <int ROWS, int RPS>
 struct RsShared {
-  alignas(16) char rp[32 * RPS];
-  alignas(16) float ra[32];
+  alignas(16) char rp[ROWS * RPS];
+  alignas(16) float ra[ROWS];
   alignas(16) int rf[8];
-  alignas(16) float rfin[2][32];
+  alignas(16) float rfin[2][ROWS];
 };
 struct RsNone {};
 
@@ -143,7 +151,7 @@ struct Smem {
   char rms[C::S + 1][C::NTG][C::T * C::RRS];   // S+1 deep: read after the exchange
   f32x4 xb[C::NW][C::XBW][64];                 // partial scores
   int pid[PIDN];
-  [[no_unique_address]] std::conditional_t<C::RSC, RsShared<C::RPS>, RsNone> rs;
+  [[no_unique_address]] std::conditional_t<C::RSC, RsShared<C::ROWS, C::RPS>, RsNone> rs;
 };
 
 
@@ -260,19 +268,28 @@ __device__ __forceinline__ void segment(const KParams& p, Smem<C>& sm, int req, 
   }
   // smallest row limit: tiles below it need no masking
   const int limmin = L - (p.qrows - 1) < te ? L - (p.qrows - 1) : te;
-  // reduce-scatter: this wave's reducer row rrow = 4c + lane/16 (token lane % 16 of each tile), its
-  // limit and rms byte offset, and the row's softmax state (the same in its 16 lanes; the sum is per
-  // lane)
-  const int rl = lane >> 4, tt = lane & 15, rrow = 4 * c + rl;
-  int rlim = 0, rhb = 0;
-  float rmref = kNegInf, rmthr = kNegInf, rlp = 0.f;
-  if constexpr (C::RSC) {
-    const int r = rbase + rrow;
-    const bool ok = r < rows_pg;
-    const int jq = ok ? r / hpg : 0, hh = ok ? r - jq * hpg : 0;
-    const int lr = L - (p.qrows - 1 - jq);
-    rlim = ok ? (lr < te ? lr : te) : 0;
-    rhb = (ok ? (g * hpg + hh) * C::RB : 0) + rdelta;
+  // reduce-scatter: score e of this lane is token tt of reducer row rrow[e] = RPW c + RLR e + lane / T;
+  // the row's limit and rms byte offset, and its softmax state (the same in its T lanes; the sum is
+  // per lane)
+  const int tt = lane % C::T;
+  int rrow[C::RE], rlim[C::RE], rhb[C::RE];
+  float rmref[C::RE], rmthr[C::RE], rlp[C::RE];
+#pragma unroll
+  for (int e = 0; e < C::RE; ++e) {
+    rrow[e] = C::RPW * c + C::RLR * e + lane / C::T;
+    rlim[e] = 0;
+    rhb[e] = 0;
+    rmref[e] = kNegInf;
+    rmthr[e] = kNegInf;
+    rlp[e] = 0.f;
+    if constexpr (C::RSC) {
+      const int r = rbase + rrow[e];
+      const bool ok = r < rows_pg;
+      const int jq = ok ? r / hpg : 0, hh = ok ? r - jq * hpg : 0;
+      const int lr = L - (p.qrows - 1 - jq);
+      rlim[e] = ok ? (lr < te ? lr : te) : 0;
+      rhb[e] = (ok ? (g * hpg + hh) * C::RB : 0) + rdelta;
+    }
   }
 
   // ---- DMA source of chunk i of the wave's tile slice: row i / CPW, chunk i % CPW of
@@ -456,90 +473,125 @@ __device__ __forceinline__ void segment(const KParams& p, Smem<C>& sm, int req, 
       bf16x8 pa8[C::MB];
       s16x4 pa4[C::MB];
       if constexpr (C::RSC) {
-        // ---- reduce-scatter: each wave writes its partial scores as a [32 rows][16 tokens] fp32
-        //      tile (row r's 4-token groups rotated by (r & 15) / 4, so the 16 rows of a write and
-        //      the 64 scores of a read fall on distinct banks); wave c sums the 8 slices' partials
-        //      of rows 4c .. 4c+3 (one score per lane) ----
+        // ---- reduce-scatter: each wave writes its partial scores as a [ROWS][T] fp32 tile (a row's
+        //      4-token groups rotated by xrot(row), so the 16 rows of a write and the 64 scores of a
+        //      read fall on distinct banks); wave c sums the 8 slices' partials of its rows ----
         float* xs = reinterpret_cast<float*>(&sm.xb[0][0][0]);
+        constexpr int NG = C::T / 4;   // 4-token groups of a row
+        auto xrot = [](int r) { return C::T == 16 ? (r & 15) >> 2 : (r >> 1) & 7; };
+#pragma unroll
+        for (int tb = 0; tb < C::NTB; ++tb)
+#pragma unroll
+          for (int mb = 0; mb < C::MB; ++mb) {
+            const int row = 16 * mb + ln16;
+            const int g0 = tok_of(tb, 4 * lg) >> 2;
+            *reinterpret_cast<f32x4*>(xs + (w * C::ROWS + row) * C::T + 4 * ((g0 + xrot(row)) & (NG - 1))) = sp[tb][mb];
+          }
+        lds_barrier();
+        int xr[C::RE][C::NCG];
+#pragma unroll
+        for (int e = 0; e < C::RE; ++e) {
+          const int xpos = 4 * (((tt >> 2) + xrot(rrow[e])) & (NG - 1)) + (tt & 3);
+#pragma unroll
+          for (int v = 0; v < C::NCG; ++v)
+            xr[e][v] = ldsr32(reinterpret_cast<const char*>(xs + (v * C::ROWS + rrow[e]) * C::T + xpos));
+        }
+        // rms divisors of (token tt, the rows' heads)
+        uint32_t cd[C::RE];
+        if constexpr (C::RMS != QMLA_RMS_NONE) {
+          const char* rsb = sm.rms[t % (C::S + 1)][tg] + tt * C::RRS;
+#pragma unroll
+          for (int e = 0; e < C::RE; ++e) cd[e] = C::RB == 1 ? ldsr8(rsb + rhb[e]) : ldsr16(rsb + rhb[e]);
+        }
+#pragma unroll
+        for (int e = 0; e < C::RE; ++e)
+#pragma unroll
+          for (int v = 0; v < C::NCG; ++v) lds_wait(xr[e][v]);
+        if constexpr (C::RMS != QMLA_RMS_NONE) {
+#pragma unroll
+          for (int e = 0; e < C::RE; ++e) lds_wait(cd[e]);
+        }
+        bool moved = false;
+        float alpha[C::RE];
+#pragma unroll
+        for (int e = 0; e < C::RE; ++e) {
+          float sv = __int_as_float(xr[e][0]);
+#pragma unroll
+          for (int v = 1; v < C::NCG; ++v) sv += __int_as_float(xr[e][v]);
+          float ri = 1.0f;
+          if constexpr (C::RMS == QMLA_RMS_LOG8) {
+            ri = fast_exp2(fmaf((float)cd[e], -6.0f / 255.0f, 3.0f));
+          } else if constexpr (C::RMS == QMLA_RMS_E4M3) {
+            const float rv = fp8_to_f32(cd[e]) * kscale;
+            ri = rv > 0.f ? __builtin_amdgcn_rcpf(rv) : 1.0f;
+          } else if constexpr (C::RMS == QMLA_RMS_BF16 || C::RMS == QMLA_RMS_BF16_BYTES) {
+            const float rv = bf16_bits_to_f32(cd[e]);
+            ri = rv > 0.f ? __builtin_amdgcn_rcpf(rv) : 1.0f;
+          }
+          float v = sv * ri * csc;
+          if constexpr (C::CAP) {
+            const float y = v / cap2;
+            const float e2 = fast_exp2(2.0f * kLog2e * y);
+            v = cap2 * (1.0f - 2.0f / (e2 + 1.0f));
+          }
+          if (tok0 + C::T > limmin && tok0 + tt >= rlim[e]) v = kNegInf;
+          // row max over the row's T lanes
+          float tm = max16(v);
+          if constexpr (C::T == 32) tm = fmaxf(tm, __shfl_xor(tm, 16));
+          // the row's reference moves as in the other layout (ref_shift of the row's sum, P <= 2^8)
+          alpha[e] = 1.0f;
+          if (__builtin_amdgcn_ballot_w64(tm > rmthr[e])) {
+            float ls = sum16(rlp[e]);
+            if constexpr (C::T == 32) ls += __shfl_xor(ls, 16);
+            rmthr[e] = rmref[e] + ref_shift(ls, 8.0f);
+            const bool mv = tm > rmthr[e];
+            if (__builtin_amdgcn_ballot_w64(mv)) {
+              const float mn = mv ? tm : rmref[e];
+              alpha[e] = rmref[e] == kNegInf ? 0.f : fast_exp2(rmref[e] - mn);
+              rlp[e] *= alpha[e];
+              rmref[e] = mn;
+              if (mv) rmthr[e] = mn;
+              moved = true;
+            }
+          }
+          const float pv = fast_exp2(v - (rmref[e] == kNegInf ? 0.f : rmref[e]));
+          rlp[e] += pv;
+          *reinterpret_cast<__bf16*>(sm.rs.rp + rrow[e] * C::RPS + 2 * tt) = (__bf16)pv;
+        }
+        if (moved && tt == 0) {
+#pragma unroll
+          for (int e = 0; e < C::RE; ++e) sm.rs.ra[rrow[e]] = alpha[e];
+        }
+        if (lane == 0) sm.rs.rf[c] = moved ? 1 : 0;
+        lds_barrier();
+        // ---- P of rows 16mb + ln16 as the A operand (16 tokens: 4lg .. 4lg+3; 32 tokens: the
+        //      k-slot order vtok), and the rows of this lane's accumulators (16mb + 4lg + i),
+        //      rescaled first where their reducer wave's reference moved ----
+        i32x2 pr[C::MB][C::NTB];
 #pragma unroll
         for (int mb = 0; mb < C::MB; ++mb)
-          *reinterpret_cast<f32x4*>(xs + (w * 32 + 16 * mb + ln16) * 16 + 4 * ((lg + (ln16 >> 2)) & 3)) = sp[0][mb];
-        lds_barrier();
-        const int xpos = 4 * (((tt >> 2) + ((rrow & 15) >> 2)) & 3) + (tt & 3);
-        int xr[C::NCG];
 #pragma unroll
-        for (int v = 0; v < C::NCG; ++v)
-          xr[v] = ldsr32(reinterpret_cast<const char*>(xs + (v * 32 + rrow) * 16 + xpos));
-#pragma unroll
-        for (int v = 0; v < C::NCG; ++v) lds_wait(xr[v]);
-        float sv = __int_as_float(xr[0]);
-#pragma unroll
-        for (int v = 1; v < C::NCG; ++v) sv += __int_as_float(xr[v]);
-        // rms divisor of (token tt, the row's head)
-        float ri = 1.0f;
-        if constexpr (C::RMS != QMLA_RMS_NONE) {
-          const char* rsb = sm.rms[t % (C::S + 1)][tg] + tt * C::RRS + rhb;
-          uint32_t cd = C::RB == 1 ? ldsr8(rsb) : ldsr16(rsb);
-          lds_wait(cd);
-          if constexpr (C::RMS == QMLA_RMS_LOG8) {
-            ri = fast_exp2(fmaf((float)cd, -6.0f / 255.0f, 3.0f));
-          } else if constexpr (C::RMS == QMLA_RMS_E4M3) {
-            const float rv = fp8_to_f32(cd) * kscale;
-            ri = rv > 0.f ? __builtin_amdgcn_rcpf(rv) : 1.0f;
-          } else {
-            const float rv = bf16_bits_to_f32(cd);
-            ri = rv > 0.f ? __builtin_amdgcn_rcpf(rv) : 1.0f;
-          }
-        }
-        float v = sv * ri * csc;
-        if constexpr (C::CAP) {
-          const float y = v / cap2;
-          const float e2 = fast_exp2(2.0f * kLog2e * y);
-          v = cap2 * (1.0f - 2.0f / (e2 + 1.0f));
-        }
-        if (tok0 + C::T > limmin && tok0 + tt >= rlim) v = kNegInf;
-        const float tm = max16(v);
-        // the row's reference moves as in the other layout (ref_shift of the row's sum, P <= 2^8)
-        bool moved = false;
-        float alpha = 1.0f;
-        if (__builtin_amdgcn_ballot_w64(tm > rmthr)) {
-          rmthr = rmref + ref_shift(sum16(rlp), 8.0f);
-          const bool mv = tm > rmthr;
-          if (__builtin_amdgcn_ballot_w64(mv)) {
-            const float mn = mv ? tm : rmref;
-            alpha = rmref == kNegInf ? 0.f : fast_exp2(rmref - mn);
-            rlp *= alpha;
-            rmref = mn;
-            if (mv) rmthr = mn;
-            moved = true;
-          }
-        }
-        if (moved && tt == 0) sm.rs.ra[rrow] = alpha;
-        if (lane == 0) sm.rs.rf[c] = moved ? 1 : 0;
-        const float pv = fast_exp2(v - (rmref == kNegInf ? 0.f : rmref));
-        rlp += pv;
-        *reinterpret_cast<__bf16*>(sm.rs.rp + rrow * C::RPS + 2 * tt) = (__bf16)pv;
-        lds_barrier();
-        // ---- P of rows 16mb + ln16, tokens 4lg .. 4lg+3 (the A operand); the rows of this lane's
-        //      accumulators (16mb + 4lg + i) belong to reducer wave 4mb + lg: rescale them first if
-        //      its reference moved ----
-        i32x2 pr[C::MB];
-#pragma unroll
-        for (int mb = 0; mb < C::MB; ++mb) pr[mb] = ldsr64(sm.rs.rp + (16 * mb + ln16) * C::RPS + 8 * lg);
+          for (int tb = 0; tb < C::NTB; ++tb)
+            pr[mb][tb] = ldsr64(sm.rs.rp + (16 * mb + ln16) * C::RPS + 2 * tok_of(tb, 4 * lg));
         i32x4 f0 = ldsr128(reinterpret_cast<const char*>(&sm.rs.rf[0])), f1 = ldsr128(reinterpret_cast<const char*>(&sm.rs.rf[4]));
         lds_wait(f0, f1);
 #pragma unroll
-        for (int mb = 0; mb < C::MB; ++mb) lds_wait(pr[mb]);
+        for (int mb = 0; mb < C::MB; ++mb)
+#pragma unroll
+          for (int tb = 0; tb < C::NTB; ++tb) lds_wait(pr[mb][tb]);
         const int fa = f0[0] | f0[1] | f0[2] | f0[3] | f1[0] | f1[1] | f1[2] | f1[3];
         if (__builtin_amdgcn_readfirstlane(fa)) {
+          const int fw[8] = {f0[0], f0[1], f0[2], f0[3], f1[0], f1[1], f1[2], f1[3]};
 #pragma unroll
           for (int mb = 0; mb < C::MB; ++mb) {
-            const int fl = (mb == 0 ? f0 : f1)[lg];
             i32x4 ar = ldsr128(reinterpret_cast<const char*>(&sm.rs.ra[16 * mb + 4 * lg]));
             lds_wait(ar);
             const f32x4 al = __builtin_bit_cast(f32x4, ar);
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
+              int fl = 0;   // the flag of row 16mb + 4lg + i's reducer wave
+#pragma unroll
+              for (int x = 0; x < 8; ++x) fl = (16 * mb + 4 * lg + i) / C::RPW == x ? fw[x] : fl;
               const float a_i = fl ? al[i] : 1.0f;
 #pragma unroll
               for (int cb = 0; cb < C::CB; ++cb) acc[mb][cb][i] *= a_i;
@@ -547,7 +599,14 @@ __device__ __forceinline__ void segment(const KParams& p, Smem<C>& sm, int req, 
           }
         }
 #pragma unroll
-        for (int mb = 0; mb < C::MB; ++mb) pa4[mb] = __builtin_bit_cast(s16x4, pr[mb]);
+        for (int mb = 0; mb < C::MB; ++mb) {
+          if constexpr (C::NTB == 1) {
+            pa4[mb] = __builtin_bit_cast(s16x4, pr[mb][0]);
+          } else {
+            const i32x4 w4 = {pr[mb][0][0], pr[mb][0][1], pr[mb][C::NTB - 1][0], pr[mb][C::NTB - 1][1]};
+            pa8[mb] = __builtin_bit_cast(bf16x8, w4);
+          }
+        }
       } else {
         // ---- sum the NCG partials of (g, tg) in slice order ----
   #pragma unroll
@@ -821,12 +880,16 @@ __device__ __forceinline__ void segment(const KParams& p, Smem<C>& sm, int req, 
 #pragma unroll
   for (int mb = 0; mb < C::MB; ++mb) lrow[mb] = sum_lg(lpart[mb]);
   // reduce-scatter: the reducer waves hand every row's max and sum to the waves holding its columns
-  float rls = 0.f;
+  float rls[C::RE];
   if constexpr (C::RSC) {
-    rls = sum16(rlp);
-    if (tt == 0) {
-      sm.rs.rfin[0][rrow] = rmref;
-      sm.rs.rfin[1][rrow] = rls;
+#pragma unroll
+    for (int e = 0; e < C::RE; ++e) {
+      rls[e] = sum16(rlp[e]);
+      if constexpr (C::T == 32) rls[e] += __shfl_xor(rls[e], 16);
+      if (tt == 0) {
+        sm.rs.rfin[0][rrow[e]] = rmref[e];
+        sm.rs.rfin[1][rrow[e]] = rls[e];
+      }
     }
     lds_barrier();
   }
@@ -937,17 +1000,20 @@ __device__ __forceinline__ void segment(const KParams& p, Smem<C>& sm, int req, 
   }
   if constexpr (C::RSC) {
     // the reducer lane of each row writes its lse
-    const int r = rbase + rrow;
-    if (tt == 0 && r < rows_pg) {
-      const int jq = r / hpg, hh = r - jq * hpg;
-      const int head = g * hpg + hh;
-      const float lse_v = row_lse(rmref, rls);
-      if (so.final_out) {
-        if (p.lse) store_out(p.lse, p.lse_dt, (int64_t)(row0 + jq) * p.lse_sr + head, lse_v);
-      } else if (so.plse) {
-        so.plse[(int64_t)jq * so.plse_sr + head] = lse_v;
-      } else {
-        so.po[(int64_t)jq * so.po_sr + (int64_t)head * so.po_sh + C::DCG] = lse_v;
+#pragma unroll
+    for (int e = 0; e < C::RE; ++e) {
+      const int r = rbase + rrow[e];
+      if (tt == 0 && r < rows_pg) {
+        const int jq = r / hpg, hh = r - jq * hpg;
+        const int head = g * hpg + hh;
+        const float lse_v = row_lse(rmref[e], rls[e]);
+        if (so.final_out) {
+          if (p.lse) store_out(p.lse, p.lse_dt, (int64_t)(row0 + jq) * p.lse_sr + head, lse_v);
+        } else if (so.plse) {
+          so.plse[(int64_t)jq * so.plse_sr + head] = lse_v;
+        } else {
+          so.po[(int64_t)jq * so.po_sr + (int64_t)head * so.po_sh + C::DCG] = lse_v;
+        }
       }
     }
   }
