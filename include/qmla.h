@@ -41,7 +41,8 @@ extern "C" {
 #define QMLA_OK 0
 #define QMLA_ERR_NULL (-1)        /* a required pointer is NULL */
 #define QMLA_ERR_SHAPE (-2)       /* unsupported or inconsistent dimension */
-#define QMLA_ERR_ALIGN (-3)       /* a row, page or base address is not 16-byte aligned */
+#define QMLA_ERR_ALIGN (-3)       /* a row, page or base address is off 4-byte boundaries, or off
+                                     16-byte ones in a layout no narrow-row kernel serves */
 #define QMLA_ERR_WORKSPACE (-4)   /* workspace missing or smaller than qmla_workspace_bytes() */
 #define QMLA_ERR_MODE (-5)        /* unknown dtype / rms mode / split mode */
 #define QMLA_ERR_LAUNCH (-6)      /* the HIP launch itself failed */
@@ -84,7 +85,10 @@ typedef struct qmla_decode_params {
   int64_t q_pe_stride_row, q_pe_stride_head;
 
   /* paged cache [num_pages, page_size, (1,) row]: element (page, slot, col) at
-   * kv_cache + page*page_stride + slot*token_stride + col */
+   * kv_cache + page*page_stride + slot*token_stride + col. Base, page and row strides on 16-byte
+   * boundaries (the plugin pads rows to 16 elements); rows on 4-byte boundaries only are served for
+   * the unpadded 12-head bf16 layouts of the reference's numerics test (rope 256, ranks 256 / 768 /
+   * 1792), else QMLA_ERR_ALIGN */
   const void* kv_cache;
   int64_t page_stride, token_stride;
   int32_t kv_dtype;               /* QMLA_KV_* */

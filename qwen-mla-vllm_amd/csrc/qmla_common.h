@@ -292,6 +292,14 @@ __device__ __forceinline__ void for_each_segment(const KParams& p, F&& f) {
   }
 }
 
+// Cached rows on 16-byte boundaries (cache base, page stride and row stride): every kernel family
+// stages them with 16-byte LDS-DMA loads. Rows on 4-byte boundaries only (the unpadded 12-head rows
+// of the reference's numerics test) take the narrow-row instances, which stage 4 bytes per lane.
+inline bool rows16(const qmla_decode_params* p) {
+  const int eb = p->kv_dtype == QMLA_KV_FP8 ? 1 : 2;
+  return ((uintptr_t)p->kv_cache & 15) == 0 && (p->page_stride * eb) % 16 == 0 && (p->token_stride * eb) % 16 == 0;
+}
+
 // ---- host-side interface of the warp-specialized translation unit (qmla_ws.hip) ----
 int ws_select(const qmla_decode_params* p);
 int ws_head_split(const qmla_decode_params* p);

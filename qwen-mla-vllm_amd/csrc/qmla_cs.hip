@@ -86,12 +86,14 @@ __device__ __forceinline__ uint32_t ldsr16(const char* p) {
 //   WP   rope columns staged per row: 64 (exactly the rope), or the padded window 128 / 256 of a
 //        partial rope (116 / 232 wide), spread over all NCG waves; columns past rope_w are zeroed
 //        in both operands (the row bytes there are rms codes, which may read as fp8 NaN)
+//   DW   narrow rows: cached rows on 4-byte boundaries only, staged 4 bytes per lane (four DMA
+//        instructions per 64 chunks, the same LDS image)
 template <int EB_, int RMS_, int DCG_, int G_, int NCG_, int NTG_, int NTB_, int MB_, int S_, int CRM_,
-          bool CAP_, bool RTR_, int WP_>
+          bool CAP_, bool RTR_, int WP_, bool DW_ = false>
 struct CS {
   static constexpr int EB = EB_, RMS = RMS_, DCG = DCG_, G = G_, NCG = NCG_, NTG = NTG_, NTB = NTB_;
   static constexpr int MB = MB_, S = S_, CRM = CRM_, WP = WP_;
-  static constexpr bool CAP = CAP_, RTR = RTR_;
+  static constexpr bool CAP = CAP_, RTR = RTR_, DW = DW_;
   static constexpr bool PR = WP != 64;                   // partial rope: mask columns >= rope_w
   static constexpr int NW = G * NCG * NTG, NTHR = 64 * NW;
   static constexpr int T = 16 * NTB, TT = NTG * T;
@@ -110,6 +112,9 @@ struct CS {
   static constexpr int RB = (RMS == QMLA_RMS_NONE) ? 0 : ((RMS == QMLA_RMS_BF16 || RMS == QMLA_RMS_BF16_BYTES) ? 2 : 1);
   static constexpr int RRS = 16 * (CRM > 0 ? CRM : 1);   // staged rms row bytes
   static constexpr int NRI = CRM > 0 ? (T * CRM + 63) / 64 : 0;   // rms DMA instructions per tile
+  // DMA instructions per tile as issued: 64 chunks each, or 16 with narrow rows
+  static constexpr int NID = DW ? (NCH + 15) / 16 : NI;
+  static constexpr int NRID = DW ? (T * CRM + 15) / 16 : NRI;
   static constexpr int ROWS = 16 * MB;
   static constexpr int XBW = NTB * MB;                   // partial-score f32x4 per lane
   // reduce-scatter of the partial scores over the 8 slices (one latent group and token group: bf16
@@ -130,7 +135,8 @@ struct CS {
   static_assert(EB == 2 || NTB == 2, "fp8 values are read 8 tokens at a time");
   static_assert(RW == 16 || RW == 32 || RW == 64, "rope slice");
   static_assert(!PR || (WP % NCG == 0 && (WP == 128 || WP == 256)), "padded rope window");
-  static_assert((S - 1) * (NI + NRI) < 64, "vmcnt range");
+  static_assert((S - 1) * (NID + NRID) < 64, "vmcnt range");
+  static_assert(!DW || !RTR, "narrow rows take per-row rms reads");
   static_assert(!RTR || CRM * 16 >= RB * ROWS, "transposed rms reads cover all row heads");
 };
 
@@ -163,8 +169,8 @@ __device__ __forceinline__ constexpr int vtok(int q, int r) { return r < 4 ? tok
 template <class C>
 __device__ __forceinline__ void wait_tile(bool steady, bool rms_wave) {
   if (!steady) wait_vmcnt<0>();
-  else if (rms_wave) wait_vmcnt<(C::S - 1) * (C::NI + C::NRI)>();
-  else wait_vmcnt<(C::S - 1) * C::NI>();
+  else if (rms_wave) wait_vmcnt<(C::S - 1) * (C::NID + C::NRID)>();
+  else wait_vmcnt<(C::S - 1) * C::NID>();
 }
 
 // One contiguous token range [ta, te) of request `req` (length L), all query rows.
@@ -296,8 +302,7 @@ __device__ __forceinline__ void segment(const KParams& p, Smem<C>& sm, int req, 
   //      [latent slice | rope slice | pad]; recomputed at every issue rather than held ----
   const int lat_off = (g * C::DCG + c * C::DCW) * C::EB;
   const int rope_off = C::DC * C::EB + rope_col * C::EB;
-  auto src_off = [&](int k, int ln, int& row) {
-    const int i = 64 * k + ln;
+  auto src_chunk = [&](int i, int& row) {
     const int t = i / C::CPW, ch = i - t * C::CPW;
     int off;
     if (ch < C::CL) off = lat_off + 16 * ch;
@@ -347,50 +352,66 @@ __device__ __forceinline__ void segment(const KParams& p, Smem<C>& sm, int req, 
         // rows past the range end read as zeros (outside the resource)
         const __amdgpu_buffer_rsrc_t rs = make_rsrc(base, (uint32_t)(nvalid * TS));
         const int tb0 = tg * C::T;
+        // chunk i of the stage lands at 16 i: instruction k carries chunks 64k.. (16 bytes a lane),
+        // or 16k.. (narrow rows: lane ln the 4 bytes at 4 (ln & 3) of chunk 16k + ln / 4)
+        constexpr int CPI = C::DW ? 16 : 64;
+        const int cl = C::DW ? ln >> 2 : ln, bl = C::DW ? 4 * (ln & 3) : 0;
 #pragma unroll
-        for (int k = 0; k < C::NI; ++k) {
+        for (int k = 0; k < C::NID; ++k) {
           int row;
-          const int off = src_off(k, ln, row);
-          if (64 * k + 64 <= C::NCH || 64 * k + ln < C::NCH)
-            dma16_buf<kCpolDefault>(rs, (uint32_t)((tb0 + row) * (int)TS + off), dst + k * 1024);
+          const int off = src_chunk(CPI * k + cl, row) + bl;
+          if (CPI * k + CPI <= C::NCH || CPI * k + cl < C::NCH) {
+            if constexpr (C::DW) dma4_buf(rs, (uint32_t)((tb0 + row) * (int)TS + off), dst + k * 256);
+            else dma16_buf<kCpolDefault>(rs, (uint32_t)((tb0 + row) * (int)TS + off), dst + k * 1024);
+          }
         }
         if (rms_wave) {
 #pragma unroll
-          for (int k = 0; k < C::NRI; ++k) {
-            const int j = 64 * k + ln;
+          for (int k = 0; k < C::NRID; ++k) {
+            const int j = CPI * k + cl;
             const int row = j / (C::CRM > 0 ? C::CRM : 1);
-            if (64 * k + 64 <= C::T * C::CRM || j < C::T * C::CRM)
-              dma16_buf<kCpolDefault>(rs, (uint32_t)((tb0 + row) * (int)TS + roff_al + 16 * (j - row * C::CRM)), rdst + k * 1024);
+            if (CPI * k + CPI <= C::T * C::CRM || j < C::T * C::CRM) {
+              const uint32_t o = (uint32_t)((tb0 + row) * (int)TS + roff_al + 16 * (j - row * C::CRM) + bl);
+              if constexpr (C::DW) dma4_buf(rs, o, rdst + k * 256);
+              else dma16_buf<kCpolDefault>(rs, o, rdst + k * 1024);
+            }
           }
         }
       } else {
         // pages change inside a tile: per-lane page lookup; rows past the end repeat the last row
         const int tb0 = tok0 + tg * C::T;
         const int nv = se - tb0;   // rows of this token group inside the range (may be <= 0)
+        constexpr int CPI = C::DW ? 16 : 64;
+        const int cl = C::DW ? ln >> 2 : ln, bl = C::DW ? 4 * (ln & 3) : 0;
 #pragma unroll
-        for (int k = 0; k < C::NI; ++k) {
+        for (int k = 0; k < C::NID; ++k) {
           int row;
-          const int off = src_off(k, ln, row);
-          if (64 * k + 64 <= C::NCH || 64 * k + ln < C::NCH) {
+          const int off = src_chunk(CPI * k + cl, row) + bl;
+          if (CPI * k + CPI <= C::NCH || CPI * k + cl < C::NCH) {
             const int rr = row < nv ? row : (nv > 0 ? nv - 1 : 0);
             const int tok = nv > 0 ? tb0 + rr : se - 1;
             const int q = tok / P;
             const int pg = sm.pid[q - pbase];
-            dma16<kCpolDefault>(p.kv + (int64_t)pg * PS + (int64_t)(tok - q * P) * TS + off, dst + k * 1024);
+            const char* src = p.kv + (int64_t)pg * PS + (int64_t)(tok - q * P) * TS + off;
+            if constexpr (C::DW) dma4(src, dst + k * 256);
+            else dma16<kCpolDefault>(src, dst + k * 1024);
           }
         }
         if (rms_wave) {
 #pragma unroll
-          for (int k = 0; k < C::NRI; ++k) {
-            const int j = 64 * k + ln;
+          for (int k = 0; k < C::NRID; ++k) {
+            const int j = CPI * k + cl;
             const int row = j / (C::CRM > 0 ? C::CRM : 1);
-            if (64 * k + 64 <= C::T * C::CRM || j < C::T * C::CRM) {
+            const int ob = roff_al + 16 * (j - row * C::CRM) + bl;   // byte of the row
+            // narrow rows: the staged tail may end past the row; those bytes are not read
+            if ((CPI * k + CPI <= C::T * C::CRM || j < C::T * C::CRM) && (!C::DW || ob < (int)TS)) {
               const int rr = row < nv ? row : (nv > 0 ? nv - 1 : 0);
               const int tok = nv > 0 ? tb0 + rr : se - 1;
               const int q = tok / P;
               const int pg = sm.pid[q - pbase];
-              dma16<kCpolDefault>(p.kv + (int64_t)pg * PS + (int64_t)(tok - q * P) * TS + roff_al + 16 * (j - row * C::CRM),
-                    rdst + k * 1024);
+              const char* src = p.kv + (int64_t)pg * PS + (int64_t)(tok - q * P) * TS + ob;
+              if constexpr (C::DW) dma4(src, rdst + k * 256);
+              else dma16<kCpolDefault>(src, rdst + k * 1024);
             }
           }
         }
@@ -1039,13 +1060,15 @@ __global__ __launch_bounds__(C::NTHR, 1) void cs_kernel(const KParams p) {
 
 struct Inst {
   int eb, rms, dcg, g, mb, crm, wp, nthr;
-  bool cap, rtr;
+  bool cap, rtr, dw;
   void (*fn)(const KParams);
 };
 
-#define QMLA_CS(EB, RMS, DCG, G, NCG, NTG, NTB, MB, S, CRM, CAP, RTR, WP)                                    \
-  {EB, RMS, DCG, G, MB, CRM, WP, CS<EB, RMS, DCG, G, NCG, NTG, NTB, MB, S, CRM, CAP, RTR, WP>::NTHR, CAP, RTR, \
-   &cs_kernel<CS<EB, RMS, DCG, G, NCG, NTG, NTB, MB, S, CRM, CAP, RTR, WP>>}
+#define QMLA_CSX(EB, RMS, DCG, G, NCG, NTG, NTB, MB, S, CRM, CAP, RTR, WP, DW)                                    \
+  {EB, RMS, DCG, G, MB, CRM, WP, CS<EB, RMS, DCG, G, NCG, NTG, NTB, MB, S, CRM, CAP, RTR, WP, DW>::NTHR, CAP, RTR, DW, \
+   &cs_kernel<CS<EB, RMS, DCG, G, NCG, NTG, NTB, MB, S, CRM, CAP, RTR, WP, DW>>}
+#define QMLA_CS(EB, RMS, DCG, G, NCG, NTG, NTB, MB, S, CRM, CAP, RTR, WP) \
+  QMLA_CSX(EB, RMS, DCG, G, NCG, NTG, NTB, MB, S, CRM, CAP, RTR, WP, false)
 
 // One entry per compiled shape; rows [latent | rope | rms | pad].
 static const Inst kInst[] = {
@@ -1069,6 +1092,10 @@ static const Inst kInst[] = {
     QMLA_CS(2, QMLA_RMS_BF16, 1792, 1, 8, 1, 1, 1, 2, 3, false, false, 256),
     QMLA_CS(2, QMLA_RMS_BF16, 1792, 1, 8, 1, 1, 1, 2, 2, false, false, 256),   // 12 heads: 32-byte tail
     QMLA_CS(2, QMLA_RMS_BF16, 1792, 1, 8, 1, 1, 1, 2, 2, false, false, 128),
+    // the unpadded 12-head rows of the reference's numerics test (rank + 256 + 12 bf16 elements:
+    // 2072 / 4120 bytes, on 8-byte boundaries, tests/test_decode_numerics.py:60-67): narrow rows
+    QMLA_CSX(2, QMLA_RMS_BF16, 768, 1, 8, 1, 1, 1, 3, 2, false, false, 256, true),
+    QMLA_CSX(2, QMLA_RMS_BF16, 1792, 1, 8, 1, 1, 1, 2, 2, false, false, 256, true),
     // fp8 cache, d_c 1792: 32-token tiles, 16 rows per workgroup (32 rows of 1792 accumulator and
     // query columns exceed the register file), more heads split over gridDim.z.
     // Rope 64, log8 codes (transposed rms reads: 2 chunks cover the heads of two row blocks):
@@ -1103,6 +1130,7 @@ int cs_select(const qmla_decode_params* p) {
   for (int i = 0; i < (int)(sizeof(cs::kInst) / sizeof(cs::kInst[0])); ++i) {
     const cs::Inst& in = cs::kInst[i];
     if (in.eb != eb || in.rms != p->rms_mode || in.dcg != dcg || in.g != p->groups || in.cap != cap) continue;
+    if (in.dw == rows16(p)) continue;   // narrow-row instances serve exactly the rows off 16-byte boundaries
     const int hs = cs::row_splits(in, p);
     if (hs > 4) continue;   // at most 4 workgroups read each token range
     if (in.rtr && (p->qrows != 1 || p->groups != 1)) continue;
@@ -1115,7 +1143,7 @@ int cs_select(const qmla_decode_params* p) {
       const int64_t delta = roff % 16;   // staged from the 16-byte boundary below the tail
       if (in.rtr && delta) continue;     // transposed reads need an aligned tail
       const int64_t need = in.rtr ? 16 * in.mb * hs * rb : delta + (int64_t)p->heads * rb;   // transposed reads cover 16*MB*hs heads
-      if (need > 16 * in.crm || roff - delta + 16 * in.crm > ts) continue;
+      if (need > 16 * in.crm || (!in.dw && roff - delta + 16 * in.crm > ts)) continue;
       if (!in.rtr && delta + (int64_t)p->rms_heads * rb > 16 * in.crm) continue;
     }
     if (best < 0 || hs < best_hs || (hs == best_hs && in.mb < cs::kInst[best].mb)) {

@@ -43,6 +43,8 @@ namespace qmla {
 //   MB   16-row MFMA blocks per group (rows per group = qrows * heads/G <= 16*MB)
 //   S    LDS ring stages, CPR 16-byte chunks staged per row (LDS row = 16*CPR bytes)
 //   TILE tokens per pipeline step (32 or 64), WGPC workgroups resident per compute unit
+//   DW   narrow rows: cached rows on 4-byte boundaries only, staged 4 bytes per lane (four DMA
+//        instructions per 64 chunks, the same LDS image; two stages, so every wait is for all)
 //
 // Work split inside a workgroup (4 waves, WPG = 4/G per latent group):
 //   scores  the group's (16-token block, 16-row block) items are dealt to its waves so that a
@@ -50,12 +52,12 @@ namespace qmla {
 //           blocks; its query fragments (B operand) stay in VGPRs for the whole segment.
 //   P.V     each wave owns NCOL latent output columns for all rows of its group.
 template <int EB_, int RMS_, int DCG_, int WP_, int MB_, int G_, int S_, int CPR_, bool CAP_, int TILE_, int WGPC_,
-          int NW_>
+          int NW_, bool DW_ = false>
 struct Cfg {
   static constexpr int EB = EB_, RMS = RMS_, DCG = DCG_, WP = WP_, MB = MB_, G = G_, S = S_;
   static constexpr int NW = NW_, NTHR = 64 * NW_;   // waves per workgroup
   static constexpr int CPR = CPR_;
-  static constexpr bool CAP = CAP_;
+  static constexpr bool CAP = CAP_, DW = DW_;
   static constexpr int TILE = TILE_, WGPC = WGPC_;
   static constexpr int DC = G * DCG;
   static constexpr int RB = 16 * CPR;              // LDS row stride (bytes)
@@ -82,6 +84,7 @@ struct Cfg {
   static_assert(NTB % WPM == 0 && TBW >= 1, "token-block split");
   static_assert(TILE % 32 == 0 && PLAN_TILE % TILE == 0, "tile");
   static_assert(S >= 2 && CPR >= 16, "ring");
+  static_assert(!DW || (S == 2 && 4 * NDMA + 1 < 64), "narrow rows: one tile in flight, within the vmcnt range");
 };
 
 // Staged rows are rotated by 16-byte chunks: chunk c of LDS row r sits at position
@@ -190,7 +193,7 @@ __device__ __forceinline__ void process_segment(const KParams& p, Smem<C>& sm, i
     const int tok0 = tok_a + t * TILE;
     const int* pidt = sm.pid[t % (2 * C::S)];
     char* dst = sm.kv[t % C::S];
-    if (tok0 / P == (tok0 + TILE - 1) / P && p.token_stride_b == C::RB) {
+    if (!C::DW && tok0 / P == (tok0 + TILE - 1) / P && p.token_stride_b == C::RB) {
       // the TILE rows are consecutive in one page: one contiguous block, addressed through a
       // buffer resource so the per-tile cost is scalar (rows past tok_e stay inside the page)
       const int page = checked_page(p, __builtin_amdgcn_readfirstlane(pidt[0]), bad);
@@ -208,6 +211,30 @@ __device__ __forceinline__ void process_segment(const KParams& p, Smem<C>& sm, i
     const int64_t off = (int64_t)checked_page(p, pidt[lane < TILE ? lane : TILE - 1], bad) * p.page_stride_b +
                         (int64_t)(tok % P) * p.token_stride_b;
     const int off_lo = (int)(uint32_t)off, off_hi = (int)(uint32_t)((uint64_t)off >> 32);
+    if constexpr (C::DW) {
+      // instruction i's 64 chunks as four 16-chunk quarters: lane l of quarter s carries the 4 bytes
+      // at 4 (l & 3) of LDS chunk 64 i + 16 s + l / 4; bytes past the row (the next row's) are skipped
+#pragma unroll
+      for (int j = 0; j < C::NDMA; ++j) {
+        const int i = wave + C::NW * j;
+        if (i < C::NI) {
+#pragma unroll
+          for (int s = 0; s < 4; ++s) {
+            int q = 64 * i + 16 * s + (lane >> 2);
+            const bool live = q < TILE * C::CPR;
+            q = live ? q : TILE * C::CPR - 1;
+            const int r = q / C::CPR, pp = q - r * C::CPR;
+            int c = pp - (r & 15);
+            c = c < 0 ? c + C::CPR : c;
+            const int ib = 16 * c + 4 * (lane & 3);
+            const uint32_t lo = (uint32_t)__shfl(off_lo, r), hi = (uint32_t)__shfl(off_hi, r);
+            const int64_t roff = (int64_t)(((uint64_t)hi << 32) | lo);
+            if (live && ib < p.token_stride_b) dma4(p.kv + roff + ib, dst + i * 1024 + 256 * s);
+          }
+        }
+      }
+      return;
+    }
 #pragma unroll
     for (int j = 0; j < C::NDMA; ++j) {
       const int i = wave + C::NW * j;
@@ -839,11 +866,15 @@ struct Inst {
   bool cap;
   int tile, wgpc, nthr;
   PartialFn fn;
+  bool dw;
 };
 
 #define QMLA_INST(EB, RMS, DCG, WP, MB, G, S, CPR, CAP, TILE, WGPC, NW)                    \
   {EB, RMS, DCG, WP, MB, G, S, CPR, CAP, TILE, WGPC, 64 * NW,                                \
-   &partial_kernel<Cfg<EB, RMS, DCG, WP, MB, G, S, CPR, CAP, TILE, WGPC, NW>>}
+   &partial_kernel<Cfg<EB, RMS, DCG, WP, MB, G, S, CPR, CAP, TILE, WGPC, NW>>, false}
+#define QMLA_INST_DW(EB, RMS, DCG, WP, MB, G, S, CPR, CAP, TILE, WGPC, NW) \
+  {EB, RMS, DCG, WP, MB, G, S, CPR, CAP, TILE, WGPC, 64 * NW,             \
+   &partial_kernel<Cfg<EB, RMS, DCG, WP, MB, G, S, CPR, CAP, TILE, WGPC, NW, true>>, true}
 
 // One entry per compiled shape. Rows are [latent | rope | rms | pad]; CPR*16 bytes are staged.
 static const Inst kInst[] = {
@@ -886,6 +917,9 @@ static const Inst kInst[] = {
     QMLA_INST(2, QMLA_RMS_BF16, 256, 256, 2, 1, 3, 67, false, 32, 1, 4),
     QMLA_INST(2, QMLA_RMS_BF16, 256, 256, 1, 1, 2, 66, false, 64, 1, 4),
     QMLA_INST(2, QMLA_RMS_BF16, 768, 128, 2, 1, 2, 112, false, 32, 1, 4),
+    // the unpadded 12-head rows of the reference's numerics test at rank 256 (rank + 256 + 12 bf16
+    // elements: 1048 bytes, on 8-byte boundaries, tests/test_decode_numerics.py:60-67): narrow rows
+    QMLA_INST_DW(2, QMLA_RMS_BF16, 256, 256, 2, 1, 2, 66, false, 32, 1, 4),
 };
 
 static int g_cu_count[64];
@@ -956,13 +990,18 @@ static int validate(const qmla_decode_params* p, bool ptrs = true) {
     return QMLA_ERR_SHAPE;
   if (p->num_splits < 0 || p->num_splits > CF_MAXS || p->split_align < 0 || p->num_pages < 0) return QMLA_ERR_SHAPE;
   const int eb = elem_bytes(p->kv_dtype);
-  if ((ptrs && !aligned16(p->kv_cache)) || (p->page_stride * eb) % 16 || (p->token_stride * eb) % 16)
+  // 4-byte boundaries here; rows off 16-byte boundaries are served by the narrow-row instances only
+  if ((ptrs && (uintptr_t)p->kv_cache % 4) || (p->page_stride * eb) % 4 || (p->token_stride * eb) % 4)
     return QMLA_ERR_ALIGN;
   if (needed_row_bytes(p) > p->token_stride * eb && p->page_size > 1) return QMLA_ERR_SHAPE;
   // queries: element alignment (16-byte aligned rows take the vector loads)
   if (ptrs && ((uintptr_t)p->q_nope % 2 || (p->rope_w > 0 && (uintptr_t)p->q_pe % 2))) return QMLA_ERR_ALIGN;
   return QMLA_OK;
 }
+
+// No compiled kernel for these params: rows off 16-byte boundaries that no narrow-row instance
+// serves report the alignment, everything else the missing kernel.
+static int no_kernel(const qmla_decode_params* p) { return rows16(p) ? QMLA_ERR_NOKERNEL : QMLA_ERR_ALIGN; }
 
 // Workgroups per token range of a per-group instance: a request's rows per group (verify tokens x
 // heads) in blocks of 16*MB, at most kMaxRowSplit of them (each reads the range's cached rows; the
@@ -985,10 +1024,11 @@ static const Inst* find_inst(const qmla_decode_params* p) {
   for (const Inst& in : kInst) {
     if (in.eb != eb || in.rms != p->rms_mode || in.dcg != dcg || in.g != p->groups || in.cap != cap) continue;
     if (in.wp != wp_of(p->rope_w)) continue;
+    if (in.dw == rows16(p)) continue;   // narrow-row instances serve exactly the rows off 16-byte boundaries
     const int hs = row_splits(in, p);
     if (hs > kMaxRowSplit) continue;
     if ((int64_t)in.cpr * 16 < need) continue;
-    if ((int64_t)in.cpr * 16 > p->token_stride * eb) continue;   // never read past the row
+    if (!in.dw && (int64_t)in.cpr * 16 > p->token_stride * eb) continue;   // never read past the row
     if (!best || hs < best_hs || (hs == best_hs && (in.mb < best->mb || (in.mb == best->mb && in.cpr < best->cpr)))) {
       best = &in;
       best_hs = hs;
@@ -1214,7 +1254,7 @@ int qmla_decode_supported(const qmla_decode_params* p) {
   const int rc = validate(p, false);
   if (rc) return rc;
   if (p->d_c / p->groups > 2048) return QMLA_ERR_SHAPE;
-  return (ws_select(p) >= 0 || cs_select(p) >= 0 || find_inst(p)) ? QMLA_OK : QMLA_ERR_NOKERNEL;
+  return (ws_select(p) >= 0 || cs_select(p) >= 0 || find_inst(p)) ? QMLA_OK : no_kernel(p);
 }
 
 int qmla_plan_switch_tiles(const qmla_decode_params* p) {
@@ -1239,7 +1279,7 @@ int qmla_decode_partial(const qmla_decode_params* p, void* stream) {
   const int si = ws_select(p);
   const int wi = si >= 0 ? -1 : cs_select(p);
   const Inst* in = (si >= 0 || wi >= 0) ? nullptr : find_inst(p);
-  if (!in && wi < 0 && si < 0) return QMLA_ERR_NOKERNEL;
+  if (!in && wi < 0 && si < 0) return no_kernel(p);
   rc = p->num_splits == 0 ? check_balanced_ws(p) : check_fixed_ws(p);
   if (rc) return rc;
   KParams k = make_kparams(p);
@@ -1253,6 +1293,8 @@ int qmla_decode_partial(const qmla_decode_params* p, void* stream) {
 int qmla_combine(const qmla_decode_params* p, void* stream) {
   int rc = validate(p);
   if (rc) return rc;
+  // the same refusal as the decode pass for rows no kernel can stage
+  if (!rows16(p) && ws_select(p) < 0 && cs_select(p) < 0 && !find_inst(p)) return QMLA_ERR_ALIGN;
   if (p->num_splits == 1) return QMLA_OK;
   if (p->d_c / p->groups > 2048) return QMLA_ERR_SHAPE;
   rc = p->num_splits == 0 ? check_balanced_ws(p) : check_fixed_ws(p);
@@ -1314,7 +1356,7 @@ int qmla_decode(const qmla_decode_params* p, void* stream) {
   const int si = ws_select(p);
   const int wi = si >= 0 ? -1 : cs_select(p);
   const Inst* in = (si >= 0 || wi >= 0) ? nullptr : find_inst(p);
-  if (!in && wi < 0 && si < 0) return QMLA_ERR_NOKERNEL;
+  if (!in && wi < 0 && si < 0) return no_kernel(p);
   hipStream_t st = (hipStream_t)stream;
   if (p->num_splits > 0) {
     rc = check_fixed_ws(p);

@@ -142,6 +142,10 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, ui
 __device__ __forceinline__ void dma4(const void* gsrc, char* lds_base) {
   __builtin_amdgcn_global_load_lds(gsrc, QMLA_LDS(void, lds_base), 4, 0, 0);
 }
+// 4 bytes per lane from a buffer resource (lane l writes base + 4*l; outside the resource: zeros)
+__device__ __forceinline__ void dma4_buf(__amdgpu_buffer_rsrc_t rsrc, uint32_t voff, char* lds_base) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, QMLA_LDS(void, lds_base), 4, voff, 0, 0, 0);
+}
 
 // s_waitcnt vmcnt(N) with expcnt/lgkmcnt left unconstrained (gfx9 encoding).
 template <int N>

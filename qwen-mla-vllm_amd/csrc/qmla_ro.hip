@@ -618,6 +618,7 @@ static const RoFn kRo[] = {&ro_kernel<RO<3, true>>, &ro_kernel<RO<3, false>>};
 // The row-owner kernel serves GLA-g2 on fp8 + log8 rows: two groups of 256 latent columns, rope 64,
 // at most 48 rows per group, 608-byte staged rows holding every head's code, no logit cap.
 int ro_select(const qmla_decode_params* p) {
+  if (!rows16(p)) return -1;
   if (p->groups != 2 || p->kv_dtype != QMLA_KV_FP8 || p->rms_mode != QMLA_RMS_LOG8) return -1;
   if (p->d_c != 512 || p->rope_w != 64 || p->logit_cap > 0.f) return -1;
   if (p->qrows * (p->heads / 2) > 48) return -1;

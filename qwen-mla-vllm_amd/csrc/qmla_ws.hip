@@ -1009,6 +1009,7 @@ static int ws_table_select(const qmla_decode_params* p) {
 }
 
 int ws_select(const qmla_decode_params* p) {
+  if (!rows16(p)) return -1;
   const int ri = ro_select(p);
   if (ri >= 0) return kRoBase + ri;
   const int wi = ws_table_select(p);

@@ -22,7 +22,8 @@ ERR_NULL, ERR_SHAPE, ERR_ALIGN, ERR_WORKSPACE, ERR_MODE, ERR_LAUNCH, ERR_NOKERNE
 ERR_NAMES = {
     ERR_NULL: "QMLA_ERR_NULL (a required pointer is NULL)",
     ERR_SHAPE: "QMLA_ERR_SHAPE (unsupported or inconsistent dimension)",
-    ERR_ALIGN: "QMLA_ERR_ALIGN (row, page or base address not 16-byte aligned)",
+    ERR_ALIGN: "QMLA_ERR_ALIGN (row, page or base address off 4-byte boundaries, or off 16-byte ones in a layout "
+               "no narrow-row kernel serves)",
     ERR_WORKSPACE: "QMLA_ERR_WORKSPACE (workspace missing or too small)",
     ERR_MODE: "QMLA_ERR_MODE (unknown dtype / rms mode / split mode)",
     ERR_LAUNCH: "QMLA_ERR_LAUNCH (HIP launch failed)",

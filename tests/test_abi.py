@@ -94,8 +94,10 @@ def _valid_params(**over) -> _lib.DecodeParams:
     (dict(rms_mode=_lib.RMS_BF16), _lib.ERR_MODE),          # bf16 rms element in an fp8 cache
     (dict(rms_offset=-1), _lib.ERR_MODE),                    # mode says rms, offset says none
     (dict(out_dtype=9), _lib.ERR_MODE),
-    (dict(kv_cache=0x200008), _lib.ERR_ALIGN),
+    (dict(kv_cache=0x200008), _lib.ERR_ALIGN),               # 8-byte rows of a layout with no narrow-row kernel
     (dict(token_stride=600), _lib.ERR_ALIGN),
+    (dict(kv_cache=0x200002), _lib.ERR_ALIGN),               # off 4-byte boundaries: no kernel at all
+    (dict(token_stride=602), _lib.ERR_ALIGN),
     (dict(q_nope=0x100001), _lib.ERR_ALIGN),                 # queries need element alignment
     (dict(rows=9, qrows=2), _lib.ERR_SHAPE),
     (dict(heads=24, groups=5), _lib.ERR_SHAPE),
@@ -466,36 +468,33 @@ def test_prep_error_codes(over, code):
 
 
 @pytest.mark.parametrize("rank", [256, 768, 1792])
-def test_unpadded_rows_are_refused(rank):
+def test_unpadded_rows_take_narrow_row_kernels(rank):
     """The reference's standalone numerics test decodes rows of rank + 256 rope + 12 rms bf16 elements
-    with no padding (tests/test_decode_numerics.py:60-67, 89-91): 1048 / 2072 / 4120 bytes, 8-byte
-    aligned. The kernels stage rows with 16-byte LDS-DMA loads, so such rows are refused with
-    QMLA_ERR_ALIGN before any device work, and the Python entries raise it. The plugin pads
-    every cache row to 16 elements for its own 128-bit path (qwen_mla/mla_impl.py:252-271,
-    cp_async_safe in qwen_mla/fi_decode.py:117-127), so no deployed layout is affected; the 24-head
-    rows of the same test (1072 / 2096 / 4144 bytes) are 16-byte aligned and served."""
+    with no padding (tests/test_decode_numerics.py:60-67, 89-91): 1048 / 2072 / 4120 bytes, on 8-byte
+    boundaries. The plugin pads every cache row to 16 elements for its 128-bit path
+    (qwen_mla/mla_impl.py:252-271, cp_async_safe in qwen_mla/fi_decode.py:117-127); here such rows
+    route to the narrow-row instances (4 bytes a lane), which exist for exactly these layouts. Rows
+    off 4-byte boundaries, and narrow rows of any other layout, are refused with QMLA_ERR_ALIGN
+    before any device work, and the Python entries raise it (no launch here)."""
     from qmla.layout import row_dma_safe
     heads, page = 12, 400
     entry = rank + 256 + heads
     assert not row_dma_safe(entry, page, rank, rank + 256, 2)
-    cache = torch.zeros(3, page, 1, entry, dtype=torch.bfloat16)
-    q = torch.zeros(2, heads, rank + 256, dtype=torch.bfloat16)
-    o = torch.empty(2, heads, rank, dtype=torch.bfloat16)
-    lse = torch.empty(2, heads)
-    logits = torch.empty(2, heads, 8, rank + 1)
-    bt = torch.zeros(2, 3, dtype=torch.int32)
-    sl = torch.full((2,), 900, dtype=torch.int32)
-    from qmla.decode import build_params
-    p = build_params(q_nope=q, q_pe=q[..., rank:], kv_cache=cache, block_table=bt, seq_lens=sl, out=o, lse=lse,
-                     d_c=rank, rope_w=256, rms_offset=rank + 256, rms_mode=_lib.RMS_BF16, kv=_lib.KV_BF16,
-                     page_size=page, sm_scale=1 / 16.0, num_splits=8, split_align=16, workspace=logits,
-                     ws_strides=(logits.stride(0), logits.stride(1), logits.stride(2)))
-    assert _lib.lib().qmla_decode(ctypes.byref(p), None) == _lib.ERR_ALIGN
-    assert _lib.lib().qmla_decode_supported(ctypes.byref(p)) == _lib.ERR_ALIGN
-    # the 24-head rows of the same test are 16-byte aligned: the routing finds a kernel
+    p = _layout(_lib.KV_BF16, rank, 256, heads, _lib.RMS_BF16)
+    p.token_stride, p.page_stride, p.page_size = entry, entry * page, page
+    assert _lib.lib().qmla_decode_supported(ctypes.byref(p)) == _lib.OK
+    p.page_size, p.page_stride = 401, entry * 401          # pages off 16-byte boundaries as well
+    assert _lib.lib().qmla_decode_supported(ctypes.byref(p)) == _lib.OK
+    # the 24-head rows of the same test are on 16-byte boundaries: the ordinary kernels
     p24 = _layout(_lib.KV_BF16, rank, 256, 24, _lib.RMS_BF16)
     p24.token_stride, p24.page_stride, p24.page_size = rank + 256 + 24, (rank + 256 + 24) * page, page
     assert _lib.lib().qmla_decode_supported(ctypes.byref(p24)) == _lib.OK
+    # a narrow row of a layout no narrow-row instance serves (rope 64), and rows on 2-byte boundaries
+    pn = _layout(_lib.KV_BF16, rank, 64, heads, _lib.RMS_BF16)
+    pn.token_stride, pn.page_stride, pn.page_size = rank + 64 + heads, (rank + 64 + heads) * page, page
+    assert _lib.lib().qmla_decode_supported(ctypes.byref(pn)) == _lib.ERR_ALIGN
+    p.token_stride, p.page_stride = entry + 1, (entry + 1) * page
+    assert _lib.lib().qmla_decode_supported(ctypes.byref(p)) == _lib.ERR_ALIGN
     # what the Python entries raise on it (the error names the alignment)
     with pytest.raises(RuntimeError, match="ALIGN"):
-        _lib.check("qmla_decode", _lib.lib().qmla_decode(ctypes.byref(p), None))
+        _lib.check("qmla_decode_supported", _lib.lib().qmla_decode_supported(ctypes.byref(p)))

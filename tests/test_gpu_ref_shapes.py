@@ -161,3 +161,58 @@ def test_deployed_bf16_rank1792(gpu, heads, rope, ctx, batch):
         print(f"[bf16 rank 1792 heads {heads} rope {rope} ctx {ctx} {name}] max-abs {err:.3e} "
               f"(reference roundings {ref_err:.3e}, bound {bound:.3e}) lse {lerr:.3e}", flush=True)
         assert err < bound and lerr < 1e-2
+
+
+def _numerics_case(batch, heads, rank, page, lens, seed, shuffle):
+    """tests/test_decode_numerics.py:60-67: unpadded rows [latent | 256 packed rope | one bf16 rms per
+    head] (rank + 256 + heads elements), entries N(0, 0.05), rms |x| + 0.3, query N(0, 0.05)."""
+    g = torch.Generator().manual_seed(seed)
+    entry = rank + 256 + heads
+    pps = (max(lens) + page - 1) // page
+    cache = (torch.randn(batch * pps + 4, page, 1, entry, generator=g) * 0.05).to(torch.bfloat16)
+    cache[..., rank + 256:] = cache[..., rank + 256:].abs() + 0.3
+    q = (torch.randn(batch, heads, rank + 256, generator=g) * 0.05).to(torch.bfloat16)
+    order = torch.randperm(batch * pps, generator=g) if shuffle else torch.arange(batch * pps)
+    bt = order.reshape(batch, pps).to(torch.int32)
+    return cache, q, bt, torch.tensor(lens, dtype=torch.int32), entry
+
+
+@pytest.mark.parametrize("page", [400, 401])
+@pytest.mark.parametrize("heads", [12, 24])
+@pytest.mark.parametrize("rank", [256, 768, 1792])
+def test_numerics_test_rows(gpu, rank, heads, page):
+    """The reference's standalone numerics test (tests/test_decode_numerics.py:60-91): B 2 x 900 tokens
+    on 400-token pages, 8 fixed splits, sm_scale 1/16, through decode_attention_fwd. Its 12-head rows
+    (1048 / 2072 / 4120 bytes) sit on 8-byte boundaries and take the narrow-row kernels; the 24-head
+    rows are 16-byte aligned. Also a ragged, shuffled batch in the balanced mode (forward), and
+    401-token pages, whose page starts are off 16-byte boundaries too and whose tiles straddle pages.
+    Checked against the oracle at the bf16 bar and at the reference test's own bar (norm-relative
+    error < 5e-2)."""
+    import qmla
+    kw = dict(page_size=page, d_c=rank, rope_w=256, rms_offset=rank + 256, kv="bf16", rms_mode=ora.RMS_BF16,
+              sm_scale=1.0 / 16, rms_heads=heads)
+    for name, lens, shuffle in (("fixed", [900, 900], False), ("balanced", [2500, 1, 900, 0, 1777], True)):
+        batch = len(lens)
+        cache, q, bt, sl, entry = _numerics_case(batch, heads, rank, page, lens, seed=rank + heads + page, shuffle=shuffle)
+        cd, qd = cache.to(gpu), q.to(gpu)
+        if name == "fixed":
+            o = torch.zeros(batch, heads, rank, dtype=torch.bfloat16, device=gpu)
+            lse = torch.zeros(batch, heads, dtype=torch.bfloat16, device=gpu)
+            logits = torch.zeros(batch, heads, 8, rank + 1, dtype=torch.float32, device=gpu)
+            qmla.decode_attention_fwd(qd, cd, cd[..., :rank], o, lse, bt.to(gpu), sl.to(gpu), logits, 8, 1.0 / 16,
+                                      page, is_mla=True, rms_offset=rank + 256)
+        else:
+            o, lse = qmla.forward(qd[..., :rank], qd[..., rank:], cd, bt.to(gpu), sl.to(gpu), d_c=rank, rope_w=256,
+                                  rms_offset=rank + 256, page_size=page, sm_scale=1.0 / 16, rms_heads=heads)
+        torch.cuda.synchronize()
+        cu8 = cache.view(torch.uint8).view(cache.shape[0], page, entry * 2)
+        ro, rl = ora.mla_decode(q[..., :rank].float(), q[..., rank:].float(), cu8, bt, sl, **kw)
+        got = o.float().cpu()
+        err = (got - ro).abs().max().item()
+        rel = ((got - ro).norm() / ro.norm().clamp(min=1e-9)).item()
+        live = sl > 0
+        lerr = (lse.float().cpu()[live] - rl[live]).abs().max().item()
+        print(f"[numerics rows rank {rank} heads {heads} page {page} {name}] max-abs {err:.3e} rel {rel:.2e} "
+              f"lse {lerr:.3e}", flush=True)
+        assert err < TOL["bf16"] and rel < 5e-2, (err, rel)
+        assert lerr < 2e-2
