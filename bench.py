@@ -64,11 +64,19 @@ WORKLOADS = {
     # with the headline's batch and lengths
     "fp8_r768_b128": dict(batch=128, heads=24, d_c=768, rope_w=232, page_size=64, kv="fp8", rms_mode="log8",
                           seed=14, amp=4.0, lens=("lognormal", 16384, 0.5, 1024, 65536)),
+    # the plugin's deployed rows at rank 1792 (tests/test_fp8_kv.py:136-138, tests/test_two_pass_1792.py:
+    # 12-19): packed rope 232, 24 heads; FP8 with log8 codes at the headline's batch and lengths, and
+    # bf16 at B 64 (column-split kernel)
+    "fp8_r1792_b128": dict(batch=128, heads=24, d_c=1792, rope_w=232, page_size=64, kv="fp8", rms_mode="log8",
+                           seed=16, amp=4.0, lens=("lognormal", 16384, 0.5, 1024, 65536)),
+    "bf16_r1792_b64": dict(batch=64, heads=24, d_c=1792, rope_w=232, page_size=64, kv="bf16", rms_mode="bf16",
+                           seed=17, amp=1.0, lens=("lognormal", 16384, 0.5, 1024, 65536)),
     # wide latent: 16 fixed splits in the reference's attn_logits layout, then the combine
     "wide_b32": dict(batch=32, heads=24, d_c=1792, rope_w=64, page_size=1600, kv="bf16", rms_mode="bf16", seed=3,
                      amp=1.0, lens=("fixed", 65536), splits=16),
 }
-CPU_EVERY = {"wide_b32": 8, "pub_r256_h12": 4, "pub_r768_h12": 8, "pub_r1792_h12": 16}
+CPU_EVERY = {"wide_b32": 8, "pub_r256_h12": 4, "pub_r768_h12": 8, "pub_r1792_h12": 16, "fp8_r1792_b128": 16,
+             "bf16_r1792_b64": 16}
 GRAPH_CALLS = 16   # decode calls recorded into one HIP graph (one per layer of a 16-layer forward)
 
 
