@@ -117,8 +117,8 @@ struct CS {
   static constexpr int NRID = DW ? (T * CRM + 15) / 16 : NRI;
   static constexpr int ROWS = 16 * MB;
   static constexpr int XBW = NTB * MB;                   // partial-score f32x4 per lane
-  // reduce-scatter of the partial scores over the 8 slices (one latent group and token group: bf16
-  // rows with 16-token tiles and 32 rows, fp8 rows with 32-token tiles and 16 or 32 rows): wave c
+  // reduce-scatter of the partial scores over the 8 slices (one latent group and token group:
+  // 16-token tiles and 32 rows, fp8 rows with 32-token tiles and 16 or 32 rows): wave c
   // sums and softmaxes its RPW rows only, RE scores per lane, and P reaches the other waves through
   // LDS; otherwise every wave sums all partials and repeats the whole softmax
   static constexpr int RPW = ROWS / 8;                   // rows per reducer wave
@@ -128,11 +128,11 @@ struct CS {
   static constexpr int LDS0 = S * NW * SB + (S + 1) * NTG * T * RRS + NW * XBW * 64 * 16 + 4 * PIDN;
   static constexpr int LDSR = ROWS * RPS + 12 * ROWS + 32 + 48;
   static constexpr bool RSC = G == 1 && NCG == 8 && NTG == 1 && LDS0 + LDSR <= 163840 &&
-                              ((EB == 2 && NTB == 1 && MB == 2) || (EB == 1 && NTB == 2));
+                              ((NTB == 1 && MB == 2) || (EB == 1 && NTB == 2));
   static constexpr int RE = RSC ? RPW / RLR : 1;         // scores per lane
   static_assert(DCG % (32 * NCG) == 0, "whole 32-column k-steps per wave");
   static_assert(NTB == 1 || NTB == 2, "score tiles per token group");
-  static_assert(EB == 2 || NTB == 2, "fp8 values are read 8 tokens at a time");
+  static_assert(EB == 2 || NTB == 2 || CB % 2 == 0, "fp8 values of 16-token tiles are read two column blocks at a time");
   static_assert(RW == 16 || RW == 32 || RW == 64, "rope slice");
   static_assert(!PR || (WP % NCG == 0 && (WP == 128 || WP == 256)), "padded rope window");
   static_assert((S - 1) * (NID + NRID) < 64, "vmcnt range");
@@ -823,7 +823,7 @@ __device__ __forceinline__ void segment(const KParams& p, Smem<C>& sm, int req, 
       }
 
       // ---- P.V over this wave's columns ----
-      if constexpr (C::EB == 1) {
+      if constexpr (C::EB == 1 && C::NTB == 2) {
         // tr_b8: lanes 2r, 2r+1 of block q supply token row vtok(q, r); lane n gets column n
         const char* vb = st + vtok(lg, ln16 >> 1) * C::RS + 8 * (ln16 & 1);
         constexpr int VB = 4;
@@ -840,6 +840,32 @@ __device__ __forceinline__ void segment(const KParams& p, Smem<C>& sm, int req, 
               const bf16x8 vf = fp8x8_to_bf16(vr[j]);
 #pragma unroll
               for (int mb = 0; mb < C::MB; ++mb) acc[mb][c0 + j] = mfma16(pa8[mb], vf, acc[mb][c0 + j]);
+            }
+        }
+      } else if constexpr (C::EB == 1) {
+        // 16-token tiles: tr_b8 rows r = 0..3 of lane block q are tokens 4q .. 4q+3 of column block
+        // 2j, rows 4..7 the same tokens of block 2j+1, so lane n gets both blocks' column n for the
+        // k-slots 4q .. 4q+3 of two 16x16x16 products
+        const int r8 = ln16 >> 1;
+        const char* vb = st + (4 * lg + (r8 & 3)) * C::RS + 16 * (r8 >> 2) + 8 * (ln16 & 1);
+        constexpr int NP = C::CB / 2, VB = 4;
+#pragma unroll
+        for (int j0 = 0; j0 < NP; j0 += VB) {
+          i32x2 vr[VB];
+#pragma unroll
+          for (int j = 0; j < VB; ++j)
+            if (j0 + j < NP) vr[j] = lds_read_tr8_async(vb + 32 * (j0 + j));
+#pragma unroll
+          for (int j = 0; j < VB; ++j)
+            if (j0 + j < NP) {
+              lds_wait(vr[j]);
+              const s16x8 v8 = __builtin_bit_cast(s16x8, fp8x8_to_bf16(vr[j]));
+              const s16x4 va = {v8[0], v8[1], v8[2], v8[3]}, vc = {v8[4], v8[5], v8[6], v8[7]};
+#pragma unroll
+              for (int mb = 0; mb < C::MB; ++mb) {
+                acc[mb][2 * (j0 + j)] = mfma16k16(pa4[mb], va, acc[mb][2 * (j0 + j)]);
+                acc[mb][2 * (j0 + j) + 1] = mfma16k16(pa4[mb], vc, acc[mb][2 * (j0 + j) + 1]);
+              }
             }
         }
       } else if constexpr (C::NTB == 2) {
@@ -1096,16 +1122,21 @@ static const Inst kInst[] = {
     // 2072 / 4120 bytes, on 8-byte boundaries, tests/test_decode_numerics.py:60-67): narrow rows
     QMLA_CSX(2, QMLA_RMS_BF16, 768, 1, 8, 1, 1, 1, 3, 2, false, false, 256, true),
     QMLA_CSX(2, QMLA_RMS_BF16, 1792, 1, 8, 1, 1, 1, 2, 2, false, false, 256, true),
-    // fp8 cache, d_c 1792: 32-token tiles, 16 rows per workgroup (32 rows of 1792 accumulator and
-    // query columns exceed the register file), more heads split over gridDim.z.
-    // Rope 64, log8 codes (transposed rms reads: 2 chunks cover the heads of two row blocks):
+    // fp8 cache, d_c 1792, rope 64, log8 codes: 32-token tiles, 16 rows per workgroup, more heads
+    // split over gridDim.z (transposed rms reads: 2 chunks cover the heads of two row blocks):
     QMLA_CS(1, QMLA_RMS_LOG8, 1792, 1, 8, 1, 2, 1, 2, 2, false, true, 64),
     // the plugin's deployed fp8 layouts at rank 1792 (tests/test_fp8_kv.py:136-138): rope 116 with
     // 12 heads (window 128) and rope 232 with 24 heads (window 256); log8 / e4m3 / bf16-byte rms
-    // tails at offsets that are not 16-byte aligned (general rms reads)
+    // tails at offsets that are not 16-byte aligned (general rms reads). 24 heads in one workgroup
+    // per token range: 16-token tiles of 32 rows (the ring of 32-token tiles and their partial
+    // scores exceed the LDS at 32 rows; the reduce-scatter keeps the tile loop free of spills);
+    // 16 rows in 32-token tiles otherwise
     QMLA_CS(1, QMLA_RMS_LOG8, 1792, 1, 8, 1, 2, 1, 2, 1, false, false, 128),
     QMLA_CS(1, QMLA_RMS_E4M3, 1792, 1, 8, 1, 2, 1, 2, 1, false, false, 128),
     QMLA_CS(1, QMLA_RMS_BF16_BYTES, 1792, 1, 8, 1, 2, 1, 2, 2, false, false, 128),
+    QMLA_CS(1, QMLA_RMS_LOG8, 1792, 1, 8, 1, 1, 2, 3, 2, false, false, 256),
+    QMLA_CS(1, QMLA_RMS_E4M3, 1792, 1, 8, 1, 1, 2, 3, 2, false, false, 256),
+    QMLA_CS(1, QMLA_RMS_BF16_BYTES, 1792, 1, 8, 1, 1, 2, 3, 4, false, false, 256),
     QMLA_CS(1, QMLA_RMS_LOG8, 1792, 1, 8, 1, 2, 1, 2, 2, false, false, 256),
     QMLA_CS(1, QMLA_RMS_E4M3, 1792, 1, 8, 1, 2, 1, 2, 2, false, false, 256),
     QMLA_CS(1, QMLA_RMS_BF16_BYTES, 1792, 1, 8, 1, 2, 1, 2, 4, false, false, 256),

@@ -209,16 +209,16 @@ def test_plan_switch_tiles(kv, rms, qrows, groups, splits, tiles):
     (_lib.KV_FP8, 256, 232, 24, _lib.RMS_BF16_BYTES, 4),
     (_lib.KV_FP8, 768, 116, 12, _lib.RMS_LOG8, 4),         # ... rope 116, 12 heads (TP 2)
     (_lib.KV_BF16, 768, 232, 24, _lib.RMS_BF16, 4),        # column-split, 32 rows per workgroup
-    (_lib.KV_FP8, 1792, 232, 24, _lib.RMS_LOG8, 2),        # column-split, 16 rows per workgroup:
-                                                           # two tokens x 24 heads over 3 workgroups
+    (_lib.KV_FP8, 1792, 232, 24, _lib.RMS_LOG8, 4),        # column-split, 16-token tiles of 32 rows
     (_lib.KV_BF16, 1792, 232, 24, _lib.RMS_BF16, 4),       # column-split, 32 rows per workgroup
     (_lib.KV_BF16, 1792, 64, 24, _lib.RMS_BF16, 2),
     (_lib.KV_BF16, 1792, 300, 24, _lib.RMS_BF16, 1),       # no instance at all: no fold
 ])
 def test_verify_fold_every_format(kv, d_c, rope, heads, rms, fold):
     """Spec-verify folding asks the library which fold a compiled kernel serves: 4 query tokens x 24
-    heads fold into one request for every cache format and deployed layout up to rank 768 (2 on the
-    rank-1792 column-split instances with 16 rows per workgroup), so the cache is read once per
+    heads fold into one request for every cache format and deployed layout up to rank 768 and on the
+    rank-1792 rope-window layouts (2 on the rank-1792 rope-64 instances with 16 rows per workgroup
+    and per-row rms reads), so the cache is read once per
     request, or once per pair of tokens, instead of once per token (no launch, no pointers). The
     reference folds 2 tokens at 24 heads (64-row groups, mla_decode_attention.py:1291-1300)."""
     from qmla.decode import fold_rows

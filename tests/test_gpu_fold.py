@@ -22,7 +22,7 @@ FAMILIES = [
     ("fp8", "log8", 768, 12, 116, 4),          # ... rope 116, 12 heads (TP 2): 48 rows
     ("bf16", "bf16", 768, 24, 232, 4),         # column-split kernel, 32 rows per workgroup
     ("bf16", "bf16", 1792, 24, 64, 2),         # column-split kernel, 16 rows per workgroup
-    ("fp8", "log8", 1792, 24, 232, 2),
+    ("fp8", "log8", 1792, 24, 232, 4),         # column-split kernel, 16-token tiles of 32 rows
     ("bf16", "bf16", 1792, 24, 232, 4),        # column-split kernel, 32 rows per workgroup
 ]
 QTOK = 4
