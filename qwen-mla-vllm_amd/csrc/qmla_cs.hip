@@ -1175,6 +1175,7 @@ int cs_select(const qmla_decode_params* p) {
       if (in.rtr && delta) continue;     // transposed reads need an aligned tail
       const int64_t need = in.rtr ? 16 * in.mb * hs * rb : delta + (int64_t)p->heads * rb;   // transposed reads cover 16*MB*hs heads
       if (need > 16 * in.crm || (!in.dw && roff - delta + 16 * in.crm > ts)) continue;
+      if (in.dw && roff + (int64_t)p->rms_heads * rb > ts) continue;   // narrow rows load the row stride's bytes only
       if (!in.rtr && delta + (int64_t)p->rms_heads * rb > 16 * in.crm) continue;
     }
     if (best < 0 || hs < best_hs || (hs == best_hs && in.mb < cs::kInst[best].mb)) {

@@ -1029,6 +1029,7 @@ static const Inst* find_inst(const qmla_decode_params* p) {
     if (hs > kMaxRowSplit) continue;
     if ((int64_t)in.cpr * 16 < need) continue;
     if (!in.dw && (int64_t)in.cpr * 16 > p->token_stride * eb) continue;   // never read past the row
+    if (in.dw && need > p->token_stride * eb) continue;   // narrow rows load the row stride's bytes only
     if (!best || hs < best_hs || (hs == best_hs && (in.mb < best->mb || (in.mb == best->mb && in.cpr < best->cpr)))) {
       best = &in;
       best_hs = hs;
