@@ -302,12 +302,26 @@ __device__ __forceinline__ void segment(const KParams& p, Smem<C>& sm, int req, 
   //      [latent slice | rope slice | pad]; recomputed at every issue rather than held ----
   const int lat_off = (g * C::DCG + c * C::DCW) * C::EB;
   const int rope_off = C::DC * C::EB + rope_col * C::EB;
+  // fp8 rows (i < 64 NI): the quotient by CPW from a 24-bit multiply, exact below 2^20 / CPW, and
+  // selects instead of branches, so the issue costs a few full-rate VALU instructions per DMA
+  // instruction (fp8 rank 1792, rope 232, B 128: 1325 -> 1280 us; the bf16 rank-1792 instances
+  // measured 1% slower with it and keep the plain form)
+  constexpr uint32_t CPW_M = ((1u << 20) + C::CPW - 1) / C::CPW;
+  static_assert(64 * C::NI * C::CPW < (1 << 20) && 64 * C::NI < (1 << 10), "exact 24-bit quotient");
   auto src_chunk = [&](int i, int& row) {
-    const int t = i / C::CPW, ch = i - t * C::CPW;
-    int off;
-    if (ch < C::CL) off = lat_off + 16 * ch;
-    else if (ch < C::CL + C::CR) off = rope_off + 16 * (ch - C::CL);
-    else off = 0;
+    int t, ch, off;
+    if constexpr (C::EB == 1) {
+      t = (int)(__umul24((uint32_t)i, CPW_M) >> 20);
+      ch = i - (int)__umul24((uint32_t)t, (uint32_t)C::CPW);
+      off = ch < C::CL ? lat_off + 16 * ch : rope_off + 16 * (ch - C::CL);
+      off = ch < C::CL + C::CR ? off : 0;
+    } else {
+      t = i / C::CPW;
+      ch = i - t * C::CPW;
+      if (ch < C::CL) off = lat_off + 16 * ch;
+      else if (ch < C::CL + C::CR) off = rope_off + 16 * (ch - C::CL);
+      else off = 0;
+    }
     row = i < C::NCH ? t : 0;
     return off;
   };
@@ -352,6 +366,7 @@ __device__ __forceinline__ void segment(const KParams& p, Smem<C>& sm, int req, 
         // rows past the range end read as zeros (outside the resource)
         const __amdgpu_buffer_rsrc_t rs = make_rsrc(base, (uint32_t)(nvalid * TS));
         const int tb0 = tg * C::T;
+        const uint32_t ts24 = (uint32_t)TS;   // < 2^24 (the host checks)
         // chunk i of the stage lands at 16 i: instruction k carries chunks 64k.. (16 bytes a lane),
         // or 16k.. (narrow rows: lane ln the 4 bytes at 4 (ln & 3) of chunk 16k + ln / 4)
         constexpr int CPI = C::DW ? 16 : 64;
@@ -361,8 +376,10 @@ __device__ __forceinline__ void segment(const KParams& p, Smem<C>& sm, int req, 
           int row;
           const int off = src_chunk(CPI * k + cl, row) + bl;
           if (CPI * k + CPI <= C::NCH || CPI * k + cl < C::NCH) {
-            if constexpr (C::DW) dma4_buf(rs, (uint32_t)((tb0 + row) * (int)TS + off), dst + k * 256);
-            else dma16_buf<kCpolDefault>(rs, (uint32_t)((tb0 + row) * (int)TS + off), dst + k * 1024);
+            const uint32_t vo = C::EB == 1 ? __umul24((uint32_t)(tb0 + row), ts24) + (uint32_t)off
+                                           : (uint32_t)((tb0 + row) * (int)TS + off);
+            if constexpr (C::DW) dma4_buf(rs, vo, dst + k * 256);
+            else dma16_buf<kCpolDefault>(rs, vo, dst + k * 1024);
           }
         }
         if (rms_wave) {
@@ -371,7 +388,8 @@ __device__ __forceinline__ void segment(const KParams& p, Smem<C>& sm, int req, 
             const int j = CPI * k + cl;
             const int row = j / (C::CRM > 0 ? C::CRM : 1);
             if (CPI * k + CPI <= C::T * C::CRM || j < C::T * C::CRM) {
-              const uint32_t o = (uint32_t)((tb0 + row) * (int)TS + roff_al + 16 * (j - row * C::CRM) + bl);
+              const uint32_t o = (C::EB == 1 ? __umul24((uint32_t)(tb0 + row), ts24) : (uint32_t)((tb0 + row) * (int)TS)) +
+                                 (uint32_t)(roff_al + 16 * (j - row * C::CRM) + bl);
               if constexpr (C::DW) dma4_buf(rs, o, rdst + k * 256);
               else dma16_buf<kCpolDefault>(rs, o, rdst + k * 1024);
             }
@@ -1168,6 +1186,7 @@ int cs_select(const qmla_decode_params* p) {
     // rope 64 exactly, or a partial rope inside the instance's padded window
     if (in.wp == 64 ? p->rope_w != 64 : (p->rope_w < 1 || p->rope_w > in.wp)) continue;
     if ((int64_t)p->d_c * eb + (int64_t)in.wp * eb > ts) continue;   // latent + rope window inside the row
+    if (ts >= (1 << 24)) continue;                                     // 24-bit row offsets in the DMA issue
     if (in.crm > 0) {
       const int rb = (p->rms_mode == QMLA_RMS_BF16 || p->rms_mode == QMLA_RMS_BF16_BYTES) ? 2 : 1;
       const int64_t roff = (int64_t)p->rms_offset * eb;
