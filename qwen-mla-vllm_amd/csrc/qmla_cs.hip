@@ -130,6 +130,10 @@ struct CS {
   static constexpr bool RSC = G == 1 && NCG == 8 && NTG == 1 && LDS0 + LDSR <= 163840 &&
                               ((NTB == 1 && MB == 2) || (EB == 1 && NTB == 2));
   static constexpr int RE = RSC ? RPW / RLR : 1;         // scores per lane
+  // fp8 rows: the per-lane DMA offsets of a tile (the same for every tile of a call) in an LDS
+  // table, where it fits, instead of recomputing them at every issue
+  static constexpr int NDV = NID + NRID;
+  static constexpr bool DVT = EB == 1 && !DW && LDS0 + (RSC ? LDSR : 0) + NW * NDV * 256 + 64 <= 163840;
   static_assert(DCG % (32 * NCG) == 0, "whole 32-column k-steps per wave");
   static_assert(NTB == 1 || NTB == 2, "score tiles per token group");
   static_assert(EB == 2 || NTB == 2 || CB % 2 == 0, "fp8 values of 16-token tiles are read two column blocks at a time");
@@ -150,6 +154,11 @@ struct RsShared {
   alignas(16) float rfin[2][ROWS];
 };
 struct RsNone {};
+template <int NW, int NDV>
+struct DvTable {
+  uint32_t o[NW][NDV][64];
+};
+struct DvNone {};
 
 template <class C>
 struct Smem {
@@ -158,6 +167,7 @@ struct Smem {
   f32x4 xb[C::NW][C::XBW][64];                 // partial scores
   int pid[PIDN];
   [[no_unique_address]] std::conditional_t<C::RSC, RsShared<C::ROWS, C::RPS>, RsNone> rs;
+  [[no_unique_address]] std::conditional_t<C::DVT, DvTable<C::NW, C::NDV>, DvNone> dv;
 };
 
 
@@ -339,6 +349,26 @@ __device__ __forceinline__ void segment(const KParams& p, Smem<C>& sm, int req, 
     for (int cb = 0; cb < C::CB; ++cb) acc[mb][cb] = f32x4{0.f, 0.f, 0.f, 0.f};
   }
 
+  if constexpr (C::DVT) {
+    // this wave's DMA offsets inside a contiguous tile (rows from the token group's first row)
+    const uint32_t ts24 = (uint32_t)TS;   // < 2^24 (the host checks)
+#pragma unroll
+    for (int k = 0; k < C::NID; ++k) {
+      int row;
+      const int off = src_chunk(64 * k + lane, row);
+      sm.dv.o[w][k][lane] = __umul24((uint32_t)(tg * C::T + row), ts24) + (uint32_t)off;
+    }
+    if (rms_wave) {
+#pragma unroll
+      for (int k = 0; k < C::NRID; ++k) {
+        const int j = 64 * k + lane;
+        const int row = j / (C::CRM > 0 ? C::CRM : 1);
+        sm.dv.o[w][C::NID + k][lane] =
+            __umul24((uint32_t)(tg * C::T + row), ts24) + (uint32_t)(roff_al + 16 * (j - row * C::CRM));
+      }
+    }
+  }
+
   // sub-ranges of at most PIDN pages, in whole tiles
   int sub = (PIDN - 1) * P;
   sub = sub < C::TT ? C::TT : sub / C::TT * C::TT;
@@ -371,6 +401,20 @@ __device__ __forceinline__ void segment(const KParams& p, Smem<C>& sm, int req, 
         // or 16k.. (narrow rows: lane ln the 4 bytes at 4 (ln & 3) of chunk 16k + ln / 4)
         constexpr int CPI = C::DW ? 16 : 64;
         const int cl = C::DW ? ln >> 2 : ln, bl = C::DW ? 4 * (ln & 3) : 0;
+        if constexpr (C::DVT) {
+          uint32_t vo[C::NDV];
+#pragma unroll
+          for (int k = 0; k < C::NDV; ++k) vo[k] = sm.dv.o[w][k][ln];
+#pragma unroll
+          for (int k = 0; k < C::NID; ++k)
+            if (64 * k + 64 <= C::NCH || 64 * k + ln < C::NCH) dma16_buf<kCpolDefault>(rs, vo[k], dst + k * 1024);
+          if (rms_wave) {
+#pragma unroll
+            for (int k = 0; k < C::NRID; ++k)
+              if (64 * k + 64 <= C::T * C::CRM || 64 * k + ln < C::T * C::CRM)
+                dma16_buf<kCpolDefault>(rs, vo[C::NID + k], rdst + k * 1024);
+          }
+        } else {
 #pragma unroll
         for (int k = 0; k < C::NID; ++k) {
           int row;
@@ -394,6 +438,7 @@ __device__ __forceinline__ void segment(const KParams& p, Smem<C>& sm, int req, 
               else dma16_buf<kCpolDefault>(rs, o, rdst + k * 1024);
             }
           }
+        }
         }
       } else {
         // pages change inside a tile: per-lane page lookup; rows past the end repeat the last row
