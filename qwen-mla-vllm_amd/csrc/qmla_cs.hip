@@ -55,6 +55,33 @@ __device__ __forceinline__ i32x4 ldsr128(const char* p) {
   asm volatile("ds_read_b128 %0, %1" : "=v"(r) : "v"(lds_addr(p)));
   return r;
 }
+// reads at a base register plus an immediate offset, and a wait for all but the N youngest LDS
+// operations of the wave (LDS operations complete in order, so the older reads are in)
+template <int OFF>
+__device__ __forceinline__ i32x2 ldsr64_off(uint32_t a) {
+  i32x2 r;
+  asm volatile("ds_read_b64 %0, %1 offset:%2" : "=v"(r) : "v"(a), "n"(OFF));
+  return r;
+}
+template <int OFF>
+__device__ __forceinline__ i32x2 ldstr8_off(uint32_t a) {
+  i32x2 r;
+  asm volatile("ds_read_b64_tr_b8 %0, %1 offset:%2" : "=v"(r) : "v"(a), "n"(OFF));
+  return r;
+}
+template <int N, class T>
+__device__ __forceinline__ void lds_wait_n(T& v) {
+  static_assert(N >= 0 && N < 16, "lgkmcnt range");
+  asm volatile("s_waitcnt lgkmcnt(%1)" : "+v"(v) : "n"(N));
+}
+// f(integral_constant<int, I>) for I = B .. E-1
+template <int B, int E, class F>
+__device__ __forceinline__ void sfor(F&& f) {
+  if constexpr (B < E) {
+    f(std::integral_constant<int, B>{});
+    sfor<B + 1, E>(f);
+  }
+}
 __device__ __forceinline__ i32x2 ldsr64(const char* p) {
   i32x2 r;
   asm volatile("ds_read_b64 %0, %1" : "=v"(r) : "v"(lds_addr(p)));
@@ -497,20 +524,21 @@ __device__ __forceinline__ void segment(const KParams& p, Smem<C>& sm, int req, 
         for (int mb = 0; mb < C::MB; ++mb) sp[tb][mb] = f32x4{0.f, 0.f, 0.f, 0.f};
         const char* kr = st + tok_of(tb, ln16) * C::RS;
         if constexpr (C::EB == 1) {
+          // all K reads at once (base register + immediate offsets), each k-step as soon as its
+          // read is in
           i32x2 kv[C::KS];
-#pragma unroll
-          for (int ks = 0; ks < C::KS; ++ks) kv[ks] = ldsr64(kr + 32 * ks + 8 * lg);
+          const uint32_t kb = lds_addr(kr + 8 * lg);
+          sfor<0, C::KS>([&](auto ks) { kv[ks] = ldsr64_off<32 * ks>(kb); });
           i32x2 rv[RKS];
 #pragma unroll
           for (int k = 0; k < RKS; ++k)
             rv[k] = ldsr64(kr + 16 * C::CL + (C::RW == 16 ? 8 * (lg & 1) : 32 * k + 8 * lg));
-#pragma unroll
-          for (int ks = 0; ks < C::KS; ++ks) {
-            lds_wait(kv[ks]);
+          sfor<0, C::KS>([&](auto ks) {
+            lds_wait_n<C::KS - 1 - ks + RKS>(kv[ks]);
             const bf16x8 kf = fp8x8_to_bf16(kv[ks]);
 #pragma unroll
             for (int mb = 0; mb < C::MB; ++mb) sp[tb][mb] = mfma16(kf, qf[ks][mb], sp[tb][mb]);
-          }
+          });
 #pragma unroll
           for (int k = 0; k < RKS; ++k) {
             lds_wait(rv[k]);
@@ -910,27 +938,20 @@ __device__ __forceinline__ void segment(const KParams& p, Smem<C>& sm, int req, 
         // 2j, rows 4..7 the same tokens of block 2j+1, so lane n gets both blocks' column n for the
         // k-slots 4q .. 4q+3 of two 16x16x16 products
         const int r8 = ln16 >> 1;
-        const char* vb = st + (4 * lg + (r8 & 3)) * C::RS + 16 * (r8 >> 2) + 8 * (ln16 & 1);
-        constexpr int NP = C::CB / 2, VB = 4;
+        const uint32_t vb = lds_addr(st + (4 * lg + (r8 & 3)) * C::RS + 16 * (r8 >> 2) + 8 * (ln16 & 1));
+        constexpr int NP = C::CB / 2;
+        i32x2 vr[NP];
+        sfor<0, NP>([&](auto j) { vr[j] = ldstr8_off<32 * j>(vb); });
+        sfor<0, NP>([&](auto j) {
+          lds_wait_n<NP - 1 - j>(vr[j]);
+          const s16x8 v8 = __builtin_bit_cast(s16x8, fp8x8_to_bf16(vr[j]));
+          const s16x4 va = {v8[0], v8[1], v8[2], v8[3]}, vc = {v8[4], v8[5], v8[6], v8[7]};
 #pragma unroll
-        for (int j0 = 0; j0 < NP; j0 += VB) {
-          i32x2 vr[VB];
-#pragma unroll
-          for (int j = 0; j < VB; ++j)
-            if (j0 + j < NP) vr[j] = lds_read_tr8_async(vb + 32 * (j0 + j));
-#pragma unroll
-          for (int j = 0; j < VB; ++j)
-            if (j0 + j < NP) {
-              lds_wait(vr[j]);
-              const s16x8 v8 = __builtin_bit_cast(s16x8, fp8x8_to_bf16(vr[j]));
-              const s16x4 va = {v8[0], v8[1], v8[2], v8[3]}, vc = {v8[4], v8[5], v8[6], v8[7]};
-#pragma unroll
-              for (int mb = 0; mb < C::MB; ++mb) {
-                acc[mb][2 * (j0 + j)] = mfma16k16(pa4[mb], va, acc[mb][2 * (j0 + j)]);
-                acc[mb][2 * (j0 + j) + 1] = mfma16k16(pa4[mb], vc, acc[mb][2 * (j0 + j) + 1]);
-              }
-            }
-        }
+          for (int mb = 0; mb < C::MB; ++mb) {
+            acc[mb][2 * j] = mfma16k16(pa4[mb], va, acc[mb][2 * j]);
+            acc[mb][2 * j + 1] = mfma16k16(pa4[mb], vc, acc[mb][2 * j + 1]);
+          }
+        });
       } else if constexpr (C::NTB == 2) {
         // tr_b16 twice: k-slots 8q..8q+3 (score tile 0) and 8q+4..8q+7 (score tile 1)
         const char* v0 = st + tok_of(0, 4 * lg + (ln16 >> 2)) * C::RS + 8 * (ln16 & 3);
