@@ -64,6 +64,18 @@ __device__ __forceinline__ i32x2 ldsr64_off(uint32_t a) {
   return r;
 }
 template <int OFF>
+__device__ __forceinline__ i32x4 ldsr128_off(uint32_t a) {
+  i32x4 r;
+  asm volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(r) : "v"(a), "n"(OFF));
+  return r;
+}
+template <int OFF>
+__device__ __forceinline__ i32x2 ldstr16_off(uint32_t a) {
+  i32x2 r;
+  asm volatile("ds_read_b64_tr_b16 %0, %1 offset:%2" : "=v"(r) : "v"(a), "n"(OFF));
+  return r;
+}
+template <int OFF>
 __device__ __forceinline__ i32x2 ldstr8_off(uint32_t a) {
   i32x2 r;
   asm volatile("ds_read_b64_tr_b8 %0, %1 offset:%2" : "=v"(r) : "v"(a), "n"(OFF));
@@ -551,22 +563,19 @@ __device__ __forceinline__ void segment(const KParams& p, Smem<C>& sm, int req, 
             for (int mb = 0; mb < C::MB; ++mb) sp[tb][mb] = mfma16(rf, qr8[k][mb], sp[tb][mb]);
           }
         } else {
-          constexpr int KB = 4;   // k-steps per batch of LDS reads
-#pragma unroll
-          for (int k0 = 0; k0 < C::KS; k0 += KB) {
+          constexpr int KB = 4;   // k-steps per batch of LDS reads, each used as soon as it is in
+          const uint32_t kb = lds_addr(kr + 16 * lg);
+          sfor<0, (C::KS + KB - 1) / KB>([&](auto b) {
+            constexpr int k0 = KB * b, nb = C::KS - k0 < KB ? C::KS - k0 : KB;
             i32x4 kv[KB];
+            sfor<0, nb>([&](auto j) { kv[j] = ldsr128_off<64 * (k0 + j)>(kb); });
+            sfor<0, nb>([&](auto j) {
+              lds_wait_n<nb - 1 - j>(kv[j]);
+              const bf16x8 kf = __builtin_bit_cast(bf16x8, kv[j]);
 #pragma unroll
-            for (int j = 0; j < KB; ++j)
-              if (k0 + j < C::KS) kv[j] = ldsr128(kr + 64 * (k0 + j) + 16 * lg);
-#pragma unroll
-            for (int j = 0; j < KB; ++j)
-              if (k0 + j < C::KS) {
-                lds_wait(kv[j]);
-                const bf16x8 kf = __builtin_bit_cast(bf16x8, kv[j]);
-#pragma unroll
-                for (int mb = 0; mb < C::MB; ++mb) sp[tb][mb] = mfma16(kf, qf[k0 + j][mb], sp[tb][mb]);
-              }
-          }
+              for (int mb = 0; mb < C::MB; ++mb) sp[tb][mb] = mfma16(kf, qf[k0 + j][mb], sp[tb][mb]);
+            });
+          });
 #pragma unroll
           for (int k = 0; k < RKS; ++k) {
             i32x4 rv = ldsr128(kr + 16 * C::CL + (C::RW == 16 ? 16 * (lg & 1) : 64 * k + 16 * lg));
@@ -983,23 +992,19 @@ __device__ __forceinline__ void segment(const KParams& p, Smem<C>& sm, int req, 
             }
         }
       } else {
-        const char* vb = st + (4 * lg + (ln16 >> 2)) * C::RS + 8 * (ln16 & 3);
-        constexpr int VB = 7;
-#pragma unroll
-        for (int c0 = 0; c0 < C::CB; c0 += VB) {
+        const uint32_t vb = lds_addr(st + (4 * lg + (ln16 >> 2)) * C::RS + 8 * (ln16 & 3));
+        constexpr int VB = 7;   // column blocks per batch of reads, each used as soon as it is in
+        sfor<0, (C::CB + VB - 1) / VB>([&](auto b) {
+          constexpr int c0 = VB * b, nb = C::CB - c0 < VB ? C::CB - c0 : VB;
           i32x2 vr[VB];
+          sfor<0, nb>([&](auto j) { vr[j] = ldstr16_off<32 * (c0 + j)>(vb); });
+          sfor<0, nb>([&](auto j) {
+            lds_wait_n<nb - 1 - j>(vr[j]);
+            const s16x4 vf = __builtin_bit_cast(s16x4, vr[j]);
 #pragma unroll
-          for (int j = 0; j < VB; ++j)
-            if (c0 + j < C::CB) vr[j] = lds_read_tr16_async(vb + 32 * (c0 + j));
-#pragma unroll
-          for (int j = 0; j < VB; ++j)
-            if (c0 + j < C::CB) {
-              lds_wait(vr[j]);
-              const s16x4 vf = __builtin_bit_cast(s16x4, vr[j]);
-#pragma unroll
-              for (int mb = 0; mb < C::MB; ++mb) acc[mb][c0 + j] = mfma16k16(pa4[mb], vf, acc[mb][c0 + j]);
-            }
-        }
+            for (int mb = 0; mb < C::MB; ++mb) acc[mb][c0 + j] = mfma16k16(pa4[mb], vf, acc[mb][c0 + j]);
+          });
+        });
       }
       if (t + C::S < nt) issue(t + C::S);
     }
