@@ -47,10 +47,12 @@ class Case:
         return int(self.seq_lens.to(torch.int64).sum())
 
 
-def row_width(d_c: int, rope_w: int, heads: int, kv: str, rms_mode: str) -> int:
+def row_width(d_c: int, rope_w: int, heads: int, kv: str, rms_mode: str, pad: bool = True) -> int:
+    """Cache row elements: [latent | rope | rms], padded to 16 elements as the plugin pads its rows
+    (mla_impl.py:261-271), or unpadded as the reference's numerics test builds them."""
     per = 2 if (kv == "fp8" and rms_mode == "bf16_bytes") else 1
     raw = d_c + rope_w + (0 if rms_mode == "none" else heads * per)
-    return ((raw + 15) // 16) * 16
+    return ((raw + 15) // 16) * 16 if pad else raw
 
 
 def _log8(rms: torch.Tensor) -> torch.Tensor:
@@ -67,7 +69,7 @@ def _e4m3_bytes(x: torch.Tensor, inv: torch.Tensor) -> torch.Tensor:
 def make_case(*, batch: int, heads: int, d_c: int, rope_w: int, page_size: int, lens, kv: str = "bf16",
               rms_mode: str | None = None, seed: int = 0, device="cpu", qrows: int = 1, groups: int = 1,
               amp: float = 1.0, rms: str = "row", q_amp: float = 1.0, shuffle: bool = True,
-              extra_pages: int = 3, chunk_tokens: int = 1 << 20) -> Case:
+              extra_pages: int = 3, chunk_tokens: int = 1 << 20, pad: bool = True) -> Case:
     """Build a case. `lens` are per-request lengths (the last verify row's length when qrows > 1).
 
     rms = "row": every head's divisor is the RMS of the row's (amplified) latent; "spread": per-head
@@ -88,7 +90,7 @@ def make_case(*, batch: int, heads: int, d_c: int, rope_w: int, page_size: int, 
     for b in range(n_req):
         bt_req[b, :pages_per[b]] = perm[k:k + pages_per[b]].to(torch.int32)
         k += pages_per[b]
-    row = row_width(d_c, rope_w, heads, kv, rms_mode)
+    row = row_width(d_c, rope_w, heads, kv, rms_mode, pad)
     dev = torch.device(device)
     gd = torch.Generator(device=dev).manual_seed(seed + 1)
     # per-layer fp8 scale from an unscaled calibration draw (absmax / 448)

@@ -216,3 +216,24 @@ def test_numerics_test_rows(gpu, rank, heads, page):
               f"lse {lerr:.3e}", flush=True)
         assert err < TOL["bf16"] and rel < 5e-2, (err, rel)
         assert lerr < 2e-2
+
+
+@pytest.mark.parametrize("qrows", [2, 4])
+@pytest.mark.parametrize("rank", [256, 768, 1792])
+def test_numerics_test_rows_verify(gpu, rank, qrows):
+    """The same unpadded 12-head rows (rank + 256 + 12 bf16 elements, on 8-byte boundaries) with
+    spec-verify rows folded into one request (2 or 4 tokens x 12 heads: 24 or 48 rows, split over the
+    narrow-row instances' workgroups where they exceed one), 401-token pages, short and empty requests,
+    through forward in the balanced mode and with 8 fixed splits."""
+    import qmla
+    from tests.mla_cases import check_decode, make_case
+    c = make_case(batch=5, heads=12, d_c=rank, rope_w=256, page_size=401, lens=[2500, 3, 900, 0, 1777],
+                  kv="bf16", rms_mode="bf16", seed=rank + qrows, device=gpu, qrows=qrows, rms="spread", pad=False)
+    assert c.cache.shape[-1] == rank + 256 + 12
+    for splits in (0, 8):
+        kw = dict(num_splits=splits) if splits else {}
+        o, lse = qmla.forward(c.q_nope, c.q_pe, c.cache, c.block_table, c.seq_lens, d_c=c.d_c, rope_w=c.rope_w,
+                              rms_offset=c.d_c + c.rope_w, page_size=c.page_size, sm_scale=c.sm_scale, qrows=qrows,
+                              **kw)
+        torch.cuda.synchronize()
+        check_decode(f"numerics rows rank {rank} q{qrows} splits {splits}", c, o, lse, num_splits=max(splits, 1))
