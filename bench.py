@@ -418,7 +418,7 @@ def main():
                     help="time a kernel either side of the decode instead (writer, gather, prep)")
     args = ap.parse_args()
     if args.gpus != 1:
-        print(json.dumps({"error": "this build measures one GPU only: the decode shards by request "
+        print(json.dumps({"error": "the benchmark measures one GPU only: the decode shards by request "
                                    "(no collectives); run with --gpus 1"}))
         sys.exit(2)
 
