@@ -240,8 +240,12 @@ def cpu_reference_small():
 ADJACENT = {
     # FP8 log8 rows for a 16384-token prefill chunk written to random free slots
     "write_n16384": dict(n=16384, heads=24, d_c=512, rope_w=64, page_size=64, seed=5),
+    # ... a 262144-token prefill (long prompts), where launch and ramp no longer dominate
+    "write_n262144": dict(n=262144, heads=24, d_c=512, rope_w=64, page_size=64, seed=5),
     # 4 x 4096 cached tokens of FP8 log8 rows gathered into a bf16 workspace
     "gather_n16384": dict(n=16384, seqs=4, heads=24, d_c=512, rope_w=64, page_size=64, seed=6),
+    # ... 4 x 65536 cached tokens
+    "gather_n262144": dict(n=262144, seqs=4, heads=24, d_c=512, rope_w=64, page_size=64, seed=6),
     # the decode step's q / k_pe prep at B=128: 24 heads of 256, rope 64 in 4 groups, d_c 512
     "prep_b128": dict(n=128, heads=24, head_dim=256, rd=64, kv_heads=4, rope_group=6, d_c=512, declared=296,
                       max_pos=65536, seed=7),
@@ -299,7 +303,7 @@ def adjacent(args):
         ksf = float(ks.cpu())
         cpu_fn = lambda: ora.fp8_row_bytes(kc, kp, packed_rope=W, n_heads=H, k_scale=ksf, rms_mode=ora.RMS_LOG8)
         cpu_rows, sample = n, f"all {n} rows, numpy oracle (fp8_row_bytes)"
-        cfg = {"workload": "mla_cache_write_n16384", "tokens": n, "heads": H, "d_c": d_c, "d_r": W,
+        cfg = {"workload": f"mla_cache_write_n{n}", "tokens": n, "heads": H, "d_c": d_c, "d_r": W,
                "kv": "fp8", "rms": "log8", "row_bytes": 608}
         metric, dtype = "MLA FP8 cache-row writer rows/s + achieved HBM GB/s", "bf16->e4m3"
     elif kind == "gather":
@@ -326,7 +330,7 @@ def adjacent(args):
         cpu_fn = lambda: ora.gather_context(cb, btn, cu.numpy(), t2s.numpy(), n, None, kv="fp8", scale=ks,
                                             rms_offset=c.rms_offset, n_heads=H, rms_mode=ora.RMS_LOG8)
         cpu_rows, sample = n, f"all {n} rows, numpy oracle (gather_context)"
-        cfg = {"workload": "mla_gather_n16384", "tokens": n, "seqs": S, "heads": H, "d_c": w["d_c"],
+        cfg = {"workload": f"mla_gather_n{n}", "tokens": n, "seqs": S, "heads": H, "d_c": w["d_c"],
                "d_r": w["rope_w"], "page_size": P, "kv": "fp8", "rms": "log8", "dst": "bf16"}
         metric, dtype = "MLA prefill context gather rows/s + achieved HBM GB/s", "e4m3->bf16"
     else:

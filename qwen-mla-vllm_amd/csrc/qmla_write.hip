@@ -14,6 +14,9 @@
 #include "qmla_device.h"
 
 namespace qmla {
+// rows from which the writer and the gather take several rows a wave (measured on MI355X: at 16384
+// rows one row a wave is as fast or faster, at 262144 several rows a wave 23% / 37% faster)
+constexpr int kMultiRowMin = 65536;
 namespace wr {
 
 constexpr int ROWS_PER_WG = 4;
@@ -48,8 +51,7 @@ __device__ __forceinline__ uint32_t pack_e4m3(float a, float b, float c, float d
 }
 
 // 8 bf16 inputs -> 8 e4m3 bytes
-__device__ __forceinline__ uint2 quant8(const uint16_t* src, float inv) {
-  const uint4 raw = *reinterpret_cast<const uint4*>(src);
+__device__ __forceinline__ uint2 quant8r(const uint4 raw, float inv) {
   const uint32_t w[4] = {raw.x, raw.y, raw.z, raw.w};
   float f[8];
 #pragma unroll
@@ -59,6 +61,9 @@ __device__ __forceinline__ uint2 quant8(const uint16_t* src, float inv) {
   }
   return make_uint2(pack_e4m3(f[0], f[1], f[2], f[3]), pack_e4m3(f[4], f[5], f[6], f[7]));
 }
+__device__ __forceinline__ uint2 quant8(const uint16_t* src, float inv) {
+  return quant8r(*reinterpret_cast<const uint4*>(src), inv);
+}
 
 // log8 code of one rms value: round-half-even((log2(max(r, 1e-30)) + 3) * (255 / 6)), clamped to
 // [0, 255]; the logarithm is evaluated in double and rounded once to fp32, the rest in fp32
@@ -66,6 +71,16 @@ __device__ __forceinline__ uint32_t log8_code(float r) {
   const float rc = r < 1e-30f ? 1e-30f : r;   // clamp_min keeps NaN
   const float lg = (float)log2((double)rc);
   const float c = rintf((lg - (-3.0f)) * 42.5f);
+  return (uint32_t)(c < 0.0f ? 0.0f : (c > 255.0f ? 255.0f : c));
+}
+// The same code from the hardware log2 (within 2 ulp of the rounded double one): (lg + 3) * 42.5
+// then moves by less than 2e-4 inside the code range, so wherever it lies 1e-3 or more from a
+// rounding midpoint it rounds as the double path does; the few values nearer one take that path.
+__device__ __forceinline__ uint32_t log8_code_fast(float r) {
+  const float rc = r < 1e-30f ? 1e-30f : r;
+  const float y = (__builtin_amdgcn_logf(rc) - (-3.0f)) * 42.5f;
+  if (fabsf(y - floorf(y) - 0.5f) < 1e-3f) return log8_code(r);
+  const float c = rintf(y);
   return (uint32_t)(c < 0.0f ? 0.0f : (c > 255.0f ? 255.0f : c));
 }
 
@@ -112,6 +127,65 @@ __global__ __launch_bounds__(64 * ROWS_PER_WG) void write_kernel(const WParams p
       *reinterpret_cast<uint4*>(d16 + c) = *reinterpret_cast<const uint4*>(kc + c);
     const int pe = p.rope_w + (p.rms_mode == QMLA_RMS_BF16 ? p.rms_heads : 0);
     for (int c = lane; c < pe; c += 64) d16[p.d_c + c] = kp[c];
+  }
+}
+
+// FP8 rows with latents up to 512 * NCL columns, a rope up to 512 and up to 64 rms heads: one wave
+// writes WROWS rows, all of their input loads in flight before the first conversion (a lone row's
+// load latency would otherwise bound a wave), the same bytes as write_kernel.
+constexpr int WROWS = 4;
+template <int NCL>
+__global__ __launch_bounds__(256) void write_fp8_kernel(const WParams p) {
+  const int lane = threadIdx.x & 63;
+  const int r0 = ((int)blockIdx.x * 4 + (int)(threadIdx.x >> 6)) * WROWS;
+  if (r0 >= p.n) return;
+  const float inv = 1.0f / *p.k_scale;
+  const int r8 = p.rope_w & ~7;
+  uint4 lat[WROWS][NCL], rp[WROWS];
+  uint16_t rt[WROWS], rm[WROWS];
+  int64_t slot[WROWS];
+#pragma unroll
+  for (int i = 0; i < WROWS; ++i) {
+    const int row = r0 + i < p.n ? r0 + i : p.n - 1;   // past the end: a valid row, not written
+    const uint16_t* kc = p.kv_c + (int64_t)row * p.kv_c_stride;
+    const uint16_t* kp = p.k_pe + (int64_t)row * p.k_pe_stride;
+    slot[i] = p.slots[row];
+#pragma unroll
+    for (int k = 0; k < NCL; ++k) {
+      const int c = 8 * lane + 512 * k;
+      lat[i][k] = c < p.d_c ? *reinterpret_cast<const uint4*>(kc + c) : make_uint4(0u, 0u, 0u, 0u);
+    }
+    rp[i] = 8 * lane < r8 ? *reinterpret_cast<const uint4*>(kp + 8 * lane) : make_uint4(0u, 0u, 0u, 0u);
+    rt[i] = lane < p.rope_w - r8 ? kp[r8 + lane] : (uint16_t)0;
+    rm[i] = lane < p.rms_heads ? kp[p.rope_w + lane] : (uint16_t)0;
+  }
+#pragma unroll
+  for (int i = 0; i < WROWS; ++i) {
+    if (r0 + i >= p.n) break;
+    int64_t sl = slot[i];
+    if (sl < 0) sl = 0;
+    if (sl >= p.num_slots) continue;
+    const int64_t page = sl / p.page_size, tok = sl - page * p.page_size;
+    char* dst = p.cache + page * p.page_stride + tok * p.token_stride;
+#pragma unroll
+    for (int k = 0; k < NCL; ++k) {
+      const int c = 8 * lane + 512 * k;
+      if (c < p.d_c) *reinterpret_cast<uint2*>(dst + c) = quant8r(lat[i][k], inv);
+    }
+    if (8 * lane < r8) *reinterpret_cast<uint2*>(dst + p.d_c + 8 * lane) = quant8r(rp[i], inv);
+    if (lane < p.rope_w - r8)
+      dst[p.d_c + r8 + lane] = (char)(pack_e4m3(sat448(bf16_to_f32(rt[i]), inv), 0.f, 0.f, 0.f) & 0xFF);
+    if (lane < p.rms_heads) {
+      char* rtl = dst + p.d_c + p.rope_w;
+      if (p.rms_mode == QMLA_RMS_LOG8) {
+        rtl[lane] = (char)log8_code_fast(bf16_to_f32(rm[i]));
+      } else if (p.rms_mode == QMLA_RMS_BF16_BYTES) {
+        rtl[2 * lane] = (char)(rm[i] & 0xFF);
+        rtl[2 * lane + 1] = (char)(rm[i] >> 8);
+      } else if (p.rms_mode == QMLA_RMS_E4M3) {
+        rtl[lane] = (char)(pack_e4m3(sat448(bf16_to_f32(rm[i]), inv), 0.f, 0.f, 0.f) & 0xFF);
+      }
+    }
   }
 }
 
@@ -164,6 +238,14 @@ extern "C" int qmla_cache_write(const qmla_cache_write_params* p, void* stream) 
   k.page_size = p->page_size;
   k.num_slots = p->num_slots;
   void* args[] = {&k};
+  // large batches (a long prefill): WROWS rows a wave; smaller ones keep one row a wave, which
+  // spreads them over more waves
+  if (fp8 && p->n >= kMultiRowMin && p->d_c <= 1024 && p->rope_w <= 512 && p->rms_heads <= 64) {
+    const unsigned grid = (unsigned)((p->n + 4 * wr::WROWS - 1) / (4 * wr::WROWS));
+    const void* fn = p->d_c <= 512 ? (const void*)wr::write_fp8_kernel<1> : (const void*)wr::write_fp8_kernel<2>;
+    const hipError_t e = hipLaunchKernel(fn, dim3(grid), dim3(256), args, 0, (hipStream_t)stream);
+    return e == hipSuccess ? QMLA_OK : QMLA_ERR_LAUNCH;
+  }
   const unsigned grid = (unsigned)((p->n + wr::ROWS_PER_WG - 1) / wr::ROWS_PER_WG);
   const hipError_t e = hipLaunchKernel((const void*)wr::write_kernel, dim3(grid), dim3(64 * wr::ROWS_PER_WG), args,
                                        0, (hipStream_t)stream);
@@ -287,6 +369,104 @@ __global__ __launch_bounds__(64 * ROWS_PER_WG) void gather_kernel(const GParams 
   }
 }
 
+// FP8 rows whose latent + rope span at most 512 * NCB bytes and whose rms tail holds at most 64 heads:
+// one wave gathers GROWS destination rows. Lanes 0 .. GROWS-1 resolve the rows' sequence, token and
+// page together, and every row's loads are in flight before the first conversion (the per-row
+// kernel waits for that chain of dependent loads once per row); the same values as gather_kernel.
+constexpr int GROWS = 8;
+template <int NCB>
+__global__ __launch_bounds__(256) void gather_fp8_kernel(const GParams p) {
+  const int lane = threadIdx.x & 63;
+  const int j0 = ((int)blockIdx.x * 4 + (int)(threadIdx.x >> 6)) * GROWS;
+  // the 256 log8 divisors, 2^(-3 + code*6/255) rounded once from double, one per thread (every
+  // thread of the workgroup takes part, before any leaves)
+  __shared__ float l8[256];
+  if (p.rms_mode == QMLA_RMS_LOG8) {
+    l8[threadIdx.x] = (float)exp2(-3.0 + (double)threadIdx.x * (6.0 / 255.0));
+    __syncthreads();
+  }
+  if (j0 >= p.num_tokens) return;
+  // lane r < GROWS: byte offset of row j0 + r in the cache, or -1 (nothing to write)
+  int64_t roff = -1;
+  if (lane < GROWS && j0 + lane < p.num_tokens) {
+    const int j = j0 + lane;
+    const int s = p.token_to_seq[j];
+    if (s >= 0 && s < p.num_seqs) {
+      int64_t tok = (int64_t)j - p.cu_seq_lens[s];
+      if (p.seq_starts) tok += p.seq_starts[s];
+      if (tok >= 0) {
+        const int64_t pi = tok / p.page_size;
+        if (pi < p.bt_cols) {
+          const int blk = p.block_table[(int64_t)s * p.bt_stride + pi];
+          if (blk >= 0 && blk < p.num_pages)
+            roff = (int64_t)blk * p.page_stride + (tok - pi * p.page_size) * p.token_stride;
+        }
+      }
+    }
+  }
+  const int c8 = p.rms_offset & ~7;
+  const int rb = p.rms_mode == QMLA_RMS_BF16_BYTES ? 2 : 1;
+  uint2 raw[GROWS][NCB];
+  uint32_t tb[GROWS];   // this lane's rms element (one or two bytes), or the 1-7 bytes before the tail
+  unsigned char pre[GROWS];
+  int64_t ro[GROWS];
+#pragma unroll
+  for (int r = 0; r < GROWS; ++r) {
+    const uint32_t lo = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)roff, r);
+    const uint32_t hi = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)((uint64_t)roff >> 32), r);
+    ro[r] = (int64_t)(((uint64_t)hi << 32) | lo);
+    const char* row = p.cache + (ro[r] >= 0 ? ro[r] : 0);
+#pragma unroll
+    for (int k = 0; k < NCB; ++k) {
+      const int c = 8 * lane + 512 * k;
+      raw[r][k] = (ro[r] >= 0 && c < c8) ? *reinterpret_cast<const uint2*>(row + c) : make_uint2(0u, 0u);
+    }
+    pre[r] = (ro[r] >= 0 && lane < p.rms_offset - c8) ? (unsigned char)row[c8 + lane] : (unsigned char)0;
+    const unsigned char* tail = reinterpret_cast<const unsigned char*>(row) + p.rms_offset;
+    tb[r] = 0u;
+    if (ro[r] >= 0 && lane < p.rms_heads)
+      tb[r] = rb == 2 ? ((uint32_t)tail[2 * lane] | ((uint32_t)tail[2 * lane + 1] << 8)) : (uint32_t)tail[lane];
+  }
+  const float sc = *p.scale;
+#pragma unroll
+  for (int r = 0; r < GROWS; ++r) {
+    if (ro[r] < 0) continue;
+    uint16_t* out = reinterpret_cast<uint16_t*>(p.dst) + (int64_t)(j0 + r) * p.dst_stride;
+#pragma unroll
+    for (int k = 0; k < NCB; ++k) {
+      const int c = 8 * lane + 512 * k;
+      if (c >= c8) continue;
+      const uint32_t w[2] = {raw[r][k].x, raw[r][k].y};
+      uint32_t o[4];
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        const int wv = (int)w[h];
+        const float f0 = e4m3_f32(wv, 0) * sc, f1 = e4m3_f32(wv, 1) * sc;
+        const float f2 = e4m3_f32(wv, 2) * sc, f3 = e4m3_f32(wv, 3) * sc;
+        o[2 * h] = (uint32_t)to_out(f0, p.dst_dtype) | ((uint32_t)to_out(f1, p.dst_dtype) << 16);
+        o[2 * h + 1] = (uint32_t)to_out(f2, p.dst_dtype) | ((uint32_t)to_out(f3, p.dst_dtype) << 16);
+      }
+      *reinterpret_cast<uint4*>(out + c) = make_uint4(o[0], o[1], o[2], o[3]);
+    }
+    if (lane < p.rms_offset - c8) out[c8 + lane] = to_out(e4m3_f32((int)pre[r], 0) * sc, p.dst_dtype);
+    if (lane < p.rms_heads) {
+      float v;
+      if (p.rms_mode == QMLA_RMS_LOG8) {
+        v = l8[tb[r]];
+      } else if (p.rms_mode == QMLA_RMS_BF16_BYTES) {
+        if (p.dst_dtype == QMLA_DT_BF16) {
+          out[p.rms_offset + lane] = (uint16_t)tb[r];
+          continue;
+        }
+        v = __uint_as_float(tb[r] << 16);
+      } else {
+        v = e4m3_f32((int)tb[r], 0) * sc;
+      }
+      out[p.rms_offset + lane] = to_out(v, p.dst_dtype);
+    }
+  }
+}
+
 }  // namespace ga
 }  // namespace qmla
 
@@ -342,6 +522,12 @@ extern "C" int qmla_gather(const qmla_gather_params* p, void* stream) {
   k.dst_stride = p->dst_stride;
   k.dst_dtype = p->dst_dtype;
   void* args[] = {&k};
+  if (fp8 && p->num_tokens >= kMultiRowMin && p->rms_offset <= 1024 && p->rms_heads <= 64) {
+    const unsigned grid = (unsigned)((p->num_tokens + 4 * ga::GROWS - 1) / (4 * ga::GROWS));
+    const void* fn = (p->rms_offset & ~7) <= 512 ? (const void*)ga::gather_fp8_kernel<1> : (const void*)ga::gather_fp8_kernel<2>;
+    const hipError_t e = hipLaunchKernel(fn, dim3(grid), dim3(256), args, 0, (hipStream_t)stream);
+    return e == hipSuccess ? QMLA_OK : QMLA_ERR_LAUNCH;
+  }
   const unsigned grid = (unsigned)((p->num_tokens + ga::ROWS_PER_WG - 1) / ga::ROWS_PER_WG);
   const hipError_t e = hipLaunchKernel((const void*)ga::gather_kernel, dim3(grid), dim3(64 * ga::ROWS_PER_WG), args,
                                        0, (hipStream_t)stream);
