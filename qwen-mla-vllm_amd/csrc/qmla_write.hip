@@ -369,13 +369,18 @@ __global__ __launch_bounds__(64 * ROWS_PER_WG) void gather_kernel(const GParams 
   }
 }
 
-// FP8 rows whose latent + rope span at most 512 * NCB bytes and whose rms tail holds at most 64 heads:
+// FP8 rows whose latent + rope span at most 1024 bytes and whose rms tail holds at most 64 heads:
 // one wave gathers GROWS destination rows. Lanes 0 .. GROWS-1 resolve the rows' sequence, token and
-// page together, and every row's loads are in flight before the first conversion (the per-row
-// kernel waits for that chain of dependent loads once per row); the same values as gather_kernel.
+// page together (the per-row kernel waits for that chain of dependent loads once per row). The
+// rows' 8-byte chunks are then dealt out flat, chunk q of the wave to lane q % 64, so every issued
+// conversion is a full one (a row of 72 chunks would leave 56 lanes idle in its second pass), and
+// all their loads are in flight before the first conversion; likewise the rms elements. The same
+// values as gather_kernel.
 constexpr int GROWS = 8;
-template <int NCB>
+template <int DT>
 __global__ __launch_bounds__(256) void gather_fp8_kernel(const GParams p) {
+  constexpr int NQ = GROWS * 128 / 64;   // chunk passes at most (1024-byte rows)
+  constexpr int NT = GROWS * 64 / 64;    // rms passes at most (64 heads)
   const int lane = threadIdx.x & 63;
   const int j0 = ((int)blockIdx.x * 4 + (int)(threadIdx.x >> 6)) * GROWS;
   // the 256 log8 divisors, 2^(-3 + code*6/255) rounded once from double, one per thread (every
@@ -404,66 +409,97 @@ __global__ __launch_bounds__(256) void gather_fp8_kernel(const GParams p) {
       }
     }
   }
-  const int c8 = p.rms_offset & ~7;
+  const int roff_lo = (int)(uint32_t)roff, roff_hi = (int)(uint32_t)((uint64_t)roff >> 32);
+  const int c8 = p.rms_offset & ~7, nch = c8 >> 3, npre = p.rms_offset - c8;
   const int rb = p.rms_mode == QMLA_RMS_BF16_BYTES ? 2 : 1;
-  uint2 raw[GROWS][NCB];
-  uint32_t tb[GROWS];   // this lane's rms element (one or two bytes), or the 1-7 bytes before the tail
-  unsigned char pre[GROWS];
-  int64_t ro[GROWS];
+  const int nel = nch + (npre > 0 ? 1 : 0);            // chunk slots a row: whole chunks + the pre-tail
+  const int total = GROWS * nel, nt = GROWS * p.rms_heads;
+  // q / nel and t / rms_heads from 24-bit multiplies (q, t < 2^11; exact below 2^20 / divisor)
+  const uint32_t mq = ((1u << 20) + nel - 1) / nel, mt = p.rms_heads > 0 ? ((1u << 20) + p.rms_heads - 1) / p.rms_heads : 0u;
+  uint2 raw[NQ];
+  uint32_t tb[NT];
+  uint32_t live = 0u;   // bit i: this lane's chunk slot of pass i belongs to a row to write
 #pragma unroll
-  for (int r = 0; r < GROWS; ++r) {
-    const uint32_t lo = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)roff, r);
-    const uint32_t hi = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)((uint64_t)roff >> 32), r);
-    ro[r] = (int64_t)(((uint64_t)hi << 32) | lo);
-    const char* row = p.cache + (ro[r] >= 0 ? ro[r] : 0);
-#pragma unroll
-    for (int k = 0; k < NCB; ++k) {
-      const int c = 8 * lane + 512 * k;
-      raw[r][k] = (ro[r] >= 0 && c < c8) ? *reinterpret_cast<const uint2*>(row + c) : make_uint2(0u, 0u);
+  for (int i = 0; i < NQ; ++i) {
+    raw[i] = make_uint2(0u, 0u);
+    if (64 * i < total) {   // wave-uniform
+      const int q = lane + 64 * i;
+      const int r = (int)(__umul24((uint32_t)(q < total ? q : 0), mq) >> 20);
+      const uint32_t lo = (uint32_t)__shfl(roff_lo, r), hi = (uint32_t)__shfl(roff_hi, r);
+      const int64_t ro = (int64_t)(((uint64_t)hi << 32) | lo);
+      if (q < total && ro >= 0) {
+        live |= 1u << i;
+        const int c = q - (int)__umul24((uint32_t)r, (uint32_t)nel);
+        if (c < nch) raw[i] = *reinterpret_cast<const uint2*>(p.cache + ro + 8 * c);
+      }
     }
-    pre[r] = (ro[r] >= 0 && lane < p.rms_offset - c8) ? (unsigned char)row[c8 + lane] : (unsigned char)0;
-    const unsigned char* tail = reinterpret_cast<const unsigned char*>(row) + p.rms_offset;
-    tb[r] = 0u;
-    if (ro[r] >= 0 && lane < p.rms_heads)
-      tb[r] = rb == 2 ? ((uint32_t)tail[2 * lane] | ((uint32_t)tail[2 * lane + 1] << 8)) : (uint32_t)tail[lane];
+  }
+#pragma unroll
+  for (int i = 0; i < NT; ++i) {
+    tb[i] = 0u;
+    if (64 * i < nt) {
+      const int t = lane + 64 * i;
+      const int r = (int)(__umul24((uint32_t)(t < nt ? t : 0), mt) >> 20);
+      const uint32_t lo = (uint32_t)__shfl(roff_lo, r), hi = (uint32_t)__shfl(roff_hi, r);
+      const int64_t ro = (int64_t)(((uint64_t)hi << 32) | lo);
+      if (t < nt && ro >= 0) {
+        const int h = t - (int)__umul24((uint32_t)r, (uint32_t)p.rms_heads);
+        const unsigned char* tail = reinterpret_cast<const unsigned char*>(p.cache + ro) + p.rms_offset;
+        tb[i] = rb == 2 ? ((uint32_t)tail[2 * h] | ((uint32_t)tail[2 * h + 1] << 8)) : (uint32_t)tail[h];
+      }
+    }
   }
   const float sc = *p.scale;
 #pragma unroll
-  for (int r = 0; r < GROWS; ++r) {
-    if (ro[r] < 0) continue;
+  for (int i = 0; i < NQ; ++i) {
+    if (64 * i >= total) break;
+    const int q = lane + 64 * i;
+    if (!(live & (1u << i))) continue;
+    const int r = (int)(__umul24((uint32_t)q, mq) >> 20);
+    const int c = q - (int)__umul24((uint32_t)r, (uint32_t)nel);
     uint16_t* out = reinterpret_cast<uint16_t*>(p.dst) + (int64_t)(j0 + r) * p.dst_stride;
-#pragma unroll
-    for (int k = 0; k < NCB; ++k) {
-      const int c = 8 * lane + 512 * k;
-      if (c >= c8) continue;
-      const uint32_t w[2] = {raw[r][k].x, raw[r][k].y};
+    if (c < nch) {
+      const uint32_t w[2] = {raw[i].x, raw[i].y};
       uint32_t o[4];
 #pragma unroll
       for (int h = 0; h < 2; ++h) {
         const int wv = (int)w[h];
         const float f0 = e4m3_f32(wv, 0) * sc, f1 = e4m3_f32(wv, 1) * sc;
         const float f2 = e4m3_f32(wv, 2) * sc, f3 = e4m3_f32(wv, 3) * sc;
-        o[2 * h] = (uint32_t)to_out(f0, p.dst_dtype) | ((uint32_t)to_out(f1, p.dst_dtype) << 16);
-        o[2 * h + 1] = (uint32_t)to_out(f2, p.dst_dtype) | ((uint32_t)to_out(f3, p.dst_dtype) << 16);
+        o[2 * h] = (uint32_t)to_out(f0, DT) | ((uint32_t)to_out(f1, DT) << 16);
+        o[2 * h + 1] = (uint32_t)to_out(f2, DT) | ((uint32_t)to_out(f3, DT) << 16);
       }
-      *reinterpret_cast<uint4*>(out + c) = make_uint4(o[0], o[1], o[2], o[3]);
+      *reinterpret_cast<uint4*>(out + 8 * c) = make_uint4(o[0], o[1], o[2], o[3]);
+    } else {
+      // the 1-7 bytes between the last whole chunk and the rms tail (the plugin's rope-116 rows)
+      const uint32_t lo = (uint32_t)__shfl(roff_lo, r), hi = (uint32_t)__shfl(roff_hi, r);
+      const unsigned char* row = reinterpret_cast<const unsigned char*>(p.cache + (int64_t)(((uint64_t)hi << 32) | lo));
+      for (int e = 0; e < npre; ++e) out[c8 + e] = to_out(e4m3_f32((int)row[c8 + e], 0) * sc, DT);
     }
-    if (lane < p.rms_offset - c8) out[c8 + lane] = to_out(e4m3_f32((int)pre[r], 0) * sc, p.dst_dtype);
-    if (lane < p.rms_heads) {
-      float v;
-      if (p.rms_mode == QMLA_RMS_LOG8) {
-        v = l8[tb[r]];
-      } else if (p.rms_mode == QMLA_RMS_BF16_BYTES) {
-        if (p.dst_dtype == QMLA_DT_BF16) {
-          out[p.rms_offset + lane] = (uint16_t)tb[r];
-          continue;
-        }
-        v = __uint_as_float(tb[r] << 16);
-      } else {
-        v = e4m3_f32((int)tb[r], 0) * sc;
+  }
+#pragma unroll
+  for (int i = 0; i < NT; ++i) {
+    if (64 * i >= nt) break;
+    const int t = lane + 64 * i;
+    const int r = (int)(__umul24((uint32_t)(t < nt ? t : 0), mt) >> 20);
+    const uint32_t lo = (uint32_t)__shfl(roff_lo, r), hi = (uint32_t)__shfl(roff_hi, r);
+    const int64_t ro = (int64_t)(((uint64_t)hi << 32) | lo);
+    if (t >= nt || ro < 0) continue;
+    const int h = t - (int)__umul24((uint32_t)r, (uint32_t)p.rms_heads);
+    uint16_t* out = reinterpret_cast<uint16_t*>(p.dst) + (int64_t)(j0 + r) * p.dst_stride + p.rms_offset;
+    float v;
+    if (p.rms_mode == QMLA_RMS_LOG8) {
+      v = l8[tb[i]];
+    } else if (p.rms_mode == QMLA_RMS_BF16_BYTES) {
+      if (DT == QMLA_DT_BF16) {
+        out[h] = (uint16_t)tb[i];
+        continue;
       }
-      out[p.rms_offset + lane] = to_out(v, p.dst_dtype);
+      v = __uint_as_float(tb[i] << 16);
+    } else {
+      v = e4m3_f32((int)tb[i], 0) * sc;
     }
+    out[h] = to_out(v, DT);
   }
 }
 
@@ -524,7 +560,8 @@ extern "C" int qmla_gather(const qmla_gather_params* p, void* stream) {
   void* args[] = {&k};
   if (fp8 && p->num_tokens >= kMultiRowMin && p->rms_offset <= 1024 && p->rms_heads <= 64) {
     const unsigned grid = (unsigned)((p->num_tokens + 4 * ga::GROWS - 1) / (4 * ga::GROWS));
-    const void* fn = (p->rms_offset & ~7) <= 512 ? (const void*)ga::gather_fp8_kernel<1> : (const void*)ga::gather_fp8_kernel<2>;
+    const void* fn = p->dst_dtype == QMLA_DT_F16 ? (const void*)ga::gather_fp8_kernel<QMLA_DT_F16>
+                                                 : (const void*)ga::gather_fp8_kernel<QMLA_DT_BF16>;
     const hipError_t e = hipLaunchKernel(fn, dim3(grid), dim3(256), args, 0, (hipStream_t)stream);
     return e == hipSuccess ? QMLA_OK : QMLA_ERR_LAUNCH;
   }
