@@ -124,3 +124,21 @@ def test_wide_fp8_partial_rope(gpu, heads, rope, rms, qrows, splits):
                           qrows=qrows, num_splits=splits, num_workgroups=0 if splits else 9)
     torch.cuda.synchronize()
     check_decode(f"wide fp8 rope {rope} {rms} q{qrows} S={splits}", c, o, lse, num_splits=max(splits, 1))
+
+
+@pytest.mark.parametrize("page_size", [1, 40, 100])
+@pytest.mark.parametrize("rms,qrows,splits", [("log8", 1, 0), ("e4m3", 4, 0), ("bf16_bytes", 2, 8)])
+def test_wide_fp8_rope232_odd_pages(gpu, page_size, rms, qrows, splits):
+    """The deployed FP8 rank-1792 rope-232 rows with 24 heads (16-token tiles of 32 rows) on pages
+    that are not a multiple of the tile: tiles straddle pages, so every row's page is looked up per
+    lane instead of one resource per tile."""
+    import qmla
+    lens = [3, 700, 1301, 260]
+    c = make_case(batch=len(lens), heads=24, d_c=DC, rope_w=232, page_size=page_size, lens=lens, kv="fp8",
+                  rms_mode=rms, seed=31 + page_size + qrows, device=gpu, rms="spread", amp=4.0, qrows=qrows)
+    o, lse = qmla.forward(c.q_nope, c.q_pe, c.cache, c.block_table, c.seq_lens, page_size=page_size,
+                          sm_scale=c.sm_scale, kv_fp8=True, fp8_rms={"bf16_bytes": "bf16"}.get(rms, rms),
+                          k_scale=c.k_scale, qrows=qrows, num_splits=splits, num_workgroups=0 if splits else 7)
+    torch.cuda.synchronize()
+    check_decode(f"wide fp8 rope 232 {rms} q{qrows} S={splits} pages {page_size}", c, o, lse,
+                 num_splits=max(splits, 1))
