@@ -44,6 +44,13 @@ typedef __attribute__((__vector_size__(8 * sizeof(short)))) short s16x8;
 
 constexpr int PIDN = 512;    // page ids staged per sub-range
 
+typedef __attribute__((__vector_size__(16 * sizeof(float)))) float f32x16;
+// 32 x 32 x 16 bf16 product (A: lane l holds row l % 32, k 8 (l / 32) .. +8; B: column l % 32, the
+// same k; D: lane l, register v holds row 8 (v / 4) + 4 (l / 32) + v % 4, column l % 32). Twice the
+// flops of the 16x16x16 form per cycle on gfx950.
+__device__ __forceinline__ f32x16 mfma32(const bf16x8& a, const bf16x8& b, const f32x16& c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+}
 __device__ __forceinline__ f32x4 mfma16k16(const s16x4& a, const s16x4& b, const f32x4& c) {
   return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(a, b, c, 0, 0, 0);
 }
@@ -169,6 +176,10 @@ struct CS {
   static constexpr bool RSC = G == 1 && NCG == 8 && NTG == 1 && LDS0 + LDSR <= 163840 &&
                               ((NTB == 1 && MB == 2) || (EB == 1 && NTB == 2));
   static constexpr int RE = RSC ? RPW / RLR : 1;         // scores per lane
+  // fp8 16-token tiles of 32 rows: P.V on the 32x32x16 MFMA (32 rows x 32 columns per
+  // instruction) instead of four 16x16x16 ones, which run at half the flops per cycle (bf16 rows
+  // keep the 16x16x16 form: there the 32x32 one measured slower)
+  static constexpr bool W32 = EB == 1 && RSC && NTB == 1 && MB == 2 && CB % 2 == 0 && NTG == 1;
   // fp8 rows: the per-lane DMA offsets of a tile (the same for every tile of a call) in an LDS
   // table, where it fits, instead of recomputing them at every issue
   static constexpr int NDV = NID + NRID;
@@ -378,14 +389,25 @@ __device__ __forceinline__ void segment(const KParams& p, Smem<C>& sm, int req, 
   // mref: the softmax reference; mthr: mref + ref_shift of the running sum at its last evaluation
   // (the sum only grows while mref stays, so a tile max at or below mthr cannot move mref)
   float mref[C::MB], mthr[C::MB], lpart[C::MB];
-  f32x4 acc[C::MB][C::CB];
+  // accumulators: [row block][16-column block] of 16x16 tiles, or [32-column block] of 32x32 ones
+  f32x4 acc[C::W32 ? 1 : C::MB][C::W32 ? 1 : C::CB];
+  f32x16 acc32[C::W32 ? C::CB / 2 : 1];
 #pragma unroll
   for (int mb = 0; mb < C::MB; ++mb) {
     mref[mb] = kNegInf;
     mthr[mb] = kNegInf;
     lpart[mb] = 0.f;
+  }
+  if constexpr (C::W32) {
 #pragma unroll
-    for (int cb = 0; cb < C::CB; ++cb) acc[mb][cb] = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int j = 0; j < C::CB / 2; ++j)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) acc32[j][v] = 0.f;
+  } else {
+#pragma unroll
+    for (int mb = 0; mb < C::MB; ++mb)
+#pragma unroll
+      for (int cb = 0; cb < C::CB; ++cb) acc[mb][cb] = f32x4{0.f, 0.f, 0.f, 0.f};
   }
 
   if constexpr (C::DVT) {
@@ -593,6 +615,7 @@ __device__ __forceinline__ void segment(const KParams& p, Smem<C>& sm, int req, 
 
       bf16x8 pa8[C::MB];
       s16x4 pa4[C::MB];
+      bf16x8 pa32;   // 32x32x16 A operand (W32)
       if constexpr (C::RSC) {
         // ---- reduce-scatter: each wave writes its partial scores as a [ROWS][T] fp32 tile (a row's
         //      4-token groups rotated by xrot(row), so the 16 rows of a write and the 64 scores of a
@@ -689,11 +712,18 @@ __device__ __forceinline__ void segment(const KParams& p, Smem<C>& sm, int req, 
         //      k-slot order vtok), and the rows of this lane's accumulators (16mb + 4lg + i),
         //      rescaled first where their reducer wave's reference moved ----
         i32x2 pr[C::MB][C::NTB];
+        if constexpr (C::W32) {
+          // P of row lane % 32, tokens 8 (lane / 32) .. +8: the 32x32x16 A operand
+          const char* pp = sm.rs.rp + (lane & 31) * C::RPS + 16 * (lane >> 5);
+          pr[0][0] = ldsr64(pp);
+          pr[1][0] = ldsr64(pp + 8);
+        } else {
 #pragma unroll
-        for (int mb = 0; mb < C::MB; ++mb)
+          for (int mb = 0; mb < C::MB; ++mb)
 #pragma unroll
-          for (int tb = 0; tb < C::NTB; ++tb)
-            pr[mb][tb] = ldsr64(sm.rs.rp + (16 * mb + ln16) * C::RPS + 2 * tok_of(tb, 4 * lg));
+            for (int tb = 0; tb < C::NTB; ++tb)
+              pr[mb][tb] = ldsr64(sm.rs.rp + (16 * mb + ln16) * C::RPS + 2 * tok_of(tb, 4 * lg));
+        }
         i32x4 f0 = ldsr128(reinterpret_cast<const char*>(&sm.rs.rf[0])), f1 = ldsr128(reinterpret_cast<const char*>(&sm.rs.rf[4]));
         lds_wait(f0, f1);
 #pragma unroll
@@ -703,22 +733,41 @@ __device__ __forceinline__ void segment(const KParams& p, Smem<C>& sm, int req, 
         const int fa = f0[0] | f0[1] | f0[2] | f0[3] | f1[0] | f1[1] | f1[2] | f1[3];
         if (__builtin_amdgcn_readfirstlane(fa)) {
           const int fw[8] = {f0[0], f0[1], f0[2], f0[3], f1[0], f1[1], f1[2], f1[3]};
+          if constexpr (C::W32) {
+            // rows 8k + 4 (lane / 32) + i of register 4k + i; their reducer wave is 2k + lane / 32
+            const int h32 = lane >> 5;
 #pragma unroll
-          for (int mb = 0; mb < C::MB; ++mb) {
-            i32x4 ar = ldsr128(reinterpret_cast<const char*>(&sm.rs.ra[16 * mb + 4 * lg]));
-            lds_wait(ar);
-            const f32x4 al = __builtin_bit_cast(f32x4, ar);
+            for (int k = 0; k < 4; ++k) {
+              i32x4 ar = ldsr128(reinterpret_cast<const char*>(&sm.rs.ra[8 * k + 4 * h32]));
+              lds_wait(ar);
+              const f32x4 al = __builtin_bit_cast(f32x4, ar);
+              const int fl = (fw[2 * k + 1] & -h32) | (fw[2 * k] & (h32 - 1));   // no indexed private array
 #pragma unroll
-            for (int i = 0; i < 4; ++i) {
-              int fl = 0;   // the flag of row 16mb + 4lg + i's reducer wave
+              for (int i = 0; i < 4; ++i) {
+                const float a_i = fl ? al[i] : 1.0f;
 #pragma unroll
-              for (int x = 0; x < 8; ++x) fl = (16 * mb + 4 * lg + i) / C::RPW == x ? fw[x] : fl;
-              const float a_i = fl ? al[i] : 1.0f;
+                for (int j = 0; j < C::CB / 2; ++j) acc32[j][4 * k + i] *= a_i;
+              }
+            }
+          } else {
 #pragma unroll
-              for (int cb = 0; cb < C::CB; ++cb) acc[mb][cb][i] *= a_i;
+            for (int mb = 0; mb < C::MB; ++mb) {
+              i32x4 ar = ldsr128(reinterpret_cast<const char*>(&sm.rs.ra[16 * mb + 4 * lg]));
+              lds_wait(ar);
+              const f32x4 al = __builtin_bit_cast(f32x4, ar);
+#pragma unroll
+              for (int i = 0; i < 4; ++i) {
+                int fl = 0;   // the flag of row 16mb + 4lg + i's reducer wave
+#pragma unroll
+                for (int x = 0; x < 8; ++x) fl = (16 * mb + 4 * lg + i) / C::RPW == x ? fw[x] : fl;
+                const float a_i = fl ? al[i] : 1.0f;
+#pragma unroll
+                for (int cb = 0; cb < C::CB; ++cb) acc[mb][cb][i] *= a_i;
+              }
             }
           }
         }
+        if constexpr (C::W32) pa32 = __builtin_bit_cast(bf16x8, i32x4{pr[0][0][0], pr[0][0][1], pr[1][0][0], pr[1][0][1]});
 #pragma unroll
         for (int mb = 0; mb < C::MB; ++mb) {
           if constexpr (C::NTB == 1) {
@@ -942,6 +991,19 @@ __device__ __forceinline__ void segment(const KParams& p, Smem<C>& sm, int req, 
               for (int mb = 0; mb < C::MB; ++mb) acc[mb][c0 + j] = mfma16(pa8[mb], vf, acc[mb][c0 + j]);
             }
         }
+      } else if constexpr (C::EB == 1 && C::W32) {
+        // 32x32x16: lane block b reads tokens 8 (b / 2) .. +8 of columns 16 (b % 2) .. +16 of each
+        // 32-column block (tr_b8: lanes 2r, 2r+1 supply token row r), so lane l gets column l % 32
+        // for the k-slots 8 (l / 32) .. +8
+        const int b16 = lane >> 4, li = lane & 15;
+        const uint32_t vb = lds_addr(st + (8 * (b16 >> 1) + (li >> 1)) * C::RS + 16 * (b16 & 1) + 8 * (li & 1));
+        constexpr int NJ = C::CB / 2;
+        i32x2 vr[NJ];
+        sfor<0, NJ>([&](auto j) { vr[j] = ldstr8_off<32 * j>(vb); });
+        sfor<0, NJ>([&](auto j) {
+          lds_wait_n<NJ - 1 - j>(vr[j]);
+          acc32[j] = mfma32(pa32, fp8x8_to_bf16(vr[j]), acc32[j]);
+        });
       } else if constexpr (C::EB == 1) {
         // 16-token tiles: tr_b8 rows r = 0..3 of lane block q are tokens 4q .. 4q+3 of column block
         // 2j, rows 4..7 the same tokens of block 2j+1, so lane n gets both blocks' column n for the
@@ -1070,6 +1132,45 @@ __device__ __forceinline__ void segment(const KParams& p, Smem<C>& sm, int req, 
           acc[mb][cb][i] = acc[mb][cb][i] * b0[i] + mine[((mb * C::CB + cb) * 4 + i) * 64 + lane] * b1[i];
     }
   }
+  if constexpr (C::W32) {
+    // 32x32 accumulators: register v of lane l holds row 8 (v / 4) + 4 (l / 32) + v % 4, column l % 32
+    const bool ph = !so.final_out && so.plse && p.part_h;
+    const int col = c * C::DCW + (lane & 31);
+#pragma unroll
+    for (int v = 0; v < 16; ++v) {
+      const int rl = 8 * (v >> 2) + 4 * (lane >> 5) + (v & 3);
+      const float l_i = sm.rs.rfin[1][rl];
+      const float ivv = ph ? inv_sum(1.0f, l_i) : inv_sum(kscale, l_i);
+      const int r = rbase + rl;
+      if (r >= rows_pg) continue;
+      const int jq = r / hpg, hh = r - jq * hpg;
+      const int head = g * hpg + hh;
+      if (so.final_out) {
+        const int64_t ob = (int64_t)(row0 + jq) * p.o_sr + (int64_t)head * p.o_sh + col;
+        if (p.out_dt == QMLA_DT_BF16) {
+          __bf16* o = reinterpret_cast<__bf16*>(p.out) + ob;
+#pragma unroll
+          for (int j = 0; j < C::CB / 2; ++j) o[32 * j] = (__bf16)(acc32[j][v] * ivv);
+        } else if (p.out_dt == QMLA_DT_F16) {
+          _Float16* o = reinterpret_cast<_Float16*>(p.out) + ob;
+#pragma unroll
+          for (int j = 0; j < C::CB / 2; ++j) o[32 * j] = (_Float16)(acc32[j][v] * ivv);
+        } else {
+          float* o = reinterpret_cast<float*>(p.out) + ob;
+#pragma unroll
+          for (int j = 0; j < C::CB / 2; ++j) o[32 * j] = acc32[j][v] * ivv;
+        }
+      } else if (ph) {
+        _Float16* ob = reinterpret_cast<_Float16*>(so.po) + (int64_t)jq * so.po_sr + (int64_t)head * so.po_sh + col;
+#pragma unroll
+        for (int j = 0; j < C::CB / 2; ++j) ob[32 * j] = (_Float16)(acc32[j][v] * ivv);
+      } else {
+        float* ob = so.po + (int64_t)jq * so.po_sr + (int64_t)head * so.po_sh + col;
+#pragma unroll
+        for (int j = 0; j < C::CB / 2; ++j) ob[32 * j] = acc32[j][v] * ivv;
+      }
+    }
+  } else
 #pragma unroll
   for (int mb = 0; mb < C::MB; ++mb) {
     const float l = lrow[mb];
