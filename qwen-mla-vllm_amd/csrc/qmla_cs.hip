@@ -180,6 +180,32 @@ struct CS {
   // instruction) instead of four 16x16x16 ones, which run at half the flops per cycle (bf16 rows
   // keep the 16x16x16 form: there the 32x32 one measured slower)
   static constexpr bool W32 = EB == 1 && RSC && NTB == 1 && MB == 2 && CB % 2 == 0 && NTG == 1;
+  // The 32 columns of a 32x32 block are two 16-column blocks (a, a + d): lanes 0-31 of a
+  // transposed V read cover 8 rows x 16 bytes of each, and with the odd 16-byte row stride the 8
+  // rows of one block fill one half of the 64 LDS banks, the other block the other half exactly
+  // when d blocks are 128 bytes (mod 256): d = 8. A leftover pair takes d = 1 (two-way conflicts
+  // in that read).
+  static constexpr int PD = 8;
+  struct Pairs {
+    int a[CB / 2 > 0 ? CB / 2 : 1], d[CB / 2 > 0 ? CB / 2 : 1];
+    constexpr Pairs() : a(), d() {
+      bool used[CB > 0 ? CB : 1] = {};
+      int n = 0;
+      for (int x = 0; x < CB; ++x) {
+        if (used[x]) continue;
+        int y = x + PD;
+        if (y >= CB || used[y]) {
+          y = x + 1;
+          while (y < CB && used[y]) ++y;
+        }
+        used[x] = used[y] = true;
+        a[n] = x;
+        d[n] = y - x;
+        ++n;
+      }
+    }
+  };
+  static constexpr Pairs PAIRS{};
   // fp8 rows: the per-lane DMA offsets of a tile (the same for every tile of a call) in an LDS
   // table, where it fits, instead of recomputing them at every issue
   static constexpr int NDV = NID + NRID;
@@ -992,14 +1018,18 @@ __device__ __forceinline__ void segment(const KParams& p, Smem<C>& sm, int req, 
             }
         }
       } else if constexpr (C::EB == 1 && C::W32) {
-        // 32x32x16: lane block b reads tokens 8 (b / 2) .. +8 of columns 16 (b % 2) .. +16 of each
-        // 32-column block (tr_b8: lanes 2r, 2r+1 supply token row r), so lane l gets column l % 32
-        // for the k-slots 8 (l / 32) .. +8
+        // 32x32x16: lane block b reads tokens 8 (b / 2) .. +8 of 16-column block a_j (b even) or
+        // a_j + d_j (b odd) (tr_b8: lanes 2r, 2r+1 supply token row r), so lane l gets column
+        // l % 32 of the pair for the k-slots 8 (l / 32) .. +8
         const int b16 = lane >> 4, li = lane & 15;
-        const uint32_t vb = lds_addr(st + (8 * (b16 >> 1) + (li >> 1)) * C::RS + 16 * (b16 & 1) + 8 * (li & 1));
+        const char* vrow = st + (8 * (b16 >> 1) + (li >> 1)) * C::RS + 8 * (li & 1);
+        const uint32_t vbd = lds_addr(vrow + 16 * C::PD * (b16 & 1)), vb1 = lds_addr(vrow + 16 * (b16 & 1));
         constexpr int NJ = C::CB / 2;
         i32x2 vr[NJ];
-        sfor<0, NJ>([&](auto j) { vr[j] = ldstr8_off<32 * j>(vb); });
+        sfor<0, NJ>([&](auto j) {
+          constexpr int a = C::PAIRS.a[j];
+          vr[j] = ldstr8_off<16 * a>(C::PAIRS.d[j] == C::PD ? vbd : vb1);
+        });
         sfor<0, NJ>([&](auto j) {
           lds_wait_n<NJ - 1 - j>(vr[j]);
           acc32[j] = mfma32(pa32, fp8x8_to_bf16(vr[j]), acc32[j]);
@@ -1133,9 +1163,11 @@ __device__ __forceinline__ void segment(const KParams& p, Smem<C>& sm, int req, 
     }
   }
   if constexpr (C::W32) {
-    // 32x32 accumulators: register v of lane l holds row 8 (v / 4) + 4 (l / 32) + v % 4, column l % 32
+    // 32x32 accumulators: register v of lane l holds row 8 (v / 4) + 4 (l / 32) + v % 4, column
+    // l % 16 of 16-column block a_j (l % 32 < 16) or a_j + d_j
     const bool ph = !so.final_out && so.plse && p.part_h;
-    const int col = c * C::DCW + (lane & 31);
+    const int hi = (lane >> 4) & 1;
+    const int cold = c * C::DCW + (lane & 15) + 16 * C::PD * hi, col1 = c * C::DCW + (lane & 15) + 16 * hi;
 #pragma unroll
     for (int v = 0; v < 16; ++v) {
       const int rl = 8 * (v >> 2) + 4 * (lane >> 5) + (v & 3);
@@ -1145,29 +1177,26 @@ __device__ __forceinline__ void segment(const KParams& p, Smem<C>& sm, int req, 
       if (r >= rows_pg) continue;
       const int jq = r / hpg, hh = r - jq * hpg;
       const int head = g * hpg + hh;
+      // element j of this lane's output row: column a_j * 16 + (d_j == PD ? cold : col1)
+      auto put = [&](auto* o0, auto cvt) {
+        sfor<0, C::CB / 2>([&](auto j) {
+          constexpr int a = C::PAIRS.a[j];
+          (C::PAIRS.d[j] == C::PD ? o0 + cold : o0 + col1)[16 * a] = cvt(acc32[j][v] * ivv);
+        });
+      };
       if (so.final_out) {
-        const int64_t ob = (int64_t)(row0 + jq) * p.o_sr + (int64_t)head * p.o_sh + col;
-        if (p.out_dt == QMLA_DT_BF16) {
-          __bf16* o = reinterpret_cast<__bf16*>(p.out) + ob;
-#pragma unroll
-          for (int j = 0; j < C::CB / 2; ++j) o[32 * j] = (__bf16)(acc32[j][v] * ivv);
-        } else if (p.out_dt == QMLA_DT_F16) {
-          _Float16* o = reinterpret_cast<_Float16*>(p.out) + ob;
-#pragma unroll
-          for (int j = 0; j < C::CB / 2; ++j) o[32 * j] = (_Float16)(acc32[j][v] * ivv);
-        } else {
-          float* o = reinterpret_cast<float*>(p.out) + ob;
-#pragma unroll
-          for (int j = 0; j < C::CB / 2; ++j) o[32 * j] = acc32[j][v] * ivv;
-        }
+        const int64_t ob = (int64_t)(row0 + jq) * p.o_sr + (int64_t)head * p.o_sh;
+        if (p.out_dt == QMLA_DT_BF16)
+          put(reinterpret_cast<__bf16*>(p.out) + ob, [](float x) { return (__bf16)x; });
+        else if (p.out_dt == QMLA_DT_F16)
+          put(reinterpret_cast<_Float16*>(p.out) + ob, [](float x) { return (_Float16)x; });
+        else
+          put(reinterpret_cast<float*>(p.out) + ob, [](float x) { return x; });
       } else if (ph) {
-        _Float16* ob = reinterpret_cast<_Float16*>(so.po) + (int64_t)jq * so.po_sr + (int64_t)head * so.po_sh + col;
-#pragma unroll
-        for (int j = 0; j < C::CB / 2; ++j) ob[32 * j] = (_Float16)(acc32[j][v] * ivv);
+        put(reinterpret_cast<_Float16*>(so.po) + (int64_t)jq * so.po_sr + (int64_t)head * so.po_sh,
+            [](float x) { return (_Float16)x; });
       } else {
-        float* ob = so.po + (int64_t)jq * so.po_sr + (int64_t)head * so.po_sh + col;
-#pragma unroll
-        for (int j = 0; j < C::CB / 2; ++j) ob[32 * j] = acc32[j][v] * ivv;
+        put(so.po + (int64_t)jq * so.po_sr + (int64_t)head * so.po_sh, [](float x) { return x; });
       }
     }
   } else
