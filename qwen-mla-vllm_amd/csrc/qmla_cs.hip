@@ -726,7 +726,9 @@ __device__ __forceinline__ void segment(const KParams& p, Smem<C>& sm, int req, 
           }
           const float pv = fast_exp2(v - (rmref[e] == kNegInf ? 0.f : rmref[e]));
           rlp[e] += pv;
-          *reinterpret_cast<__bf16*>(sm.rs.rp + rrow[e] * C::RPS + 2 * tt) = (__bf16)pv;
+          // bf16 rows: k-slot 4q + i of the P.V operand is token 2i + 8 (q & 1) + (q >> 1)
+          const int ks = C::EB == 2 ? (8 * (tt & 1) + 4 * ((tt >> 3) & 1) + ((tt >> 1) & 3)) : tt;
+          *reinterpret_cast<__bf16*>(sm.rs.rp + rrow[e] * C::RPS + 2 * ks) = (__bf16)pv;
         }
         if (moved && tt == 0) {
 #pragma unroll
@@ -1084,7 +1086,12 @@ __device__ __forceinline__ void segment(const KParams& p, Smem<C>& sm, int req, 
             }
         }
       } else {
-        const uint32_t vb = lds_addr(st + (4 * lg + (ln16 >> 2)) * C::RS + 8 * (ln16 & 3));
+        // lane block q reads tokens 4q .. 4q+3 (tr_b16: lanes 4r .. 4r+3 supply token row r); with
+        // the reduce-scatter's P, tokens 2r + 8 (q & 1) + (q >> 1) instead: lanes 0-31 then cover
+        // the 8 even rows (the odd ones in lanes 32-63), which with the odd 16-byte row stride
+        // fill the 64 LDS banks once instead of twice
+        const int vrow = C::RSC ? 2 * (ln16 >> 2) + 8 * (lg & 1) + (lg >> 1) : 4 * lg + (ln16 >> 2);
+        const uint32_t vb = lds_addr(st + vrow * C::RS + 8 * (ln16 & 3));
         constexpr int VB = 7;   // column blocks per batch of reads, each used as soon as it is in
         sfor<0, (C::CB + VB - 1) / VB>([&](auto b) {
           constexpr int c0 = VB * b, nb = C::CB - c0 < VB ? C::CB - c0 : VB;
