@@ -1173,11 +1173,15 @@ __device__ __forceinline__ void segment(const KParams& p, Smem<C>& sm, int req, 
     // 32x32 accumulators: register v of lane l holds row 8 (v / 4) + 4 (l / 32) + v % 4, column
     // l % 16 of 16-column block a_j (l % 32 < 16) or a_j + d_j
     const bool ph = !so.final_out && so.plse && p.part_h;
-    const int hi = (lane >> 4) & 1;
-    const int cold = c * C::DCW + (lane & 15) + 16 * C::PD * hi, col1 = c * C::DCW + (lane & 15) + 16 * hi;
+    // the lane index through an empty asm: the rows, heads and offsets below are then computed
+    // here, at each range's end, instead of once before the range loop and kept (spilled) across it
+    int ln = lane;
+    asm volatile("" : "+v"(ln));
+    const int hi = (ln >> 4) & 1;
+    const int cold = c * C::DCW + (ln & 15) + 16 * C::PD * hi, col1 = c * C::DCW + (ln & 15) + 16 * hi;
 #pragma unroll
     for (int v = 0; v < 16; ++v) {
-      const int rl = 8 * (v >> 2) + 4 * (lane >> 5) + (v & 3);
+      const int rl = 8 * (v >> 2) + 4 * (ln >> 5) + (v & 3);
       const float l_i = sm.rs.rfin[1][rl];
       const float ivv = ph ? inv_sum(1.0f, l_i) : inv_sum(kscale, l_i);
       const int r = rbase + rl;
@@ -1206,7 +1210,10 @@ __device__ __forceinline__ void segment(const KParams& p, Smem<C>& sm, int req, 
         put(so.po + (int64_t)jq * so.po_sr + (int64_t)head * so.po_sh, [](float x) { return x; });
       }
     }
-  } else
+  } else {
+  // the lane's row group and column through an empty asm (as above)
+  int lgx = lg, lnx = ln16;
+  asm volatile("" : "+v"(lgx), "+v"(lnx));
 #pragma unroll
   for (int mb = 0; mb < C::MB; ++mb) {
     const float l = lrow[mb];
@@ -1218,20 +1225,20 @@ __device__ __forceinline__ void segment(const KParams& p, Smem<C>& sm, int req, 
     if constexpr (C::RSC) {
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        const float l_i = sm.rs.rfin[1][16 * mb + 4 * lg + i];
+        const float l_i = sm.rs.rfin[1][16 * mb + 4 * lgx + i];
         iv[i] = ph ? inv_sum(1.0f, l_i) : inv_sum(kscale, l_i);
       }
     } else {
 #pragma unroll
-      for (int i = 0; i < 4; ++i) iv[i] = __shfl(ph ? invh : inv, 4 * lg + i);
+      for (int i = 0; i < 4; ++i) iv[i] = __shfl(ph ? invh : inv, 4 * lgx + i);
     }
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      const int r = rbase + 16 * mb + 4 * lg + i;
+      const int r = rbase + 16 * mb + 4 * lgx + i;
       if (r >= rows_pg) continue;
       const int jq = r / hpg, hh = r - jq * hpg;
       const int head = g * hpg + hh;
-      const int col = c * C::DCW + ln16;
+      const int col = c * C::DCW + lnx;
       if (so.final_out) {
         const int64_t ob = (int64_t)(row0 + jq) * p.o_sr + (int64_t)head * p.o_sh + col;
         if (p.out_dt == QMLA_DT_BF16) {
@@ -1257,9 +1264,9 @@ __device__ __forceinline__ void segment(const KParams& p, Smem<C>& sm, int req, 
         for (int cb = 0; cb < C::CB; ++cb) ob[16 * cb] = acc[mb][cb][i] * iv[i];
       }
     }
-    // lse from the score layout (row ln16 + 16mb), one lane per row (reduce-scatter: below)
-    const int r = rbase + ln16 + 16 * mb;
-    if (!C::RSC && c == 0 && lg == 0 && r < rows_pg) {
+    // lse from the score layout (row lnx + 16mb), one lane per row (reduce-scatter: below)
+    const int r = rbase + lnx + 16 * mb;
+    if (!C::RSC && c == 0 && lgx == 0 && r < rows_pg) {
       const int jq = r / hpg, hh = r - jq * hpg;
       const int head = g * hpg + hh;
       if (so.final_out) {
@@ -1270,6 +1277,7 @@ __device__ __forceinline__ void segment(const KParams& p, Smem<C>& sm, int req, 
         so.po[(int64_t)jq * so.po_sr + (int64_t)head * so.po_sh + C::DCG] = lse_v;
       }
     }
+  }
   }
   if constexpr (C::RSC) {
     // the reducer lane of each row writes its lse
