@@ -176,16 +176,15 @@ struct CS {
   static constexpr bool RSC = G == 1 && NCG == 8 && NTG == 1 && LDS0 + LDSR <= 163840 &&
                               ((NTB == 1 && MB == 2) || (EB == 1 && NTB == 2));
   static constexpr int RE = RSC ? RPW / RLR : 1;         // scores per lane
-  // fp8 16-token tiles of 32 rows: P.V on the 32x32x16 MFMA (32 rows x 32 columns per
-  // instruction) instead of four 16x16x16 ones, which run at half the flops per cycle (bf16 rows
-  // keep the 16x16x16 form: there the 32x32 one measured slower)
-  static constexpr bool W32 = EB == 1 && RSC && NTB == 1 && MB == 2 && CB % 2 == 0 && NTG == 1;
+  // 16-token tiles of 32 rows: P.V on the 32x32x16 MFMA (32 rows x 32 columns per instruction)
+  // instead of four 16x16x16 ones, which run at half the flops per cycle
+  static constexpr bool W32 = RSC && NTB == 1 && MB == 2 && CB % 2 == 0 && NTG == 1;
   // The 32 columns of a 32x32 block are two 16-column blocks (a, a + d): lanes 0-31 of a
-  // transposed V read cover 8 rows x 16 bytes of each, and with the odd 16-byte row stride the 8
-  // rows of one block fill one half of the 64 LDS banks, the other block the other half exactly
-  // when d blocks are 128 bytes (mod 256): d = 8. A leftover pair takes d = 1 (two-way conflicts
-  // in that read).
-  static constexpr int PD = 8;
+  // transposed V read cover 8 rows x 16 bytes (fp8) or 4 rows x 32 bytes (bf16: token rows 2r,
+  // then 2r + 1) of each, and with the odd 16-byte row stride the rows of one block fill one half
+  // of the 64 LDS banks, the other block the other half exactly when d blocks are 128 bytes
+  // (mod 256): fp8 d = 8, bf16 d = 4. A leftover pair takes d = 1 (two-way conflicts in that read).
+  static constexpr int PD = EB == 1 ? 8 : 4;
   struct Pairs {
     int a[CB / 2 > 0 ? CB / 2 : 1], d[CB / 2 > 0 ? CB / 2 : 1];
     constexpr Pairs() : a(), d() {
@@ -726,8 +725,11 @@ __device__ __forceinline__ void segment(const KParams& p, Smem<C>& sm, int req, 
           }
           const float pv = fast_exp2(v - (rmref[e] == kNegInf ? 0.f : rmref[e]));
           rlp[e] += pv;
-          // bf16 rows: k-slot 4q + i of the P.V operand is token 2i + 8 (q & 1) + (q >> 1)
-          const int ks = C::EB == 2 ? (8 * (tt & 1) + 4 * ((tt >> 3) & 1) + ((tt >> 1) & 3)) : tt;
+          // bf16 rows: k-slot 8h + 4b + a of the 32x32 P.V operand is token 8h + 2a + b (16x16:
+          // k-slot 4q + i is token 2i + 8 (q & 1) + (q >> 1)), the order of the V reads below
+          const int ks = C::EB == 1 ? tt
+                         : C::W32   ? ((tt & 8) | ((tt & 1) << 2) | ((tt >> 1) & 3))
+                                    : (8 * (tt & 1) + 4 * ((tt >> 3) & 1) + ((tt >> 1) & 3));
           *reinterpret_cast<__bf16*>(sm.rs.rp + rrow[e] * C::RPS + 2 * ks) = (__bf16)pv;
         }
         if (moved && tt == 0) {
@@ -1085,6 +1087,30 @@ __device__ __forceinline__ void segment(const KParams& p, Smem<C>& sm, int req, 
               for (int mb = 0; mb < C::MB; ++mb) acc[mb][c0 + j] = mfma16(pa8[mb], vf, acc[mb][c0 + j]);
             }
         }
+      } else if constexpr (C::W32) {
+        // 32x32x16: lane block b reads token rows 8 (b / 2) + 2r (then + 1) of 16-column block a_j
+        // (b even) or a_j + d_j (b odd) (tr_b16: lanes 4r .. 4r+3 supply row r), so lane l gets
+        // column l % 32 of the pair for the k-slots 8 (l / 32) .. +8 in the order P was written
+        const int b16 = lane >> 4, li = lane & 15;
+        const char* vrow = st + (8 * (b16 >> 1) + 2 * (li >> 2)) * C::RS + 8 * (li & 3);
+        const uint32_t vbd = lds_addr(vrow + 32 * C::PD * (b16 & 1)), vb1 = lds_addr(vrow + 32 * (b16 & 1));
+        constexpr int NJ = C::CB / 2, VB = 4;   // 32-column blocks per batch of reads
+        sfor<0, (NJ + VB - 1) / VB>([&](auto bb) {
+          constexpr int j0 = VB * bb, nb = NJ - j0 < VB ? NJ - j0 : VB;
+          i32x2 va[VB], vc[VB];
+          sfor<0, nb>([&](auto j) {
+            constexpr int a = C::PAIRS.a[j0 + j];
+            const uint32_t v = C::PAIRS.d[j0 + j] == C::PD ? vbd : vb1;
+            va[j] = ldstr16_off<32 * a>(v);
+            vc[j] = ldstr16_off<32 * a + C::RS>(v);
+          });
+          sfor<0, nb>([&](auto j) {
+            lds_wait_n<2 * (nb - 1 - j)>(vc[j]);
+            lds_wait_n<2 * (nb - 1 - j)>(va[j]);
+            const bf16x8 vf = __builtin_bit_cast(bf16x8, i32x4{va[j][0], va[j][1], vc[j][0], vc[j][1]});
+            acc32[j0 + j] = mfma32(pa32, vf, acc32[j0 + j]);
+          });
+        });
       } else {
         // lane block q reads tokens 4q .. 4q+3 (tr_b16: lanes 4r .. 4r+3 supply token row r); with
         // the reduce-scatter's P, tokens 2r + 8 (q & 1) + (q >> 1) instead: lanes 0-31 then cover
