@@ -44,7 +44,6 @@ typedef __attribute__((__vector_size__(8 * sizeof(short)))) short s16x8;
 
 constexpr int PIDN = 512;    // page ids staged per sub-range
 
-typedef __attribute__((__vector_size__(16 * sizeof(float)))) float f32x16;
 // 32 x 32 x 16 bf16 product (A: lane l holds row l % 32, k 8 (l / 32) .. +8; B: column l % 32, the
 // same k; D: lane l, register v holds row 8 (v / 4) + 4 (l / 32) + v % 4, column l % 32). Twice the
 // flops of the 16x16x16 form per cycle on gfx950.
