@@ -756,23 +756,30 @@ __global__ __launch_bounds__(256) void combine_kernel(const KParams p, int dv) {
 // per workgroup: at 128 x 24 rows the merge took 11.0 us against 11.9 (4 heads) and 15.1 (8 heads).
 constexpr int CH_HB = 2;
 constexpr int CH_NS = 4;   // segments per batch of loads
-// the columns of one (row, head block): H = fp16 partials without the fp8 scale, osc applies it
-template <bool H>
+// the columns of one (row, head block): H = fp16 partials without the fp8 scale, osc applies it;
+// NC adjacent columns per thread (2, or 8 for the wide latent rows, whose partials are then read
+// 16 or 32 bytes a load instead of 4 or 8, in one pass over the columns instead of four), NS
+// segments per batch of loads
+template <bool H, int NC, int NS = CH_NS>
 __device__ __forceinline__ void combine_cols(const KParams& p, int dv, int row, int jq, int req, int h0, int nh,
                                              int w0, int nseg) {
   const int tid = threadIdx.x;
   const int64_t nrow = (int64_t)p.qrows * p.heads;
   const int rl0 = jq * p.heads + h0;
   const float osc = H && p.k_scale ? *p.k_scale : 1.0f;
-  for (int cb = 2 * tid; cb < dv; cb += 512) {
-    float m[CH_HB], l[CH_HB], a0[CH_HB], a1[CH_HB];
+  for (int cb = NC * tid; cb < dv; cb += NC * 256) {
+    float m[CH_HB], l[CH_HB], a[CH_HB][NC];
 #pragma unroll
-    for (int h = 0; h < CH_HB; ++h) m[h] = kNegInf, l[h] = 0.f, a0[h] = 0.f, a1[h] = 0.f;
-    for (int s0 = 0; s0 < nseg; s0 += CH_NS) {
-      float ls[CH_NS][CH_HB];
-      float2 v[CH_NS][CH_HB];
+    for (int h = 0; h < CH_HB; ++h) {
+      m[h] = kNegInf, l[h] = 0.f;
 #pragma unroll
-      for (int k = 0; k < CH_NS; ++k) {
+      for (int c = 0; c < NC; ++c) a[h][c] = 0.f;
+    }
+    for (int s0 = 0; s0 < nseg; s0 += NS) {
+      float ls[NS][CH_HB];
+      float v[NS][CH_HB][NC];
+#pragma unroll
+      for (int k = 0; k < NS; ++k) {
         const int sg = s0 + k < nseg ? s0 + k : nseg - 1;   // past the end: a valid slot, weight 0
         const int64_t slot = (int64_t)w0 + sg + req;
         const float* pl = p.part_lse + slot * nrow + rl0;
@@ -783,11 +790,31 @@ __device__ __forceinline__ void combine_cols(const KParams& p, int dv, int row, 
           const int64_t e = (slot * nrow + rl0 + hh) * (int64_t)dv + cb;   // the slot's element
           if constexpr (H) {
             // fp16 partials: the slot's rows at the start of its (fp32-sized) area
-            const f16x2 t = *reinterpret_cast<const f16x2*>(reinterpret_cast<const _Float16*>(
-                                p.part_o + slot * nrow * (int64_t)dv) + (e - slot * nrow * (int64_t)dv));
-            v[k][h] = make_float2((float)t[0], (float)t[1]);
+            const _Float16* src = reinterpret_cast<const _Float16*>(p.part_o + slot * nrow * (int64_t)dv) +
+                                  (e - slot * nrow * (int64_t)dv);
+            if constexpr (NC == 2) {
+              const f16x2 t = *reinterpret_cast<const f16x2*>(src);
+              v[k][h][0] = (float)t[0];
+              v[k][h][1] = (float)t[1];
+            } else {
+              const f16x8 t = *reinterpret_cast<const f16x8*>(src);
+#pragma unroll
+              for (int c = 0; c < 8; ++c) v[k][h][c] = (float)t[c];
+            }
           } else {
-            v[k][h] = *reinterpret_cast<const float2*>(p.part_o + e);
+            if constexpr (NC == 2) {
+              const float2 t = *reinterpret_cast<const float2*>(p.part_o + e);
+              v[k][h][0] = t.x;
+              v[k][h][1] = t.y;
+            } else {
+              const f32x4 t0 = *reinterpret_cast<const f32x4*>(p.part_o + e);
+              const f32x4 t1 = *reinterpret_cast<const f32x4*>(p.part_o + e + 4);
+#pragma unroll
+              for (int c = 0; c < 4; ++c) {
+                v[k][h][c] = t0[c];
+                v[k][h][4 + c] = t1[c];
+              }
+            }
           }
         }
       }
@@ -798,21 +825,21 @@ __device__ __forceinline__ void combine_cols(const KParams& p, int dv, int row, 
         float mm = m[h];
         bool live = false;
 #pragma unroll
-        for (int k = 0; k < CH_NS; ++k) {
+        for (int k = 0; k < NS; ++k) {
           mm = fmaxf(mm, ls[k][h]);
           live |= !is_neg_inf(ls[k][h]);
         }
         if (!live) continue;
         const float sc = m[h] == kNegInf ? 0.f : __expf(m[h] - mm);
         l[h] *= sc;
-        a0[h] *= sc;
-        a1[h] *= sc;
 #pragma unroll
-        for (int k = 0; k < CH_NS; ++k) {
+        for (int c = 0; c < NC; ++c) a[h][c] *= sc;
+#pragma unroll
+        for (int k = 0; k < NS; ++k) {
           const float wgt = is_neg_inf(ls[k][h]) ? 0.f : __expf(ls[k][h] - mm);
           l[h] += wgt;
-          a0[h] += wgt * v[k][h].x;
-          a1[h] += wgt * v[k][h].y;
+#pragma unroll
+          for (int c = 0; c < NC; ++c) a[h][c] += wgt * v[k][h][c];
         }
         m[h] = mm;
       }
@@ -822,8 +849,9 @@ __device__ __forceinline__ void combine_cols(const KParams& p, int dv, int row, 
       if (h >= nh) continue;
       const float inv = inv_sum(osc, l[h]);
       const int64_t ob = (int64_t)row * p.o_sr + (int64_t)(h0 + h) * p.o_sh + cb;
-      store_out(p.out, p.out_dt, ob, a0[h] * inv);
-      if (cb + 1 < dv) store_out(p.out, p.out_dt, ob + 1, a1[h] * inv);
+#pragma unroll
+      for (int c = 0; c < NC; ++c)
+        if (cb + c < dv) store_out(p.out, p.out_dt, ob + c, a[h][c] * inv);
       if (cb == 0 && p.lse) store_out(p.lse, p.lse_dt, (int64_t)row * p.lse_sr + h0 + h, empty_sum(l[h]) ? kNegInf : m[h] + __logf(l[h]));
     }
   }
@@ -848,8 +876,17 @@ __global__ __launch_bounds__(256) void combine_bal_kernel(const KParams p, int d
   const int w0 = (c0 + p.plan_sw) / chunk, w1 = (c1 - 1) / chunk;
   if (w0 == w1) return;
   const int nseg = w1 - w0 + 1;
-  if (p.part_h) combine_cols<true>(p, dv, row, jq, req, h0, nh, w0, nseg);
-  else combine_cols<false>(p, dv, row, jq, req, h0, nh, w0, nseg);
+  // the wide latent rows: 8 columns a thread (partials 16-byte aligned: dv % 8). Measured at d_c
+  // 1792 (combine stage, bf16 / fp8 rows): 25.4 / 23.8 us with 2 columns, 18.8 / 18.9 with 8; 8
+  // segments a batch instead of 4: 19.0 / 22.3
+  const bool w8 = dv > 1024 && dv % 8 == 0;
+  if (p.part_h) {
+    if (w8) combine_cols<true, 8>(p, dv, row, jq, req, h0, nh, w0, nseg);
+    else combine_cols<true, 2>(p, dv, row, jq, req, h0, nh, w0, nseg);
+  } else {
+    if (w8) combine_cols<false, 8>(p, dv, row, jq, req, h0, nh, w0, nseg);
+    else combine_cols<false, 2>(p, dv, row, jq, req, h0, nh, w0, nseg);
+  }
 }
 
 }  // namespace qmla
