@@ -11,12 +11,14 @@ from tests.mla_cases import check_decode, make_case
 
 pytestmark = pytest.mark.gpu
 
-# (kv, rms, d_c, heads, qrows, groups)
+# (kv, rms, d_c, heads, qrows, groups, rope_w); wide_fp8: the plugin's FP8 rank-1792 row (rope 232 in a
+# 256-column window, 32x32 P.V, fp16 partials through the 8-column combine)
 FAMILIES = {
-    "ws": ("fp8", "log8", 512, 24, 1, 1),
-    "gla": ("fp8", "log8", 512, 24, 4, 2),
-    "partial": ("bf16", "bf16", 512, 24, 1, 1),
-    "wide": ("bf16", "bf16", 1792, 24, 1, 1),
+    "ws": ("fp8", "log8", 512, 24, 1, 1, 64),
+    "gla": ("fp8", "log8", 512, 24, 4, 2, 64),
+    "partial": ("bf16", "bf16", 512, 24, 1, 1, 64),
+    "wide": ("bf16", "bf16", 1792, 24, 1, 1, 64),
+    "wide_fp8": ("fp8", "log8", 1792, 24, 1, 1, 232),
 }
 DTYPES = {"f16": torch.float16, "f32": torch.float32}
 
@@ -26,9 +28,9 @@ DTYPES = {"f16": torch.float16, "f32": torch.float32}
 @pytest.mark.parametrize("family", sorted(FAMILIES))
 def test_output_types(gpu, family, dt, splits):
     import qmla
-    kv, rms, d_c, heads, qrows, groups = FAMILIES[family]
+    kv, rms, d_c, heads, qrows, groups, rope_w = FAMILIES[family]
     lens = [0, 900, 2500, 5]
-    c = make_case(batch=len(lens), heads=heads, d_c=d_c, rope_w=64, page_size=64, lens=lens, kv=kv, rms_mode=rms,
+    c = make_case(batch=len(lens), heads=heads, d_c=d_c, rope_w=rope_w, page_size=64, lens=lens, kv=kv, rms_mode=rms,
                   seed=71, device=gpu, qrows=qrows, groups=groups, rms="spread")
     rows = c.q_nope.shape[0]
     o = torch.full((rows, heads, d_c // groups), float("nan"), dtype=DTYPES[dt], device=gpu)
