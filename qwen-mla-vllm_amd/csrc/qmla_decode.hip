@@ -760,7 +760,7 @@ constexpr int CH_NS = 4;   // segments per batch of loads
 // NC adjacent columns per thread (2, or 8 for the wide latent rows, whose partials are then read
 // 16 or 32 bytes a load instead of 4 or 8, in one pass over the columns instead of four), NS
 // segments per batch of loads
-template <bool H, int NC, int NS = CH_NS>
+template <bool H, int NC, int HB, int NS = CH_NS>
 __device__ __forceinline__ void combine_cols(const KParams& p, int dv, int row, int jq, int req, int h0, int nh,
                                              int w0, int nseg) {
   const int tid = threadIdx.x;
@@ -768,23 +768,23 @@ __device__ __forceinline__ void combine_cols(const KParams& p, int dv, int row, 
   const int rl0 = jq * p.heads + h0;
   const float osc = H && p.k_scale ? *p.k_scale : 1.0f;
   for (int cb = NC * tid; cb < dv; cb += NC * 256) {
-    float m[CH_HB], l[CH_HB], a[CH_HB][NC];
+    float m[HB], l[HB], a[HB][NC];
 #pragma unroll
-    for (int h = 0; h < CH_HB; ++h) {
+    for (int h = 0; h < HB; ++h) {
       m[h] = kNegInf, l[h] = 0.f;
 #pragma unroll
       for (int c = 0; c < NC; ++c) a[h][c] = 0.f;
     }
     for (int s0 = 0; s0 < nseg; s0 += NS) {
-      float ls[NS][CH_HB];
-      float v[NS][CH_HB][NC];
+      float ls[NS][HB];
+      float v[NS][HB][NC];
 #pragma unroll
       for (int k = 0; k < NS; ++k) {
         const int sg = s0 + k < nseg ? s0 + k : nseg - 1;   // past the end: a valid slot, weight 0
         const int64_t slot = (int64_t)w0 + sg + req;
         const float* pl = p.part_lse + slot * nrow + rl0;
 #pragma unroll
-        for (int h = 0; h < CH_HB; ++h) {
+        for (int h = 0; h < HB; ++h) {
           const int hh = h < nh ? h : 0;
           ls[k][h] = s0 + k < nseg ? pl[hh] : kNegInf;
           const int64_t e = (slot * nrow + rl0 + hh) * (int64_t)dv + cb;   // the slot's element
@@ -819,7 +819,7 @@ __device__ __forceinline__ void combine_cols(const KParams& p, int dv, int row, 
         }
       }
 #pragma unroll
-      for (int h = 0; h < CH_HB; ++h) {
+      for (int h = 0; h < HB; ++h) {
         // segments without tokens (lse -inf) weigh 0 and a batch of them only is skipped; a NaN lse
         // (fmaxf skips it) weighs NaN, so a row whose inputs hold a NaN merges to NaN
         float mm = m[h];
@@ -845,7 +845,7 @@ __device__ __forceinline__ void combine_cols(const KParams& p, int dv, int row, 
       }
     }
 #pragma unroll
-    for (int h = 0; h < CH_HB; ++h) {
+    for (int h = 0; h < HB; ++h) {
       if (h >= nh) continue;
       const float inv = inv_sum(osc, l[h]);
       const int64_t ob = (int64_t)row * p.o_sr + (int64_t)(h0 + h) * p.o_sh + cb;
@@ -857,12 +857,15 @@ __device__ __forceinline__ void combine_cols(const KParams& p, int dv, int row, 
   }
 }
 
+// HB heads per workgroup: CH_HB, or 1 on the wide latent rows (d_c 1792 rank 1792, combine stage
+// bf16 / fp8 rows: 18.9 / 18.6 us with 2 heads, 17.4 / 16.9 with 1, 21.5 / 22.4 with 4)
+template <int HB>
 __global__ __launch_bounds__(256) void combine_bal_kernel(const KParams p, int dv) {
   const int hblk = blockIdx.x, row = blockIdx.y;
   const int tid = threadIdx.x;
   const int req = row / p.qrows, jq = row - req * p.qrows;
-  const int h0 = hblk * CH_HB;
-  const int nh = p.heads - h0 < CH_HB ? p.heads - h0 : CH_HB;
+  const int h0 = hblk * HB;
+  const int nh = p.heads - h0 < HB ? p.heads - h0 : HB;
   const int chunk = p.plan[0];
   const int c0 = p.plan[2 + req], c1 = p.plan[3 + req];
   if (c1 <= c0) {  // empty request: zero output, -inf lse
@@ -881,11 +884,11 @@ __global__ __launch_bounds__(256) void combine_bal_kernel(const KParams p, int d
   // segments a batch instead of 4: 19.0 / 22.3
   const bool w8 = dv > 1024 && dv % 8 == 0;
   if (p.part_h) {
-    if (w8) combine_cols<true, 8>(p, dv, row, jq, req, h0, nh, w0, nseg);
-    else combine_cols<true, 2>(p, dv, row, jq, req, h0, nh, w0, nseg);
+    if (w8) combine_cols<true, 8, HB>(p, dv, row, jq, req, h0, nh, w0, nseg);
+    else combine_cols<true, 2, HB>(p, dv, row, jq, req, h0, nh, w0, nseg);
   } else {
-    if (w8) combine_cols<false, 8>(p, dv, row, jq, req, h0, nh, w0, nseg);
-    else combine_cols<false, 2>(p, dv, row, jq, req, h0, nh, w0, nseg);
+    if (w8) combine_cols<false, 8, HB>(p, dv, row, jq, req, h0, nh, w0, nseg);
+    else combine_cols<false, 2, HB>(p, dv, row, jq, req, h0, nh, w0, nseg);
   }
 }
 
@@ -1226,8 +1229,9 @@ static int run_combine(const qmla_decode_params* p, KParams& k, hipStream_t st) 
   void* args[] = {&k, &dv};
   if (p->num_splits == 0 && (dv & 1)) return QMLA_ERR_SHAPE;   // the balanced combine reads column pairs
   if (p->num_splits == 0)
-    return launch((const void*)&combine_bal_kernel, dim3((p->heads + CH_HB - 1) / CH_HB, p->rows, 1),
-                  dim3(256, 1, 1), args, st);
+    return dv > 1024 ? launch((const void*)&combine_bal_kernel<1>, dim3(p->heads, p->rows, 1), dim3(256, 1, 1), args, st)
+                     : launch((const void*)&combine_bal_kernel<CH_HB>, dim3((p->heads + CH_HB - 1) / CH_HB, p->rows, 1),
+                              dim3(256, 1, 1), args, st);
   return launch((const void*)&combine_kernel, dim3(p->heads, p->rows, 1), dim3(256, 1, 1), args, st);
 }
 
