@@ -99,6 +99,21 @@ def test_wsb_scalar_loads_drained_before_lds(tmp_path):
     assert n >= 1
 
 
+def test_cs_scalar_loads_drained_before_lds(tmp_path):
+    """The column-split decode (d_c 1792 and the rank-768 window) counts its LDS waits the same way;
+    its inline-asm read statements keep their addresses too."""
+    lines = _assembly(tmp_path, "qmla_cs.hip")
+    n = 0
+    for name, body in _kernels(lines, r"^_ZN4qmla2cs9cs_kernel\S*:"):
+        n += 1
+        hz = _hazards(body)
+        assert not hz, f"{name}: scalar load in flight at an LDS operation: {hz[:3]}"
+        assert any("lgkmcnt(" in l and "lgkmcnt(0)" not in l for l in body), "counted waits expected"
+        ov = _asm_read_overlaps(body)
+        assert not ov, f"{name}: a read's destination is a later read's address: {ov[:2]}"
+    assert n >= 1
+
+
 def test_hazard_check_sees_a_planted_overlap():
     body = ["s_load_dword s4, s[0:1], 0x10", "ds_read_b128 v[0:3], v4", "s_waitcnt lgkmcnt(0)"]
     assert _hazards(body)
