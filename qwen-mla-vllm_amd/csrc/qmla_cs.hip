@@ -1236,73 +1236,73 @@ __device__ __forceinline__ void segment(const KParams& p, Smem<C>& sm, int req, 
       }
     }
   } else {
-  // the lane's row group and column through an empty asm (as above)
-  int lgx = lg, lnx = ln16;
-  asm volatile("" : "+v"(lgx), "+v"(lnx));
+    // the lane's row group and column through an empty asm (as above)
+    int lgx = lg, lnx = ln16;
+    asm volatile("" : "+v"(lgx), "+v"(lnx));
 #pragma unroll
-  for (int mb = 0; mb < C::MB; ++mb) {
-    const float l = lrow[mb];
-    const float lse_v = row_lse(mref[mb], l);
-    const float inv = inv_sum(kscale, l);   // fp8 values were accumulated unscaled
-    const float invh = inv_sum(1.0f, l);    // ... and are stored so as fp16 partials
-    const bool ph = !so.final_out && so.plse && p.part_h;
-    float iv[4];
-    if constexpr (C::RSC) {
+    for (int mb = 0; mb < C::MB; ++mb) {
+      const float l = lrow[mb];
+      const float lse_v = row_lse(mref[mb], l);
+      const float inv = inv_sum(kscale, l);   // fp8 values were accumulated unscaled
+      const float invh = inv_sum(1.0f, l);    // ... and are stored so as fp16 partials
+      const bool ph = !so.final_out && so.plse && p.part_h;
+      float iv[4];
+      if constexpr (C::RSC) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const float l_i = sm.rs.rfin[1][16 * mb + 4 * lgx + i];
+          iv[i] = ph ? inv_sum(1.0f, l_i) : inv_sum(kscale, l_i);
+        }
+      } else {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) iv[i] = __shfl(ph ? invh : inv, 4 * lgx + i);
+      }
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        const float l_i = sm.rs.rfin[1][16 * mb + 4 * lgx + i];
-        iv[i] = ph ? inv_sum(1.0f, l_i) : inv_sum(kscale, l_i);
-      }
-    } else {
+        const int r = rbase + 16 * mb + 4 * lgx + i;
+        if (r >= rows_pg) continue;
+        const int jq = r / hpg, hh = r - jq * hpg;
+        const int head = g * hpg + hh;
+        const int col = c * C::DCW + lnx;
+        if (so.final_out) {
+          const int64_t ob = (int64_t)(row0 + jq) * p.o_sr + (int64_t)head * p.o_sh + col;
+          if (p.out_dt == QMLA_DT_BF16) {
+            __bf16* o = reinterpret_cast<__bf16*>(p.out) + ob;
 #pragma unroll
-      for (int i = 0; i < 4; ++i) iv[i] = __shfl(ph ? invh : inv, 4 * lgx + i);
-    }
+            for (int cb = 0; cb < C::CB; ++cb) o[16 * cb] = (__bf16)(acc[mb][cb][i] * iv[i]);
+          } else if (p.out_dt == QMLA_DT_F16) {
+            _Float16* o = reinterpret_cast<_Float16*>(p.out) + ob;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int r = rbase + 16 * mb + 4 * lgx + i;
-      if (r >= rows_pg) continue;
-      const int jq = r / hpg, hh = r - jq * hpg;
-      const int head = g * hpg + hh;
-      const int col = c * C::DCW + lnx;
-      if (so.final_out) {
-        const int64_t ob = (int64_t)(row0 + jq) * p.o_sr + (int64_t)head * p.o_sh + col;
-        if (p.out_dt == QMLA_DT_BF16) {
-          __bf16* o = reinterpret_cast<__bf16*>(p.out) + ob;
+            for (int cb = 0; cb < C::CB; ++cb) o[16 * cb] = (_Float16)(acc[mb][cb][i] * iv[i]);
+          } else {
+            float* o = reinterpret_cast<float*>(p.out) + ob;
 #pragma unroll
-          for (int cb = 0; cb < C::CB; ++cb) o[16 * cb] = (__bf16)(acc[mb][cb][i] * iv[i]);
-        } else if (p.out_dt == QMLA_DT_F16) {
-          _Float16* o = reinterpret_cast<_Float16*>(p.out) + ob;
+            for (int cb = 0; cb < C::CB; ++cb) o[16 * cb] = acc[mb][cb][i] * iv[i];
+          }
+        } else if (ph) {
+          _Float16* ob = reinterpret_cast<_Float16*>(so.po) + (int64_t)jq * so.po_sr + (int64_t)head * so.po_sh + col;
 #pragma unroll
-          for (int cb = 0; cb < C::CB; ++cb) o[16 * cb] = (_Float16)(acc[mb][cb][i] * iv[i]);
+          for (int cb = 0; cb < C::CB; ++cb) ob[16 * cb] = (_Float16)(acc[mb][cb][i] * iv[i]);
         } else {
-          float* o = reinterpret_cast<float*>(p.out) + ob;
+          float* ob = so.po + (int64_t)jq * so.po_sr + (int64_t)head * so.po_sh + col;
 #pragma unroll
-          for (int cb = 0; cb < C::CB; ++cb) o[16 * cb] = acc[mb][cb][i] * iv[i];
+          for (int cb = 0; cb < C::CB; ++cb) ob[16 * cb] = acc[mb][cb][i] * iv[i];
         }
-      } else if (ph) {
-        _Float16* ob = reinterpret_cast<_Float16*>(so.po) + (int64_t)jq * so.po_sr + (int64_t)head * so.po_sh + col;
-#pragma unroll
-        for (int cb = 0; cb < C::CB; ++cb) ob[16 * cb] = (_Float16)(acc[mb][cb][i] * iv[i]);
-      } else {
-        float* ob = so.po + (int64_t)jq * so.po_sr + (int64_t)head * so.po_sh + col;
-#pragma unroll
-        for (int cb = 0; cb < C::CB; ++cb) ob[16 * cb] = acc[mb][cb][i] * iv[i];
+      }
+      // lse from the score layout (row lnx + 16mb), one lane per row (reduce-scatter: below)
+      const int r = rbase + lnx + 16 * mb;
+      if (!C::RSC && c == 0 && lgx == 0 && r < rows_pg) {
+        const int jq = r / hpg, hh = r - jq * hpg;
+        const int head = g * hpg + hh;
+        if (so.final_out) {
+          if (p.lse) store_out(p.lse, p.lse_dt, (int64_t)(row0 + jq) * p.lse_sr + head, lse_v);
+        } else if (so.plse) {
+          so.plse[(int64_t)jq * so.plse_sr + head] = lse_v;
+        } else {
+          so.po[(int64_t)jq * so.po_sr + (int64_t)head * so.po_sh + C::DCG] = lse_v;
+        }
       }
     }
-    // lse from the score layout (row lnx + 16mb), one lane per row (reduce-scatter: below)
-    const int r = rbase + lnx + 16 * mb;
-    if (!C::RSC && c == 0 && lgx == 0 && r < rows_pg) {
-      const int jq = r / hpg, hh = r - jq * hpg;
-      const int head = g * hpg + hh;
-      if (so.final_out) {
-        if (p.lse) store_out(p.lse, p.lse_dt, (int64_t)(row0 + jq) * p.lse_sr + head, lse_v);
-      } else if (so.plse) {
-        so.plse[(int64_t)jq * so.plse_sr + head] = lse_v;
-      } else {
-        so.po[(int64_t)jq * so.po_sr + (int64_t)head * so.po_sh + C::DCG] = lse_v;
-      }
-    }
-  }
   }
   if constexpr (C::RSC) {
     // the reducer lane of each row writes its lse
