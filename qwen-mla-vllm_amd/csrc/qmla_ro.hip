@@ -82,6 +82,13 @@ struct Smem {
   int win[4];
 };
 
+// Chunk rotation of staged row r (chunk_pos / pos_chunk of the shared row layout): odd rows shift
+// their chunks by one inside each region. A ds_read_b128 is served 32 lanes at a time over 128
+// banks here (measured: 16 rows of 608 bytes x two 16-byte chunks two apart run at 32 cycles per
+// read and wave with four waves, contiguous lanes at 25), and with this rotation the compute
+// waves' K reads (16 rows x the chunks of two lane groups per 32 lanes) fill the 128 banks once
+__device__ __forceinline__ int rflip(int r) { return r & 1; }
+
 // byte offset of staged row r in a stage (two halves of 16 rows)
 template <class C>
 __device__ __forceinline__ int rowoff(int r) {
@@ -245,7 +252,7 @@ __device__ __forceinline__ void role_main(const KParams& p, Smem<C>& sm, float k
       const bool pad = qq >= 16 * C::CPR;
       const int q = pad ? 0 : qq;
       const int rr = 16 * dw + q / C::CPR, pp = q % C::CPR;
-      doff[j] = pad ? 0x80000000u : (uint32_t)(rr * C::RB + 16 * pos_chunk<C::CPR>(pp, lflip<C::CPR>(rr)));
+      doff[j] = pad ? 0x80000000u : (uint32_t)(rr * C::RB + 16 * pos_chunk<C::CPR>(pp, rflip(rr)));
       drow[j] = pad ? -1 : rr;
     }
   }
@@ -254,7 +261,7 @@ __device__ __forceinline__ void role_main(const KParams& p, Smem<C>& sm, float k
   // column n's tokens for lane group 2(L >> 1) and bytes 4-7 for lane group 2(L >> 1) + 1
   uint32_t cva = 0, cvb = 0, cvw = 0;
   if constexpr (ROLE == DMA) {
-    const int R = 16 * dw + 8 * (lg >> 1) + (ln16 >> 1), fr = lflip<C::CPR>(R), k0 = lg & 1;
+    const int R = 16 * dw + 8 * (lg >> 1) + (ln16 >> 1), fr = rflip(R), k0 = lg & 1;
     cva = (uint32_t)(rowoff<C>(R) + 16 * (k0 + fr) + 8 * (ln16 & 1));
     cvb = (uint32_t)(rowoff<C>(R) + 16 * ((6 + k0 + fr) & 7) + 8 * (ln16 & 1));
     cvw = (uint32_t)(k0 * 1024 + (32 * (lg >> 1) + ln16) * 16 + 8 * dw);
@@ -409,7 +416,7 @@ __device__ __forceinline__ void role_main(const KParams& p, Smem<C>& sm, float k
       for (int tb = 0; tb < 2; ++tb)
 #pragma unroll
         for (int h = 0; h < 2; ++h) {
-          const int krow = 16 * tb + ln16, fk = lflip<C::CPR>(krow);
+          const int krow = 16 * tb + ln16, fk = rflip(krow);
           koff[tb][h] = (uint32_t)(rowoff<C>(krow) + 16 * (grp * (C::DCG / 16) + ((2 * lg + h + fk) & 7)));
           kofr[tb][h] = (uint32_t)(rowoff<C>(krow) + 16 * (C::DC / 16 + ((2 * lg + h + fk) & 3)));
         }
@@ -421,7 +428,7 @@ __device__ __forceinline__ void role_main(const KParams& p, Smem<C>& sm, float k
 #pragma unroll
         for (int i = 0; i < NCI; ++i) {
           const int row = 16 * tb + 4 * lg + (quad ? (ln16 & 3) : i);
-          coff[tb][i] = (uint32_t)(rowoff<C>(row) + 16 * chunk_pos<C::CPR>(rms_b >> 4, lflip<C::CPR>(row)) + (rms_b & 15));
+          coff[tb][i] = (uint32_t)(rowoff<C>(row) + 16 * chunk_pos<C::CPR>(rms_b >> 4, rflip(row)) + (rms_b & 15));
         }
 #pragma clang loop unroll(disable)
       for (int g = 0; g < ntot; ++g) {
