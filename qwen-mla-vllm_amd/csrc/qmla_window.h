@@ -102,14 +102,16 @@ struct SegD {
 
 // Staged row layout of fp8 MLA rows (4 latent blocks of 8 16-byte chunks, the rope's 4 chunks, then
 // the rms codes' CPR - 36): each chunk stays in its region, rotated there by the row's flip f(r).
-// 608-byte rows (CPR 38, 152 dwords: rows 24 banks apart, 8 rows per bank period) flip by
-// ((r >> 3) + (r >> 4)) & 1, so 16 consecutive rows (K reads) and rows r, r + 16 (transposed V reads
-// of one lane group) land on distinct banks; 592-byte rows (CPR 37, 20 banks apart) need no flip for
-// those patterns. Reads of one latent block then share a base register per lane and pattern, the
+// A ds_read_b128 is served 32 lanes at a time over 128 banks (measured: 16 rows of 608 bytes x two
+// chunks two apart run at 32 cycles per read and wave with four waves, contiguous lanes at 25). So
+// 608-byte rows (CPR 38, 152 dwords: rows 24 banks apart mod 128) flip by (r & 1) ^ ((r >> 4) & 1):
+// the K reads of 16 consecutive rows by two lane groups (chunks 2lg + h) and the transposed V reads
+// of rows 8lg .. 8lg+7 (32 or 64 lanes a pass) then fill the banks once; 592-byte rows (CPR 37)
+// take no flip. Reads of one latent block then share a base register per lane and pattern, the
 // block and chunk going into the instructions' offset fields.
 template <int CPR>
 __device__ __forceinline__ int lflip(int r) {
-  return CPR == 38 ? ((r >> 3) + (r >> 4)) & 1 : 0;
+  return CPR == 38 ? (r & 1) ^ ((r >> 4) & 1) : 0;
 }
 template <int CPR>
 __device__ __forceinline__ int region_base(int c) {
