@@ -180,9 +180,10 @@ struct CS {
   static constexpr bool W32 = RSC && NTB == 1 && MB == 2 && CB % 2 == 0 && NTG == 1;
   // The 32 columns of a 32x32 block are two 16-column blocks (a, a + d): lanes 0-31 of a
   // transposed V read cover 8 rows x 16 bytes (fp8) or 4 rows x 32 bytes (bf16: token rows 2r,
-  // then 2r + 1) of each, and with the odd 16-byte row stride the rows of one block fill one half
-  // of the 64 LDS banks, the other block the other half exactly when d blocks are 128 bytes
-  // (mod 256): fp8 d = 8, bf16 d = 4. A leftover pair takes d = 1 (two-way conflicts in that read).
+  // then 2r + 1) of each. The LDS serves 32 lanes at a time over 128 four-byte banks; with the odd
+  // 16-byte row stride the rows of one block take half of the four-bank groups they can reach and
+  // the block 128 bytes away (fp8 d = 8, bf16 d = 4) the other half, so the read has no conflicts.
+  // A leftover pair takes d = 1 (two-way conflicts in that read).
   static constexpr int PD = EB == 1 ? 8 : 4;
   struct Pairs {
     int a[CB / 2 > 0 ? CB / 2 : 1], d[CB / 2 > 0 ? CB / 2 : 1];
@@ -1114,7 +1115,7 @@ __device__ __forceinline__ void segment(const KParams& p, Smem<C>& sm, int req, 
         // lane block q reads tokens 4q .. 4q+3 (tr_b16: lanes 4r .. 4r+3 supply token row r); with
         // the reduce-scatter's P, tokens 2r + 8 (q & 1) + (q >> 1) instead: lanes 0-31 then cover
         // the 8 even rows (the odd ones in lanes 32-63), which with the odd 16-byte row stride
-        // fill the 64 LDS banks once instead of twice
+        // touch each LDS bank once instead of twice
         const int vrow = C::RSC ? 2 * (ln16 >> 2) + 8 * (lg & 1) + (lg >> 1) : 4 * lg + (ln16 >> 2);
         const uint32_t vb = lds_addr(st + vrow * C::RS + 8 * (ln16 & 3));
         constexpr int VB = 7;   // column blocks per batch of reads, each used as soon as it is in
